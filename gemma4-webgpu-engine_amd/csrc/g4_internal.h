@@ -1,0 +1,113 @@
+// Shared internals of libg4w8a8: status plumbing (host) and the SRQ / epilogue arithmetic (device).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <string>
+
+#include "../../include/g4w8a8.h"
+
+namespace g4 {
+
+// ---- host: status and last error ----------------------------------------------------------------
+
+int set_error(int status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+int hip_status(hipError_t err, const char *what);
+
+#define G4_HIP(call)                                              \
+    do {                                                          \
+        hipError_t g4_err_ = (call);                              \
+        if (g4_err_ != hipSuccess) return ::g4::hip_status(g4_err_, #call); \
+    } while (0)
+
+// The launch error of the last kernel, checked right after every launch.
+#define G4_LAUNCHED(what)                                         \
+    do {                                                          \
+        hipError_t g4_err_ = hipGetLastError();                   \
+        if (g4_err_ != hipSuccess) return ::g4::hip_status(g4_err_, what); \
+    } while (0)
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+// ---- device: the static range quantization arithmetic (src/quant.ts:248-357) -----------------
+
+// srqCodes at 8 bits: clamp(RNE(f32(v / s)), -128, 127). __fdiv_rn is the IEEE binary32 divide;
+// rintf is round-half-to-even (v_rndne_f32). fmaxf drops a NaN, so NaN lands on -128 exactly as
+// WGSL's clamp = min(max(e, lo), hi) does on the reference (qgemv.ts:620-626).
+__device__ __forceinline__ float srq_code_f(float v, float s) {
+    float r = rintf(__fdiv_rn(v, s));
+    return fminf(fmaxf(r, -128.0f), 127.0f);
+}
+
+__device__ __forceinline__ int srq_code_i(float v, float s) { return (int)srq_code_f(v, s); }
+
+// The closing expression of every quantized linear (qgemv.ts:1168-1172, :680-686), in its order:
+// one f32 multiply folds the input scale into the row scale, one more multiplies the reduced sum.
+__device__ __forceinline__ float linear_epilogue(float in_scale, float row_scale, float sum) {
+    return __fmul_rn(__fmul_rn(in_scale, row_scale), sum);
+}
+
+// Stores one output element of a linear in the requested kind. `y` is the pre-snap f32 value and
+// `acc` the exact integer sum (calibrated path only; 0 on the f32 path).
+__device__ __forceinline__ void store_linear_out(void *dst, int64_t idx, int out_kind, float y,
+                                                 int acc, float out_scale) {
+    if (out_kind == G4_KIND_I8) {
+        reinterpret_cast<int8_t *>(dst)[idx] = (int8_t)srq_code_i(y, out_scale);
+    } else if (out_kind == G4_KIND_I32) {
+        reinterpret_cast<int32_t *>(dst)[idx] = acc;
+    } else {
+        float v = y;
+        if (out_scale != 0.0f) v = __fmul_rn(srq_code_f(y, out_scale), out_scale);
+        reinterpret_cast<float *>(dst)[idx] = v;
+    }
+}
+
+// Reads activation element i of kind f32 / f16 as f32 (f16 widening is exact).
+__device__ __forceinline__ float load_act(const void *x, int kind, int64_t i) {
+    if (kind == G4_KIND_F16) return __half2float(reinterpret_cast<const __half *>(x)[i]);
+    return reinterpret_cast<const float *>(x)[i];
+}
+
+// ---- device: cross-lane sums --------------------------------------------------------------------
+
+// Sum over each aligned group of 16 lanes (one DPP row), result in every lane of the group.
+// quad_perm(1,0,3,2), quad_perm(2,3,0,1), row_half_mirror, row_mirror.
+__device__ __forceinline__ int row16_sum_i32(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+    return v;
+}
+
+__device__ __forceinline__ float dpp_f32_b1(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_f32_4e(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_f32_half_mirror(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_f32_mirror(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false));
+}
+
+// The same 16-lane tree in f32: ((l0+l1)+(l2+l3)) + ((l4+l5)+(l6+l7)) + ... pairwise, every lane
+// ends with the identical value because each step adds a commutative pair.
+__device__ __forceinline__ float row16_sum_f32(float v) {
+    v = __fadd_rn(v, dpp_f32_b1(v));
+    v = __fadd_rn(v, dpp_f32_4e(v));
+    v = __fadd_rn(v, dpp_f32_half_mirror(v));
+    v = __fadd_rn(v, dpp_f32_mirror(v));
+    return v;
+}
+
+}  // namespace g4

@@ -1,0 +1,593 @@
+// The M-column quantized linears on gfx950 int8 MFMA: qgemm-4bit (src/kernels/qgemm.ts) and
+// qmatmul-8bit (src/kernels/pleMatmul.ts), plus the shape routing of src/execute.ts:372-430.
+//
+// Pipeline of one call (calibrated path):
+//  1. quantize_rows_kernel snaps x [M][K] once into int8 codes (the SRQ input prologue), written
+//     to a per-stream workspace with each 8-code group interleaved [x0 x2 x4 x6 x1 x3 x5 x7] for
+//     4-bit weights (so a weight word's low and high nibble lanes line up with the codes without
+//     a shuffle), and sum(xq) per row for the 4-bit zero point.
+//  2. An MFMA kernel contracts codes x weights with v_mfma_i32_16x16x64_i8. The 4-bit weights are
+//     unpacked to unsigned nibbles (w & 0x0F0F0F0F, (w >> 4) & 0x0F0F0F0F) and the zero point comes
+//     off once per output as -8 * sum(xq[m]). The int32 accumulators are exact, so the k order the
+//     MFMA uses internally is irrelevant; only the A and B operands have to agree on it, and they
+//     do because both are filled with the same (lane group, byte) -> k assignment.
+//  3. The epilogue is the reference's f32(f32(inScale * scale[n]) * f32(acc)) and output snap.
+//
+// Kernels by M (chosen per shape, see pick_kernel):
+//   M <= 2         the GEMV family (qgemv.hip): bit-identical, cheaper than any tile at this M.
+//   3 <= M <= 32   qgemm_skinny_kernel: 16 weight rows per block, the 4 waves split K, the weight
+//                  stream is read once with 16-byte lane loads, an LDS fold of the 4 partials.
+//   M > 32         qgemm_tile_kernel: 128 x 128 output tiles, 4 waves of 64 x 64, K staged through
+//                  double-buffered LDS in 128-code steps, XCD-aware tile order.
+#include "g4_internal.h"
+
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <utility>
+
+namespace g4 {
+
+int gemv_columns(int bits, const void *wq, const float *scales, const void *x, int x_kind,
+                 void *dst, int out_kind, int k, int num_rows, int m_cols, float in_scale,
+                 float out_scale, hipStream_t stream, const char *who);
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kQuantThreads = 256;
+constexpr int kTileBK = 128;
+
+__device__ __forceinline__ uint32_t pack4b(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+           ((uint32_t)(d & 0xff) << 24);
+}
+
+// One block per token row: snap K activations into codes (interleaved when PERM), zero the pad to
+// kp, and write sum(codes) for the row.
+template <bool PERM>
+__global__ __launch_bounds__(kQuantThreads) void quantize_rows_kernel(
+    const void *x, int x_kind, int k, int kp, float scale, int8_t *codes, int *row_sums) {
+    __shared__ int s_sum;
+    const int m = blockIdx.x;
+    const int tid = threadIdx.x;
+    if (tid == 0) s_sum = 0;
+    __syncthreads();
+    int local = 0;
+    const int groups = kp >> 3;
+    const int live = k >> 3;
+    for (int g = tid; g < groups; g += kQuantThreads) {
+        int c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (g < live) {
+            const int64_t e = (int64_t)m * k + (int64_t)g * 8;
+            if (x_kind == G4_KIND_I8) {
+                const uint2 v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const int8_t *>(x) + e);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    c[i] = (int)(int8_t)((v.x >> (8 * i)) & 0xff);
+                    c[4 + i] = (int)(int8_t)((v.y >> (8 * i)) & 0xff);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) c[i] = srq_code_i(load_act(x, x_kind, e + i), scale);
+            }
+        }
+        uint2 out;
+        if (PERM) {
+            out.x = pack4b(c[0], c[2], c[4], c[6]);
+            out.y = pack4b(c[1], c[3], c[5], c[7]);
+        } else {
+            out.x = pack4b(c[0], c[1], c[2], c[3]);
+            out.y = pack4b(c[4], c[5], c[6], c[7]);
+        }
+        *reinterpret_cast<uint2 *>(codes + (int64_t)m * kp + (int64_t)g * 8) = out;
+        local += c[0] + c[1] + c[2] + c[3] + c[4] + c[5] + c[6] + c[7];
+    }
+    local = row16_sum_i32(local);
+    if ((tid & 15) == 0 && local != 0) atomicAdd(&s_sum, local);
+    __syncthreads();
+    if (tid == 0) row_sums[m] = s_sum;
+}
+
+// srqCodes as a kernel (quant.ts:309-334), natural order.
+__global__ void srq_quantize_kernel(const void *x, int x_kind, int8_t *codes, int64_t n, float s) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = i; e < n; e += stride) codes[e] = (int8_t)srq_code_i(load_act(x, x_kind, e), s);
+}
+
+// The B operand of one 16x16x64 step from 8 bytes (16 codes) of weights at `p`.
+template <int BITS>
+__device__ __forceinline__ v4i b_operand(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                         int step) {
+    v4i b;
+    if (BITS == 4) {
+        const uint32_t a = step == 0 ? w0 : w2;
+        const uint32_t c = step == 0 ? w1 : w3;
+        b.x = (int)(a & 0x0F0F0F0Fu);
+        b.y = (int)((a >> 4) & 0x0F0F0F0Fu);
+        b.z = (int)(c & 0x0F0F0F0Fu);
+        b.w = (int)((c >> 4) & 0x0F0F0F0Fu);
+    } else {
+        (void)w2;
+        (void)w3;
+        b.x = (int)w0;
+        b.y = (int)w1;
+        b.z = (int)w2;
+        b.w = (int)w3;
+    }
+    return b;
+}
+
+__device__ __forceinline__ void store_tile_out(void *dst, int m, int n, int N, int out_kind,
+                                               int acc, float in_scale, float scale,
+                                               float out_scale) {
+    const float y = linear_epilogue(in_scale, scale, (float)acc);
+    store_linear_out(dst, (int64_t)m * N + n, out_kind, y, acc, out_scale);
+}
+
+// ---- skinny: M <= MT token rows, 16 weight rows per block, K split over the 4 waves ---------
+// Lane (j = lane % 16, g = lane / 16) owns weight row n0 + j. Per 128-code step kb it loads 16
+// bytes of that row: 4-bit codes kb*128 + g*32 .. +32 (8-bit: kb*128 + g*32 .. +16 per half
+// step). MFMA half-step s in {0,1} takes codes g*32 + s*16 .. +16 of the step from both operands.
+template <int BITS, int MT>
+__global__ __launch_bounds__(256) void qgemm_skinny_kernel(
+    const int8_t *__restrict__ A, const int *__restrict__ row_sums, const uint8_t *__restrict__ W,
+    const float *__restrict__ scales, void *dst, int M, int N, int K, int kp, float in_scale,
+    float out_scale, int out_kind) {
+    constexpr int TM = MT / 16;
+    __shared__ v4i red[3][TM][64];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int j = lane & 15;
+    const int g = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int m0 = blockIdx.y * MT;
+    const int n = min(n0 + j, N - 1);
+    const int row_bytes = BITS == 4 ? (K >> 1) : K;
+    const int ksteps = K / kTileBK;
+    const uint8_t *wrow = W + (int64_t)n * row_bytes;
+
+    v4i acc[TM];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) acc[t] = v4i{0, 0, 0, 0};
+
+    const int8_t *arow[TM];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) arow[t] = A + (int64_t)min(m0 + t * 16 + j, M - 1) * kp;
+
+    constexpr int BATCH = 4;
+    for (int kb0 = wave; kb0 < ksteps; kb0 += 4 * BATCH) {
+        uint4 bw[BATCH][BITS == 4 ? 1 : 2];
+        uint4 av[BATCH][TM][2];
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+            const int kb = kb0 + 4 * u;
+            if (kb < ksteps) {
+                if (BITS == 4) {
+                    bw[u][0] = *reinterpret_cast<const uint4 *>(wrow + kb * 64 + g * 16);
+                } else {
+                    bw[u][0] = *reinterpret_cast<const uint4 *>(wrow + kb * 128 + g * 32);
+                    bw[u][BITS == 4 ? 0 : 1] =
+                        *reinterpret_cast<const uint4 *>(wrow + kb * 128 + g * 32 + 16);
+                }
+#pragma unroll
+                for (int t = 0; t < TM; ++t) {
+                    const uint4 *ap = reinterpret_cast<const uint4 *>(arow[t] + kb * 128 + g * 32);
+                    av[u][t][0] = ap[0];
+                    av[u][t][1] = ap[1];
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+            const int kb = kb0 + 4 * u;
+            if (kb < ksteps) {
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    v4i b;
+                    if (BITS == 4) {
+                        b = b_operand<4>(bw[u][0].x, bw[u][0].y, bw[u][0].z, bw[u][0].w, s);
+                    } else {
+                        const uint4 q = bw[u][BITS == 4 ? 0 : s];
+                        b = v4i{(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+                    }
+#pragma unroll
+                    for (int t = 0; t < TM; ++t) {
+                        const uint4 q = av[u][t][s];
+                        const v4i a = v4i{(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+                        acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[t], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+    // Fold the four waves' partial tiles through LDS, then wave 0 writes.
+    if (wave > 0) {
+#pragma unroll
+        for (int t = 0; t < TM; ++t) red[wave - 1][t][lane] = acc[t];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+            v4i a = acc[t];
+#pragma unroll
+            for (int w = 0; w < 3; ++w) a += red[w][t][lane];
+            // D layout: lane l, register r -> row 4 * (l / 16) + r of A, column l % 16 of B.
+            const int nn = n0 + j;
+            if (nn < N) {
+                const float scale = scales[nn];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = m0 + t * 16 + 4 * g + r;
+                    if (m < M) {
+                        int v = a[r];
+                        if (BITS == 4) v -= 8 * row_sums[m];
+                        store_tile_out(dst, m, nn, N, out_kind, v, in_scale, scale, out_scale);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ---- tile: 128 x 128 outputs per block, 4 waves of 64 x 64, K in 128-code LDS stages --------
+template <int BITS>
+__global__ __launch_bounds__(256) void qgemm_tile_kernel(
+    const int8_t *__restrict__ A, const int *__restrict__ row_sums, const uint8_t *__restrict__ W,
+    const float *__restrict__ scales, void *dst, int M, int N, int K, int kp, float in_scale,
+    float out_scale, int out_kind, int tiles_m, int tiles_n, int xcd_swizzle) {
+    constexpr int BM = 128, BN = 128, BK = kTileBK;
+    constexpr int A_STRIDE = BK + 16;
+    constexpr int B_ROW = BITS == 4 ? BK / 2 : BK;
+    constexpr int B_STRIDE = B_ROW + 16;
+    constexpr int A_CHUNKS = BM * BK / 16 / 256;      // 16-byte chunks per thread per stage
+    constexpr int B_CHUNKS = BN * B_ROW / 16 / 256;
+    __shared__ __align__(16) uint8_t sA[2][BM * A_STRIDE];
+    __shared__ __align__(16) uint8_t sB[2][BN * B_STRIDE];
+
+    const int b = blockIdx.x;
+    int tm, tn;
+    if (xcd_swizzle) {
+        // Blocks are dealt to the 8 XCDs round robin; keep the blocks of one weight tile (all its
+        // M tiles) on one XCD so its L2 fetches those weight bytes once.
+        const int xcd = b & 7;
+        const int idx = b >> 3;
+        tm = idx % tiles_m;
+        tn = (idx / tiles_m) * 8 + xcd;
+    } else {
+        tm = b % tiles_m;
+        tn = b / tiles_m;
+    }
+    if (tn >= tiles_n) return;
+    const int m0 = tm * BM;
+    const int n0 = tn * BN;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+    const int j = lane & 15;
+    const int g = lane >> 4;
+    const int row_bytes = BITS == 4 ? (K >> 1) : K;
+    const int ksteps = K / BK;
+
+    // Global source addresses of this thread's staging chunks (rows clamped; stores are guarded).
+    const int8_t *a_src[A_CHUNKS];
+    int a_dst[A_CHUNKS];
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; ++i) {
+        const int q = tid + 256 * i;
+        const int row = q >> 3, c16 = q & 7;
+        a_src[i] = A + (int64_t)min(m0 + row, M - 1) * kp + c16 * 16;
+        a_dst[i] = row * A_STRIDE + c16 * 16;
+    }
+    const uint8_t *b_src[B_CHUNKS];
+    int b_dst[B_CHUNKS];
+#pragma unroll
+    for (int i = 0; i < B_CHUNKS; ++i) {
+        const int q = tid + 256 * i;
+        const int per_row = B_ROW / 16;
+        const int row = q / per_row, c16 = q % per_row;
+        b_src[i] = W + (int64_t)min(n0 + row, N - 1) * row_bytes + c16 * 16;
+        b_dst[i] = row * B_STRIDE + c16 * 16;
+    }
+
+    uint4 ra[A_CHUNKS], rb[B_CHUNKS];
+    auto load_stage = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < A_CHUNKS; ++i)
+            ra[i] = *reinterpret_cast<const uint4 *>(a_src[i] + kb * BK);
+#pragma unroll
+        for (int i = 0; i < B_CHUNKS; ++i)
+            rb[i] = *reinterpret_cast<const uint4 *>(b_src[i] + kb * B_ROW);
+    };
+    auto store_stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < A_CHUNKS; ++i) *reinterpret_cast<uint4 *>(&sA[buf][a_dst[i]]) = ra[i];
+#pragma unroll
+        for (int i = 0; i < B_CHUNKS; ++i) *reinterpret_cast<uint4 *>(&sB[buf][b_dst[i]]) = rb[i];
+    };
+
+    v4i acc[4][4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y) acc[x][y] = v4i{0, 0, 0, 0};
+
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+    for (int kb = 0; kb < ksteps; ++kb) {
+        const int buf = kb & 1;
+        if (kb + 1 < ksteps) load_stage(kb + 1);
+        const uint8_t *la = sA[buf];
+        const uint8_t *lb = sB[buf];
+        uint4 bq[4][BITS == 4 ? 1 : 2];
+#pragma unroll
+        for (int y = 0; y < 4; ++y) {
+            const int col = wn * 64 + y * 16 + j;
+            if (BITS == 4) {
+                bq[y][0] = *reinterpret_cast<const uint4 *>(lb + col * B_STRIDE + g * 16);
+            } else {
+                bq[y][0] = *reinterpret_cast<const uint4 *>(lb + col * B_STRIDE + g * 32);
+                bq[y][BITS == 4 ? 0 : 1] =
+                    *reinterpret_cast<const uint4 *>(lb + col * B_STRIDE + g * 32 + 16);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            v4i bo[4];
+#pragma unroll
+            for (int y = 0; y < 4; ++y) {
+                if (BITS == 4) {
+                    bo[y] = b_operand<4>(bq[y][0].x, bq[y][0].y, bq[y][0].z, bq[y][0].w, s);
+                } else {
+                    const uint4 q = bq[y][BITS == 4 ? 0 : s];
+                    bo[y] = v4i{(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+                }
+            }
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                const int row = wm * 64 + x * 16 + j;
+                const uint4 q = *reinterpret_cast<const uint4 *>(la + row * A_STRIDE + g * 32 + s * 16);
+                const v4i ao = v4i{(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+#pragma unroll
+                for (int y = 0; y < 4; ++y)
+                    acc[x][y] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ao, bo[y], acc[x][y], 0, 0, 0);
+            }
+        }
+        if (kb + 1 < ksteps) store_stage(buf ^ 1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int y = 0; y < 4; ++y) {
+        const int n = n0 + wn * 64 + y * 16 + j;
+        if (n >= N) continue;
+        const float scale = scales[n];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + wm * 64 + x * 16 + 4 * g + r;
+                if (m < M) {
+                    int v = acc[x][y][r];
+                    if (BITS == 4) v -= 8 * row_sums[m];
+                    store_tile_out(dst, m, n, N, out_kind, v, in_scale, scale, out_scale);
+                }
+            }
+        }
+    }
+}
+
+// ---- per-stream workspace for the snapped activation codes ------------------------------------
+
+struct Workspace {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+
+static std::mutex g_ws_mu;
+static std::map<std::pair<int, void *>, Workspace> g_ws;
+
+// Returns a device buffer of at least `bytes` owned by (device, stream). Calls on one stream are
+// ordered, so they may share it; calls on different streams get different buffers.
+static int workspace(void *stream, size_t bytes, void **out) {
+    int dev = 0;
+    G4_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    Workspace &ws = g_ws[{dev, stream}];
+    if (ws.bytes < bytes) {
+        if (ws.ptr) {
+            G4_HIP(hipStreamSynchronize(as_stream(stream)));
+            G4_HIP(hipFree(ws.ptr));
+            ws.ptr = nullptr;
+            ws.bytes = 0;
+        }
+        size_t grow = std::max(bytes, (size_t)4 << 20);
+        G4_HIP(hipMalloc(&ws.ptr, grow));
+        ws.bytes = grow;
+    }
+    *out = ws.ptr;
+    return G4_OK;
+}
+
+enum KernelChoice { K_GEMV = 0, K_SKINNY16, K_SKINNY32, K_TILE128, K_GEMV_F32, K_GEMV_COLS };
+
+static KernelChoice pick_kernel(int bits, int m, int n, int k, float in_scale) {
+    (void)n;
+    if (in_scale == 0.0f) return K_GEMV_F32;
+    if (m <= 2) return K_GEMV;
+    if (k % kTileBK != 0) return K_GEMV_COLS;
+    if (m <= 16) return K_SKINNY16;
+    if (m <= 32) return K_SKINNY32;
+    (void)bits;
+    return K_TILE128;
+}
+
+static const char *choice_name(KernelChoice c, int bits) {
+    switch (c) {
+        case K_GEMV: return bits == 4 ? "qgemv-4bit" : "qgemv-8bit";
+        case K_SKINNY16: return bits == 4 ? "qgemm-4bit-mfma-skinny16" : "qmatmul-8bit-mfma-skinny16";
+        case K_SKINNY32: return bits == 4 ? "qgemm-4bit-mfma-skinny32" : "qmatmul-8bit-mfma-skinny32";
+        case K_TILE128: return bits == 4 ? "qgemm-4bit-mfma-tile128" : "qmatmul-8bit-mfma-tile128";
+        case K_GEMV_F32: return bits == 4 ? "qgemv-4bit-f32" : "qgemv-8bit-f32";
+        default: return bits == 4 ? "qgemv-4bit-columns" : "qgemv-8bit-columns";
+    }
+}
+
+template <int BITS>
+static int launch_mfma(KernelChoice c, const int8_t *codes, const int *sums, const uint8_t *w,
+                       const float *scales, void *dst, int m, int n, int k, int kp,
+                       float in_scale, float out_scale, int out_kind, hipStream_t stream) {
+    if (c == K_SKINNY16 || c == K_SKINNY32) {
+        const int mt = c == K_SKINNY16 ? 16 : 32;
+        dim3 grid((n + 15) / 16, (m + mt - 1) / mt);
+        if (c == K_SKINNY16)
+            hipLaunchKernelGGL((qgemm_skinny_kernel<BITS, 16>), grid, dim3(256), 0, stream, codes,
+                               sums, w, scales, dst, m, n, k, kp, in_scale, out_scale, out_kind);
+        else
+            hipLaunchKernelGGL((qgemm_skinny_kernel<BITS, 32>), grid, dim3(256), 0, stream, codes,
+                               sums, w, scales, dst, m, n, k, kp, in_scale, out_scale, out_kind);
+        G4_LAUNCHED("qgemm_skinny_kernel");
+        return G4_OK;
+    }
+    const int tiles_m = (m + 127) / 128;
+    const int tiles_n = (n + 127) / 128;
+    const int swizzle = (tiles_n % 8 == 0) ? 1 : 0;
+    hipLaunchKernelGGL((qgemm_tile_kernel<BITS>), dim3(tiles_m * tiles_n), dim3(256), 0, stream,
+                       codes, sums, w, scales, dst, m, n, k, kp, in_scale, out_scale, out_kind,
+                       tiles_m, tiles_n, swizzle);
+    G4_LAUNCHED("qgemm_tile_kernel");
+    return G4_OK;
+}
+
+static int check_linear(int bits, const void *wq, const float *scales, const void *x, int x_kind,
+                        void *dst, int out_kind, int k, int n, int m, float in_scale,
+                        float out_scale, const char *who) {
+    if (!wq || !scales || !x || !dst)
+        return set_error(G4_ERR_INVALID, "%s needs inputs named wq, scales and x", who);
+    if (k <= 0 || n <= 0 || m <= 0)
+        return set_error(G4_ERR_INVALID, "%s needs params.k, params.numRows and params.mCols", who);
+    if (bits != 4 && bits != 8) return set_error(G4_ERR_INVALID, "%s: bits must be 4 or 8", who);
+    if (x_kind != G4_KIND_F32 && x_kind != G4_KIND_F16 && x_kind != G4_KIND_I8)
+        return set_error(G4_ERR_INVALID, "%s: x_kind %d is not f32, f16 or int8", who, x_kind);
+    if (out_kind != G4_KIND_F32 && out_kind != G4_KIND_I8 && out_kind != G4_KIND_I32)
+        return set_error(G4_ERR_INVALID, "%s: out_kind %d is not f32, int8 or int32", who, out_kind);
+    if (out_kind == G4_KIND_I8 && out_scale == 0.0f)
+        return set_error(G4_ERR_INVALID, "%s: int8 output codes need a calibrated outScale", who);
+    if (in_scale == 0.0f && (x_kind == G4_KIND_I8 || out_kind == G4_KIND_I32))
+        return set_error(G4_ERR_INVALID,
+                         "%s: inScale 0.0 is the uncalibrated f32 path (no int8 codes, no int32 "
+                         "accumulator)", who);
+    if ((reinterpret_cast<uintptr_t>(wq) & 15) || (reinterpret_cast<uintptr_t>(x) & 15))
+        return set_error(G4_ERR_INVALID, "%s: wq and x must be 16-byte aligned", who);
+    if ((int64_t)m * (int64_t)n > (int64_t)INT32_MAX)
+        return set_error(G4_ERR_INVALID, "%s: M * N exceeds the 32-bit index range", who);
+    return G4_OK;
+}
+
+static int run_linear(int bits, const void *wq, const float *scales, const void *x, int x_kind,
+                      void *dst, int out_kind, int k, int n, int m, float in_scale,
+                      float out_scale, hipStream_t stream, const char *who) {
+    const KernelChoice c = pick_kernel(bits, m, n, k, in_scale);
+    if (c == K_GEMV || c == K_GEMV_F32 || c == K_GEMV_COLS)
+        return gemv_columns(bits, wq, scales, x, x_kind, dst, out_kind, k, n, m, in_scale,
+                            out_scale, stream, who);
+    if (k > 16384)
+        return set_error(G4_ERR_INVALID, "%s: K %d exceeds 16384 (the exact int32/f32 bound)", who, k);
+    const int kp = k;  // k % 128 == 0 on the MFMA kernels
+    const size_t code_bytes = (size_t)m * kp;
+    const size_t sum_off = (code_bytes + 255) & ~(size_t)255;
+    void *ws = nullptr;
+    int rc = workspace(stream, sum_off + (size_t)m * sizeof(int), &ws);
+    if (rc) return rc;
+    int8_t *codes = reinterpret_cast<int8_t *>(ws);
+    int *sums = reinterpret_cast<int *>(reinterpret_cast<uint8_t *>(ws) + sum_off);
+    if (bits == 4)
+        hipLaunchKernelGGL(quantize_rows_kernel<true>, dim3(m), dim3(kQuantThreads), 0, stream, x,
+                           x_kind, k, kp, in_scale, codes, sums);
+    else
+        hipLaunchKernelGGL(quantize_rows_kernel<false>, dim3(m), dim3(kQuantThreads), 0, stream, x,
+                           x_kind, k, kp, in_scale, codes, sums);
+    G4_LAUNCHED("quantize_rows_kernel");
+    const uint8_t *w = reinterpret_cast<const uint8_t *>(wq);
+    if (bits == 4)
+        return launch_mfma<4>(c, codes, sums, w, scales, dst, m, n, k, kp, in_scale, out_scale,
+                              out_kind, stream);
+    return launch_mfma<8>(c, codes, sums, w, scales, dst, m, n, k, kp, in_scale, out_scale,
+                          out_kind, stream);
+}
+
+}  // namespace g4
+
+using namespace g4;
+
+extern "C" {
+
+// qgemm-4bit (qgemm.ts:589-639) and qmatmul-8bit (pleMatmul.ts:257-303).
+int g4_qgemm(int bits, const void *wq, const float *scales, const void *x, int x_kind, void *dst,
+             int out_kind, int k, int num_rows, int m_cols, float in_scale, float out_scale,
+             void *stream) {
+    const char *who = bits == 4 ? "qgemm-4bit" : "qmatmul-8bit";
+    if (bits == 4) {
+        if (k <= 0 || num_rows <= 0 || m_cols <= 0)
+            return set_error(G4_ERR_INVALID, "qgemm needs params.k, params.numRows and params.mCols");
+        if (k % 256 != 0)
+            return set_error(G4_ERR_INVALID, "qgemm-4bit needs K a multiple of 256, got %d", k);
+    } else if (bits == 8) {
+        if (k <= 0 || num_rows <= 0 || m_cols <= 0)
+            return set_error(G4_ERR_INVALID,
+                             "qmatmul-8bit needs params.k and params.numRows, with params.mCols "
+                             "absent for a decode step");
+        if (k % 4 != 0)
+            return set_error(G4_ERR_INVALID,
+                             "qmatmul-8bit needs K a multiple of 4, got %d. Both real tensors are 1536 "
+                             "and 256, so a caller that does not is packing the wrong tensor.", k);
+        if (k % 16 != 0)
+            return set_error(G4_ERR_UNSUPPORTED,
+                             "qmatmul-8bit: K %d is a multiple of 4 but not of 16, which this path "
+                             "does not implement", k);
+    } else {
+        return set_error(G4_ERR_INVALID, "qgemm: bits must be 4 or 8, got %d", bits);
+    }
+    int rc = check_linear(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols,
+                          in_scale, out_scale, who);
+    if (rc) return rc;
+    return run_linear(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols, in_scale,
+                      out_scale, as_stream(stream), who);
+}
+
+int g4_linear(int bits, const void *wq, const float *scales, const void *x, int x_kind, void *dst,
+              int out_kind, int k, int num_rows, int m_cols, float in_scale, float out_scale,
+              void *stream) {
+    return g4_qgemm(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols, in_scale,
+                    out_scale, stream);
+}
+
+int g4_kernel_for_shape(int bits, int m_cols, int num_rows, int k, char *buf, size_t buf_len) {
+    if (!buf || buf_len == 0) return set_error(G4_ERR_INVALID, "g4_kernel_for_shape: no buffer");
+    const char *name = choice_name(pick_kernel(bits, m_cols, num_rows, k, 1.0f), bits);
+    snprintf(buf, buf_len, "%s", name);
+    return G4_OK;
+}
+
+int g4_srq_quantize(const void *x, int x_kind, int8_t *codes, int64_t n, float scale,
+                    void *stream) {
+    if (!x || !codes || n < 0) return set_error(G4_ERR_INVALID, "srq quantize: bad arguments");
+    if (x_kind != G4_KIND_F32 && x_kind != G4_KIND_F16)
+        return set_error(G4_ERR_INVALID, "srq quantize: x_kind must be f32 or f16");
+    if (scale == 0.0f)
+        return set_error(G4_ERR_INVALID, "srq quantize: a scale of 0.0 means uncalibrated; there are no codes");
+    if (n == 0) return G4_OK;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(srq_quantize_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                       x, x_kind, codes, n, scale);
+    G4_LAUNCHED("srq_quantize_kernel");
+    return G4_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,647 @@
+// The decode GEMV family on gfx950: qgemv-4bit / qgemv-8bit (M = 1), the wide -m2 forms (M = 2),
+// the projection batches (qkv / gate-up), the grouped layer GEMV, and the split-K build with its
+// two folds (src/kernels/qgemv.ts, qgemvWide.ts, projectionBatch.ts, exactSplit.ts).
+//
+// Layout of one launch. A block is 256 threads = 4 wave64s. Each wave serves 4 output rows at a
+// time, one per 16-lane DPP row, so a block covers 16 rows per pass and `passes` passes. A lane
+// streams 16-byte chunks of its row (chunk lane16 + 16 t), so the 16 lanes of a row read 256
+// contiguous bytes per load instruction and the 4 rows of a wave read 4 such runs.
+//
+// The calibrated (integer) path. The block snaps its activation columns once into LDS as int8
+// codes (IEEE f32 divide, ties to even, clamp), and accumulates sum(u * xq) with v_dot4_i32_i8,
+// where u = nibble in [0, 15] (4-bit) or the signed byte (8-bit). The 4-bit zero point comes off
+// once per row as -8 * sum(xq), which is exact integer arithmetic: sum((u - 8) * x) =
+// sum(u * x) - 8 sum(x). To dot a word's low nibbles [k0 k2 k4 k6] and high nibbles [k1 k3 k5 k7]
+// without shuffling the weights, the LDS code layout interleaves each 8-code group as
+// [x0 x2 x4 x6 | x1 x3 x5 x7]. The int32 row sum is exact (|sum| <= K * 8 * 128 < 2^31), so the
+// order of the reduction does not matter, and the epilogue is the reference's expression.
+//
+// The uncalibrated (inScale == 0) path keeps the f32 code dot: per lane in k order, then the fixed
+// 16-lane DPP tree (row16_sum_f32).
+#include "g4_internal.h"
+
+#include <algorithm>
+#include <vector>
+
+namespace g4 {
+
+constexpr int kGemvThreads = 256;
+constexpr int kRowsPerPass = 16;
+constexpr int kMaxGemvK = 16384;
+constexpr int kChunkBatch = 4;
+
+struct GemvJob {
+    const uint8_t *w;
+    const float *scales;
+    const void *x;
+    void *dst;
+    int bits;
+    int x_kind;
+    int out_kind;
+    int k;
+    int rows;
+    float in_scale;
+    float out_scale;
+    int wg_begin;
+    int passes;
+};
+
+struct GemvLaunch {
+    GemvJob job[G4_MAX_GROUP];
+    int count;
+    int splits;       // 1: plain GEMV. > 1: split-K partials [rows][splits] (one job, one column)
+    int split_exact;  // split only: 1 writes raw integer partials, 0 the scaled ones
+};
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+           ((uint32_t)(d & 0xff) << 24);
+}
+
+// Band of the split-K cut in codes, mirroring qgemv.ts:521-548 at one word per lane: kIters whole
+// 32-word iterations plus the guarded tail slot (always counted unless the partials are exact).
+__device__ __forceinline__ void split_band(int k, int bits, int splits, int split, int exact,
+                                           int &c_lo, int &c_hi) {
+    if (splits <= 1) {
+        c_lo = 0;
+        c_hi = k;
+        return;
+    }
+    int cpw = bits == 4 ? 8 : 4;
+    int k_words = k / cpw;
+    int k_iters = k_words / 32;
+    int slots = k_iters + (exact ? ((k_words % 32) != 0 ? 1 : 0) : 1);
+    int per = (slots + splits - 1) / splits;
+    int lo = min(split * per, slots);
+    int hi = min(lo + per, slots);
+    int w_lo = lo * 32;
+    int w_hi = min(hi, k_iters) * 32;
+    if (hi > k_iters) w_hi = k_words;
+    if (w_lo > w_hi) w_lo = w_hi;
+    c_lo = w_lo * cpw;
+    c_hi = w_hi * cpw;
+}
+
+__device__ __forceinline__ int find_job(const GemvLaunch &L, int b) {
+    int j = 0;
+#pragma unroll
+    for (int i = 1; i < G4_MAX_GROUP; ++i)
+        if (i < L.count && b >= L.job[i].wg_begin) j = i;
+    return j;
+}
+
+// Snap 8 activations starting at element e (f32, f16 or ready int8 codes) into codes c[0..7].
+__device__ __forceinline__ void load_codes8(const void *x, int kind, int64_t e, float s, int c[8]) {
+    if (kind == G4_KIND_I8) {
+        uint2 v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const int8_t *>(x) + e);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            c[i] = (int)(int8_t)((v.x >> (8 * i)) & 0xff);
+            c[4 + i] = (int)(int8_t)((v.y >> (8 * i)) & 0xff);
+        }
+    } else if (kind == G4_KIND_F16) {
+        uint4 v = *reinterpret_cast<const uint4 *>(reinterpret_cast<const __half *>(x) + e);
+        uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __half lo = __ushort_as_half((unsigned short)(w[i] & 0xffff));
+            __half hi = __ushort_as_half((unsigned short)(w[i] >> 16));
+            c[2 * i] = srq_code_i(__half2float(lo), s);
+            c[2 * i + 1] = srq_code_i(__half2float(hi), s);
+        }
+    } else {
+        const float4 *p = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(x) + e);
+        float4 a = p[0], b = p[1];
+        c[0] = srq_code_i(a.x, s);
+        c[1] = srq_code_i(a.y, s);
+        c[2] = srq_code_i(a.z, s);
+        c[3] = srq_code_i(a.w, s);
+        c[4] = srq_code_i(b.x, s);
+        c[5] = srq_code_i(b.y, s);
+        c[6] = srq_code_i(b.z, s);
+        c[7] = srq_code_i(b.w, s);
+    }
+}
+
+template <int COLS>
+__global__ __launch_bounds__(kGemvThreads) void qgemv_int_kernel(GemvLaunch L) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int s_sum[COLS];
+
+    const int j = find_job(L, blockIdx.x);
+    const GemvJob &J = L.job[j];
+    const int tid = threadIdx.x;
+    const int bits = J.bits;
+    const int k = J.k;
+    const int split = blockIdx.y;
+    int c_lo, c_hi;
+    split_band(k, bits, L.splits, split, L.split_exact, c_lo, c_hi);
+    const int kl = c_hi - c_lo;              // codes in this block's band (multiple of 32 or 16)
+    const int lds_stride = (kl + 15) & ~15;  // bytes of codes per column in LDS
+
+    if (tid < COLS) s_sum[tid] = 0;
+    __syncthreads();
+
+    // ---- snap the activation band into LDS (once per block) ----
+    {
+        const int groups = kl >> 3;
+        int local = 0;
+        int my_col = 0;
+        for (int g = tid; g < groups * COLS; g += kGemvThreads) {
+            const int col = COLS == 1 ? 0 : g / groups;
+            const int gi = COLS == 1 ? g : g - col * groups;
+            int c[8];
+            const int64_t e = (int64_t)col * k + c_lo + gi * 8;
+            load_codes8(J.x, J.x_kind, e, J.in_scale, c);
+            uint2 packed;
+            if (bits == 4) {
+                packed.x = pack4(c[0], c[2], c[4], c[6]);
+                packed.y = pack4(c[1], c[3], c[5], c[7]);
+            } else {
+                packed.x = pack4(c[0], c[1], c[2], c[3]);
+                packed.y = pack4(c[4], c[5], c[6], c[7]);
+            }
+            *reinterpret_cast<uint2 *>(smem + col * lds_stride + gi * 8) = packed;
+            int sum8 = c[0] + c[1] + c[2] + c[3] + c[4] + c[5] + c[6] + c[7];
+            if (COLS == 1) {
+                local += sum8;
+            } else {
+                atomicAdd(&s_sum[col], sum8);
+            }
+            my_col = col;
+        }
+        (void)my_col;
+        if (COLS == 1) {
+            local = row16_sum_i32(local);
+            if ((tid & 15) == 0 && local != 0) atomicAdd(&s_sum[0], local);
+        }
+    }
+    __syncthreads();
+
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lane16 = lane & 15;
+    const int row_bytes = bits == 4 ? (k >> 1) : k;
+    const int cpc = bits == 4 ? 32 : 16;  // codes per 16-byte chunk
+    const int cb0 = c_lo / cpc;
+    const int nch = kl / cpc;
+    const int T = (nch + 15) >> 4;
+    const int row_block = (blockIdx.x - J.wg_begin) * (J.passes * kRowsPerPass);
+
+    int sx[COLS];
+#pragma unroll
+    for (int c = 0; c < COLS; ++c) sx[c] = s_sum[c];
+
+    for (int p = 0; p < J.passes; ++p) {
+        const int wave_row0 = row_block + p * kRowsPerPass + wave * 4;
+        if (wave_row0 >= J.rows) break;  // uniform per wave
+        const int row = wave_row0 + (lane >> 4);
+        const int rrow = min(row, J.rows - 1);
+        const uint8_t *wrow = J.w + (int64_t)rrow * row_bytes + (int64_t)cb0 * 16;
+
+        int acc[COLS];
+#pragma unroll
+        for (int c = 0; c < COLS; ++c) acc[c] = 0;
+
+        uint4 cur[kChunkBatch];
+#pragma unroll
+        for (int u = 0; u < kChunkBatch; ++u) {
+            const int ch = u * 16 + lane16;
+            cur[u] = (u < T && ch < nch) ? *reinterpret_cast<const uint4 *>(wrow + (int64_t)ch * 16)
+                                         : make_uint4(0, 0, 0, 0);
+        }
+        for (int t0 = 0; t0 < T; t0 += kChunkBatch) {
+            uint4 nxt[kChunkBatch];
+#pragma unroll
+            for (int u = 0; u < kChunkBatch; ++u) {
+                const int t = t0 + kChunkBatch + u;
+                const int ch = t * 16 + lane16;
+                nxt[u] = (t < T && ch < nch)
+                             ? *reinterpret_cast<const uint4 *>(wrow + (int64_t)ch * 16)
+                             : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < kChunkBatch; ++u) {
+                const int t = t0 + u;
+                const int ch = t * 16 + lane16;
+                if (t < T && ch < nch) {
+                    const uint32_t wv[4] = {cur[u].x, cur[u].y, cur[u].z, cur[u].w};
+#pragma unroll
+                    for (int c = 0; c < COLS; ++c) {
+                        const uint8_t *xl = smem + c * lds_stride;
+                        if (bits == 4) {
+                            const uint4 xa = *reinterpret_cast<const uint4 *>(xl + ch * 32);
+                            const uint4 xb = *reinterpret_cast<const uint4 *>(xl + ch * 32 + 16);
+                            const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+                            int a = acc[c];
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const uint32_t lo = wv[i] & 0x0F0F0F0Fu;
+                                const uint32_t hi = (wv[i] >> 4) & 0x0F0F0F0Fu;
+                                a = __builtin_amdgcn_sdot4((int)lo, (int)xv[2 * i], a, false);
+                                a = __builtin_amdgcn_sdot4((int)hi, (int)xv[2 * i + 1], a, false);
+                            }
+                            acc[c] = a;
+                        } else {
+                            const uint4 xa = *reinterpret_cast<const uint4 *>(xl + ch * 16);
+                            int a = acc[c];
+                            a = __builtin_amdgcn_sdot4((int)wv[0], (int)xa.x, a, false);
+                            a = __builtin_amdgcn_sdot4((int)wv[1], (int)xa.y, a, false);
+                            a = __builtin_amdgcn_sdot4((int)wv[2], (int)xa.z, a, false);
+                            a = __builtin_amdgcn_sdot4((int)wv[3], (int)xa.w, a, false);
+                            acc[c] = a;
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kChunkBatch; ++u) cur[u] = nxt[u];
+        }
+
+#pragma unroll
+        for (int c = 0; c < COLS; ++c) {
+            int s = row16_sum_i32(acc[c]);
+            if (bits == 4) s -= 8 * sx[c];
+            acc[c] = s;
+        }
+        if (lane16 == 0 && row < J.rows) {
+            const float scale = J.scales[row];
+            if (L.splits > 1) {
+                const float part = L.split_exact
+                                       ? (float)acc[0]
+                                       : linear_epilogue(J.in_scale, scale, (float)acc[0]);
+                reinterpret_cast<float *>(J.dst)[(int64_t)row * L.splits + split] = part;
+            } else {
+#pragma unroll
+                for (int c = 0; c < COLS; ++c) {
+                    const float y = linear_epilogue(J.in_scale, scale, (float)acc[c]);
+                    store_linear_out(J.dst, (int64_t)c * J.rows + row, J.out_kind, y, acc[c],
+                                     J.out_scale);
+                }
+            }
+        }
+    }
+}
+
+// The uncalibrated f32 code dot (inScale == 0, qgemv.ts:666-675): x stays f32 in LDS, each lane
+// sums code * x over its chunks in k order (separate rounded multiply and add), then the 16-lane
+// tree. One column per blockIdx.z. Parity against the reference's order is unpinned beyond the
+// exact-grid fixtures (the reference's own f32 order is adapter dependent).
+__global__ __launch_bounds__(kGemvThreads) void qgemv_f32_kernel(GemvLaunch L) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    float *xs = reinterpret_cast<float *>(smem);
+    const int j = find_job(L, blockIdx.x);
+    const GemvJob &J = L.job[j];
+    const int tid = threadIdx.x;
+    const int k = J.k;
+    const int col = blockIdx.z;
+    for (int i = tid; i < k; i += kGemvThreads) xs[i] = load_act(J.x, J.x_kind, (int64_t)col * k + i);
+    __syncthreads();
+    const int lane = tid & 63, wave = tid >> 6, lane16 = lane & 15;
+    const int bits = J.bits;
+    const int row_bytes = bits == 4 ? (k >> 1) : k;
+    const int cpc = bits == 4 ? 32 : 16;
+    const int nch = k / cpc;
+    const int row_block = (blockIdx.x - J.wg_begin) * (J.passes * kRowsPerPass);
+    for (int p = 0; p < J.passes; ++p) {
+        const int wave_row0 = row_block + p * kRowsPerPass + wave * 4;
+        if (wave_row0 >= J.rows) break;
+        const int row = wave_row0 + (lane >> 4);
+        const int rrow = min(row, J.rows - 1);
+        const uint8_t *wrow = J.w + (int64_t)rrow * row_bytes;
+        float acc = 0.0f;
+        for (int ch = lane16; ch < nch; ch += 16) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(wrow + (int64_t)ch * 16);
+            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+            const float *xc = xs + ch * cpc;
+            if (bits == 4) {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const int code = (int)((wv[i >> 3] >> (4 * (i & 7))) & 0xf) - 8;
+                    acc = __fadd_rn(acc, __fmul_rn((float)code, xc[i]));
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int code = (int)(int8_t)((wv[i >> 2] >> (8 * (i & 3))) & 0xff);
+                    acc = __fadd_rn(acc, __fmul_rn((float)code, xc[i]));
+                }
+            }
+        }
+        const float sum = row16_sum_f32(acc);
+        if (lane16 == 0 && row < J.rows) {
+            const float y = linear_epilogue(1.0f, J.scales[row], sum);
+            store_linear_out(J.dst, (int64_t)col * J.rows + row, J.out_kind, y, 0, J.out_scale);
+        }
+    }
+}
+
+// qgemv-merge (qgemv.ts:1027-1072) and qgemv-exact-merge (exactSplit.ts:45-57).
+__global__ void qgemv_merge_kernel(const float *part, const float *scales, void *dst, int out_kind,
+                                   int rows, int splits, int exact, float in_scale,
+                                   float out_scale) {
+    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    float t = 0.0f;
+    for (int s = 0; s < splits; ++s) t = __fadd_rn(t, part[(int64_t)row * splits + s]);
+    const float y = exact ? linear_epilogue(in_scale, scales[row], t) : t;
+    store_linear_out(dst, row, out_kind, y, 0, out_scale);
+}
+
+// ---- host side ----------------------------------------------------------------------------------
+
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Validates one job against what the kernels assume (shape, alignment, kinds). `who` names the
+// registry kernel in the message.
+int check_job(const GemvJob &J, int cols, const char *who) {
+    if (!J.w || !J.scales || !J.x || !J.dst)
+        return set_error(G4_ERR_INVALID, "%s needs inputs named wq, scales and x, and an output", who);
+    if (J.bits != 4 && J.bits != 8)
+        return set_error(G4_ERR_INVALID, "%s: bits must be 4 or 8, got %d", who, J.bits);
+    if (J.k <= 0 || J.rows <= 0)
+        return set_error(G4_ERR_INVALID, "%s needs params.k and params.numRows", who);
+    const int cpc = J.bits == 4 ? 32 : 16;
+    if (J.k % cpc != 0)
+        return set_error(G4_ERR_INVALID, "%s: K %d does not fill whole 16-byte chunks", who, J.k);
+    if (J.k > kMaxGemvK)
+        return set_error(G4_ERR_INVALID, "%s: K %d exceeds %d (the exact int32/f32 bound)", who, J.k,
+                         kMaxGemvK);
+    if (J.x_kind != G4_KIND_F32 && J.x_kind != G4_KIND_F16 && J.x_kind != G4_KIND_I8)
+        return set_error(G4_ERR_INVALID, "%s: x_kind %d is not f32, f16 or int8", who, J.x_kind);
+    if (J.out_kind != G4_KIND_F32 && J.out_kind != G4_KIND_I8 && J.out_kind != G4_KIND_I32)
+        return set_error(G4_ERR_INVALID, "%s: out_kind %d is not f32, int8 or int32", who,
+                         J.out_kind);
+    if (J.out_kind == G4_KIND_I8 && J.out_scale == 0.0f)
+        return set_error(G4_ERR_INVALID,
+                         "%s: int8 output codes need a calibrated outScale (0.0 means no output snap)",
+                         who);
+    if (J.in_scale == 0.0f && (J.x_kind == G4_KIND_I8 || J.out_kind == G4_KIND_I32))
+        return set_error(G4_ERR_INVALID,
+                         "%s: inScale 0.0 is the uncalibrated f32 path, which has no int8 input codes "
+                         "and no integer accumulator", who);
+    if (!std::isfinite(J.in_scale) || !std::isfinite(J.out_scale))
+        return set_error(G4_ERR_INVALID, "%s: scales must be finite", who);
+    if (!aligned16(J.w) || !aligned16(J.x))
+        return set_error(G4_ERR_INVALID, "%s: wq and x must be 16-byte aligned", who);
+    if (cols < 1 || cols > 2) return set_error(G4_ERR_INVALID, "%s: cols %d not in 1..2", who, cols);
+    return G4_OK;
+}
+
+// Picks passes per block so the launch offers a few blocks per CU without starving small jobs.
+static void plan_blocks(GemvLaunch &L, int max_passes) {
+    int64_t total_groups = 0;
+    for (int i = 0; i < L.count; ++i) total_groups += (L.job[i].rows + kRowsPerPass - 1) / kRowsPerPass;
+    const int64_t target_blocks = 8LL * device_cu_count();
+    int passes = 1;
+    while (passes < max_passes && total_groups / passes > target_blocks) passes *= 2;
+    int wg = 0;
+    for (int i = 0; i < L.count; ++i) {
+        L.job[i].passes = passes;
+        L.job[i].wg_begin = wg;
+        wg += (L.job[i].rows + passes * kRowsPerPass - 1) / (passes * kRowsPerPass);
+    }
+}
+
+static int total_blocks(const GemvLaunch &L) {
+    const GemvJob &last = L.job[L.count - 1];
+    return last.wg_begin + (last.rows + last.passes * kRowsPerPass - 1) / (last.passes * kRowsPerPass);
+}
+
+// Launches the integer or f32 GEMV over L.count jobs with `cols` token columns (1 or 2).
+int launch_gemv(GemvLaunch &L, int cols, hipStream_t stream) {
+    if (L.count < 1 || L.count > G4_MAX_GROUP)
+        return set_error(G4_ERR_INVALID, "grouped GEMV: count %d not in 1..%d", L.count, G4_MAX_GROUP);
+    const bool calibrated = L.job[0].in_scale != 0.0f;
+    for (int i = 1; i < L.count; ++i)
+        if ((L.job[i].in_scale != 0.0f) != calibrated)
+            return set_error(G4_ERR_UNSUPPORTED,
+                             "grouped GEMV: calibrated and uncalibrated projections in one launch");
+    if (L.splits > 1 && (L.count != 1 || cols != 1 || !calibrated))
+        return set_error(G4_ERR_UNSUPPORTED, "split-K needs one calibrated single-column job");
+    plan_blocks(L, L.splits > 1 ? 1 : 8);
+    const int blocks = total_blocks(L);
+    int max_k = 0;
+    for (int i = 0; i < L.count; ++i) max_k = std::max(max_k, L.job[i].k);
+    if (calibrated) {
+        const size_t lds = (size_t)cols * ((max_k + 15) & ~15);
+        dim3 grid(blocks, std::max(1, L.splits), 1);
+        if (cols == 1)
+            hipLaunchKernelGGL(qgemv_int_kernel<1>, grid, dim3(kGemvThreads), lds, stream, L);
+        else
+            hipLaunchKernelGGL(qgemv_int_kernel<2>, grid, dim3(kGemvThreads), lds, stream, L);
+        G4_LAUNCHED("qgemv_int_kernel");
+    } else {
+        const size_t lds = (size_t)max_k * sizeof(float);
+        dim3 grid(blocks, 1, cols);
+        hipLaunchKernelGGL(qgemv_f32_kernel, grid, dim3(kGemvThreads), lds, stream, L);
+        G4_LAUNCHED("qgemv_f32_kernel");
+    }
+    return G4_OK;
+}
+
+// One GEMV job over m_cols columns, issued as launches of at most 2 columns (the wide kernel).
+int gemv_columns(int bits, const void *wq, const float *scales, const void *x, int x_kind,
+                 void *dst, int out_kind, int k, int num_rows, int m_cols, float in_scale,
+                 float out_scale, hipStream_t stream, const char *who) {
+    const size_t x_elem = x_kind == G4_KIND_F32 ? 4 : x_kind == G4_KIND_F16 ? 2 : 1;
+    const size_t d_elem = out_kind == G4_KIND_I8 ? 1 : 4;
+    for (int c0 = 0; c0 < m_cols; c0 += 2) {
+        const int cols = std::min(2, m_cols - c0);
+        GemvLaunch L{};
+        L.count = 1;
+        L.splits = 1;
+        GemvJob &J = L.job[0];
+        J.w = reinterpret_cast<const uint8_t *>(wq);
+        J.scales = scales;
+        J.x = reinterpret_cast<const uint8_t *>(x) + (size_t)c0 * k * x_elem;
+        J.dst = reinterpret_cast<uint8_t *>(dst) + (size_t)c0 * num_rows * d_elem;
+        J.bits = bits;
+        J.x_kind = x_kind;
+        J.out_kind = out_kind;
+        J.k = k;
+        J.rows = num_rows;
+        J.in_scale = in_scale;
+        J.out_scale = out_scale;
+        int rc = check_job(J, cols, who);
+        if (rc) return rc;
+        rc = launch_gemv(L, cols, stream);
+        if (rc) return rc;
+    }
+    return G4_OK;
+}
+
+}  // namespace g4
+
+using namespace g4;
+
+extern "C" {
+
+// qgemv-4bit / qgemv-8bit / -m2 (qgemv.ts:1299-1363, qgemvWide.ts:515-574).
+int g4_qgemv(int bits, const void *wq, const float *scales, const void *x, int x_kind, void *dst,
+             int out_kind, int k, int num_rows, int cols, float in_scale, float out_scale,
+             void *stream) {
+    char who[32];
+    snprintf(who, sizeof who, "qgemv-%dbit%s", bits, cols > 1 ? "-m2" : "");
+    if (k <= 0 || num_rows <= 0) return set_error(G4_ERR_INVALID, "qgemv needs params.k and params.numRows");
+    if (bits != 4 && bits != 8) return set_error(G4_ERR_INVALID, "qgemv: bits must be 4 or 8, got %d", bits);
+    const int span = bits == 4 ? 256 : 128;  // K_SPAN_PER_ITER, qgemv.ts:1258
+    if (k % span != 0)
+        return set_error(G4_ERR_INVALID,
+                         "qgemv-%dbit needs K a multiple of %d, got %d. Every text tensor satisfies "
+                         "this; a caller that does not is packing the wrong tensor.",
+                         bits, span, k);
+    if (cols <= 0 || cols > 2)
+        return set_error(G4_ERR_INVALID, "%s needs params.cols in 1..2, got %d", who, cols);
+    return gemv_columns(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, cols, in_scale,
+                        out_scale, as_stream(stream), who);
+}
+
+// qkv-batch-4bit / gate-up-batch-4bit (projectionBatch.ts:85-128).
+int g4_projection_batch(int bits, int count, const void *const *w, const float *const *scales,
+                        const void *x, int x_kind, void *const *out, int out_kind, const int *rows,
+                        const float *in_scales, const float *out_scales, int k, void *stream) {
+    if (count != 2 && count != 3)
+        return set_error(G4_ERR_INVALID, "projection batch count must be 2 (gate/up) or 3 (q/k/v), got %d", count);
+    if (k <= 0 || k % 128 != 0)
+        return set_error(G4_ERR_INVALID, "batched projection K must be a positive multiple of 128");
+    if (!w || !scales || !out || !rows || !in_scales || !out_scales || !x)
+        return set_error(G4_ERR_INVALID, "batched projection is missing an input buffer");
+    for (int i = 0; i < count; ++i)
+        if (rows[i] <= 0) return set_error(G4_ERR_INVALID, "batched projection rows must be positive integers");
+    if (count == 2 && rows[0] != rows[1])
+        return set_error(G4_ERR_INVALID, "gate/up batch requires equal row counts");
+    GemvLaunch L{};
+    L.count = count;
+    L.splits = 1;
+    const char *who = count == 3 ? "qkv-batch-4bit" : "gate-up-batch-4bit";
+    for (int i = 0; i < count; ++i) {
+        GemvJob &J = L.job[i];
+        J.w = reinterpret_cast<const uint8_t *>(w[i]);
+        J.scales = scales[i];
+        J.x = x;
+        J.dst = out[i];
+        J.bits = bits;
+        J.x_kind = x_kind;
+        J.out_kind = out_kind;
+        J.k = k;
+        J.rows = rows[i];
+        J.in_scale = in_scales[i];
+        J.out_scale = out_scales[i];
+        int rc = check_job(J, 1, who);
+        if (rc) return rc;
+    }
+    // A mix of calibrated and uncalibrated projections (the reference's cases mix them) runs as
+    // one launch per side.
+    bool mixed = false;
+    for (int i = 1; i < count; ++i) mixed |= (L.job[i].in_scale != 0.0f) != (L.job[0].in_scale != 0.0f);
+    if (!mixed) return launch_gemv(L, 1, as_stream(stream));
+    for (int side = 0; side < 2; ++side) {
+        GemvLaunch S{};
+        S.splits = 1;
+        for (int i = 0; i < count; ++i)
+            if ((L.job[i].in_scale != 0.0f) == (side == 0)) S.job[S.count++] = L.job[i];
+        if (S.count) {
+            int rc = launch_gemv(S, 1, as_stream(stream));
+            if (rc) return rc;
+        }
+    }
+    return G4_OK;
+}
+
+int g4_qgemv_grouped(const g4_gemv_desc *descs, int count, void *stream) {
+    if (!descs || count < 1 || count > G4_MAX_GROUP)
+        return set_error(G4_ERR_INVALID, "grouped GEMV: count %d not in 1..%d", count, G4_MAX_GROUP);
+    GemvLaunch L{};
+    L.count = count;
+    L.splits = 1;
+    for (int i = 0; i < count; ++i) {
+        const g4_gemv_desc &d = descs[i];
+        GemvJob &J = L.job[i];
+        J.w = reinterpret_cast<const uint8_t *>(d.wq);
+        J.scales = d.scales;
+        J.x = d.x;
+        J.dst = d.dst;
+        J.bits = d.bits;
+        J.x_kind = d.x_kind;
+        J.out_kind = d.out_kind;
+        J.k = d.k;
+        J.rows = d.num_rows;
+        J.in_scale = d.in_scale;
+        J.out_scale = d.out_scale;
+        int rc = check_job(J, 1, "grouped GEMV");
+        if (rc) return rc;
+        if (d.in_scale == 0.0f)
+            return set_error(G4_ERR_UNSUPPORTED, "grouped GEMV runs calibrated projections only");
+    }
+    return launch_gemv(L, 1, as_stream(stream));
+}
+
+// qgemv-4bit-split / qgemv-8bit-split / exact split (qgemv.ts:521-548, exactSplit.ts:19-31).
+int g4_qgemv_split(int bits, const void *wq, const float *scales, const void *x, int x_kind,
+                   float *partials, int k, int num_rows, int k_splits, int exact, float in_scale,
+                   void *stream) {
+    if (k_splits != 1 && k_splits != 2 && k_splits != 4 && k_splits != 8)
+        return set_error(G4_ERR_INVALID, "gemv geometry: kSplits must be 1, 2, 4 or 8, got %d", k_splits);
+    if (exact && (!(in_scale > 0.0f) || k > 16384))
+        return set_error(G4_ERR_INVALID, "exact split needs calibrated int8 input and K <= 16384");
+    if (in_scale == 0.0f)
+        return set_error(G4_ERR_UNSUPPORTED, "the split-K build runs the calibrated path only");
+    const int span = bits == 4 ? 256 : 128;
+    if (k <= 0 || num_rows <= 0) return set_error(G4_ERR_INVALID, "qgemv needs params.k and params.numRows");
+    if (k % span != 0)
+        return set_error(G4_ERR_INVALID, "qgemv-%dbit needs K a multiple of %d, got %d", bits, span, k);
+    GemvLaunch L{};
+    L.count = 1;
+    L.splits = k_splits;
+    L.split_exact = exact ? 1 : 0;
+    GemvJob &J = L.job[0];
+    J.w = reinterpret_cast<const uint8_t *>(wq);
+    J.scales = scales;
+    J.x = x;
+    J.dst = partials;
+    J.bits = bits;
+    J.x_kind = x_kind;
+    J.out_kind = G4_KIND_F32;
+    J.k = k;
+    J.rows = num_rows;
+    J.in_scale = in_scale;
+    J.out_scale = 0.0f;
+    int rc = check_job(J, 1, bits == 4 ? "qgemv-4bit-split" : "qgemv-8bit-split");
+    if (rc) return rc;
+    return launch_gemv(L, 1, as_stream(stream));
+}
+
+static int merge_common(const float *partials, const float *scales, void *dst, int out_kind,
+                        int num_rows, int k_splits, int exact, float in_scale, float out_scale,
+                        void *stream, const char *who) {
+    if (num_rows <= 0) return set_error(G4_ERR_INVALID, "%s needs a positive params.numRows", who);
+    if (k_splits < 2)
+        return set_error(G4_ERR_INVALID, "%s only exists on a split dispatch, got kSplits %d", who, k_splits);
+    if (!partials || !dst || (exact && !scales))
+        return set_error(G4_ERR_INVALID, "%s needs an input named part", who);
+    if (out_kind != G4_KIND_F32 && out_kind != G4_KIND_I8)
+        return set_error(G4_ERR_INVALID, "%s: out_kind must be f32 or int8", who);
+    if (out_kind == G4_KIND_I8 && out_scale == 0.0f)
+        return set_error(G4_ERR_INVALID, "%s: int8 output codes need a calibrated outScale", who);
+    hipLaunchKernelGGL(qgemv_merge_kernel, dim3((num_rows + 63) / 64), dim3(64), 0,
+                       as_stream(stream), partials, scales, dst, out_kind, num_rows, k_splits,
+                       exact, in_scale, out_scale);
+    G4_LAUNCHED("qgemv_merge_kernel");
+    return G4_OK;
+}
+
+int g4_qgemv_merge(const float *partials, void *dst, int out_kind, int num_rows, int k_splits,
+                   float out_scale, void *stream) {
+    return merge_common(partials, nullptr, dst, out_kind, num_rows, k_splits, 0, 0.0f, out_scale,
+                        stream, "qgemv-merge");
+}
+
+int g4_qgemv_exact_merge(const float *partials, const float *scales, void *dst, int out_kind,
+                         int num_rows, int k_splits, float in_scale, float out_scale,
+                         void *stream) {
+    return merge_common(partials, scales, dst, out_kind, num_rows, k_splits, 1, in_scale,
+                        out_scale, stream, "qgemv-exact-merge");
+}
+
+}  // extern "C"

@@ -1,0 +1,255 @@
+// Host runtime of libg4w8a8: the last-error string, device memory, streams and events, the byte
+// fill kernel and the pure table split planner (src/tableSplit.ts).
+#include "g4_internal.h"
+
+#include <cstdio>
+#include <mutex>
+#include <vector>
+
+namespace g4 {
+
+static thread_local std::string t_last_error;
+
+int set_error(int status, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    t_last_error = buf;
+    return status;
+}
+
+void clear_error() { t_last_error.clear(); }
+
+int hip_status(hipError_t err, const char *what) {
+    return set_error(err == hipErrorNoDevice ? G4_ERR_NO_DEVICE : G4_ERR_HIP, "%s failed: %s (%d)",
+                     what, hipGetErrorString(err), (int)err);
+}
+
+int device_cu_count() {
+    static std::mutex mu;
+    static std::vector<int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lock(mu);
+    if ((int)cache.size() <= dev) cache.resize(dev + 1, 0);
+    if (cache[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            cus = 256;
+        cache[dev] = cus;
+    }
+    return cache[dev];
+}
+
+__global__ void fill_u8_kernel(uint8_t *dst, uint8_t value, size_t bytes) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    uint32_t v4 = 0x01010101u * value;
+    size_t words = bytes / 4;
+    if (((uintptr_t)dst & 3) == 0) {
+        uint32_t *d = reinterpret_cast<uint32_t *>(dst);
+        for (size_t w = i; w < words; w += stride) d[w] = v4;
+        for (size_t b = words * 4 + i; b < bytes; b += stride) dst[b] = value;
+    } else {
+        for (size_t b = i; b < bytes; b += stride) dst[b] = value;
+    }
+}
+
+}  // namespace g4
+
+using namespace g4;
+
+extern "C" {
+
+int g4_abi_version(void) { return G4_ABI_VERSION; }
+
+const char *g4_last_error(void) { return t_last_error.c_str(); }
+
+int g4_device_count(int *count) {
+    if (!count) return set_error(G4_ERR_INVALID, "g4_device_count: count is NULL");
+    int n = 0;
+    hipError_t err = hipGetDeviceCount(&n);
+    if (err != hipSuccess) {
+        *count = 0;
+        return hip_status(err, "hipGetDeviceCount");
+    }
+    *count = n;
+    return G4_OK;
+}
+
+int g4_set_device(int device) {
+    G4_HIP(hipSetDevice(device));
+    return G4_OK;
+}
+
+int g4_malloc(void **ptr, size_t bytes) {
+    if (!ptr) return set_error(G4_ERR_INVALID, "g4_malloc: ptr is NULL");
+    *ptr = nullptr;
+    if (bytes == 0) bytes = 1;
+    G4_HIP(hipMalloc(ptr, bytes));
+    return G4_OK;
+}
+
+int g4_free(void *ptr) {
+    if (ptr) G4_HIP(hipFree(ptr));
+    return G4_OK;
+}
+
+int g4_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream) {
+    if (bytes == 0) return G4_OK;
+    G4_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream)));
+    G4_HIP(hipStreamSynchronize(as_stream(stream)));
+    return G4_OK;
+}
+
+int g4_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream) {
+    if (bytes == 0) return G4_OK;
+    G4_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream)));
+    G4_HIP(hipStreamSynchronize(as_stream(stream)));
+    return G4_OK;
+}
+
+int g4_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream) {
+    if (bytes == 0) return G4_OK;
+    G4_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)));
+    return G4_OK;
+}
+
+int g4_fill_u8(void *dst, uint8_t value, size_t bytes, void *stream) {
+    if (bytes == 0) return G4_OK;
+    if (!dst) return set_error(G4_ERR_INVALID, "g4_fill_u8: dst is NULL");
+    size_t words = (bytes + 3) / 4;
+    size_t blocks = (words + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(fill_u8_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                       reinterpret_cast<uint8_t *>(dst), value, bytes);
+    G4_LAUNCHED("fill_u8_kernel");
+    return G4_OK;
+}
+
+int g4_stream_create(void **stream) {
+    if (!stream) return set_error(G4_ERR_INVALID, "g4_stream_create: stream is NULL");
+    hipStream_t s = nullptr;
+    // Default priority on purpose: streams of different priorities have hung on this pool.
+    G4_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = s;
+    return G4_OK;
+}
+
+int g4_stream_destroy(void *stream) {
+    if (stream) G4_HIP(hipStreamDestroy(as_stream(stream)));
+    return G4_OK;
+}
+
+int g4_stream_synchronize(void *stream) {
+    G4_HIP(hipStreamSynchronize(as_stream(stream)));
+    return G4_OK;
+}
+
+int g4_device_synchronize(void) {
+    G4_HIP(hipDeviceSynchronize());
+    return G4_OK;
+}
+
+int g4_event_create(void **event) {
+    if (!event) return set_error(G4_ERR_INVALID, "g4_event_create: event is NULL");
+    hipEvent_t e = nullptr;
+    G4_HIP(hipEventCreate(&e));
+    *event = e;
+    return G4_OK;
+}
+
+int g4_event_destroy(void *event) {
+    if (event) G4_HIP(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)));
+    return G4_OK;
+}
+
+int g4_event_record(void *event, void *stream) {
+    G4_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(event), as_stream(stream)));
+    return G4_OK;
+}
+
+int g4_event_synchronize(void *event) {
+    G4_HIP(hipEventSynchronize(reinterpret_cast<hipEvent_t>(event)));
+    return G4_OK;
+}
+
+int g4_event_elapsed_ms(float *ms, void *start, void *end) {
+    if (!ms) return set_error(G4_ERR_INVALID, "g4_event_elapsed_ms: ms is NULL");
+    G4_HIP(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
+                               reinterpret_cast<hipEvent_t>(end)));
+    return G4_OK;
+}
+
+// tableSplit.ts:125-215 planTableSplit. Pure: limits go in as numbers.
+int g4_plan_table_split(const g4_table_split_input *in, g4_table_split_plan *plan,
+                        g4_table_slice *slices, int64_t max_slices) {
+    if (!in || !plan) return set_error(G4_ERR_INVALID, "g4_plan_table_split: NULL argument");
+    if (max_slices > 0 && !slices)
+        return set_error(G4_ERR_INVALID, "g4_plan_table_split: slices is NULL");
+    const int64_t kDefaultMaxSliceBytes = 256LL * 1024 * 1024;  // DEFAULT_MAX_SLICE_BYTES
+    const int64_t kGatherBindings = 4;                          // GATHER_STORAGE_BINDINGS
+    int64_t rows = in->rows > 0 ? in->rows : 0;
+    int64_t row_bytes = in->row_bytes > 1 ? in->row_bytes : 1;
+    int64_t total = rows * row_bytes;
+    int64_t limit = in->max_storage_buffer_binding_size < in->max_buffer_size
+                        ? in->max_storage_buffer_binding_size
+                        : in->max_buffer_size;
+    if (limit < 0) limit = 0;
+    *plan = g4_table_split_plan{};
+    plan->rows = rows;
+    plan->row_bytes = row_bytes;
+    plan->total_bytes = total;
+    plan->limit_bytes = limit;
+    plan->storage_bindings_per_dispatch = kGatherBindings;
+    plan->binding_budget = in->max_storage_buffers_per_shader_stage;
+    bool fits_whole = total > 0 && total <= limit;
+    int64_t cap = in->max_slice_bytes > 0 ? in->max_slice_bytes : kDefaultMaxSliceBytes;
+    int64_t slice_cap = limit < cap ? limit : cap;
+    if (slice_cap < 1) slice_cap = 1;
+    int64_t rows_per_slice = (fits_whole ? limit : slice_cap) / row_bytes;
+    if (rows_per_slice < 1) {
+        // One row does not fit in one binding: infeasible, no slices (tableSplit.ts:147-167).
+        plan->rows_per_slice = 0;
+        plan->num_slices = 0;
+        plan->single = 0;
+        plan->feasible = 0;
+        plan->dispatches_per_gather = 0;
+        return G4_OK;
+    }
+    // Slices start on a sixteen row boundary (tableSplit.ts:170-173).
+    int64_t aligned = rows_per_slice >= 16 ? rows_per_slice - (rows_per_slice % 16) : rows_per_slice;
+    int64_t per = rows < aligned ? rows : aligned;
+    int64_t n = 0;
+    for (int64_t start = 0; per > 0 && start < rows; start += per, ++n) {
+        if (n < max_slices) {
+            int64_t count = per < rows - start ? per : rows - start;
+            slices[n] = g4_table_slice{n, start, count, start * row_bytes, count * row_bytes};
+        }
+    }
+    if (n == 0) {
+        if (max_slices > 0) slices[0] = g4_table_slice{0, 0, 0, 0, 0};
+        n = 1;
+    }
+    plan->rows_per_slice = per;
+    plan->num_slices = n;
+    plan->single = n == 1;
+    plan->dispatches_per_gather = n;
+    plan->feasible = kGatherBindings <= plan->binding_budget;
+    return G4_OK;
+}
+
+// tableSplit.ts:218-223 sliceForRow.
+int64_t g4_slice_for_row(const g4_table_slice *slices, int64_t num_slices, int64_t row) {
+    if (!slices) return -1;
+    for (int64_t i = 0; i < num_slices; i++) {
+        if (row >= slices[i].start_row && row < slices[i].start_row + slices[i].row_count)
+            return slices[i].index;
+    }
+    return -1;
+}
+
+}  // extern "C"

@@ -1,0 +1,244 @@
+/*
+ * g4w8a8: MI355X (gfx950) wNa8o8 quantized projection path and split PLE gather.
+ *
+ * The drop-in C ABI for the reference's operator seam (Ar5en1c/gemma4-webgpu-engine,
+ * src/kernels/registry.ts:108-119 `Kernel.bind`, fed by src/execute.ts:438 `resolveStep`).
+ * Each entry point replaces one registry kernel (named in its comment, with the file:line of the
+ * reference's bind it mirrors): the same named inputs, the same params and the same refusals. The
+ * reference's `bind` throws an Error; here every entry point returns a status and
+ * g4_last_error() gives the message, with the reference's wording where it has one.
+ *
+ * Conventions
+ *  - Plain pointers and sizes only. Device pointers are HIP device memory (hipMalloc, or any
+ *    allocator of this process such as torch); `stream` is a hipStream_t (NULL = default stream).
+ *  - Every compute entry point is enqueue-only on `stream`: it returns after the launch.
+ *  - Layouts are the reference's (src/kernels/qlayout.ts:12-26, src/quant.ts:11-20):
+ *      weights   row-major packed rows, K contiguous; 4-bit: two codes per byte, low nibble first,
+ *                zero point 8; 8-bit: the signed byte is the code.
+ *      scales    f32 [N], one per output row.
+ *      x         [M][K] row-major, f32 or f16 (widened exactly), or int8 codes already snapped.
+ *      dst       [M][N] row-major (the reference's dst[col * N + row]).
+ *  - Arithmetic (src/kernels/qgemv.ts:1131-1176): xq = clamp(RNE(f32(x / inScale)), -128, 127);
+ *    acc = sum(wcode * xq) exact in int32; y = f32(f32(inScale * scale[n]) * f32(acc));
+ *    q = clamp(RNE(f32(y / outScale)), -128, 127). Divides are IEEE binary32.
+ *    inScale == 0 selects the uncalibrated f32 code dot (lm_head), outScale == 0 skips the output
+ *    snap (quant.ts:248-357).
+ */
+#ifndef G4W8A8_H
+#define G4W8A8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define G4_ABI_VERSION 1
+
+/* Status codes. */
+#define G4_OK 0
+#define G4_ERR_INVALID 1     /* a refused argument: the reference's bind would throw */
+#define G4_ERR_UNKNOWN_KERNEL 2
+#define G4_ERR_HIP 3         /* a HIP runtime call failed */
+#define G4_ERR_NO_DEVICE 4
+#define G4_ERR_UNSUPPORTED 5 /* a combination the path does not implement */
+
+/* Element kinds of activations (x_kind) and outputs (out_kind). */
+#define G4_KIND_F32 0 /* x: f32 activations. dst: the reference's f32 dst, q * outScale (or y) */
+#define G4_KIND_F16 1 /* x: f16 activations, widened exactly. dst (gather only): f16 values */
+#define G4_KIND_I8 2  /* x: int8 codes already snapped on inScale. dst: int8 codes q */
+#define G4_KIND_I32 3 /* dst only: the exact int32 accumulator sum(wcode * xq) */
+
+/* Version of this ABI (G4_ABI_VERSION). */
+int g4_abi_version(void);
+
+/* Message of the last failed call on this thread ("" when none). Owned by the library. */
+const char *g4_last_error(void);
+
+/* ---- device memory, streams, events (what the reference's BufferManager/runtime.ts own) ---- */
+int g4_device_count(int *count);
+int g4_set_device(int device);
+int g4_malloc(void **ptr, size_t bytes);
+int g4_free(void *ptr);
+int g4_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream);
+int g4_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream);
+int g4_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream);
+/* Byte fill through a kernel (safe under graph capture). */
+int g4_fill_u8(void *dst, uint8_t value, size_t bytes, void *stream);
+int g4_stream_create(void **stream);
+int g4_stream_destroy(void *stream);
+int g4_stream_synchronize(void *stream);
+int g4_device_synchronize(void);
+int g4_event_create(void **event);
+int g4_event_destroy(void *event);
+int g4_event_record(void *event, void *stream);
+int g4_event_synchronize(void *event);
+int g4_event_elapsed_ms(float *ms, void *start, void *end);
+
+/* ---- the quantized linears --------------------------------------------------------------- */
+
+/*
+ * qgemv-4bit / qgemv-8bit and the wide qgemv-4bit-m2 / qgemv-8bit-m2.
+ * Replaces bindGemv (src/kernels/qgemv.ts:1299-1363; registry entries :1471, :1595) and
+ * bindGemvWide (src/kernels/qgemvWide.ts:515-574; entries :597-712).
+ * cols is the token count: 1 for a decode step, 2 for the draft-verify pass (cols > 2 refused,
+ * as qgemvWide.ts:522-526). K must be a multiple of 256 (4-bit) or 128 (8-bit), qgemv.ts:1305-1310.
+ */
+int g4_qgemv(int bits, const void *wq, const float *scales, const void *x, int x_kind, void *dst,
+             int out_kind, int k, int num_rows, int cols, float in_scale, float out_scale,
+             void *stream);
+
+/*
+ * qgemm-4bit (+ -single, -prefill4) and qmatmul-8bit: M token columns, any M >= 1.
+ * Replaces bindGemm (src/kernels/qgemm.ts:589-639; entries :641, :717, :725) and bindQmatmul8
+ * (src/kernels/pleMatmul.ts:257-303; entry :323). bits 4 needs K % 256 == 0 (qgemm.ts:598-600);
+ * bits 8 needs K % 4 == 0 (pleMatmul.ts:266-271). The calibrated path runs on int8 MFMA.
+ */
+int g4_qgemm(int bits, const void *wq, const float *scales, const void *x, int x_kind, void *dst,
+             int out_kind, int k, int num_rows, int m_cols, float in_scale, float out_scale,
+             void *stream);
+
+/*
+ * The execute.ts routing (src/execute.ts:372-430 matmulKernel/gemvWide/pleKernel) folded into one
+ * call: picks the kernel for (bits, M, N, K) on this GPU. M <= 2 -> the GEMV family, larger M ->
+ * the MFMA GEMM. Same arguments as g4_qgemm.
+ */
+int g4_linear(int bits, const void *wq, const float *scales, const void *x, int x_kind, void *dst,
+              int out_kind, int k, int num_rows, int m_cols, float in_scale, float out_scale,
+              void *stream);
+
+/* Name of the kernel g4_linear picks for a shape, written into buf (NUL terminated). */
+int g4_kernel_for_shape(int bits, int m_cols, int num_rows, int k, char *buf, size_t buf_len);
+
+/*
+ * qkv-batch-4bit (count 3) and gate-up-batch-4bit (count 2): several projections of one x in one
+ * launch. Replaces bindProjectionBatch (src/kernels/projectionBatch.ts:85-128; entries :161-162).
+ * w[i], scales[i], out[i], rows[i], in_scales[i], out_scales[i] per projection; K multiple of 128
+ * (projectionBatch.ts:90); gate/up (count 2) needs equal row counts (:92).
+ */
+int g4_projection_batch(int bits, int count, const void *const *w, const float *const *scales,
+                        const void *x, int x_kind, void *const *out, int out_kind, const int *rows,
+                        const float *in_scales, const float *out_scales, int k, void *stream);
+
+/*
+ * The grouped GEMV: up to G4_MAX_GROUP independent M=1 linears (each its own weights, x, K, N,
+ * width and scales) in one launch. The generalisation of projectionBatch.ts to a whole layer's
+ * projection set (q, k, v, o, gate, up, down). No reference counterpart beyond projectionBatch.
+ */
+#define G4_MAX_GROUP 16
+typedef struct g4_gemv_desc {
+    const void *wq;
+    const float *scales;
+    const void *x;
+    void *dst;
+    int bits;     /* 4 or 8 */
+    int x_kind;   /* G4_KIND_F32, _F16 or _I8 */
+    int out_kind; /* G4_KIND_I8, _F32 or _I32 */
+    int k;
+    int num_rows;
+    float in_scale;  /* non-zero: the grouped GEMV is the calibrated path only */
+    float out_scale;
+} g4_gemv_desc;
+int g4_qgemv_grouped(const g4_gemv_desc *descs, int count, void *stream);
+
+/*
+ * qgemv-4bit-split / qgemv-8bit-split (src/kernels/qgemv.ts:1753, :1772; band logic :521-548) and
+ * qgemv-4bit-gelu-exact-split without the gelu prologue (src/kernels/exactSplit.ts:19-31).
+ * Writes partials f32 [num_rows][k_splits]: exact = 0 the scaled f32(f32(xs*scale)*f32(sum_band)),
+ * exact = 1 the raw integer f32(sum_band) (needs inScale > 0 and K <= 16384, exactSplit.ts:27).
+ */
+int g4_qgemv_split(int bits, const void *wq, const float *scales, const void *x, int x_kind,
+                   float *partials, int k, int num_rows, int k_splits, int exact, float in_scale,
+                   void *stream);
+
+/* qgemv-merge (src/kernels/qgemv.ts:1405, WGSL :1027-1072): ascending f32 fold of k_splits
+ * partials per row, then the output snap. Refuses k_splits < 2 (:1444-1446). */
+int g4_qgemv_merge(const float *partials, void *dst, int out_kind, int num_rows, int k_splits,
+                   float out_scale, void *stream);
+
+/* qgemv-exact-merge (src/kernels/exactSplit.ts:32-72): fold, then f32(f32(in*scale)*t), snap. */
+int g4_qgemv_exact_merge(const float *partials, const float *scales, void *dst, int out_kind,
+                         int num_rows, int k_splits, float in_scale, float out_scale,
+                         void *stream);
+
+/* quant.ts:309-334 srqCodes as a kernel: n activations (f32 or f16) to int8 codes on scale. */
+int g4_srq_quantize(const void *x, int x_kind, int8_t *codes, int64_t n, float scale,
+                    void *stream);
+
+/* ---- the per-layer-embedding gather ------------------------------------------------------- */
+
+/*
+ * ple-gather-4bit (sliced = 0) and ple-gather-4bit-sliced (sliced = 1).
+ * Replaces makeBind (src/kernels/embedGather.ts:435-485; entries :487, :547).
+ * codes: the table (or, sliced, one vocabulary slice of it: row r of the slice is vocabulary row
+ *        slice_start_row + r), cols/2 bytes per row. scales: [rows][groups_per_row], f32 or f16
+ *        (scale_kind), addressed by the ABSOLUTE row (embedGather.ts:248). ids: int32 [slots].
+ * dst [slots][cols]: G4_KIND_F32 = the reference's f32 (code-8)*(16*scale); G4_KIND_F16 the same
+ * rounded to nearest even; G4_KIND_I8 the gathered signed codes. A sliced gather writes only the
+ * slots whose id falls inside the slice (embedGather.ts:188-196) and refuses a missing or empty
+ * range (:463-467).
+ */
+int g4_ple_gather(const void *codes, const void *scales, int scale_kind, const int32_t *ids,
+                  void *dst, int out_kind, int slots, int cols, int group_size,
+                  int groups_per_row, int sliced, int64_t slice_start_row,
+                  int64_t slice_row_count, void *stream);
+
+/*
+ * One gather over a whole split table: every slice of `plan` in order (the reference walks
+ * slicedGatherDispatches, embedGather.ts:403-419, one dispatch per slice). slice_codes[i] is the
+ * device buffer of slice i. Launches one fused kernel that routes each token to its slice.
+ */
+int g4_ple_gather_split(const void *const *slice_codes, const int64_t *slice_starts,
+                        const int64_t *slice_counts, int num_slices, const void *scales,
+                        int scale_kind, const int32_t *ids, void *dst, int out_kind, int slots,
+                        int cols, int group_size, int groups_per_row, void *stream);
+
+/* ---- the split planner (pure host code) --------------------------------------------------- */
+
+/* tableSplit.ts:51-81 TableSplitInput. max_slice_bytes 0 = DEFAULT_MAX_SLICE_BYTES (256 MiB). */
+typedef struct g4_table_split_input {
+    int64_t rows;
+    int64_t row_bytes;
+    int64_t max_storage_buffer_binding_size;
+    int64_t max_buffer_size;
+    int64_t max_storage_buffers_per_shader_stage;
+    int64_t max_slice_bytes;
+} g4_table_split_input;
+
+/* tableSplit.ts:39-50 TableSlice. */
+typedef struct g4_table_slice {
+    int64_t index;
+    int64_t start_row;
+    int64_t row_count;
+    int64_t byte_offset;
+    int64_t byte_length;
+} g4_table_slice;
+
+/* tableSplit.ts:90-118 TableSplitPlan (without the note string). */
+typedef struct g4_table_split_plan {
+    int64_t rows;
+    int64_t row_bytes;
+    int64_t total_bytes;
+    int64_t limit_bytes;
+    int64_t rows_per_slice;
+    int64_t num_slices;
+    int32_t single;
+    int32_t feasible;
+    int64_t storage_bindings_per_dispatch;
+    int64_t binding_budget;
+    int64_t dispatches_per_gather;
+} g4_table_split_plan;
+
+/* tableSplit.ts:125-215 planTableSplit. Writes the plan and up to max_slices slices. */
+int g4_plan_table_split(const g4_table_split_input *input, g4_table_split_plan *plan,
+                        g4_table_slice *slices, int64_t max_slices);
+
+/* tableSplit.ts:218-223 sliceForRow: the slice index carrying `row`, or -1. */
+int64_t g4_slice_for_row(const g4_table_slice *slices, int64_t num_slices, int64_t row);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* G4W8A8_H */

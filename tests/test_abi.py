@@ -1,0 +1,92 @@
+"""The C ABI library loads and exports every symbol include/g4w8a8.h declares, and refuses bad
+arguments with the reference's messages before touching a device (no compute calls here)."""
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "g4w8a8.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(g4_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported(g4):
+    syms = header_symbols()
+    assert len(syms) >= 30
+    for name in syms:
+        assert hasattr(g4.lib(), name), name
+    assert set(syms) == set(g4.SIGNATURES), set(syms) ^ set(g4.SIGNATURES)
+    assert g4.lib().g4_abi_version() == 1
+
+
+def expect(g4, fn, status, fragment):
+    with pytest.raises(g4.G4Error) as e:
+        fn()
+    assert e.value.status == status, str(e.value)
+    assert fragment in str(e.value), str(e.value)
+
+
+def test_gemv_refusals(g4):
+    L = g4.lib()
+    def call(bits=4, k=1536, n=16, cols=1, xk=g4.KIND_F16, ok=g4.KIND_I8, ins=0.05, outs=0.1,
+             w=0x1000, s=0x1000, x=0x1000, d=0x1000):
+        g4._check(L.g4_qgemv(bits, w, s, x, xk, d, ok, k, n, cols, ins, outs, None))
+    expect(g4, lambda: call(k=100), 1, "qgemv-4bit needs K a multiple of 256, got 100")
+    expect(g4, lambda: call(bits=8, k=1000), 1, "qgemv-8bit needs K a multiple of 128")
+    expect(g4, lambda: call(cols=3), 1, "needs params.cols in 1..2, got 3")
+    expect(g4, lambda: call(n=0), 1, "qgemv needs params.k and params.numRows")
+    expect(g4, lambda: call(outs=0.0), 1, "int8 output codes need a calibrated outScale")
+    expect(g4, lambda: call(w=0), 1, "needs inputs named wq, scales and x")
+    expect(g4, lambda: call(w=0x1008), 1, "16-byte aligned")
+    expect(g4, lambda: call(bits=2), 1, "bits must be 4 or 8")
+
+
+def test_gemm_batch_merge_gather_refusals(g4):
+    L = g4.lib()
+    expect(g4, lambda: g4._check(L.g4_qgemm(4, 0x1000, 0x1000, 0x1000, 1, 0x1000, 2, 300, 8, 11,
+                                            0.1, 0.1, None)), 1, "qgemm-4bit needs K a multiple of 256")
+    expect(g4, lambda: g4._check(L.g4_qgemm(8, 0x1000, 0x1000, 0x1000, 1, 0x1000, 2, 130, 8, 11,
+                                            0.1, 0.1, None)), 1, "qmatmul-8bit needs K a multiple of 4")
+    expect(g4, lambda: g4.projection_batch(4, [0x1000] * 2, [0x1000] * 2, _Fake(), [_Fake()] * 2,
+                                           [16, 32], [0.1, 0.1], [0.1, 0.1], 256), 1,
+           "gate/up batch requires equal row counts")
+    expect(g4, lambda: g4._check(L.g4_qgemv_merge(0x1000, 0x1000, 0, 8, 1, 0.1, None)), 1,
+           "qgemv-merge only exists on a split dispatch, got kSplits 1")
+    expect(g4, lambda: g4._check(L.g4_qgemv_split(4, 0x1000, 0x1000, 0x1000, 1, 0x1000, 256, 8, 3,
+                                                  0, 0.1, None)), 1, "kSplits must be 1, 2, 4 or 8")
+    expect(g4, lambda: g4._check(L.g4_qgemv_split(4, 0x1000, 0x1000, 0x1000, 1, 0x1000, 256, 8, 2,
+                                                  1, 0.0, None)), 1,
+           "exact split needs calibrated int8 input")
+    expect(g4, lambda: g4._check(L.g4_ple_gather(0x1000, 0x1000, 1, 0x1000, 0x1000, 1, 4, 8960, 256,
+                                                 35, 1, 0, 0, None)), 1,
+           "needs params sliceStartRow and sliceRowCount naming a non empty vocabulary range")
+    expect(g4, lambda: g4._check(L.g4_ple_gather(0x1000, 0x1000, 1, 0x1000, 0x1000, 1, 4, 8960, 250,
+                                                 35, 0, 0, 100, None)), 1, "does not divide")
+
+
+def test_registry_refuses_unknown_names_and_missing_inputs(g4):
+    expect(g4, lambda: g4.bind("qgemv-3bit", {}, None, {}), 2, "no registered kernel named qgemv-3bit")
+    expect(g4, lambda: g4.bind("qgemv-4bit", {"wq": 1}, None, {}), 1,
+           "needs inputs named wq, scales, x")
+    expect(g4, lambda: g4.bind("ple-gather-4bit-sliced", {"codes": 1, "scales": 1, "ids": 1}, None,
+                               {"slots": 4}), 1, "naming a non empty vocabulary range")
+    expect(g4, lambda: g4.bind("gate-up-batch-4bit", {"x": 1}, None, {"outputIndex": 5}), 1,
+           "invalid batch output index")
+    assert "qgemv-4bit" in g4.kernel_names() and "ple-gather-4bit-sliced" in g4.kernel_names()
+
+
+def test_kernel_choice_per_shape(g4):
+    assert g4.kernel_for_shape(4, 1, 1536, 1536) == "qgemv-4bit"
+    assert g4.kernel_for_shape(4, 2, 6144, 1536) == "qgemv-4bit"
+    assert g4.kernel_for_shape(4, 8, 6144, 1536) == "qgemm-4bit-mfma-skinny16"
+    assert g4.kernel_for_shape(4, 512, 6144, 1536) == "qgemm-4bit-mfma-tile128"
+    assert g4.kernel_for_shape(8, 4, 1536, 6144) == "qmatmul-8bit-mfma-skinny16"
+
+
+class _Fake:
+    ptr = 0x1000
+    kind = 2

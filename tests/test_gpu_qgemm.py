@@ -1,0 +1,128 @@
+"""GPU parity of the M-column linears on int8 MFMA (qgemm-4bit, qmatmul-8bit) against the oracle.
+
+Config 2: the gate projection (N 6144, K 1536) with int4 weights and f16 activations carrying 1%
+outliers at +-8 sigma, at M in {4, 8, 16, 128, 512, 2048}. Up to M = 512 every output is compared;
+at M = 2048 a seeded sample of 96 columns is compared with the oracle and, as a size-independent
+property, every sampled column also equals the GEMV kernel's answer for that column alone.
+"""
+import numpy as np
+import pytest
+
+import g4synth as syn
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(g4, a):
+    return g4.DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+def out_buf(g4, shape, dtype):
+    b = g4.DeviceBuffer.empty(shape, dtype)
+    b.fill(0x7B)
+    return b
+
+
+def f32_equal(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32),
+                          np.asarray(b, np.float32).view(np.uint32))
+
+
+def test_reference_case_m11_over_tile(gpu, oracle):
+    # qgemm.ts:648-673: 8 rows, K 512, 11 columns, grid activations; plain and SRQ.
+    g = np.random.default_rng(51)
+    w = g.integers(0, 256, size=(8, 256), dtype=np.uint8)
+    s = g.uniform(0.005, 0.02, 8).astype(np.float32)
+    x = (g.integers(-64, 65, size=(11, 512)) / 8.0).astype(np.float32)
+    for ins, outs in ((0.0, 0.0), (0.1875, 0.0625)):
+        print(f"qgemm m11 in={ins}", flush=True)
+        o = out_buf(gpu, (11, 8), np.float32)
+        gpu.bind("qgemm-4bit", {"wq": dev(gpu, w), "scales": dev(gpu, s), "x": dev(gpu, x)}, o,
+                 {"k": 512, "numRows": 8, "mCols": 11, "inScale": ins, "outScale": outs})
+        want, _, _ = oracle.qgemm(4, w, s, x, 8, 512, 11, ins, outs)
+        assert f32_equal(o.download(), want)
+
+
+@pytest.fixture(scope="module")
+def gate(gpu):
+    n, k = syn.FFN, syn.HIDDEN
+    w = syn.int4_weights("c2", "gate", n, k)
+    s = syn.row_scales("c2", "gate", n)
+    return n, k, w, s, dev(gpu, w), dev(gpu, s)
+
+
+@pytest.mark.parametrize("m", [3, 4, 8, 16, 17, 32, 33, 128, 512])
+def test_config2_gate_full_compare(gpu, oracle, gate, m):
+    n, k, w, s, wb, sb = gate
+    x = syn.activations("c2", f"x{m}", m, k, outlier_frac=0.01)
+    print(f"config2 m={m} kernel={gpu.kernel_for_shape(4, m, n, k)}", flush=True)
+    want, acc, codes = oracle.qgemm(4, w, s, x.astype(np.float32), n, k, m, syn.IN_SCALE,
+                                    syn.OUT_SCALE)
+    xb = dev(gpu, x)
+    o8 = out_buf(gpu, (m, n), np.int8)
+    gpu.qgemm(4, wb, sb, xb, o8, k, n, m, syn.IN_SCALE, syn.OUT_SCALE)
+    assert np.array_equal(o8.download(), codes)
+    o32 = out_buf(gpu, (m, n), np.int32)
+    gpu.qgemm(4, wb, sb, xb, o32, k, n, m, syn.IN_SCALE, syn.OUT_SCALE)
+    assert np.array_equal(o32.download(), acc)
+    if m in (4, 128):
+        of = out_buf(gpu, (m, n), np.float32)
+        gpu.qgemm(4, wb, sb, xb, of, k, n, m, syn.IN_SCALE, syn.OUT_SCALE)
+        assert f32_equal(of.download(), want)
+
+
+def test_config2_gate_m2048_sampled(gpu, oracle, gate):
+    n, k, w, s, wb, sb = gate
+    m = 2048
+    x = syn.activations("c2", "x2048", m, k, outlier_frac=0.01)
+    print("config2 m=2048", flush=True)
+    o8 = out_buf(gpu, (m, n), np.int8)
+    gpu.qgemm(4, wb, sb, dev(gpu, x), o8, k, n, m, syn.IN_SCALE, syn.OUT_SCALE)
+    got = o8.download()
+    cols = np.sort(np.random.default_rng(52).choice(m, size=96, replace=False))
+    cols[0], cols[-1] = 0, m - 1
+    sub = x[cols].astype(np.float32)
+    _, _, codes = oracle.qgemm(4, w, s, sub, n, k, cols.size, syn.IN_SCALE, syn.OUT_SCALE)
+    assert np.array_equal(got[cols], codes)
+    for c in cols[:8]:
+        o1 = out_buf(gpu, (n,), np.int8)
+        gpu.qgemv(4, wb, sb, dev(gpu, x[c]), o1, k, n, 1, syn.IN_SCALE, syn.OUT_SCALE)
+        assert np.array_equal(o1.download(), got[c])
+
+
+@pytest.mark.parametrize("m,n,k", [(3, 256, 1536), (9, 1536, 256), (40, 1000, 1536),
+                                   (130, 300, 6144), (200, 1536, 256)])
+def test_qmatmul8_shapes(gpu, oracle, m, n, k):
+    w = syn.int8_weights("q8", f"{m}x{n}x{k}", n, k)
+    s = syn.row_scales("q8", f"{m}x{n}x{k}", n)
+    x = syn.activations("q8", f"{m}x{n}x{k}", m, k)
+    print(f"qmatmul8 m={m} n={n} k={k} kernel={gpu.kernel_for_shape(8, m, n, k)}", flush=True)
+    want = oracle.qmatmul8(w, s, x.astype(np.float32), n, k, m, 0.05, 0.1)
+    of = out_buf(gpu, (m, n), np.float32)
+    gpu.bind("qmatmul-8bit", {"wq": dev(gpu, w), "scales": dev(gpu, s), "x": dev(gpu, x)}, of,
+             {"k": k, "numRows": n, "mCols": m, "inScale": 0.05, "outScale": 0.1})
+    assert f32_equal(of.download(), want)
+
+
+@pytest.mark.parametrize("m,n", [(37, 1000), (129, 2047), (64, 128)])
+def test_int4_partial_tiles(gpu, oracle, m, n):
+    k = 2048
+    w = syn.int4_weights("tiles", f"{m}x{n}", n, k)
+    s = syn.row_scales("tiles", f"{m}x{n}", n)
+    x = syn.activations("tiles", f"{m}x{n}", m, k)
+    print(f"partial tiles m={m} n={n}", flush=True)
+    _, acc, codes = oracle.qgemm(4, w, s, x.astype(np.float32), n, k, m, 0.05, 0.1)
+    o32 = out_buf(gpu, (m, n), np.int32)
+    gpu.qgemm(4, dev(gpu, w), dev(gpu, s), dev(gpu, x), o32, k, n, m, 0.05, 0.1)
+    assert np.array_equal(o32.download(), acc)
+
+
+def test_uncalibrated_gemm_grid_exact(gpu, oracle):
+    g = np.random.default_rng(53)
+    w = g.integers(0, 256, size=(64, 256), dtype=np.uint8)
+    s = g.uniform(0.005, 0.02, 64).astype(np.float32)
+    x = (g.integers(-64, 65, size=(5, 512)) / 8.0).astype(np.float32)
+    want, _, _ = oracle.qgemm(4, w, s, x, 64, 512, 5, 0.0, 0.0625)
+    of = out_buf(gpu, (5, 64), np.float32)
+    gpu.qgemm(4, dev(gpu, w), dev(gpu, s), dev(gpu, x), of, 512, 64, 5, 0.0, 0.0625)
+    assert f32_equal(of.download(), want)
