@@ -12,6 +12,11 @@
 
 namespace g4 {
 
+// Native 128-bit vectors for register arrays: HIP's uint4 is a union-wrapped struct that the
+// optimizer keeps in memory when it sits in an array (then promoted to LDS or scratch).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+
 // ---- host: status and last error ----------------------------------------------------------------
 
 int set_error(int status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
@@ -48,6 +53,27 @@ __device__ __forceinline__ float srq_code_f(float v, float s) {
 
 __device__ __forceinline__ int srq_code_i(float v, float s) { return (int)srq_code_f(v, s); }
 
+// The same code without a divide on the common path. With r = fl(1/s), t = fl(v * r) is within
+// |v/s| * 1.5 * 2^-23 of the correctly rounded quotient fl(v / s), so both round to the same
+// integer unless t lies within that distance of a half integer; there (about 1e-5 of the inputs)
+// the IEEE divide decides. Beyond |v/s| = 256 both clamp. `r_ok` is false when 1/s overflows, and
+// then every element takes the divide.
+__device__ __forceinline__ float srq_code_fast(float v, float s, float r, bool r_ok) {
+    const float t = __fmul_rn(v, r);
+    float n = rintf(t);
+    const float d = fabsf(t - n);
+    const float thr = fmaxf(fabsf(t), 1.0f) * 0x1p-20f;
+    if (!r_ok || d >= 0.5f - thr) n = rintf(__fdiv_rn(v, s));
+    return fminf(fmaxf(n, -128.0f), 127.0f);
+}
+
+// fl(1/s) and whether it is finite (a subnormal or zero scale leaves only the divide).
+__device__ __forceinline__ float srq_recip(float s, bool &ok) {
+    const float r = __fdiv_rn(1.0f, s);
+    ok = isfinite(r) && r != 0.0f;
+    return r;
+}
+
 // The closing expression of every quantized linear (qgemv.ts:1168-1172, :680-686), in its order:
 // one f32 multiply folds the input scale into the row scale, one more multiplies the reduced sum.
 __device__ __forceinline__ float linear_epilogue(float in_scale, float row_scale, float sum) {
@@ -73,6 +99,17 @@ __device__ __forceinline__ void store_linear_out(void *dst, int64_t idx, int out
 __device__ __forceinline__ float load_act(const void *x, int kind, int64_t i) {
     if (kind == G4_KIND_F16) return __half2float(reinterpret_cast<const __half *>(x)[i]);
     return reinterpret_cast<const float *>(x)[i];
+}
+
+// ---- device: block barrier for LDS-only communication ------------------------------------------
+
+// A workgroup barrier for kernels whose waves communicate only through LDS. __syncthreads() is a
+// release/acquire fence plus s_barrier, and the fence drains every outstanding global load of the
+// wave (vmcnt), which would empty a prefetch pipeline at each stage. Here only this wave's LDS
+// traffic is waited for (lgkmcnt(0)); the "memory" clobber keeps the compiler from moving memory
+// operations across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // ---- device: cross-lane sums --------------------------------------------------------------------

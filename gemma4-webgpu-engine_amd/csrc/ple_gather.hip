@@ -2,9 +2,9 @@
 // (src/kernels/embedGather.ts:176-261, :435-485), plus one fused launch over every slice of a
 // split table (the reference dispatches once per slice, embedGather.ts:403-419).
 //
-// One thread per 16 bytes of a gathered row: it reads 32 packed codes with one 128-bit load and
-// writes 32 outputs (64 bytes of f16, 128 of f32, 32 of int8) with 128-bit stores, so consecutive
-// threads read and write consecutive bytes of one row. The arithmetic is the reference's: fold the
+// One thread per 4 bytes of a gathered row: it reads 8 packed codes with one 32-bit load and
+// writes 8 outputs (one 16-byte f16 store, two of f32, one 8-byte of int8), so each load and store
+// instruction of a wave covers one contiguous run of the row. The arithmetic is the reference's: fold the
 // embed scale 16 into the group scale in f32 (exact, a power of two), then one multiply per
 // element, f32((code - 8) * f32(16 * scale)), rounded to f16 ties-to-even for the f16 output.
 // The scale index follows the shader (embedGather.ts:245-248): group of col = 4 j, so a group
@@ -28,39 +28,29 @@ __device__ __forceinline__ float scale_at(const void *scales, int kind, int64_t 
     return reinterpret_cast<const float *>(scales)[i];
 }
 
-// Writes the 32 outputs of chunk `ch` of slot `slot`. `src` is the 16-byte code chunk, or null
-// for an id no slice carries (written as zeros).
+// Writes the 8 outputs of chunk `ch` (codes 8 ch .. 8 ch + 7, one packed u32) of slot `slot`.
+// `src` points at the code word, or is null for an id no slice carries (written as zeros).
 __device__ __forceinline__ void gather_chunk(const uint8_t *src, const void *scales, int scale_kind,
                                              int64_t row, void *dst, int out_kind, int64_t slot,
                                              int ch, int cols, int group_size, int groups_per_row) {
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (src) v = *reinterpret_cast<const uint4 *>(src);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    const int col0 = ch * 32;
+    const uint32_t w = src ? *reinterpret_cast<const uint32_t *>(src) : 0x88888888u;
+    const int col0 = ch * 8;
     const int64_t obase = slot * (int64_t)cols + col0;
     if (out_kind == G4_KIND_I8) {
-        uint32_t o[8];
+        // code - 8 per nibble, low nibble first: bytes 0..3 from nibbles 0..3, 4..7 from 4..7.
+        uint32_t lo = 0, hi = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            // code - 8 per nibble, two words of four signed bytes per packed word
-            const uint32_t word = w[i >> 1];
-            const uint32_t nib4 = (word >> (16 * (i & 1)));
-            uint32_t packed = 0;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int code = src ? (int)((nib4 >> (4 * q)) & 0xf) - 8 : 0;
-                packed |= (uint32_t)(code & 0xff) << (8 * q);
-            }
-            o[i] = packed;
+        for (int q = 0; q < 4; ++q) {
+            lo |= (uint32_t)((int)((w >> (4 * q)) & 0xf) - 8 & 0xff) << (8 * q);
+            hi |= (uint32_t)((int)((w >> (16 + 4 * q)) & 0xf) - 8 & 0xff) << (8 * q);
         }
-        uint4 *d = reinterpret_cast<uint4 *>(reinterpret_cast<int8_t *>(dst) + obase);
-        d[0] = make_uint4(o[0], o[1], o[2], o[3]);
-        d[1] = make_uint4(o[4], o[5], o[6], o[7]);
+        *reinterpret_cast<uint2 *>(reinterpret_cast<int8_t *>(dst) + obase) = make_uint2(lo, hi);
         return;
     }
-    float out[32];
+    float out[8];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < 2; ++q) {
+        // One scale per vec4 of output, the group of its first column (embedGather.ts:245-248).
         float scale = 0.0f;
         if (src) {
             const int col = col0 + 4 * q;
@@ -70,26 +60,24 @@ __device__ __forceinline__ void gather_chunk(const uint8_t *src, const void *sca
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int i = 4 * q + e;
-            const int code = (int)((w[i >> 3] >> (4 * (i & 7))) & 0xf) - 8;
-            out[i] = src ? __fmul_rn((float)code, scale) : 0.0f;
+            const int code = (int)((w >> (4 * i)) & 0xf) - 8;
+            out[i] = __fmul_rn((float)code, scale);
         }
     }
     if (out_kind == G4_KIND_F16) {
-        uint32_t h[16];
+        uint32_t h[4];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < 4; ++i) {
             const unsigned short lo = __half_as_ushort(__float2half_rn(out[2 * i]));
             const unsigned short hi = __half_as_ushort(__float2half_rn(out[2 * i + 1]));
             h[i] = (uint32_t)lo | ((uint32_t)hi << 16);
         }
-        uint4 *d = reinterpret_cast<uint4 *>(reinterpret_cast<__half *>(dst) + obase);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) d[i] = make_uint4(h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]);
+        *reinterpret_cast<uint4 *>(reinterpret_cast<__half *>(dst) + obase) =
+            make_uint4(h[0], h[1], h[2], h[3]);
     } else {
         float4 *d = reinterpret_cast<float4 *>(reinterpret_cast<float *>(dst) + obase);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            d[i] = make_float4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
+        d[0] = make_float4(out[0], out[1], out[2], out[3]);
+        d[1] = make_float4(out[4], out[5], out[6], out[7]);
     }
 }
 
@@ -99,7 +87,7 @@ __global__ __launch_bounds__(kGatherThreads) void ple_gather_kernel(
     const uint8_t *codes, const void *scales, int scale_kind, const int32_t *ids, void *dst,
     int out_kind, int slots, int cols, int group_size, int groups_per_row, int sliced,
     int64_t start, int64_t count) {
-    const int chunks = cols >> 5;
+    const int chunks = cols >> 3;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= (int64_t)slots * chunks) return;
     const int64_t slot = t / chunks;
@@ -108,7 +96,7 @@ __global__ __launch_bounds__(kGatherThreads) void ple_gather_kernel(
     const bool inside = row >= start && row - start < count;
     if (!inside && sliced) return;
     const uint8_t *src =
-        inside ? codes + (row - start) * (int64_t)(cols >> 1) + (int64_t)ch * 16 : nullptr;
+        inside ? codes + (row - start) * (int64_t)(cols >> 1) + (int64_t)ch * 4 : nullptr;
     gather_chunk(src, scales, scale_kind, row, dst, out_kind, slot, ch, cols, group_size,
                  groups_per_row);
 }
@@ -117,7 +105,7 @@ __global__ __launch_bounds__(kGatherThreads) void ple_gather_kernel(
 __global__ __launch_bounds__(kGatherThreads) void ple_gather_split_kernel(
     SliceTable tab, const void *scales, int scale_kind, const int32_t *ids, void *dst, int out_kind,
     int slots, int cols, int group_size, int groups_per_row) {
-    const int chunks = cols >> 5;
+    const int chunks = cols >> 3;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= (int64_t)slots * chunks) return;
     const int64_t slot = t / chunks;
@@ -127,7 +115,7 @@ __global__ __launch_bounds__(kGatherThreads) void ple_gather_split_kernel(
 #pragma unroll
     for (int s = 0; s < kMaxSlices; ++s) {
         if (s < tab.n && row >= tab.start[s] && row - tab.start[s] < tab.count[s])
-            src = tab.codes[s] + (row - tab.start[s]) * (int64_t)(cols >> 1) + (int64_t)ch * 16;
+            src = tab.codes[s] + (row - tab.start[s]) * (int64_t)(cols >> 1) + (int64_t)ch * 4;
     }
     gather_chunk(src, scales, scale_kind, row, dst, out_kind, slot, ch, cols, group_size,
                  groups_per_row);
@@ -139,8 +127,8 @@ static int check_gather(const void *scales, int scale_kind, const int32_t *ids, 
     if (!scales || !ids || !dst)
         return set_error(G4_ERR_INVALID, "%s needs inputs named codes, scales and ids", who);
     if (slots <= 0) return set_error(G4_ERR_INVALID, "%s: params.slots must be positive", who);
-    if (cols <= 0 || cols % 32 != 0)
-        return set_error(G4_ERR_UNSUPPORTED, "%s: %d columns are not whole 32-code chunks", who, cols);
+    if (cols <= 0 || cols % 8 != 0)
+        return set_error(G4_ERR_INVALID, "%s: %d columns do not pack evenly at 4 bits", who, cols);
     if (group_size <= 0 || group_size % 4 != 0 || cols % group_size != 0)
         return set_error(G4_ERR_INVALID, "%s: group size %d does not divide %d in vec4 steps", who,
                          group_size, cols);
@@ -179,9 +167,9 @@ int g4_ple_gather(const void *codes, const void *scales, int scale_kind, const i
                                   "bound the ids");
     if (!sliced && slice_start_row != 0)
         return set_error(G4_ERR_INVALID, "ple-gather-4bit: an unsliced table starts at row 0");
-    if (reinterpret_cast<uintptr_t>(codes) & 15)
-        return set_error(G4_ERR_INVALID, "%s: codes must be 16-byte aligned", who);
-    const int64_t threads = (int64_t)slots * (cols / 32);
+    if (reinterpret_cast<uintptr_t>(codes) & 3)
+        return set_error(G4_ERR_INVALID, "%s: codes must be 4-byte aligned", who);
+    const int64_t threads = (int64_t)slots * (cols / 8);
     const int64_t blocks = (threads + kGatherThreads - 1) / kGatherThreads;
     hipLaunchKernelGGL(ple_gather_kernel, dim3((unsigned)blocks), dim3(kGatherThreads), 0,
                        as_stream(stream), reinterpret_cast<const uint8_t *>(codes), scales,
@@ -204,8 +192,8 @@ int g4_ple_gather_split(const void *const *slice_codes, const int64_t *slice_sta
     SliceTable tab{};
     tab.n = num_slices;
     for (int s = 0; s < num_slices; ++s) {
-        if (!slice_codes[s] || (reinterpret_cast<uintptr_t>(slice_codes[s]) & 15))
-            return set_error(G4_ERR_INVALID, "%s: slice %d codes missing or not 16-byte aligned", who, s);
+        if (!slice_codes[s] || (reinterpret_cast<uintptr_t>(slice_codes[s]) & 3))
+            return set_error(G4_ERR_INVALID, "%s: slice %d codes missing or not 4-byte aligned", who, s);
         if (slice_starts[s] < 0 || slice_counts[s] <= 0)
             return set_error(G4_ERR_INVALID,
                              "%s needs params sliceStartRow and sliceRowCount naming a non empty "
@@ -214,7 +202,7 @@ int g4_ple_gather_split(const void *const *slice_codes, const int64_t *slice_sta
         tab.start[s] = slice_starts[s];
         tab.count[s] = slice_counts[s];
     }
-    const int64_t threads = (int64_t)slots * (cols / 32);
+    const int64_t threads = (int64_t)slots * (cols / 8);
     const int64_t blocks = (threads + kGatherThreads - 1) / kGatherThreads;
     hipLaunchKernelGGL(ple_gather_split_kernel, dim3((unsigned)blocks), dim3(kGatherThreads), 0,
                        as_stream(stream), tab, scales, scale_kind, ids, dst, out_kind, slots, cols,

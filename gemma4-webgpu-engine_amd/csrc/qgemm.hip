@@ -32,7 +32,6 @@ int gemv_columns(int bits, const void *wq, const float *scales, const void *x, i
                  void *dst, int out_kind, int k, int num_rows, int m_cols, float in_scale,
                  float out_scale, hipStream_t stream, const char *who);
 
-typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kQuantThreads = 256;
 constexpr int kTileBK = 128;
@@ -55,6 +54,8 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_rows_kernel(
     int local = 0;
     const int groups = kp >> 3;
     const int live = k >> 3;
+    bool r_ok;
+    const float r = srq_recip(scale, r_ok);
     for (int g = tid; g < groups; g += kQuantThreads) {
         int c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         if (g < live) {
@@ -68,7 +69,8 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_rows_kernel(
                 }
             } else {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) c[i] = srq_code_i(load_act(x, x_kind, e + i), scale);
+                for (int i = 0; i < 8; ++i)
+                    c[i] = (int)srq_code_fast(load_act(x, x_kind, e + i), scale, r, r_ok);
             }
         }
         uint2 out;
@@ -92,7 +94,10 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_rows_kernel(
 __global__ void srq_quantize_kernel(const void *x, int x_kind, int8_t *codes, int64_t n, float s) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = i; e < n; e += stride) codes[e] = (int8_t)srq_code_i(load_act(x, x_kind, e), s);
+    bool r_ok;
+    const float r = srq_recip(s, r_ok);
+    for (int64_t e = i; e < n; e += stride)
+        codes[e] = (int8_t)srq_code_fast(load_act(x, x_kind, e), s, r, r_ok);
 }
 
 // The B operand of one 16x16x64 step from 8 bytes (16 codes) of weights at `p`.
@@ -158,22 +163,22 @@ __global__ __launch_bounds__(256) void qgemm_skinny_kernel(
 
     constexpr int BATCH = 4;
     for (int kb0 = wave; kb0 < ksteps; kb0 += 4 * BATCH) {
-        uint4 bw[BATCH][BITS == 4 ? 1 : 2];
-        uint4 av[BATCH][TM][2];
+        u32x4 bw[BATCH][BITS == 4 ? 1 : 2];
+        u32x4 av[BATCH][TM][2];
 #pragma unroll
         for (int u = 0; u < BATCH; ++u) {
             const int kb = kb0 + 4 * u;
             if (kb < ksteps) {
                 if (BITS == 4) {
-                    bw[u][0] = *reinterpret_cast<const uint4 *>(wrow + kb * 64 + g * 16);
+                    bw[u][0] = *reinterpret_cast<const u32x4 *>(wrow + kb * 64 + g * 16);
                 } else {
-                    bw[u][0] = *reinterpret_cast<const uint4 *>(wrow + kb * 128 + g * 32);
+                    bw[u][0] = *reinterpret_cast<const u32x4 *>(wrow + kb * 128 + g * 32);
                     bw[u][BITS == 4 ? 0 : 1] =
-                        *reinterpret_cast<const uint4 *>(wrow + kb * 128 + g * 32 + 16);
+                        *reinterpret_cast<const u32x4 *>(wrow + kb * 128 + g * 32 + 16);
                 }
 #pragma unroll
                 for (int t = 0; t < TM; ++t) {
-                    const uint4 *ap = reinterpret_cast<const uint4 *>(arow[t] + kb * 128 + g * 32);
+                    const u32x4 *ap = reinterpret_cast<const u32x4 *>(arow[t] + kb * 128 + g * 32);
                     av[u][t][0] = ap[0];
                     av[u][t][1] = ap[1];
                 }
@@ -189,13 +194,11 @@ __global__ __launch_bounds__(256) void qgemm_skinny_kernel(
                     if (BITS == 4) {
                         b = b_operand<4>(bw[u][0].x, bw[u][0].y, bw[u][0].z, bw[u][0].w, s);
                     } else {
-                        const uint4 q = bw[u][BITS == 4 ? 0 : s];
-                        b = v4i{(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+                        b = __builtin_bit_cast(v4i, bw[u][BITS == 4 ? 0 : s]);
                     }
 #pragma unroll
                     for (int t = 0; t < TM; ++t) {
-                        const uint4 q = av[u][t][s];
-                        const v4i a = v4i{(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+                        const v4i a = __builtin_bit_cast(v4i, av[u][t][s]);
                         acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[t], 0, 0, 0);
                     }
                 }
@@ -232,18 +235,24 @@ __global__ __launch_bounds__(256) void qgemm_skinny_kernel(
     }
 }
 
-// ---- tile: 128 x 128 outputs per block, 4 waves of 64 x 64, K in 128-code LDS stages --------
-template <int BITS>
-__global__ __launch_bounds__(256) void qgemm_tile_kernel(
+// ---- tile: 128 x BN outputs per block (BN 128 or 96), 4 waves of 64 x BN/2, K in 128-code
+// stages. Global loads run D = 4 stages ahead through a register ring; LDS is double-buffered, so
+// while a stage is contracted the next is in LDS and the two after it are in flight. Padding of 16
+// bytes per LDS row keeps the 16-byte fragment reads of 8 consecutive lanes on distinct banks.
+template <int BITS, int BN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void qgemm_tile_kernel(
     const int8_t *__restrict__ A, const int *__restrict__ row_sums, const uint8_t *__restrict__ W,
     const float *__restrict__ scales, void *dst, int M, int N, int K, int kp, float in_scale,
     float out_scale, int out_kind, int tiles_m, int tiles_n, int xcd_swizzle) {
-    constexpr int BM = 128, BN = 128, BK = kTileBK;
+    constexpr int BM = 128, BK = kTileBK, D = 4;
     constexpr int A_STRIDE = BK + 16;
     constexpr int B_ROW = BITS == 4 ? BK / 2 : BK;
     constexpr int B_STRIDE = B_ROW + 16;
-    constexpr int A_CHUNKS = BM * BK / 16 / 256;      // 16-byte chunks per thread per stage
-    constexpr int B_CHUNKS = BN * B_ROW / 16 / 256;
+    constexpr int A_CH = BM * BK / 16 / 256;  // 16-byte chunks per thread per stage
+    constexpr int B_TOTAL = BN * B_ROW / 16;
+    constexpr int B_CH = (B_TOTAL + 255) / 256;
+    constexpr int B_PER_ROW = B_ROW / 16;
+    constexpr int TN = BN / 2 / 16;  // MFMA column tiles per wave
     __shared__ __align__(16) uint8_t sA[2][BM * A_STRIDE];
     __shared__ __align__(16) uint8_t sB[2][BN * B_STRIDE];
 
@@ -273,98 +282,128 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(
     const int row_bytes = BITS == 4 ? (K >> 1) : K;
     const int ksteps = K / BK;
 
-    // Global source addresses of this thread's staging chunks (rows clamped; stores are guarded).
-    const int8_t *a_src[A_CHUNKS];
-    int a_dst[A_CHUNKS];
+    const int8_t *a_src[A_CH];
+    int a_dst[A_CH];
 #pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) {
+    for (int i = 0; i < A_CH; ++i) {
         const int q = tid + 256 * i;
         const int row = q >> 3, c16 = q & 7;
         a_src[i] = A + (int64_t)min(m0 + row, M - 1) * kp + c16 * 16;
         a_dst[i] = row * A_STRIDE + c16 * 16;
     }
-    const uint8_t *b_src[B_CHUNKS];
-    int b_dst[B_CHUNKS];
+    const uint8_t *b_src[B_CH];
+    int b_dst[B_CH];
 #pragma unroll
-    for (int i = 0; i < B_CHUNKS; ++i) {
-        const int q = tid + 256 * i;
-        const int per_row = B_ROW / 16;
-        const int row = q / per_row, c16 = q % per_row;
+    for (int i = 0; i < B_CH; ++i) {
+        const int q = min(tid + 256 * i, B_TOTAL - 1);
+        const int row = q / B_PER_ROW, c16 = q % B_PER_ROW;
         b_src[i] = W + (int64_t)min(n0 + row, N - 1) * row_bytes + c16 * 16;
         b_dst[i] = row * B_STRIDE + c16 * 16;
     }
 
-    uint4 ra[A_CHUNKS], rb[B_CHUNKS];
-    auto load_stage = [&](int kb) {
-#pragma unroll
-        for (int i = 0; i < A_CHUNKS; ++i)
-            ra[i] = *reinterpret_cast<const uint4 *>(a_src[i] + kb * BK);
-#pragma unroll
-        for (int i = 0; i < B_CHUNKS; ++i)
-            rb[i] = *reinterpret_cast<const uint4 *>(b_src[i] + kb * B_ROW);
-    };
-    auto store_stage = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < A_CHUNKS; ++i) *reinterpret_cast<uint4 *>(&sA[buf][a_dst[i]]) = ra[i];
-#pragma unroll
-        for (int i = 0; i < B_CHUNKS; ++i) *reinterpret_cast<uint4 *>(&sB[buf][b_dst[i]]) = rb[i];
-    };
+    // The ring: four named slots (not an indexed array) so each stays a fixed set of registers.
+    u32x4 ra0[A_CH], ra1[A_CH], ra2[A_CH], ra3[A_CH];
+    u32x4 rb0[B_CH], rb1[B_CH], rb2[B_CH], rb3[B_CH];
+    static_assert(D == 4, "the ring below is written out for four slots");
+    // Unconditional loads (a stage past the end re-reads the last one): a load inside a branch
+    // makes the wait-count pass drain every outstanding load at the merge. Macros rather than
+    // lambdas over array references, so the ring slots are promoted to registers.
+#define G4_LOAD_STAGE(XA, XB, KB)                                                          \
+    do {                                                                                   \
+        const int kc_ = min((KB), ksteps - 1);                                             \
+        _Pragma("unroll") for (int i_ = 0; i_ < A_CH; ++i_) XA[i_] =                       \
+            *reinterpret_cast<const u32x4 *>(a_src[i_] + kc_ * BK);                        \
+        _Pragma("unroll") for (int i_ = 0; i_ < B_CH; ++i_) XB[i_] =                       \
+            *reinterpret_cast<const u32x4 *>(b_src[i_] + kc_ * B_ROW);                     \
+    } while (0)
+    // Threads past the last B chunk hold a copy of it (their index is clamped) and store that
+    // same value to the same place: no branch, so the loads stay in flight.
+#define G4_STORE_STAGE(XA, XB, BUF)                                                        \
+    do {                                                                                   \
+        _Pragma("unroll") for (int i_ = 0; i_ < A_CH; ++i_)                                \
+            *reinterpret_cast<u32x4 *>(&sA[(BUF)][a_dst[i_]]) = XA[i_];                    \
+        _Pragma("unroll") for (int i_ = 0; i_ < B_CH; ++i_)                                \
+            *reinterpret_cast<u32x4 *>(&sB[(BUF)][b_dst[i_]]) = XB[i_];                    \
+    } while (0)
 
-    v4i acc[4][4];
+    v4i acc[4][TN];
 #pragma unroll
     for (int x = 0; x < 4; ++x)
 #pragma unroll
-        for (int y = 0; y < 4; ++y) acc[x][y] = v4i{0, 0, 0, 0};
+        for (int y = 0; y < TN; ++y) acc[x][y] = v4i{0, 0, 0, 0};
 
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
-    for (int kb = 0; kb < ksteps; ++kb) {
-        const int buf = kb & 1;
-        if (kb + 1 < ksteps) load_stage(kb + 1);
+    auto compute = [&](int buf) {
         const uint8_t *la = sA[buf];
         const uint8_t *lb = sB[buf];
-        uint4 bq[4][BITS == 4 ? 1 : 2];
+        u32x4 bq[TN][BITS == 4 ? 1 : 2];
 #pragma unroll
-        for (int y = 0; y < 4; ++y) {
-            const int col = wn * 64 + y * 16 + j;
+        for (int y = 0; y < TN; ++y) {
+            const int col = wn * (BN / 2) + y * 16 + j;
             if (BITS == 4) {
-                bq[y][0] = *reinterpret_cast<const uint4 *>(lb + col * B_STRIDE + g * 16);
+                bq[y][0] = *reinterpret_cast<const u32x4 *>(lb + col * B_STRIDE + g * 16);
             } else {
-                bq[y][0] = *reinterpret_cast<const uint4 *>(lb + col * B_STRIDE + g * 32);
+                bq[y][0] = *reinterpret_cast<const u32x4 *>(lb + col * B_STRIDE + g * 32);
                 bq[y][BITS == 4 ? 0 : 1] =
-                    *reinterpret_cast<const uint4 *>(lb + col * B_STRIDE + g * 32 + 16);
+                    *reinterpret_cast<const u32x4 *>(lb + col * B_STRIDE + g * 32 + 16);
             }
         }
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            v4i bo[4];
+            v4i bo[TN];
 #pragma unroll
-            for (int y = 0; y < 4; ++y) {
+            for (int y = 0; y < TN; ++y) {
                 if (BITS == 4) {
                     bo[y] = b_operand<4>(bq[y][0].x, bq[y][0].y, bq[y][0].z, bq[y][0].w, s);
                 } else {
-                    const uint4 q = bq[y][BITS == 4 ? 0 : s];
-                    bo[y] = v4i{(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+                    bo[y] = __builtin_bit_cast(v4i, bq[y][BITS == 4 ? 0 : s]);
                 }
             }
 #pragma unroll
             for (int x = 0; x < 4; ++x) {
                 const int row = wm * 64 + x * 16 + j;
-                const uint4 q = *reinterpret_cast<const uint4 *>(la + row * A_STRIDE + g * 32 + s * 16);
-                const v4i ao = v4i{(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+                const v4i ao = *reinterpret_cast<const v4i *>(la + row * A_STRIDE + g * 32 + s * 16);
 #pragma unroll
-                for (int y = 0; y < 4; ++y)
+                for (int y = 0; y < TN; ++y)
                     acc[x][y] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ao, bo[y], acc[x][y], 0, 0, 0);
             }
         }
-        if (kb + 1 < ksteps) store_stage(buf ^ 1);
-        __syncthreads();
+    };
+
+    // Stage s lives in ring slot s % D. Prologue: stages 0..D-1 requested, stage 0 stored to LDS
+    // and its slot refilled with stage D. Iteration kb then stores stage kb + 1 and refills that
+    // slot with stage kb + 1 + D, so D stages stay in flight behind the one being contracted.
+    G4_LOAD_STAGE(ra0, rb0, 0);
+    G4_LOAD_STAGE(ra1, rb1, 1);
+    G4_LOAD_STAGE(ra2, rb2, 2);
+    G4_LOAD_STAGE(ra3, rb3, 3);
+    G4_STORE_STAGE(ra0, rb0, 0);
+    G4_LOAD_STAGE(ra0, rb0, D);
+    lds_barrier();
+#define G4_TILE_ITER(XA, XB, KB)                 \
+    do {                                         \
+        compute((KB) & 1);                       \
+        G4_STORE_STAGE(XA, XB, ((KB) + 1) & 1);  \
+        G4_LOAD_STAGE(XA, XB, (KB) + 1 + D);     \
+        lds_barrier();                           \
+    } while (0)
+    // Whole groups of D stages run without guards; the last partial group is guarded.
+    int kb0 = 0;
+    for (; kb0 + D <= ksteps; kb0 += D) {
+        G4_TILE_ITER(ra1, rb1, kb0);
+        G4_TILE_ITER(ra2, rb2, kb0 + 1);
+        G4_TILE_ITER(ra3, rb3, kb0 + 2);
+        G4_TILE_ITER(ra0, rb0, kb0 + 3);
     }
+    if (kb0 < ksteps) G4_TILE_ITER(ra1, rb1, kb0);
+    if (kb0 + 1 < ksteps) G4_TILE_ITER(ra2, rb2, kb0 + 1);
+    if (kb0 + 2 < ksteps) G4_TILE_ITER(ra3, rb3, kb0 + 2);
+#undef G4_TILE_ITER
+#undef G4_LOAD_STAGE
+#undef G4_STORE_STAGE
 
 #pragma unroll
-    for (int y = 0; y < 4; ++y) {
-        const int n = n0 + wn * 64 + y * 16 + j;
+    for (int y = 0; y < TN; ++y) {
+        const int n = n0 + wn * (BN / 2) + y * 16 + j;
         if (n >= N) continue;
         const float scale = scales[n];
 #pragma unroll
@@ -454,12 +493,22 @@ static int launch_mfma(KernelChoice c, const int8_t *codes, const int *sums, con
         G4_LAUNCHED("qgemm_skinny_kernel");
         return G4_OK;
     }
+    // 128 x 96 tiles when they fill the CUs better than 128 x 128 (e.g. 512 x 6144: 256 tiles).
     const int tiles_m = (m + 127) / 128;
-    const int tiles_n = (n + 127) / 128;
+    const int cus = device_cu_count();
+    const bool use96 = n % 96 == 0 && (int64_t)tiles_m * ((n + 127) / 128) < cus &&
+                       (int64_t)tiles_m * (n / 96) <= (int64_t)cus + cus / 8;
+    const int bn = use96 ? 96 : 128;
+    const int tiles_n = (n + bn - 1) / bn;
     const int swizzle = (tiles_n % 8 == 0) ? 1 : 0;
-    hipLaunchKernelGGL((qgemm_tile_kernel<BITS>), dim3(tiles_m * tiles_n), dim3(256), 0, stream,
-                       codes, sums, w, scales, dst, m, n, k, kp, in_scale, out_scale, out_kind,
-                       tiles_m, tiles_n, swizzle);
+    if (use96)
+        hipLaunchKernelGGL((qgemm_tile_kernel<BITS, 96>), dim3(tiles_m * tiles_n), dim3(256), 0,
+                           stream, codes, sums, w, scales, dst, m, n, k, kp, in_scale, out_scale,
+                           out_kind, tiles_m, tiles_n, swizzle);
+    else
+        hipLaunchKernelGGL((qgemm_tile_kernel<BITS, 128>), dim3(tiles_m * tiles_n), dim3(256), 0,
+                           stream, codes, sums, w, scales, dst, m, n, k, kp, in_scale, out_scale,
+                           out_kind, tiles_m, tiles_n, swizzle);
     G4_LAUNCHED("qgemm_tile_kernel");
     return G4_OK;
 }

@@ -29,6 +29,7 @@ constexpr int kGemvThreads = 256;
 constexpr int kRowsPerPass = 16;
 constexpr int kMaxGemvK = 16384;
 constexpr int kChunkBatch = 4;
+constexpr int kMaxPasses = 8;
 
 struct GemvJob {
     const uint8_t *w;
@@ -44,6 +45,7 @@ struct GemvJob {
     float out_scale;
     int wg_begin;
     int passes;
+    int kwaves;  // waves splitting K inside a block: 1, 2 or 4
 };
 
 struct GemvLaunch {
@@ -91,7 +93,8 @@ __device__ __forceinline__ int find_job(const GemvLaunch &L, int b) {
 }
 
 // Snap 8 activations starting at element e (f32, f16 or ready int8 codes) into codes c[0..7].
-__device__ __forceinline__ void load_codes8(const void *x, int kind, int64_t e, float s, int c[8]) {
+__device__ __forceinline__ void load_codes8(const void *x, int kind, int64_t e, float s, float r,
+                                            bool r_ok, int c[8]) {
     if (kind == G4_KIND_I8) {
         uint2 v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const int8_t *>(x) + e);
 #pragma unroll
@@ -106,27 +109,89 @@ __device__ __forceinline__ void load_codes8(const void *x, int kind, int64_t e, 
         for (int i = 0; i < 4; ++i) {
             __half lo = __ushort_as_half((unsigned short)(w[i] & 0xffff));
             __half hi = __ushort_as_half((unsigned short)(w[i] >> 16));
-            c[2 * i] = srq_code_i(__half2float(lo), s);
-            c[2 * i + 1] = srq_code_i(__half2float(hi), s);
+            c[2 * i] = (int)srq_code_fast(__half2float(lo), s, r, r_ok);
+            c[2 * i + 1] = (int)srq_code_fast(__half2float(hi), s, r, r_ok);
         }
     } else {
         const float4 *p = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(x) + e);
         float4 a = p[0], b = p[1];
-        c[0] = srq_code_i(a.x, s);
-        c[1] = srq_code_i(a.y, s);
-        c[2] = srq_code_i(a.z, s);
-        c[3] = srq_code_i(a.w, s);
-        c[4] = srq_code_i(b.x, s);
-        c[5] = srq_code_i(b.y, s);
-        c[6] = srq_code_i(b.z, s);
-        c[7] = srq_code_i(b.w, s);
+        c[0] = (int)srq_code_fast(a.x, s, r, r_ok);
+        c[1] = (int)srq_code_fast(a.y, s, r, r_ok);
+        c[2] = (int)srq_code_fast(a.z, s, r, r_ok);
+        c[3] = (int)srq_code_fast(a.w, s, r, r_ok);
+        c[4] = (int)srq_code_fast(b.x, s, r, r_ok);
+        c[5] = (int)srq_code_fast(b.y, s, r, r_ok);
+        c[6] = (int)srq_code_fast(b.z, s, r, r_ok);
+        c[7] = (int)srq_code_fast(b.w, s, r, r_ok);
     }
 }
 
+// A 16-byte streaming load: weights are read once, so keep them from displacing cached data.
+__device__ __forceinline__ u32x4 load16_stream(const uint8_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+}
+
+// Loads the 16-byte chunks [t0, t0 + kChunkBatch) of this lane (chunk index t * 16 + lane16 of the
+// wave's chunk range), zero past the range.
+__device__ __forceinline__ void load_batch(u32x4 (&dst)[kChunkBatch], const uint8_t *wrow, int t0,
+                                           int T, int nchw, int lane16) {
+#pragma unroll
+    for (int u = 0; u < kChunkBatch; ++u) {
+        const int t = t0 + u;
+        const int ch = t * 16 + lane16;
+        dst[u] = (t < T && ch < nchw) ? load16_stream(wrow + (int64_t)ch * 16) : u32x4{0, 0, 0, 0};
+    }
+}
+
+// Accumulates one batch of chunks against the LDS codes (xl = this wave's first chunk's codes).
+template <int COLS>
+__device__ __forceinline__ void dot_batch(int (&acc)[COLS], const u32x4 (&w)[kChunkBatch],
+                                          const uint8_t *xl0, int lds_stride, int bits, int t0,
+                                          int T, int nchw, int lane16) {
+#pragma unroll
+    for (int u = 0; u < kChunkBatch; ++u) {
+        const int t = t0 + u;
+        const int ch = t * 16 + lane16;
+        if (t < T && ch < nchw) {
+            const uint32_t wv[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+            for (int c = 0; c < COLS; ++c) {
+                const uint8_t *xl = xl0 + c * lds_stride;
+                int a = acc[c];
+                if (bits == 4) {
+                    const u32x4 xa = *reinterpret_cast<const u32x4 *>(xl + ch * 32);
+                    const u32x4 xb = *reinterpret_cast<const u32x4 *>(xl + ch * 32 + 16);
+                    const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t lo = wv[i] & 0x0F0F0F0Fu;
+                        const uint32_t hi = (wv[i] >> 4) & 0x0F0F0F0Fu;
+                        a = __builtin_amdgcn_sdot4((int)lo, (int)xv[2 * i], a, false);
+                        a = __builtin_amdgcn_sdot4((int)hi, (int)xv[2 * i + 1], a, false);
+                    }
+                } else {
+                    const u32x4 xa = *reinterpret_cast<const u32x4 *>(xl + ch * 16);
+                    a = __builtin_amdgcn_sdot4((int)wv[0], (int)xa.x, a, false);
+                    a = __builtin_amdgcn_sdot4((int)wv[1], (int)xa.y, a, false);
+                    a = __builtin_amdgcn_sdot4((int)wv[2], (int)xa.z, a, false);
+                    a = __builtin_amdgcn_sdot4((int)wv[3], (int)xa.w, a, false);
+                }
+                acc[c] = a;
+            }
+        }
+    }
+}
+
+// Block layout: wave w serves the 4-row group w / kwaves of each pass over the K part w % kwaves,
+// so a block covers 16 / kwaves rows per pass. Long rows (K >= 3072) split K over the waves so
+// every block streams about the same bytes; the parts fold through LDS integer atomics (exact).
+// The first weight batch is requested before the activation snap, so the weight latency overlaps
+// it.
 template <int COLS>
 __global__ __launch_bounds__(kGemvThreads) void qgemv_int_kernel(GemvLaunch L) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int s_sum[COLS];
+    __shared__ int s_acc[kMaxPasses * kRowsPerPass * COLS];
 
     const int j = find_job(L, blockIdx.x);
     const GemvJob &J = L.job[j];
@@ -136,23 +201,50 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_int_kernel(GemvLaunch L) {
     const int split = blockIdx.y;
     int c_lo, c_hi;
     split_band(k, bits, L.splits, split, L.split_exact, c_lo, c_hi);
-    const int kl = c_hi - c_lo;              // codes in this block's band (multiple of 32 or 16)
+    const int kl = c_hi - c_lo;              // codes in this block's band
     const int lds_stride = (kl + 15) & ~15;  // bytes of codes per column in LDS
 
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lane16 = lane & 15;
+    const int kwaves = J.kwaves;
+    const int rows_per_pass = kRowsPerPass / kwaves;
+    const int rgroup = wave / kwaves;
+    const int kpart = wave - rgroup * kwaves;
+    const int row_bytes = bits == 4 ? (k >> 1) : k;
+    const int cpc = bits == 4 ? 32 : 16;  // codes per 16-byte chunk
+    const int nch = kl / cpc;             // chunks of the band
+    const int w_lo = (nch * kpart) / kwaves;
+    const int nchw = (nch * (kpart + 1)) / kwaves - w_lo;  // chunks of this wave's part
+    const int T = (nchw + 15) >> 4;
+    const int block_row0 = (blockIdx.x - J.wg_begin) * (J.passes * rows_per_pass);
+    const int64_t band_off = (int64_t)(c_lo / cpc + w_lo) * 16;
+
+    auto row_of = [&](int p) { return block_row0 + p * rows_per_pass + rgroup * 4 + (lane >> 4); };
+    auto wrow_of = [&](int p) {
+        return J.w + (int64_t)min(row_of(p), J.rows - 1) * row_bytes + band_off;
+    };
+
+    // Request pass 0's first weight batch before touching the activations.
+    u32x4 cur[kChunkBatch];
+    load_batch(cur, wrow_of(0), 0, T, nchw, lane16);
+
+    for (int i = tid; i < kMaxPasses * kRowsPerPass * COLS; i += kGemvThreads) s_acc[i] = 0;
     if (tid < COLS) s_sum[tid] = 0;
     __syncthreads();
 
     // ---- snap the activation band into LDS (once per block) ----
     {
+        bool r_ok;
+        const float r = srq_recip(J.in_scale, r_ok);
         const int groups = kl >> 3;
         int local = 0;
-        int my_col = 0;
         for (int g = tid; g < groups * COLS; g += kGemvThreads) {
             const int col = COLS == 1 ? 0 : g / groups;
             const int gi = COLS == 1 ? g : g - col * groups;
             int c[8];
             const int64_t e = (int64_t)col * k + c_lo + gi * 8;
-            load_codes8(J.x, J.x_kind, e, J.in_scale, c);
+            load_codes8(J.x, J.x_kind, e, J.in_scale, r, r_ok, c);
             uint2 packed;
             if (bits == 4) {
                 packed.x = pack4(c[0], c[2], c[4], c[6]);
@@ -162,122 +254,82 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_int_kernel(GemvLaunch L) {
                 packed.y = pack4(c[4], c[5], c[6], c[7]);
             }
             *reinterpret_cast<uint2 *>(smem + col * lds_stride + gi * 8) = packed;
-            int sum8 = c[0] + c[1] + c[2] + c[3] + c[4] + c[5] + c[6] + c[7];
-            if (COLS == 1) {
+            const int sum8 = c[0] + c[1] + c[2] + c[3] + c[4] + c[5] + c[6] + c[7];
+            if (COLS == 1)
                 local += sum8;
-            } else {
+            else
                 atomicAdd(&s_sum[col], sum8);
-            }
-            my_col = col;
         }
-        (void)my_col;
         if (COLS == 1) {
             local = row16_sum_i32(local);
             if ((tid & 15) == 0 && local != 0) atomicAdd(&s_sum[0], local);
         }
     }
-    __syncthreads();
-
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int lane16 = lane & 15;
-    const int row_bytes = bits == 4 ? (k >> 1) : k;
-    const int cpc = bits == 4 ? 32 : 16;  // codes per 16-byte chunk
-    const int cb0 = c_lo / cpc;
-    const int nch = kl / cpc;
-    const int T = (nch + 15) >> 4;
-    const int row_block = (blockIdx.x - J.wg_begin) * (J.passes * kRowsPerPass);
+    lds_barrier();
 
     int sx[COLS];
 #pragma unroll
     for (int c = 0; c < COLS; ++c) sx[c] = s_sum[c];
+    const uint8_t *xl0 = smem + (int64_t)w_lo * (bits == 4 ? 32 : 16);
 
     for (int p = 0; p < J.passes; ++p) {
-        const int wave_row0 = row_block + p * kRowsPerPass + wave * 4;
-        if (wave_row0 >= J.rows) break;  // uniform per wave
-        const int row = wave_row0 + (lane >> 4);
-        const int rrow = min(row, J.rows - 1);
-        const uint8_t *wrow = J.w + (int64_t)rrow * row_bytes + (int64_t)cb0 * 16;
-
+        const bool active = block_row0 + p * rows_per_pass + rgroup * 4 < J.rows;  // wave-uniform
+        const int row = row_of(p);
         int acc[COLS];
 #pragma unroll
         for (int c = 0; c < COLS; ++c) acc[c] = 0;
-
-        uint4 cur[kChunkBatch];
+        if (active) {
+            const uint8_t *wrow = wrow_of(p);
+            for (int t0 = 0; t0 < T; t0 += kChunkBatch) {
+                u32x4 nxt[kChunkBatch];
+                load_batch(nxt, wrow, t0 + kChunkBatch, T, nchw, lane16);
+                dot_batch<COLS>(acc, cur, xl0, lds_stride, bits, t0, T, nchw, lane16);
 #pragma unroll
-        for (int u = 0; u < kChunkBatch; ++u) {
-            const int ch = u * 16 + lane16;
-            cur[u] = (u < T && ch < nch) ? *reinterpret_cast<const uint4 *>(wrow + (int64_t)ch * 16)
-                                         : make_uint4(0, 0, 0, 0);
-        }
-        for (int t0 = 0; t0 < T; t0 += kChunkBatch) {
-            uint4 nxt[kChunkBatch];
-#pragma unroll
-            for (int u = 0; u < kChunkBatch; ++u) {
-                const int t = t0 + kChunkBatch + u;
-                const int ch = t * 16 + lane16;
-                nxt[u] = (t < T && ch < nch)
-                             ? *reinterpret_cast<const uint4 *>(wrow + (int64_t)ch * 16)
-                             : make_uint4(0, 0, 0, 0);
+                for (int u = 0; u < kChunkBatch; ++u) cur[u] = nxt[u];
             }
-#pragma unroll
-            for (int u = 0; u < kChunkBatch; ++u) {
-                const int t = t0 + u;
-                const int ch = t * 16 + lane16;
-                if (t < T && ch < nch) {
-                    const uint32_t wv[4] = {cur[u].x, cur[u].y, cur[u].z, cur[u].w};
-#pragma unroll
-                    for (int c = 0; c < COLS; ++c) {
-                        const uint8_t *xl = smem + c * lds_stride;
-                        if (bits == 4) {
-                            const uint4 xa = *reinterpret_cast<const uint4 *>(xl + ch * 32);
-                            const uint4 xb = *reinterpret_cast<const uint4 *>(xl + ch * 32 + 16);
-                            const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-                            int a = acc[c];
-#pragma unroll
-                            for (int i = 0; i < 4; ++i) {
-                                const uint32_t lo = wv[i] & 0x0F0F0F0Fu;
-                                const uint32_t hi = (wv[i] >> 4) & 0x0F0F0F0Fu;
-                                a = __builtin_amdgcn_sdot4((int)lo, (int)xv[2 * i], a, false);
-                                a = __builtin_amdgcn_sdot4((int)hi, (int)xv[2 * i + 1], a, false);
-                            }
-                            acc[c] = a;
-                        } else {
-                            const uint4 xa = *reinterpret_cast<const uint4 *>(xl + ch * 16);
-                            int a = acc[c];
-                            a = __builtin_amdgcn_sdot4((int)wv[0], (int)xa.x, a, false);
-                            a = __builtin_amdgcn_sdot4((int)wv[1], (int)xa.y, a, false);
-                            a = __builtin_amdgcn_sdot4((int)wv[2], (int)xa.z, a, false);
-                            a = __builtin_amdgcn_sdot4((int)wv[3], (int)xa.w, a, false);
-                            acc[c] = a;
-                        }
-                    }
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < kChunkBatch; ++u) cur[u] = nxt[u];
         }
-
+        if (p + 1 < J.passes) load_batch(cur, wrow_of(p + 1), 0, T, nchw, lane16);
+#pragma unroll
+        for (int c = 0; c < COLS; ++c) acc[c] = row16_sum_i32(acc[c]);
+        if (!active || lane16 != 0 || row >= J.rows) continue;
+        if (kwaves > 1) {
+            const int slot = p * kRowsPerPass + rgroup * 4 + (lane >> 4);
+#pragma unroll
+            for (int c = 0; c < COLS; ++c) atomicAdd(&s_acc[slot * COLS + c], acc[c]);
+            continue;
+        }
+        const float scale = J.scales[row];
 #pragma unroll
         for (int c = 0; c < COLS; ++c) {
-            int s = row16_sum_i32(acc[c]);
-            if (bits == 4) s -= 8 * sx[c];
-            acc[c] = s;
-        }
-        if (lane16 == 0 && row < J.rows) {
-            const float scale = J.scales[row];
+            const int s = bits == 4 ? acc[c] - 8 * sx[c] : acc[c];
             if (L.splits > 1) {
-                const float part = L.split_exact
-                                       ? (float)acc[0]
-                                       : linear_epilogue(J.in_scale, scale, (float)acc[0]);
+                const float part = L.split_exact ? (float)s : linear_epilogue(J.in_scale, scale, (float)s);
                 reinterpret_cast<float *>(J.dst)[(int64_t)row * L.splits + split] = part;
             } else {
-#pragma unroll
-                for (int c = 0; c < COLS; ++c) {
-                    const float y = linear_epilogue(J.in_scale, scale, (float)acc[c]);
-                    store_linear_out(J.dst, (int64_t)c * J.rows + row, J.out_kind, y, acc[c],
-                                     J.out_scale);
-                }
+                const float y = linear_epilogue(J.in_scale, scale, (float)s);
+                store_linear_out(J.dst, (int64_t)c * J.rows + row, J.out_kind, y, s, J.out_scale);
+            }
+        }
+    }
+    if (kwaves > 1) {
+        __syncthreads();
+        const int n_out = J.passes * rows_per_pass;
+        for (int i = tid; i < n_out * COLS; i += kGemvThreads) {
+            const int local_row = i / COLS;
+            const int c = i - local_row * COLS;
+            const int p = local_row / rows_per_pass;
+            const int r_in = local_row - p * rows_per_pass;
+            const int row = block_row0 + local_row;
+            if (row >= J.rows) continue;
+            const int acc = s_acc[(p * kRowsPerPass + r_in) * COLS + c];
+            const int s = bits == 4 ? acc - 8 * sx[c] : acc;
+            const float scale = J.scales[row];
+            if (L.splits > 1) {
+                const float part = L.split_exact ? (float)s : linear_epilogue(J.in_scale, scale, (float)s);
+                reinterpret_cast<float *>(J.dst)[(int64_t)row * L.splits + split] = part;
+            } else {
+                const float y = linear_epilogue(J.in_scale, scale, (float)s);
+                store_linear_out(J.dst, (int64_t)c * J.rows + row, J.out_kind, y, s, J.out_scale);
             }
         }
     }
@@ -388,10 +440,19 @@ int check_job(const GemvJob &J, int cols, const char *who) {
     return G4_OK;
 }
 
+// Waves splitting K in a block: long rows split so every block streams about the same bytes.
+static int kwaves_for(int k) { return k >= 6144 ? 4 : k >= 3072 ? 2 : 1; }
+
+static int rows_per_block(const GemvJob &J) { return J.passes * (kRowsPerPass / J.kwaves); }
+
 // Picks passes per block so the launch offers a few blocks per CU without starving small jobs.
-static void plan_blocks(GemvLaunch &L, int max_passes) {
+static void plan_blocks(GemvLaunch &L, int max_passes, bool split_k_waves) {
     int64_t total_groups = 0;
-    for (int i = 0; i < L.count; ++i) total_groups += (L.job[i].rows + kRowsPerPass - 1) / kRowsPerPass;
+    for (int i = 0; i < L.count; ++i) {
+        L.job[i].kwaves = split_k_waves ? kwaves_for(L.job[i].k) : 1;
+        total_groups += (L.job[i].rows + kRowsPerPass / L.job[i].kwaves - 1) /
+                        (kRowsPerPass / L.job[i].kwaves);
+    }
     const int64_t target_blocks = 8LL * device_cu_count();
     int passes = 1;
     while (passes < max_passes && total_groups / passes > target_blocks) passes *= 2;
@@ -399,13 +460,13 @@ static void plan_blocks(GemvLaunch &L, int max_passes) {
     for (int i = 0; i < L.count; ++i) {
         L.job[i].passes = passes;
         L.job[i].wg_begin = wg;
-        wg += (L.job[i].rows + passes * kRowsPerPass - 1) / (passes * kRowsPerPass);
+        wg += (L.job[i].rows + rows_per_block(L.job[i]) - 1) / rows_per_block(L.job[i]);
     }
 }
 
 static int total_blocks(const GemvLaunch &L) {
     const GemvJob &last = L.job[L.count - 1];
-    return last.wg_begin + (last.rows + last.passes * kRowsPerPass - 1) / (last.passes * kRowsPerPass);
+    return last.wg_begin + (last.rows + rows_per_block(last) - 1) / rows_per_block(last);
 }
 
 // Launches the integer or f32 GEMV over L.count jobs with `cols` token columns (1 or 2).
@@ -419,7 +480,7 @@ int launch_gemv(GemvLaunch &L, int cols, hipStream_t stream) {
                              "grouped GEMV: calibrated and uncalibrated projections in one launch");
     if (L.splits > 1 && (L.count != 1 || cols != 1 || !calibrated))
         return set_error(G4_ERR_UNSUPPORTED, "split-K needs one calibrated single-column job");
-    plan_blocks(L, L.splits > 1 ? 1 : 8);
+    plan_blocks(L, L.splits > 1 ? 1 : kMaxPasses, calibrated);
     const int blocks = total_blocks(L);
     int max_k = 0;
     for (int i = 0; i < L.count; ++i) max_k = std::max(max_k, L.job[i].k);

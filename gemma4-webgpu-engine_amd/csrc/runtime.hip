@@ -184,6 +184,35 @@ int g4_event_elapsed_ms(float *ms, void *start, void *end) {
     return G4_OK;
 }
 
+int g4_graph_begin_capture(void *stream) {
+    if (!stream) return set_error(G4_ERR_INVALID, "graph capture needs a created stream, not the default stream");
+    G4_HIP(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal));
+    return G4_OK;
+}
+
+int g4_graph_end_capture(void *stream, void **graph_exec) {
+    if (!stream || !graph_exec) return set_error(G4_ERR_INVALID, "g4_graph_end_capture: NULL argument");
+    hipGraph_t graph = nullptr;
+    G4_HIP(hipStreamEndCapture(as_stream(stream), &graph));
+    hipGraphExec_t exec = nullptr;
+    hipError_t err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    hipGraphDestroy(graph);
+    if (err != hipSuccess) return hip_status(err, "hipGraphInstantiate");
+    *graph_exec = exec;
+    return G4_OK;
+}
+
+int g4_graph_launch(void *graph_exec, void *stream) {
+    if (!graph_exec) return set_error(G4_ERR_INVALID, "g4_graph_launch: no graph");
+    G4_HIP(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph_exec), as_stream(stream)));
+    return G4_OK;
+}
+
+int g4_graph_destroy(void *graph_exec) {
+    if (graph_exec) G4_HIP(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph_exec)));
+    return G4_OK;
+}
+
 // tableSplit.ts:125-215 planTableSplit. Pure: limits go in as numbers.
 int g4_plan_table_split(const g4_table_split_input *in, g4_table_split_plan *plan,
                         g4_table_slice *slices, int64_t max_slices) {

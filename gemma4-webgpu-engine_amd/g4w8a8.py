@@ -78,6 +78,10 @@ SIGNATURES = {
     "g4_event_record": (_c_int, [_vp, _vp]),
     "g4_event_synchronize": (_c_int, [_vp]),
     "g4_event_elapsed_ms": (_c_int, [ctypes.POINTER(_c_float), _vp, _vp]),
+    "g4_graph_begin_capture": (_c_int, [_vp]),
+    "g4_graph_end_capture": (_c_int, [_vp, ctypes.POINTER(_vp)]),
+    "g4_graph_launch": (_c_int, [_vp, _vp]),
+    "g4_graph_destroy": (_c_int, [_vp]),
     "g4_qgemv": (_c_int, [_c_int, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
                           _c_float, _c_float, _vp]),
     "g4_qgemm": (_c_int, [_c_int, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
@@ -236,6 +240,28 @@ class Event:
     def close(self):
         if self.handle:
             lib().g4_event_destroy(self.handle)
+            self.handle = None
+
+
+class Graph:
+    """A captured sequence of enqueues, replayed with one launch (hipGraphExec)."""
+
+    def __init__(self, stream: "Stream", record):
+        _check(lib().g4_graph_begin_capture(stream.handle))
+        try:
+            record()
+        finally:
+            p = _vp()
+            _check(lib().g4_graph_end_capture(stream.handle, ctypes.byref(p)))
+        self.handle = p.value
+        self.stream = stream
+
+    def launch(self):
+        _check(lib().g4_graph_launch(self.handle, self.stream.handle))
+
+    def close(self):
+        if self.handle:
+            lib().g4_graph_destroy(self.handle)
             self.handle = None
 
 

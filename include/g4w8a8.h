@@ -76,6 +76,16 @@ int g4_event_record(void *event, void *stream);
 int g4_event_synchronize(void *event);
 int g4_event_elapsed_ms(float *ms, void *start, void *end);
 
+/* HIP graphs: capture a sequence of enqueues on `stream` once, replay it with one launch. The
+ * decode loop is launch-bound (a launch costs microseconds of host time, more than a small GEMV
+ * runs); the reference caches its per-token encode the same way (runtime.ts:702-767). Kernels of
+ * this library never allocate or memset inside a capture; g4_qgemm/g4_linear with M > 2 need their
+ * workspace to exist first (run the same shape once on the stream before capturing). */
+int g4_graph_begin_capture(void *stream);
+int g4_graph_end_capture(void *stream, void **graph_exec);
+int g4_graph_launch(void *graph_exec, void *stream);
+int g4_graph_destroy(void *graph_exec);
+
 /* ---- the quantized linears --------------------------------------------------------------- */
 
 /*
