@@ -1,17 +1,28 @@
 """Benchmark of the wNa8o8 projection path on one MI355X (prints one JSON line).
 
-The step: one E2B-shape decode projection stream at M = 1, i.e. BASELINE config 1 (a layer's
-q, k, v, o, gate, up and down projections; int4 weights, f16 activations snapped on the static
-input scale 0.05, int32 accumulation, int8 outputs on 0.1) for 35 layers with distinct seeded
-weights (623.6 MB per step, more than twice the 256 MB Infinity Cache), one grouped GEMV launch per
-layer. Inputs are resident in HBM before the timed region; the timed region is exactly `--steps`
-steps between two HIP events on the launch stream, bracketed by device synchronizations.
+The step: BASELINE config 1 (one layer's q, k, v, o, gate, up and down projections; int4 weights,
+f16 activations snapped on the static input scale 0.05, int32 accumulation, int8 outputs on 0.1)
+for 35 layers with distinct seeded weights: 245 M = 1 GEMVs, 623.6 MB per step, more than twice the
+256 MB Infinity Cache, so every step streams its weights from HBM. The step runs as one launch of
+a device-resident GEMV plan (g4_qgemv_plan_launch: the streaming kernel over all 245 projections).
+Inputs are resident in HBM before the timed region; the timed region is exactly `--steps` steps
+between two HIP events on the launch stream, bracketed by device synchronizations.
 
-Also reported (fields under "extra"): config 2's gate GEMM at M = 512 in int8 TOPS (MFMA), and
-config 3's split PLE gather (5 slices, 2048 Zipf tokens, f16 out) in GB/s.
+Reported beside it (under "extra", not the headline):
+  - the same 35 layers as one grouped launch per layer (7 projections per launch) and in the decode
+    dependency shape (4 launches per layer: qkv batch, o, gate/up batch, down), which show what
+    launch granularity costs;
+  - config 0 (one 1536 x 1536 GEMV) as a single launch;
+  - config 2's gate GEMM at M = 512 in int8 TOPS (MFMA), with and without the activation snap;
+  - config 3's split PLE gather (5 slices, 2048 Zipf tokens, f16 out) in GB/s.
 
-cpu_baseline: the oracle's C restatement (OpenMP over the host cores) timed on a bounded sample of
-the same layer set, reported in the same unit. It is a baseline, not a target.
+cpu_baseline: the oracle's C restatement (OpenMP over the host cores) on a bounded sample of the
+same layer set, in the same unit. It is a baseline, not a target.
+
+roofline.traffic: HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs
+(`--traffic-probe` runs the same launches plus a plain device copy of known size that calibrates
+the counters); the measured figure is read from profiles/traffic_qgemv_stream_config1.json when
+that file exists, else null.
 """
 from __future__ import annotations
 
@@ -34,87 +45,92 @@ METRIC = "wNa8o8 GEMV GB/s (% HBM peak) M=1; int8 TOPS M=512; E2B-shape decode t
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 LAYERS = 35
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_qgemv_stream_config1.json")
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def proj_bytes(n, k, bits=4):
+    """Algorithmic bytes of one M = 1 projection: weights + f32 scales + f16 x + int8 out."""
+    return n * k * bits // 8 + 4 * n + 2 * k + n
+
+
 def layer_bytes():
-    """Algorithmic bytes of one config-1 layer: N*K/2 weights + 4N scales + 2K f16 x + N int8."""
-    return sum(n * k // 2 + 4 * n + 2 * k + n for _, n, k in syn.LAYER_PROJECTIONS)
+    return sum(proj_bytes(n, k) for _, n, k in syn.LAYER_PROJECTIONS)
 
 
-def build_layers(stream):
+def build_layers():
+    """35 layers x 7 projections of seeded config-1 data, resident on the device."""
     layers = []
     for layer in range(LAYERS):
-        items = []
+        items = {}
         for name, n, k in syn.LAYER_PROJECTIONS:
             tag = f"{name}.L{layer}"
             w = g4.DeviceBuffer.from_array(syn.int4_weights("bench", tag, n, k))
             s = g4.DeviceBuffer.from_array(syn.row_scales("bench", tag, n))
             x = g4.DeviceBuffer.from_array(syn.activations("bench", tag, 1, k)[0])
             d = g4.DeviceBuffer.empty((n,), np.int8)
-            items.append(g4.Gemv(w, s, x, d, 4, k, n, syn.IN_SCALE, syn.OUT_SCALE))
-        layers.append((items, g4.make_group(items)))
+            items[name] = g4.Gemv(w, s, x, d, 4, k, n, syn.IN_SCALE, syn.OUT_SCALE)
+        layers.append(items)
     return layers
 
 
-def time_layers(layers, stream, steps, warmup):
+def timed(stream, fn, steps, warmup):
+    """Average ms per call of fn() over `steps` calls between two events on `stream`."""
     for _ in range(warmup):
-        for _, arr in layers:
-            g4.qgemv_grouped(arr, stream)
+        fn()
     g4.synchronize()
     e0, e1 = g4.Event(), g4.Event()
-    t0 = time.perf_counter()
     e0.record(stream)
     for _ in range(steps):
-        for _, arr in layers:
-            g4.qgemv_grouped(arr, stream)
+        fn()
     e1.record(stream)
     e1.synchronize()
     g4.synchronize()
-    wall = time.perf_counter() - t0
-    return e0.elapsed_ms(e1) / steps, wall
+    return e0.elapsed_ms(e1) / steps
 
 
-def per_launch_ms(layers, stream, reps=3):
-    """Average duration of one grouped layer launch, each bracketed by its own event pair."""
-    evs = [(g4.Event(), g4.Event()) for _ in layers]
-    total, count = 0.0, 0
-    for _ in range(reps):
-        for (a, b), (_, arr) in zip(evs, layers):
-            a.record(stream)
-            g4.qgemv_grouped(arr, stream)
-            b.record(stream)
-        g4.synchronize()
-        for a, b in evs:
-            total += a.elapsed_ms(b)
-            count += 1
-    return total / count
+def decode_shaped(layers, h):
+    """The decode dependency shape: qkv batch, o, gate/up batch, down (4 launches per layer)."""
+    def run():
+        for L in layers:
+            q, k_, v = L["q"], L["k"], L["v"]
+            g4.projection_batch(4, [q.wq, k_.wq, v.wq], [q.scales, k_.scales, v.scales], q.x,
+                                [q.dst, k_.dst, v.dst], [q.num_rows, k_.num_rows, v.num_rows],
+                                [syn.IN_SCALE] * 3, [syn.OUT_SCALE] * 3, q.k, stream=h)
+            g4.qgemv_grouped([L["o"]], h)
+            gt, up = L["gate"], L["up"]
+            g4.projection_batch(4, [gt.wq, up.wq], [gt.scales, up.scales], gt.x, [gt.dst, up.dst],
+                                [gt.num_rows, up.num_rows], [syn.IN_SCALE] * 2,
+                                [syn.OUT_SCALE] * 2, gt.k, stream=h)
+            g4.qgemv_grouped([L["down"]], h)
+    return run
 
 
-def bench_gemm(stream, m=512, reps=50):
+def bench_gemm(h, m=512, reps=50):
     n, k = syn.FFN, syn.HIDDEN
     w = g4.DeviceBuffer.from_array(syn.int4_weights("c2", "gate", n, k))
     s = g4.DeviceBuffer.from_array(syn.row_scales("c2", "gate", n))
-    x = g4.DeviceBuffer.from_array(syn.activations("c2", f"x{m}", m, k, outlier_frac=0.01))
+    xf = syn.activations("c2", f"x{m}", m, k, outlier_frac=0.01)
+    x = g4.DeviceBuffer.from_array(xf)
+    codes = g4.DeviceBuffer.empty((m, k), np.int8)
+    g4.srq_quantize(x, codes, m * k, syn.IN_SCALE, stream=h)
     d = g4.DeviceBuffer.empty((m, n), np.int8)
-    for _ in range(5):
-        g4.qgemm(4, w, s, x, d, k, n, m, syn.IN_SCALE, syn.OUT_SCALE, stream=stream)
-    g4.synchronize()
-    e0, e1 = g4.Event(), g4.Event()
-    e0.record(stream)
-    for _ in range(reps):
-        g4.qgemm(4, w, s, x, d, k, n, m, syn.IN_SCALE, syn.OUT_SCALE, stream=stream)
-    e1.record(stream)
-    e1.synchronize()
-    ms = e0.elapsed_ms(e1) / reps
-    return {"m": m, "n": n, "k": k, "ms": ms, "tops": 2.0 * m * n * k / (ms * 1e-3) / 1e12,
-            "kernel": g4.kernel_for_shape(4, m, n, k), "includes": "activation snap + MFMA GEMM"}
+    ops = 2.0 * m * n * k
+    ms_f16 = timed(h, lambda: g4.qgemm(4, w, s, x, d, k, n, m, syn.IN_SCALE, syn.OUT_SCALE,
+                                       stream=h), reps, 5)
+    ms_i8 = timed(h, lambda: g4.qgemm(4, w, s, codes, d, k, n, m, syn.IN_SCALE, syn.OUT_SCALE,
+                                      stream=h), reps, 5)
+    return {"m": m, "n": n, "k": k, "kernel": g4.kernel_for_shape(4, m, n, k),
+            "ms_f16_in": round(ms_f16, 6), "tops_f16_in": round(ops / (ms_f16 * 1e-3) / 1e12, 2),
+            "ms_int8_in": round(ms_i8, 6), "tops_int8_in": round(ops / (ms_i8 * 1e-3) / 1e12, 2),
+            "frac_int8_peak_int8_in": round(ops / (ms_i8 * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+            "note": "f16_in includes the activation snap; int8_in takes codes already snapped"}
 
 
-def bench_gather(stream, tokens=2048, reps=20):
+def bench_gather(h, tokens=2048, reps=20):
     rows, cols = syn.PLE_ROWS, syn.PLE_COLS
     codes = syn.ple_codes("c3", rows)
     scales = g4.DeviceBuffer.from_array(syn.ple_scales("c3", rows))
@@ -126,19 +142,12 @@ def bench_gather(stream, tokens=2048, reps=20):
     out = g4.DeviceBuffer.empty((tokens, cols), np.float16)
     starts = [s.start_row for s in slices]
     counts = [s.row_count for s in slices]
-    for _ in range(3):
-        g4.ple_gather_split(bufs, starts, counts, scales, ids, out, tokens, cols, 256, stream)
-    g4.synchronize()
-    e0, e1 = g4.Event(), g4.Event()
-    e0.record(stream)
-    for _ in range(reps):
-        g4.ple_gather_split(bufs, starts, counts, scales, ids, out, tokens, cols, 256, stream)
-    e1.record(stream)
-    e1.synchronize()
-    ms = e0.elapsed_ms(e1) / reps
+    ms = timed(h, lambda: g4.ple_gather_split(bufs, starts, counts, scales, ids, out, tokens, cols,
+                                              256, h), reps, 3)
     per_token = cols // 2 + 2 * (cols // 256) + 4 + 2 * cols  # codes + f16 scales + id + f16 out
-    return {"tokens": tokens, "slices": len(slices), "ms": ms,
-            "gbs": per_token * tokens / (ms * 1e-3) / 1e9}
+    return {"tokens": tokens, "slices": len(slices), "ms": round(ms, 6),
+            "gbs": round(per_token * tokens / (ms * 1e-3) / 1e9, 2),
+            "frac_hbm_peak": round(per_token * tokens / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def cpu_baseline(seconds=10.0):
@@ -165,6 +174,32 @@ def cpu_baseline(seconds=10.0):
                       f"the C oracle, {el:.1f} s"}
 
 
+def traffic():
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return t.get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def traffic_probe(plan, h):
+    """Launches for the rocprofv3 --pmc runs: 3 copies of 256 MiB (the counter calibration: a
+    plain copy reads and writes exactly that many bytes), then 5 plan launches."""
+    n = 256 << 20
+    a = g4.DeviceBuffer(n)
+    b = g4.DeviceBuffer(n)
+    a.fill(1)
+    g4.synchronize()
+    for _ in range(3):
+        g4._check(g4.lib().g4_memcpy_d2d(g4._ptr(b), g4._ptr(a), n, h))
+    g4.synchronize()
+    for _ in range(5):
+        plan.launch(h)
+    g4.synchronize()
+    log(f"traffic probe done: copy {n} B x3, plan x5")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -172,10 +207,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this path is measured on one GPU; --gpus {args.gpus} is not supported "
-              "(the multi-GPU sharding is a design note only)", file=sys.stderr)
+              "(how the path would shard is a design note only)", file=sys.stderr)
         sys.exit(2)
     if g4.device_count() < 1:
         print("bench.py: no HIP device", file=sys.stderr)
@@ -184,13 +220,18 @@ def main():
     stream = g4.Stream()
     h = stream.handle
     log("building 35 layers of config-1 weights (623.6 MB)")
-    layers = build_layers(h)
-    log("timing")
-    ms, wall = time_layers(layers, h, args.steps, args.warmup)
+    layers = build_layers()
+    items = [L[name] for L in layers for name, _, _ in syn.LAYER_PROJECTIONS]
+    plan = g4.GemvPlan(items)
+    tiles, grid = plan.info()
+    if args.traffic_probe:
+        traffic_probe(plan, h)
+        return
+    log(f"timing the plan ({len(items)} projections, {tiles} tiles, {grid} blocks)")
+    ms = timed(h, lambda: plan.launch(h), args.steps, args.warmup)
+    t_wall = time.perf_counter()
     step_bytes = layer_bytes() * LAYERS
     value = step_bytes / (ms * 1e-3) / 1e9
-    launch_ms = per_launch_ms(layers, h)
-    achieved = layer_bytes() / (launch_ms * 1e-3) / 1e9
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -198,7 +239,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
+        "ms_per_step": round(ms, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -207,36 +248,61 @@ def main():
         "config": {
             "workload": "config1 decode projection set at M=1 (q 1536->2048, k/v 1536->256, "
                         "o 2048->1536, gate/up 1536->6144, down 6144->1536), int4 weights x int8 "
-                        "activation codes, int32 accumulate, int8 out; 35 distinct layers per step, "
-                        "one grouped GEMV launch per layer",
+                        "activation codes, int32 accumulate, int8 out; 35 distinct layers per step "
+                        "(245 GEMVs) as one streaming-plan launch",
             "bytes_per_step": step_bytes,
-            "launches_per_step": LAYERS,
+            "launches_per_step": 1,
             "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
-            "wall_s": round(wall, 3),
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "qgemv_int_kernel<1> (grouped layer GEMV)",
-            "achieved": round(achieved, 2),
+            "kernel": "qgemv_stream_kernel<true> (plan launch, 245 projections)",
+            "achieved": round(value, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "bytes_per_launch": layer_bytes(),
-            "avg_launch_ms": round(launch_ms, 6),
+            "frac": round(value / HBM_PEAK_GBS, 4),
+            "traffic": traffic(),
+            "bytes_per_launch": step_bytes,
+            "avg_launch_ms": round(ms, 6),
+            "plan_tiles": tiles,
+            "plan_blocks": grid,
         },
     }
     if not args.no_extra:
+        log("per-layer grouped launches")
+        groups = [g4.make_group([L[name] for name, _, _ in syn.LAYER_PROJECTIONS]) for L in layers]
+        ms_layer = timed(h, lambda: [g4.qgemv_grouped(a, h) for a in groups], 20, 3)
+        log("decode-shaped launches")
+        ms_dec = timed(h, decode_shaped(layers, h), 20, 3)
+        log("config 0 single GEMV")
+        c0 = layers[0]["q"]
+        w0 = g4.DeviceBuffer.from_array(syn.int4_weights("c0", "w", 1536, 1536))
+        s0 = g4.DeviceBuffer.from_array(syn.row_scales("c0", "w", 1536))
+        x0 = g4.DeviceBuffer.from_array(syn.activations("c0", "x", 1, 1536)[0])
+        d0 = g4.DeviceBuffer.empty((1536,), np.int8)
+        ms_c0 = timed(h, lambda: g4.qgemv(4, w0, s0, x0, d0, 1536, 1536, 1, syn.IN_SCALE,
+                                          syn.OUT_SCALE, stream=h), 200, 10)
+        del c0
         log("config 2 gate GEMM at M=512")
         gm = bench_gemm(h)
-        gm["frac_int8_peak"] = round(gm["tops"] / INT8_PEAK_TOPS, 4)
         log("config 3 split PLE gather")
         ga = bench_gather(h)
-        ga["frac_hbm_peak"] = round(ga["gbs"] / HBM_PEAK_GBS, 4)
-        result["extra"] = {"int8_gemm_m512": gm, "ple_gather": ga}
+        result["extra"] = {
+            "per_layer_grouped": {"launches_per_step": LAYERS, "ms_per_step": round(ms_layer, 6),
+                                  "gbs": round(step_bytes / (ms_layer * 1e-3) / 1e9, 2)},
+            "decode_shaped": {"launches_per_step": 4 * LAYERS, "ms_per_step": round(ms_dec, 6),
+                              "gbs": round(step_bytes / (ms_dec * 1e-3) / 1e9, 2)},
+            "config0_single_gemv": {"bytes": proj_bytes(1536, 1536), "us": round(ms_c0 * 1e3, 3),
+                                    "gbs": round(proj_bytes(1536, 1536) / (ms_c0 * 1e-3) / 1e9, 2),
+                                    "kernel": g4.kernel_for_shape(4, 1, 1536, 1536)},
+            "int8_gemm_m512": gm,
+            "ple_gather": ga,
+        }
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle on host cores)")
         result["cpu_baseline"] = cpu_baseline()
+    result["config"]["wall_s_after_timing"] = round(time.perf_counter() - t_wall, 3)
+    plan.close()
     print(json.dumps(result), flush=True)
 
 

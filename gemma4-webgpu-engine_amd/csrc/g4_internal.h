@@ -41,6 +41,16 @@ inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s);
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 
+// Validates one GEMV descriptor against what the GEMV kernels assume (qgemv.hip).
+int check_job_desc(const g4_gemv_desc &d, const char *who);
+
+// Launches calibrated M = 1 GEMVs on the streaming kernel when every one has a compiled shape
+// class (qgemv_stream.hip); otherwise enqueues nothing and sets *launched = false.
+int stream_try_launch(const g4_gemv_desc *descs, int count, hipStream_t stream, bool *launched);
+
+// The streaming shape class of a row of K codes at `bits`, or -1 (qgemv_stream.hip).
+int stream_class_for(int bits, int k);
+
 // ---- device: the static range quantization arithmetic (src/quant.ts:248-357) -----------------
 
 // srqCodes at 8 bits: clamp(RNE(f32(v / s)), -128, 127). __fdiv_rn is the IEEE binary32 divide;

@@ -618,7 +618,10 @@ int g4_linear(int bits, const void *wq, const float *scales, const void *x, int 
 
 int g4_kernel_for_shape(int bits, int m_cols, int num_rows, int k, char *buf, size_t buf_len) {
     if (!buf || buf_len == 0) return set_error(G4_ERR_INVALID, "g4_kernel_for_shape: no buffer");
-    const char *name = choice_name(pick_kernel(bits, m_cols, num_rows, k, 1.0f), bits);
+    const KernelChoice c = pick_kernel(bits, m_cols, num_rows, k, 1.0f);
+    const char *name = choice_name(c, bits);
+    if (c == K_GEMV && m_cols == 1 && stream_class_for(bits, k) >= 0)
+        name = bits == 4 ? "qgemv-4bit-stream" : "qgemv-8bit-stream";
     snprintf(buf, buf_len, "%s", name);
     return G4_OK;
 }

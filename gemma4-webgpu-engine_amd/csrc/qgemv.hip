@@ -440,6 +440,49 @@ int check_job(const GemvJob &J, int cols, const char *who) {
     return G4_OK;
 }
 
+static g4_gemv_desc desc_of(const GemvJob &J) {
+    g4_gemv_desc d{};
+    d.wq = J.w;
+    d.scales = J.scales;
+    d.x = J.x;
+    d.dst = J.dst;
+    d.bits = J.bits;
+    d.x_kind = J.x_kind;
+    d.out_kind = J.out_kind;
+    d.k = J.k;
+    d.num_rows = J.rows;
+    d.in_scale = J.in_scale;
+    d.out_scale = J.out_scale;
+    return d;
+}
+
+static GemvJob job_of(const g4_gemv_desc &d) {
+    GemvJob J{};
+    J.w = reinterpret_cast<const uint8_t *>(d.wq);
+    J.scales = d.scales;
+    J.x = d.x;
+    J.dst = d.dst;
+    J.bits = d.bits;
+    J.x_kind = d.x_kind;
+    J.out_kind = d.out_kind;
+    J.k = d.k;
+    J.rows = d.num_rows;
+    J.in_scale = d.in_scale;
+    J.out_scale = d.out_scale;
+    return J;
+}
+
+int check_job_desc(const g4_gemv_desc &d, const char *who) { return check_job(job_of(d), 1, who); }
+
+// Single-column launches of calibrated jobs go to the streaming kernel when their shapes allow.
+static int try_stream(const GemvLaunch &L, int cols, hipStream_t stream, bool *launched) {
+    *launched = false;
+    if (cols != 1 || L.splits > 1) return G4_OK;
+    g4_gemv_desc d[G4_MAX_GROUP];
+    for (int i = 0; i < L.count; ++i) d[i] = desc_of(L.job[i]);
+    return stream_try_launch(d, L.count, stream, launched);
+}
+
 // Waves splitting K in a block: long rows split so every block streams about the same bytes.
 static int kwaves_for(int k) { return k >= 6144 ? 4 : k >= 3072 ? 2 : 1; }
 
@@ -480,6 +523,11 @@ int launch_gemv(GemvLaunch &L, int cols, hipStream_t stream) {
                              "grouped GEMV: calibrated and uncalibrated projections in one launch");
     if (L.splits > 1 && (L.count != 1 || cols != 1 || !calibrated))
         return set_error(G4_ERR_UNSUPPORTED, "split-K needs one calibrated single-column job");
+    if (calibrated) {
+        bool launched = false;
+        int rc = try_stream(L, cols, stream, &launched);
+        if (rc || launched) return rc;
+    }
     plan_blocks(L, L.splits > 1 ? 1 : kMaxPasses, calibrated);
     const int blocks = total_blocks(L);
     int max_k = 0;

@@ -1,0 +1,494 @@
+// The streaming decode GEMV (M = 1, calibrated path) for gfx950: qgemv-4bit / qgemv-8bit, the
+// projection batches and the grouped layer GEMV (src/kernels/qgemv.ts, projectionBatch.ts) when
+// the row length falls in one of the compiled shape classes.
+//
+// Shape class (BITS, LPR, CPL): a row is LPR * CPL 16-byte chunks. LPR lanes serve one row
+// (16, 32 or 64), each lane streams CPL chunks of it (chunk lr + u * LPR), so one wave covers
+// 64 / LPR rows with every weight load unguarded (the row index is clamped, the store is not).
+// A tile is the 4 waves of a block over 4 * 64 / LPR consecutive rows of one job.
+//
+// Schedule. Jobs (one projection each) are laid end to end as tiles; block b takes the contiguous
+// tile range [b * T / G, (b + 1) * T / G), so all blocks stream the same number of tiles. A block
+// snaps the activation vector of its current job once into LDS (int8 codes, the same IEEE divide
+// and ties-to-even as the reference's srqIn), then for every tile: 16-byte non-temporal weight
+// loads and the row scale, the v_dot4_i32_i8 dot against the LDS codes, the fixed DPP / shuffle
+// reduction over the row's lanes (exact int32), and the reference's epilogue on one lane.
+//
+// Why this shape: at 8 TB/s a layer's 17.8 MB is 2.2 us, so the kernel has to keep the HBM queue
+// full rather than save ALU. Every load goes through the global address space (a flat load would
+// also count against the LDS wait counter and serialize the weight stream behind the LDS reads),
+// the body needs 45 VGPRs so 8 waves per SIMD fit, and the grid holds 8 blocks per CU.
+//
+// Job descriptors travel in the kernel arguments (up to kMaxKargJobs, the per-call entry points)
+// or in a device table built once by g4_qgemv_plan_create (any count, the decode-step form: the
+// reference caches its per-token bind the same way, runtime.ts:702-767).
+#include "g4_internal.h"
+
+#include <algorithm>
+#include <vector>
+
+namespace g4 {
+
+constexpr int kStreamThreads = 256;
+constexpr int kMaxKargJobs = 16;
+constexpr int kStreamMaxK = 16384;
+constexpr int kBlocksPerCu = 8;
+
+#define G4_GLOBAL __attribute__((address_space(1)))
+
+// One projection of a streaming launch (64 bytes).
+struct StreamJob {
+    const uint8_t *w;
+    const float *scales;
+    const void *x;
+    void *dst;
+    int k;
+    int rows;
+    int tile_begin;
+    int tiles;
+    float in_scale;
+    float out_scale;
+    int8_t bits;
+    int8_t x_kind;
+    int8_t out_kind;
+    int8_t cls;
+    int pad;
+};
+static_assert(sizeof(StreamJob) == 64, "StreamJob is one 64-byte record");
+
+struct StreamArgs {
+    const StreamJob *table;  // device table (plan launches); null for kernel-argument jobs
+    const int *block_job;    // plan launches: the job of each block's first tile
+    int njobs;
+    int total_tiles;
+    StreamJob job[kMaxKargJobs];
+};
+
+// The compiled classes. Index = StreamJob::cls.
+struct ClassShape {
+    int bits, lpr, cpl;
+};
+constexpr ClassShape kClasses[] = {
+    {4, 16, 1}, {4, 16, 2}, {4, 16, 3}, {4, 16, 4}, {4, 32, 3}, {4, 32, 4}, {4, 64, 3}, {4, 64, 4},
+    {8, 16, 1}, {8, 16, 2}, {8, 16, 3}, {8, 16, 4}, {8, 32, 3}, {8, 32, 4}, {8, 64, 3}, {8, 64, 4},
+    {8, 64, 6},
+};
+constexpr int kNumClasses = sizeof(kClasses) / sizeof(kClasses[0]);
+
+// The class of a row of K codes at `bits`, or -1 when no compiled class fits.
+int stream_class_for(int bits, int k) {
+    if (k <= 0 || k > kStreamMaxK) return -1;
+    const int row_bytes = bits == 4 ? k / 2 : k;
+    if (row_bytes % 16) return -1;
+    const int chunks = row_bytes / 16;
+    for (int lpr : {16, 32, 64}) {
+        if (chunks % lpr) continue;
+        const int cpl = chunks / lpr;
+        for (int c = 0; c < kNumClasses; ++c)
+            if (kClasses[c].bits == bits && kClasses[c].lpr == lpr && kClasses[c].cpl == cpl) return c;
+    }
+    return -1;
+}
+
+static int rows_per_tile(int cls) { return 4 * (64 / kClasses[cls].lpr); }
+
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Loads and stores through the global address space (C casts: reinterpret_cast cannot change
+// the address space).
+template <typename T>
+__device__ __forceinline__ T gload(const void *p) {
+    return *(const G4_GLOBAL T *)p;
+}
+template <typename T>
+__device__ __forceinline__ void gstore(void *p, T v) {
+    *(G4_GLOBAL T *)p = v;
+}
+
+__device__ __forceinline__ u32x4 load_w16(const uint8_t *p) {
+    return __builtin_nontemporal_load((const G4_GLOBAL u32x4 *)p);
+}
+
+__device__ __forceinline__ uint32_t pack_bytes(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+           ((uint32_t)(d & 0xff) << 24);
+}
+
+// Activation groups (8 values) per thread whose loads go out together in the snap (f32 groups
+// are twice as wide, so half as many fit the register budget).
+template <int KIND>
+constexpr int snap_batch() { return KIND == G4_KIND_F32 ? 2 : 4; }
+
+template <int KIND>
+struct RawGroup {
+    u32x4 a, b;  // f32: 32 bytes; f16: a only; int8: a.xy
+};
+
+template <int KIND>
+__device__ __forceinline__ RawGroup<KIND> load_group(const void *x, int g) {
+    RawGroup<KIND> r;
+    if (KIND == G4_KIND_F32) {
+        const float *p = reinterpret_cast<const float *>(x) + g * 8;
+        r.a = gload<u32x4>(p);
+        r.b = gload<u32x4>(p + 4);
+    } else if (KIND == G4_KIND_F16) {
+        r.a = gload<u32x4>(reinterpret_cast<const __half *>(x) + g * 8);
+    } else {
+        const u32x2 v = gload<u32x2>(reinterpret_cast<const int8_t *>(x) + g * 8);
+        r.a = u32x4{v.x, v.y, 0u, 0u};
+    }
+    return r;
+}
+
+template <int KIND>
+__device__ __forceinline__ void group_codes(const RawGroup<KIND> &r, float s, float rcp, bool r_ok,
+                                            int c[8]) {
+    if (KIND == G4_KIND_F32) {
+        const uint32_t v[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c[i] = (int)srq_code_fast(__uint_as_float(v[i]), s, rcp, r_ok);
+    } else if (KIND == G4_KIND_F16) {
+        const uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            c[2 * i] = (int)srq_code_fast(
+                __half2float(__ushort_as_half((unsigned short)(w[i] & 0xffff))), s, rcp, r_ok);
+            c[2 * i + 1] = (int)srq_code_fast(
+                __half2float(__ushort_as_half((unsigned short)(w[i] >> 16))), s, rcp, r_ok);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            c[i] = (int)(int8_t)((r.a.x >> (8 * i)) & 0xff);
+            c[4 + i] = (int)(int8_t)((r.a.y >> (8 * i)) & 0xff);
+        }
+    }
+}
+
+// The snap body for one activation kind: each thread issues the loads of a batch of groups
+// (indices clamped, so every load is valid) before converting any, so a long vector costs one
+// memory latency per batch rather than one per group.
+template <int KIND>
+__device__ __forceinline__ int snap_kind(const StreamJob &J, uint8_t *xs, int tid) {
+    bool r_ok;
+    const float s = J.in_scale;
+    const float rcp = srq_recip(s, r_ok);
+    const int groups = J.k >> 3;
+    int local = 0;
+    constexpr int B = snap_batch<KIND>();
+    for (int g0 = tid; g0 < groups; g0 += B * kStreamThreads) {
+        RawGroup<KIND> raw[B];
+#pragma unroll
+        for (int i = 0; i < B; ++i)
+            raw[i] = load_group<KIND>(J.x, min(g0 + i * kStreamThreads, groups - 1));
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const int g = g0 + i * kStreamThreads;
+            if (g < groups) {
+                int c[8];
+                group_codes<KIND>(raw[i], s, rcp, r_ok, c);
+                uint2 packed;
+                if (J.bits == 4) {
+                    packed.x = pack_bytes(c[0], c[2], c[4], c[6]);
+                    packed.y = pack_bytes(c[1], c[3], c[5], c[7]);
+                } else {
+                    packed.x = pack_bytes(c[0], c[1], c[2], c[3]);
+                    packed.y = pack_bytes(c[4], c[5], c[6], c[7]);
+                }
+                *reinterpret_cast<uint2 *>(xs + g * 8) = packed;
+                local += c[0] + c[1] + c[2] + c[3] + c[4] + c[5] + c[6] + c[7];
+            }
+        }
+    }
+    return local;
+}
+
+// Snaps the K activations of job J into int8 codes in LDS (4-bit jobs: each 8-code group stored
+// as [x0 x2 x4 x6 | x1 x3 x5 x7] so a weight word's low and high nibbles each dot one half) and
+// returns sum(xq) over the whole vector, which takes the 4-bit zero point off once per row.
+__device__ __forceinline__ int snap_activations(const StreamJob &J, uint8_t *xs, int *s_sum, int tid) {
+    int local;
+    if (J.x_kind == G4_KIND_F16)
+        local = snap_kind<G4_KIND_F16>(J, xs, tid);
+    else if (J.x_kind == G4_KIND_F32)
+        local = snap_kind<G4_KIND_F32>(J, xs, tid);
+    else
+        local = snap_kind<G4_KIND_I8>(J, xs, tid);
+    if (tid == 0) *s_sum = 0;
+    lds_barrier();
+    local = row16_sum_i32(local);
+    if ((tid & 15) == 0 && local != 0) atomicAdd(s_sum, local);
+    lds_barrier();
+    return *s_sum;
+}
+
+// One output element of job J at row `row` (the reference's epilogue, qgemv.ts:680-686).
+__device__ __forceinline__ void stream_store(const StreamJob &J, int row, int s, float scale) {
+    const float y = linear_epilogue(J.in_scale, scale, (float)s);
+    if (J.out_kind == G4_KIND_I8) {
+        gstore<int8_t>(reinterpret_cast<int8_t *>(J.dst) + row, (int8_t)srq_code_i(y, J.out_scale));
+    } else if (J.out_kind == G4_KIND_I32) {
+        gstore<int32_t>(reinterpret_cast<int32_t *>(J.dst) + row, s);
+    } else {
+        float v = y;
+        if (J.out_scale != 0.0f) v = __fmul_rn(srq_code_f(y, J.out_scale), J.out_scale);
+        gstore<float>(reinterpret_cast<float *>(J.dst) + row, v);
+    }
+}
+
+// One tile of one job for class <BITS, LPR, CPL>: this lane's CPL 16-byte chunks of its row
+// (row index clamped, so every load is valid) and the row scale, the dot against the LDS codes,
+// the fixed reduction over the row's LPR lanes (exact int32), and the row's output from one lane.
+template <int BITS, int LPR, int CPL>
+__device__ __forceinline__ void stream_tile(const StreamJob &J, int t, const uint8_t *xs, int sx,
+                                            int wave, int lane) {
+    constexpr int RPW = 64 / LPR;
+    constexpr int ROW_BYTES = LPR * CPL * 16;
+    const int lr = lane & (LPR - 1);
+    const int row = (t - J.tile_begin) * (4 * RPW) + wave * RPW + lane / LPR;
+    const int rc = min(row, J.rows - 1);
+    const uint8_t *base = J.w + (int64_t)rc * ROW_BYTES + lr * 16;
+    u32x4 w[CPL];
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) w[u] = load_w16(base + u * LPR * 16);
+    const float scale = gload<float>(J.scales + rc);
+    int acc = 0;
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+        const int ch = lr + u * LPR;
+        const uint32_t wv[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+        if (BITS == 4) {
+            const u32x4 xa = *reinterpret_cast<const u32x4 *>(xs + ch * 32);
+            const u32x4 xb = *reinterpret_cast<const u32x4 *>(xs + ch * 32 + 16);
+            const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc = __builtin_amdgcn_sdot4((int)(wv[i] & 0x0F0F0F0Fu), (int)xv[2 * i], acc, false);
+                acc = __builtin_amdgcn_sdot4((int)((wv[i] >> 4) & 0x0F0F0F0Fu), (int)xv[2 * i + 1],
+                                             acc, false);
+            }
+        } else {
+            const u32x4 xa = *reinterpret_cast<const u32x4 *>(xs + ch * 16);
+            acc = __builtin_amdgcn_sdot4((int)wv[0], (int)xa.x, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)wv[1], (int)xa.y, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)wv[2], (int)xa.z, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)wv[3], (int)xa.w, acc, false);
+        }
+    }
+    acc = row16_sum_i32(acc);
+    if (LPR >= 32) acc += __shfl_xor(acc, 16);
+    if (LPR >= 64) acc += __shfl_xor(acc, 32);
+    if (lr == 0 && row < J.rows) stream_store(J, row, BITS == 4 ? acc - 8 * sx : acc, scale);
+}
+
+__device__ __forceinline__ void stream_dispatch(const StreamJob &J, int t, const uint8_t *xs,
+                                                int sx, int wave, int lane) {
+    switch (J.cls) {
+#define G4_CASE(i)                                                                              \
+    case i:                                                                                     \
+        stream_tile<kClasses[i].bits, kClasses[i].lpr, kClasses[i].cpl>(J, t, xs, sx, wave, lane); \
+        break;
+        G4_CASE(0) G4_CASE(1) G4_CASE(2) G4_CASE(3) G4_CASE(4) G4_CASE(5) G4_CASE(6) G4_CASE(7)
+        G4_CASE(8) G4_CASE(9) G4_CASE(10) G4_CASE(11) G4_CASE(12) G4_CASE(13) G4_CASE(14)
+        G4_CASE(15) G4_CASE(16)
+#undef G4_CASE
+        default:
+            break;
+    }
+}
+static_assert(kNumClasses == 17, "stream_dispatch lists every class");
+
+template <bool TABLE>
+__global__ __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void qgemv_stream_kernel(StreamArgs A) {
+    extern __shared__ __align__(16) uint8_t xs[];
+    __shared__ int s_sum;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const unsigned G = gridDim.x, b = blockIdx.x;
+    const int t0 = (int)(((uint64_t)b * (unsigned)A.total_tiles) / G);
+    const int t1 = (int)(((uint64_t)(b + 1) * (unsigned)A.total_tiles) / G);
+    if (t0 >= t1) return;
+    int j;
+    if (TABLE) {
+        j = A.block_job[b];
+    } else {
+        j = 0;
+#pragma unroll
+        for (int i = 1; i < kMaxKargJobs; ++i)
+            if (i < A.njobs && t0 >= A.job[i].tile_begin) j = i;
+    }
+    StreamJob J = TABLE ? A.table[j] : A.job[j];
+    int sx = snap_activations(J, xs, &s_sum, tid);
+    for (int t = t0; t < t1; ++t) {
+        if (t >= J.tile_begin + J.tiles) {
+            ++j;
+            J = TABLE ? A.table[j] : A.job[j];
+            __syncthreads();  // every wave is done with the previous job's codes
+            sx = snap_activations(J, xs, &s_sum, tid);
+        }
+        stream_dispatch(J, t, xs, sx, wave, lane);
+    }
+}
+
+// Fills a StreamJob from a validated descriptor; returns false when no class fits.
+bool stream_job_from(const g4_gemv_desc &d, StreamJob &J) {
+    const int cls = stream_class_for(d.bits, d.k);
+    if (cls < 0 || d.in_scale == 0.0f) return false;
+    J = StreamJob{};
+    J.w = reinterpret_cast<const uint8_t *>(d.wq);
+    J.scales = d.scales;
+    J.x = d.x;
+    J.dst = d.dst;
+    J.k = d.k;
+    J.rows = d.num_rows;
+    J.in_scale = d.in_scale;
+    J.out_scale = d.out_scale;
+    J.bits = (int8_t)d.bits;
+    J.x_kind = (int8_t)d.x_kind;
+    J.out_kind = (int8_t)d.out_kind;
+    J.cls = (int8_t)cls;
+    return true;
+}
+
+// Lays the jobs out as tiles; returns the total tile count and the widest K.
+static int layout_tiles(StreamJob *jobs, int count, int &max_k) {
+    int t = 0;
+    max_k = 0;
+    for (int i = 0; i < count; ++i) {
+        const int rpt = rows_per_tile(jobs[i].cls);
+        jobs[i].tile_begin = t;
+        jobs[i].tiles = (jobs[i].rows + rpt - 1) / rpt;
+        t += jobs[i].tiles;
+        max_k = std::max(max_k, jobs[i].k);
+    }
+    return t;
+}
+
+static int grid_for(int tiles) {
+    return std::max(1, std::min(tiles, kBlocksPerCu * device_cu_count()));
+}
+
+// Launches up to kMaxKargJobs streaming jobs with the descriptors in the kernel arguments.
+int launch_stream_karg(StreamJob *jobs, int count, hipStream_t stream) {
+    if (count < 1 || count > kMaxKargJobs)
+        return set_error(G4_ERR_INVALID, "streaming GEMV: %d jobs (1..%d per call)", count, kMaxKargJobs);
+    StreamArgs A{};
+    int max_k = 0;
+    A.total_tiles = layout_tiles(jobs, count, max_k);
+    A.njobs = count;
+    for (int i = 0; i < count; ++i) A.job[i] = jobs[i];
+    const int grid = grid_for(A.total_tiles);
+    hipLaunchKernelGGL(qgemv_stream_kernel<false>, dim3(grid), dim3(kStreamThreads),
+                       (size_t)((max_k + 15) & ~15), stream, A);
+    G4_LAUNCHED("qgemv_stream_kernel");
+    return G4_OK;
+}
+
+// Launches the jobs on the streaming kernel when every one of them is calibrated and has a shape
+// class; otherwise enqueues nothing and reports *launched = false.
+int stream_try_launch(const g4_gemv_desc *descs, int count, hipStream_t stream, bool *launched) {
+    *launched = false;
+    if (count < 1 || count > kMaxKargJobs) return G4_OK;
+    StreamJob jobs[kMaxKargJobs];
+    for (int i = 0; i < count; ++i)
+        if (!stream_job_from(descs[i], jobs[i])) return G4_OK;
+    int rc = launch_stream_karg(jobs, count, stream);
+    if (rc == G4_OK) *launched = true;
+    return rc;
+}
+
+}  // namespace g4
+
+using namespace g4;
+
+// A reusable launch over any number of projections: the job table and block map live on the
+// device, built once.
+struct g4_gemv_plan {
+    StreamJob *table = nullptr;
+    int *block_job = nullptr;
+    int njobs = 0;
+    int total_tiles = 0;
+    int grid = 0;
+    int max_k = 0;
+    int device = 0;
+};
+
+extern "C" {
+
+int g4_qgemv_plan_create(const g4_gemv_desc *descs, int count, g4_gemv_plan **out) {
+    if (!out) return set_error(G4_ERR_INVALID, "g4_qgemv_plan_create: plan is NULL");
+    *out = nullptr;
+    if (!descs || count < 1)
+        return set_error(G4_ERR_INVALID, "g4_qgemv_plan_create: needs at least one descriptor");
+    std::vector<StreamJob> jobs(count);
+    for (int i = 0; i < count; ++i) {
+        int rc = check_job_desc(descs[i], "GEMV plan");
+        if (rc) return rc;
+        if (!stream_job_from(descs[i], jobs[i]))
+            return set_error(G4_ERR_UNSUPPORTED,
+                             "GEMV plan: projection %d (bits %d, K %d, inScale %g) has no streaming "
+                             "shape class; run it through g4_qgemv",
+                             i, descs[i].bits, descs[i].k, (double)descs[i].in_scale);
+    }
+    int max_k = 0;
+    const int tiles = layout_tiles(jobs.data(), count, max_k);
+    const int grid = grid_for(tiles);
+    std::vector<int> block_job(grid);
+    for (int b = 0, j = 0; b < grid; ++b) {
+        const int tb = (int)(((uint64_t)b * (unsigned)tiles) / (unsigned)grid);
+        while (j + 1 < count && jobs[j + 1].tile_begin <= tb) ++j;
+        block_job[b] = j;
+    }
+    g4_gemv_plan *p = new g4_gemv_plan();
+    p->njobs = count;
+    p->total_tiles = tiles;
+    p->grid = grid;
+    p->max_k = max_k;
+    hipGetDevice(&p->device);
+    hipError_t err = hipMalloc(&p->table, sizeof(StreamJob) * count);
+    if (err == hipSuccess) err = hipMalloc(&p->block_job, sizeof(int) * grid);
+    if (err == hipSuccess)
+        err = hipMemcpy(p->table, jobs.data(), sizeof(StreamJob) * count, hipMemcpyHostToDevice);
+    if (err == hipSuccess)
+        err = hipMemcpy(p->block_job, block_job.data(), sizeof(int) * grid, hipMemcpyHostToDevice);
+    if (err != hipSuccess) {
+        hipFree(p->table);
+        hipFree(p->block_job);
+        delete p;
+        return hip_status(err, "g4_qgemv_plan_create");
+    }
+    *out = p;
+    return G4_OK;
+}
+
+int g4_qgemv_plan_launch(const g4_gemv_plan *p, void *stream) {
+    if (!p) return set_error(G4_ERR_INVALID, "g4_qgemv_plan_launch: plan is NULL");
+    StreamArgs A{};
+    A.table = p->table;
+    A.block_job = p->block_job;
+    A.njobs = p->njobs;
+    A.total_tiles = p->total_tiles;
+    hipLaunchKernelGGL(qgemv_stream_kernel<true>, dim3(p->grid), dim3(kStreamThreads),
+                       (size_t)((p->max_k + 15) & ~15), as_stream(stream), A);
+    G4_LAUNCHED("qgemv_stream_kernel");
+    return G4_OK;
+}
+
+int g4_qgemv_plan_info(const g4_gemv_plan *p, int *tiles, int *grid) {
+    if (!p) return set_error(G4_ERR_INVALID, "g4_qgemv_plan_info: plan is NULL");
+    if (tiles) *tiles = p->total_tiles;
+    if (grid) *grid = p->grid;
+    return G4_OK;
+}
+
+int g4_qgemv_plan_destroy(g4_gemv_plan *p) {
+    if (!p) return G4_OK;
+    hipFree(p->table);
+    hipFree(p->block_job);
+    delete p;
+    return G4_OK;
+}
+
+}  // extern "C"

@@ -95,6 +95,10 @@ SIGNATURES = {
                                      ctypes.POINTER(_c_float), ctypes.POINTER(_c_float), _c_int,
                                      _vp]),
     "g4_qgemv_grouped": (_c_int, [ctypes.POINTER(GemvDesc), _c_int, _vp]),
+    "g4_qgemv_plan_create": (_c_int, [ctypes.POINTER(GemvDesc), _c_int, ctypes.POINTER(_vp)]),
+    "g4_qgemv_plan_launch": (_c_int, [_vp, _vp]),
+    "g4_qgemv_plan_info": (_c_int, [_vp, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
+    "g4_qgemv_plan_destroy": (_c_int, [_vp]),
     "g4_qgemv_split": (_c_int, [_c_int, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
                                 _c_float, _vp]),
     "g4_qgemv_merge": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_float, _vp]),
@@ -340,6 +344,36 @@ def make_group(items) -> ctypes.Array:
 def qgemv_grouped(items_or_array, stream=None):
     arr = items_or_array if isinstance(items_or_array, ctypes.Array) else make_group(items_or_array)
     _check(lib().g4_qgemv_grouped(arr, len(arr), stream))
+
+
+class GemvPlan:
+    """A device-resident grouped GEMV over any number of projections (g4_qgemv_plan_*)."""
+
+    def __init__(self, items):
+        self._arr = make_group(items)
+        self._items = list(items)  # keeps the buffers the plan points at alive
+        h = _vp()
+        _check(lib().g4_qgemv_plan_create(self._arr, len(self._arr), ctypes.byref(h)))
+        self.handle = h.value
+
+    def launch(self, stream=None):
+        _check(lib().g4_qgemv_plan_launch(self.handle, stream))
+
+    def info(self):
+        tiles, grid = _c_int(), _c_int()
+        _check(lib().g4_qgemv_plan_info(self.handle, ctypes.byref(tiles), ctypes.byref(grid)))
+        return tiles.value, grid.value
+
+    def close(self):
+        if self.handle:
+            lib().g4_qgemv_plan_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def qgemv_split(bits, wq, scales, x, partials, k, num_rows, k_splits, exact, in_scale,

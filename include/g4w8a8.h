@@ -153,6 +153,23 @@ typedef struct g4_gemv_desc {
 int g4_qgemv_grouped(const g4_gemv_desc *descs, int count, void *stream);
 
 /*
+ * A reusable grouped GEMV over any number of projections (a whole decode step's projection set):
+ * the descriptors are validated and laid out once into a device-resident job table, and every
+ * g4_qgemv_plan_launch replays the same launch on the buffers the descriptors name. This is the
+ * reference's cached decode-step bind (src/runtime.ts:702-767: bind groups and dispatches built once,
+ * replayed per token) in C-ABI form. Every projection must be calibrated (inScale != 0) and have a
+ * streaming shape class (K * bits / 128 a multiple of 16, 32 or 64 with at most 4 chunks per lane,
+ * or 6 at 8 bits; K <= 16384); g4_qgemv_plan_create refuses others with G4_ERR_UNSUPPORTED.
+ * create allocates and copies (synchronous); launch only enqueues, so it can be graph-captured.
+ */
+typedef struct g4_gemv_plan g4_gemv_plan;
+int g4_qgemv_plan_create(const g4_gemv_desc *descs, int count, g4_gemv_plan **plan);
+int g4_qgemv_plan_launch(const g4_gemv_plan *plan, void *stream);
+/* Tiles (4 waves each) and blocks of the plan's launch. */
+int g4_qgemv_plan_info(const g4_gemv_plan *plan, int *tiles, int *grid);
+int g4_qgemv_plan_destroy(g4_gemv_plan *plan);
+
+/*
  * qgemv-4bit-split / qgemv-8bit-split (src/kernels/qgemv.ts:1753, :1772; band logic :521-548) and
  * qgemv-4bit-gelu-exact-split without the gelu prologue (src/kernels/exactSplit.ts:19-31).
  * Writes partials f32 [num_rows][k_splits]: exact = 0 the scaled f32(f32(xs*scale)*f32(sum_band)),
