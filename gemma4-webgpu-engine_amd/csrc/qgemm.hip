@@ -17,8 +17,8 @@
 //   M <= 2         the GEMV family (qgemv.hip): bit-identical, cheaper than any tile at this M.
 //   3 <= M <= 32   qgemm_skinny_kernel: 16 weight rows per block, the 4 waves split K, the weight
 //                  stream is read once with 16-byte lane loads, an LDS fold of the 4 partials.
-//   M > 32         qgemm_tile_kernel: 128 x 128 output tiles, 4 waves of 64 x 64, K staged through
-//                  double-buffered LDS in 128-code steps, XCD-aware tile order.
+//   M > 32         qgemm_mfma_kernel: 64 x 96 output tiles, activation codes straight to registers,
+//                  weights expanded to int8 in double-buffered LDS, XCD-aware tile order.
 #include "g4_internal.h"
 
 #include <algorithm>
@@ -235,189 +235,182 @@ __global__ __launch_bounds__(256) void qgemm_skinny_kernel(
     }
 }
 
-// ---- tile: 128 x BN outputs per block (BN 128 or 96), 4 waves of 64 x BN/2, K in 128-code
-// stages. Global loads run D = 4 stages ahead through a register ring; LDS is double-buffered, so
-// while a stage is contracted the next is in LDS and the two after it are in flight. Padding of 16
-// bytes per LDS row keeps the 16-byte fragment reads of 8 consecutive lanes on distinct banks.
-template <int BITS, int BN>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void qgemm_tile_kernel(
+// ---- tile: 64 x 96 outputs per block, K in 128-code stages ---------------------------------------
+// Block = 4 waves stacked along M; wave w owns rows m0 + 16 w .. +16 and all 96 columns (6 MFMA
+// column tiles). Two blocks share a CU (two waves per SIMD), so one wave's MFMAs cover the other's
+// LDS and barrier latency.
+//  A (activation codes) goes straight from global memory into registers: lane (j = lane % 16,
+//    g = lane / 16) loads bytes s * 64 + g * 16 .. +16 of its row for MFMA half-step s, so one
+//    load instruction covers 16 rows x 64 contiguous bytes. No LDS traffic for A.
+//  B (weights) is staged through double-buffered LDS once per block, expanded to int8 codes on the
+//    way (4-bit: nibbles into the activation interleave [k0 k2 k4 k6 k1 k3 k5 k7]; 8-bit: as is),
+//    so the inner loop is LDS reads plus MFMAs. Column stride 144 bytes keeps the 16-lane reads on
+//    distinct banks.
+//  Loads run D stages ahead through a register ring written out with compile-time slots, so the
+//  wait counts stay partial (a load behind a branch would drain them).
+// The integer sums are exact; A and B agree on the k assignment inside every MFMA, so the order
+// the matrix core sums in does not matter.
+constexpr int kMfmaBN = 96;
+constexpr int kMfmaBM = 64;
+
+template <int BITS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void qgemm_mfma_kernel(
     const int8_t *__restrict__ A, const int *__restrict__ row_sums, const uint8_t *__restrict__ W,
     const float *__restrict__ scales, void *dst, int M, int N, int K, int kp, float in_scale,
-    float out_scale, int out_kind, int tiles_m, int tiles_n, int xcd_swizzle) {
-    constexpr int BM = 128, BK = kTileBK, D = 4;
-    constexpr int A_STRIDE = BK + 16;
-    constexpr int B_ROW = BITS == 4 ? BK / 2 : BK;
-    constexpr int B_STRIDE = B_ROW + 16;
-    constexpr int A_CH = BM * BK / 16 / 256;  // 16-byte chunks per thread per stage
-    constexpr int B_TOTAL = BN * B_ROW / 16;
-    constexpr int B_CH = (B_TOTAL + 255) / 256;
-    constexpr int B_PER_ROW = B_ROW / 16;
-    constexpr int TN = BN / 2 / 16;  // MFMA column tiles per wave
-    __shared__ __align__(16) uint8_t sA[2][BM * A_STRIDE];
-    __shared__ __align__(16) uint8_t sB[2][BN * B_STRIDE];
+    float out_scale, int out_kind, int tiles_m, int tiles_n) {
+    constexpr int BN = kMfmaBN, TN = BN / 16, D = 2;
+    constexpr int BROW = BITS == 4 ? 64 : 128;  // weight bytes of one column per stage
+    constexpr int BSTR = 144;                   // LDS bytes per column: 128 codes + 16 pad
+    constexpr int B_CHUNKS = BN * BROW / 16;
+    constexpr int B_CH = (B_CHUNKS + 255) / 256;
+    constexpr int CPC = BROW / 16;              // 16-byte weight chunks per column per stage
+    __shared__ __align__(16) uint8_t sB[2][BN * BSTR];
 
     const int b = blockIdx.x;
-    int tm, tn;
-    if (xcd_swizzle) {
-        // Blocks are dealt to the 8 XCDs round robin; keep the blocks of one weight tile (all its
-        // M tiles) on one XCD so its L2 fetches those weight bytes once.
-        const int xcd = b & 7;
-        const int idx = b >> 3;
-        tm = idx % tiles_m;
-        tn = (idx / tiles_m) * 8 + xcd;
-    } else {
-        tm = b % tiles_m;
-        tn = b / tiles_m;
-    }
+    // Blocks are dealt to the 8 XCDs round robin: give one XCD every M tile of a run of N tiles,
+    // so its L2 fetches those weight columns once.
+    const int xcd = b & 7, idx = b >> 3;
+    const int tm = idx % tiles_m;
+    const int tn = (idx / tiles_m) * 8 + xcd;
     if (tn >= tiles_n) return;
-    const int m0 = tm * BM;
-    const int n0 = tn * BN;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 1;
-    const int wn = wave & 1;
-    const int j = lane & 15;
-    const int g = lane >> 4;
-    const int row_bytes = BITS == 4 ? (K >> 1) : K;
-    const int ksteps = K / BK;
-
-    const int8_t *a_src[A_CH];
-    int a_dst[A_CH];
-#pragma unroll
-    for (int i = 0; i < A_CH; ++i) {
-        const int q = tid + 256 * i;
-        const int row = q >> 3, c16 = q & 7;
-        a_src[i] = A + (int64_t)min(m0 + row, M - 1) * kp + c16 * 16;
-        a_dst[i] = row * A_STRIDE + c16 * 16;
-    }
-    const uint8_t *b_src[B_CH];
-    int b_dst[B_CH];
+    const int m0 = tm * kMfmaBM, n0 = tn * BN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j = lane & 15, g = lane >> 4;
+    const int ksteps = K / 128;
+    const int row_bytes = BITS == 4 ? K / 2 : K;
+    const int8_t *arow = A + (int64_t)min(m0 + wave * 16 + j, M - 1) * kp + g * 16;
+    const uint8_t *bsrc[B_CH];
+    int bdst[B_CH];
 #pragma unroll
     for (int i = 0; i < B_CH; ++i) {
-        const int q = min(tid + 256 * i, B_TOTAL - 1);
-        const int row = q / B_PER_ROW, c16 = q % B_PER_ROW;
-        b_src[i] = W + (int64_t)min(n0 + row, N - 1) * row_bytes + c16 * 16;
-        b_dst[i] = row * B_STRIDE + c16 * 16;
+        const int q = min(tid + 256 * i, B_CHUNKS - 1);
+        const int col = q / CPC, c = q % CPC;
+        bsrc[i] = W + (int64_t)min(n0 + col, N - 1) * row_bytes + c * 16;
+        bdst[i] = col * BSTR + c * (BITS == 4 ? 32 : 16);
     }
-
-    // The ring: four named slots (not an indexed array) so each stays a fixed set of registers.
-    u32x4 ra0[A_CH], ra1[A_CH], ra2[A_CH], ra3[A_CH];
-    u32x4 rb0[B_CH], rb1[B_CH], rb2[B_CH], rb3[B_CH];
-    static_assert(D == 4, "the ring below is written out for four slots");
-    // Unconditional loads (a stage past the end re-reads the last one): a load inside a branch
-    // makes the wait-count pass drain every outstanding load at the merge. Macros rather than
-    // lambdas over array references, so the ring slots are promoted to registers.
-#define G4_LOAD_STAGE(XA, XB, KB)                                                          \
-    do {                                                                                   \
-        const int kc_ = min((KB), ksteps - 1);                                             \
-        _Pragma("unroll") for (int i_ = 0; i_ < A_CH; ++i_) XA[i_] =                       \
-            *reinterpret_cast<const u32x4 *>(a_src[i_] + kc_ * BK);                        \
-        _Pragma("unroll") for (int i_ = 0; i_ < B_CH; ++i_) XB[i_] =                       \
-            *reinterpret_cast<const u32x4 *>(b_src[i_] + kc_ * B_ROW);                     \
-    } while (0)
-    // Threads past the last B chunk hold a copy of it (their index is clamped) and store that
-    // same value to the same place: no branch, so the loads stay in flight.
-#define G4_STORE_STAGE(XA, XB, BUF)                                                        \
-    do {                                                                                   \
-        _Pragma("unroll") for (int i_ = 0; i_ < A_CH; ++i_)                                \
-            *reinterpret_cast<u32x4 *>(&sA[(BUF)][a_dst[i_]]) = XA[i_];                    \
-        _Pragma("unroll") for (int i_ = 0; i_ < B_CH; ++i_)                                \
-            *reinterpret_cast<u32x4 *>(&sB[(BUF)][b_dst[i_]]) = XB[i_];                    \
-    } while (0)
-
-    v4i acc[4][TN];
+    // The epilogue's per-row zero-point sums and per-column scales, requested before the K loop so
+    // their latency is not added after it.
+    int rsum[4];
 #pragma unroll
-    for (int x = 0; x < 4; ++x)
+    for (int r = 0; r < 4; ++r)
+        rsum[r] = BITS == 4 ? 8 * row_sums[min(m0 + wave * 16 + 4 * g + r, M - 1)] : 0;
+    float col_scale[TN];
 #pragma unroll
-        for (int y = 0; y < TN; ++y) acc[x][y] = v4i{0, 0, 0, 0};
-
-    auto compute = [&](int buf) {
-        const uint8_t *la = sA[buf];
-        const uint8_t *lb = sB[buf];
-        u32x4 bq[TN][BITS == 4 ? 1 : 2];
+    for (int y = 0; y < TN; ++y) col_scale[y] = __fmul_rn(in_scale, scales[min(n0 + y * 16 + j, N - 1)]);
+    v4i acc[TN];
 #pragma unroll
-        for (int y = 0; y < TN; ++y) {
-            const int col = wn * (BN / 2) + y * 16 + j;
+    for (int y = 0; y < TN; ++y) acc[y] = v4i{0, 0, 0, 0};
+    u32x4 ra[D][2];
+    u32x4 rb[D][B_CH];
+    auto load = [&](u32x4 (&xa)[2], u32x4 (&xb)[B_CH], int st) {
+        const int s_ = min(st, ksteps - 1);  // past the end: re-read the last stage, unguarded
+        xa[0] = *reinterpret_cast<const u32x4 *>(arow + s_ * 128);
+        xa[1] = *reinterpret_cast<const u32x4 *>(arow + s_ * 128 + 64);
+#pragma unroll
+        for (int i = 0; i < B_CH; ++i) xb[i] = *reinterpret_cast<const u32x4 *>(bsrc[i] + s_ * BROW);
+    };
+    // Threads past the last chunk hold a copy of it (clamped index) and store it to the same place.
+    auto store_b = [&](const u32x4 (&xb)[B_CH], int buf) {
+#pragma unroll
+        for (int i = 0; i < B_CH; ++i) {
+            const u32x4 w = xb[i];
             if (BITS == 4) {
-                bq[y][0] = *reinterpret_cast<const u32x4 *>(lb + col * B_STRIDE + g * 16);
+                const u32x4 e0{w.x & 0x0F0F0F0Fu, (w.x >> 4) & 0x0F0F0F0Fu, w.y & 0x0F0F0F0Fu,
+                               (w.y >> 4) & 0x0F0F0F0Fu};
+                const u32x4 e1{w.z & 0x0F0F0F0Fu, (w.z >> 4) & 0x0F0F0F0Fu, w.w & 0x0F0F0F0Fu,
+                               (w.w >> 4) & 0x0F0F0F0Fu};
+                *reinterpret_cast<u32x4 *>(&sB[buf][bdst[i]]) = e0;
+                *reinterpret_cast<u32x4 *>(&sB[buf][bdst[i] + 16]) = e1;
             } else {
-                bq[y][0] = *reinterpret_cast<const u32x4 *>(lb + col * B_STRIDE + g * 32);
-                bq[y][BITS == 4 ? 0 : 1] =
-                    *reinterpret_cast<const u32x4 *>(lb + col * B_STRIDE + g * 32 + 16);
+                *reinterpret_cast<u32x4 *>(&sB[buf][bdst[i]]) = w;
             }
         }
+    };
+#pragma unroll
+    for (int i = 0; i < D; ++i) load(ra[i], rb[i], i);
+    store_b(rb[0], 0);
+    lds_barrier();
+    // Stage st consumes ring slot st % D and refills it with stage st + D. Whole groups of D stages
+    // run unguarded (a branch around the loads would make the wait counts drain at the loop head);
+    // a final odd stage is peeled.
+    auto stage = [&](u32x4 (&xa)[2], u32x4 (&xb)[B_CH], const u32x4 (&xb_next)[B_CH], int st) {
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             v4i bo[TN];
 #pragma unroll
-            for (int y = 0; y < TN; ++y) {
-                if (BITS == 4) {
-                    bo[y] = b_operand<4>(bq[y][0].x, bq[y][0].y, bq[y][0].z, bq[y][0].w, s);
-                } else {
-                    bo[y] = __builtin_bit_cast(v4i, bq[y][BITS == 4 ? 0 : s]);
-                }
-            }
+            for (int y = 0; y < TN; ++y)
+                bo[y] = *reinterpret_cast<const v4i *>(
+                    &sB[st & 1][(y * 16 + j) * BSTR + (s * 4 + g) * 16]);
 #pragma unroll
-            for (int x = 0; x < 4; ++x) {
-                const int row = wm * 64 + x * 16 + j;
-                const v4i ao = *reinterpret_cast<const v4i *>(la + row * A_STRIDE + g * 32 + s * 16);
-#pragma unroll
-                for (int y = 0; y < TN; ++y)
-                    acc[x][y] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ao, bo[y], acc[x][y], 0, 0, 0);
-            }
+            for (int y = 0; y < TN; ++y)
+                acc[y] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, xa[s]), bo[y],
+                                                               acc[y], 0, 0, 0);
         }
+        store_b(xb_next, (st + 1) & 1);
+        load(xa, xb, st + D);
+        lds_barrier();
     };
-
-    // Stage s lives in ring slot s % D. Prologue: stages 0..D-1 requested, stage 0 stored to LDS
-    // and its slot refilled with stage D. Iteration kb then stores stage kb + 1 and refills that
-    // slot with stage kb + 1 + D, so D stages stay in flight behind the one being contracted.
-    G4_LOAD_STAGE(ra0, rb0, 0);
-    G4_LOAD_STAGE(ra1, rb1, 1);
-    G4_LOAD_STAGE(ra2, rb2, 2);
-    G4_LOAD_STAGE(ra3, rb3, 3);
-    G4_STORE_STAGE(ra0, rb0, 0);
-    G4_LOAD_STAGE(ra0, rb0, D);
-    lds_barrier();
-#define G4_TILE_ITER(XA, XB, KB)                 \
-    do {                                         \
-        compute((KB) & 1);                       \
-        G4_STORE_STAGE(XA, XB, ((KB) + 1) & 1);  \
-        G4_LOAD_STAGE(XA, XB, (KB) + 1 + D);     \
-        lds_barrier();                           \
-    } while (0)
-    // Whole groups of D stages run without guards; the last partial group is guarded.
-    int kb0 = 0;
-    for (; kb0 + D <= ksteps; kb0 += D) {
-        G4_TILE_ITER(ra1, rb1, kb0);
-        G4_TILE_ITER(ra2, rb2, kb0 + 1);
-        G4_TILE_ITER(ra3, rb3, kb0 + 2);
-        G4_TILE_ITER(ra0, rb0, kb0 + 3);
+    static_assert(D == 2, "the ring below is written out for two slots");
+    int st = 0;
+    for (; st + 2 <= ksteps; st += 2) {
+        stage(ra[0], rb[0], rb[1], st);
+        stage(ra[1], rb[1], rb[0], st + 1);
     }
-    if (kb0 < ksteps) G4_TILE_ITER(ra1, rb1, kb0);
-    if (kb0 + 1 < ksteps) G4_TILE_ITER(ra2, rb2, kb0 + 1);
-    if (kb0 + 2 < ksteps) G4_TILE_ITER(ra3, rb3, kb0 + 2);
-#undef G4_TILE_ITER
-#undef G4_LOAD_STAGE
-#undef G4_STORE_STAGE
-
+    if (st < ksteps) stage(ra[0], rb[0], rb[1], st);
+    // D layout of a 16 x 16 MFMA tile: lane l, register r -> row 4 (l / 16) + r, column l % 16.
+    // The outputs go through LDS so each row of the tile leaves as whole 16-byte stores (scattered
+    // byte stores of 16-byte runs cost more than the contraction). Edge tiles and rows whose start
+    // is not 16-byte aligned keep per-element stores.
+    bool r_ok;
+    const float rcp = srq_recip(out_scale, r_ok);
+    const int esz = out_kind == G4_KIND_I8 ? 1 : 4;
+    const bool full = m0 + kMfmaBM <= M && n0 + BN <= N && ((int64_t)N * esz) % 16 == 0;
+    lds_barrier();  // every wave is done reading the last stage's weights
+    uint8_t *stile = &sB[0][0];  // 64 x 96 outputs: 6 KB (int8) or 24 KB (f32 / int32) of LDS
+    static_assert(2 * BN * BSTR >= kMfmaBM * BN * 4, "the output tile fits the weight buffers");
 #pragma unroll
     for (int y = 0; y < TN; ++y) {
-        const int n = n0 + wn * (BN / 2) + y * 16 + j;
-        if (n >= N) continue;
-        const float scale = scales[n];
+        const int n = n0 + y * 16 + j;
+        const float rs = col_scale[y];
 #pragma unroll
-        for (int x = 0; x < 4; ++x) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = m0 + wm * 64 + x * 16 + 4 * g + r;
-                if (m < M) {
-                    int v = acc[x][y][r];
-                    if (BITS == 4) v -= 8 * row_sums[m];
-                    store_tile_out(dst, m, n, N, out_kind, v, in_scale, scale, out_scale);
+        for (int r = 0; r < 4; ++r) {
+            const int lr = wave * 16 + 4 * g + r;
+            const int m = m0 + lr;
+            const int v = acc[y][r] - rsum[r];
+            const float yv = __fmul_rn(rs, (float)v);
+            if (full) {
+                const int o = lr * BN + y * 16 + j;
+                if (out_kind == G4_KIND_I8) {
+                    stile[o] = (uint8_t)(int8_t)srq_code_fast(yv, out_scale, rcp, r_ok);
+                } else if (out_kind == G4_KIND_I32) {
+                    reinterpret_cast<int32_t *>(stile)[o] = v;
+                } else {
+                    float f = yv;
+                    if (out_scale != 0.0f) f = __fmul_rn(srq_code_fast(yv, out_scale, rcp, r_ok), out_scale);
+                    reinterpret_cast<float *>(stile)[o] = f;
+                }
+            } else if (m < M && n < N) {
+                const int64_t o = (int64_t)m * N + n;
+                if (out_kind == G4_KIND_I8) {
+                    reinterpret_cast<int8_t *>(dst)[o] = (int8_t)srq_code_fast(yv, out_scale, rcp, r_ok);
+                } else if (out_kind == G4_KIND_I32) {
+                    reinterpret_cast<int32_t *>(dst)[o] = v;
+                } else {
+                    float f = yv;
+                    if (out_scale != 0.0f) f = __fmul_rn(srq_code_fast(yv, out_scale, rcp, r_ok), out_scale);
+                    reinterpret_cast<float *>(dst)[o] = f;
                 }
             }
         }
+    }
+    if (!full) return;  // uniform
+    lds_barrier();
+    const int row_chunks = BN * esz / 16;  // 6 (int8) or 24 (f32 / int32)
+    for (int q = tid; q < kMfmaBM * row_chunks; q += 256) {
+        const int lr = q / row_chunks, c = q - lr * row_chunks;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(stile + lr * BN * esz + c * 16);
+        *reinterpret_cast<u32x4 *>(reinterpret_cast<uint8_t *>(dst) +
+                                   ((int64_t)(m0 + lr) * N + n0) * esz + c * 16) = v;
     }
 }
 
@@ -471,7 +464,7 @@ static const char *choice_name(KernelChoice c, int bits) {
         case K_GEMV: return bits == 4 ? "qgemv-4bit" : "qgemv-8bit";
         case K_SKINNY16: return bits == 4 ? "qgemm-4bit-mfma-skinny16" : "qmatmul-8bit-mfma-skinny16";
         case K_SKINNY32: return bits == 4 ? "qgemm-4bit-mfma-skinny32" : "qmatmul-8bit-mfma-skinny32";
-        case K_TILE128: return bits == 4 ? "qgemm-4bit-mfma-tile128" : "qmatmul-8bit-mfma-tile128";
+        case K_TILE128: return bits == 4 ? "qgemm-4bit-mfma-tile" : "qmatmul-8bit-mfma-tile";
         case K_GEMV_F32: return bits == 4 ? "qgemv-4bit-f32" : "qgemv-8bit-f32";
         default: return bits == 4 ? "qgemv-4bit-columns" : "qgemv-8bit-columns";
     }
@@ -493,23 +486,12 @@ static int launch_mfma(KernelChoice c, const int8_t *codes, const int *sums, con
         G4_LAUNCHED("qgemm_skinny_kernel");
         return G4_OK;
     }
-    // 128 x 96 tiles when they fill the CUs better than 128 x 128 (e.g. 512 x 6144: 256 tiles).
-    const int tiles_m = (m + 127) / 128;
-    const int cus = device_cu_count();
-    const bool use96 = n % 96 == 0 && (int64_t)tiles_m * ((n + 127) / 128) < cus &&
-                       (int64_t)tiles_m * (n / 96) <= (int64_t)cus + cus / 8;
-    const int bn = use96 ? 96 : 128;
-    const int tiles_n = (n + bn - 1) / bn;
-    const int swizzle = (tiles_n % 8 == 0) ? 1 : 0;
-    if (use96)
-        hipLaunchKernelGGL((qgemm_tile_kernel<BITS, 96>), dim3(tiles_m * tiles_n), dim3(256), 0,
-                           stream, codes, sums, w, scales, dst, m, n, k, kp, in_scale, out_scale,
-                           out_kind, tiles_m, tiles_n, swizzle);
-    else
-        hipLaunchKernelGGL((qgemm_tile_kernel<BITS, 128>), dim3(tiles_m * tiles_n), dim3(256), 0,
-                           stream, codes, sums, w, scales, dst, m, n, k, kp, in_scale, out_scale,
-                           out_kind, tiles_m, tiles_n, swizzle);
-    G4_LAUNCHED("qgemm_tile_kernel");
+    const int tiles_m = (m + kMfmaBM - 1) / kMfmaBM;
+    const int tiles_n = (n + kMfmaBN - 1) / kMfmaBN;
+    const int blocks = tiles_m * ((tiles_n + 7) / 8) * 8;  // XCD-aware order: whole groups of 8
+    hipLaunchKernelGGL((qgemm_mfma_kernel<BITS>), dim3(blocks), dim3(256), 0, stream, codes, sums,
+                       w, scales, dst, m, n, k, kp, in_scale, out_scale, out_kind, tiles_m, tiles_n);
+    G4_LAUNCHED("qgemm_mfma_kernel");
     return G4_OK;
 }
 
