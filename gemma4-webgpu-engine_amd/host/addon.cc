@@ -303,6 +303,59 @@ napi_value QgemvGrouped(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// Descriptors of a grouped GEMV from an array of plain objects (the qgemvGrouped shape).
+bool gemv_descs(napi_env env, napi_value arr, std::vector<g4_gemv_desc> &d) {
+    bool is_arr = false;
+    if (napi_is_array(env, arr, &is_arr) != napi_ok || !is_arr) return false;
+    uint32_t n = 0;
+    napi_get_array_length(env, arr, &n);
+    d.resize(n);
+    for (uint32_t i = 0; i < n; ++i) {
+        napi_value o;
+        napi_get_element(env, arr, i, &o);
+        d[i].wq = reinterpret_cast<const void *>((uintptr_t)prop(env, o, "wq"));
+        d[i].scales = reinterpret_cast<const float *>((uintptr_t)prop(env, o, "scales"));
+        d[i].x = reinterpret_cast<const void *>((uintptr_t)prop(env, o, "x"));
+        d[i].dst = reinterpret_cast<void *>((uintptr_t)prop(env, o, "dst"));
+        d[i].bits = (int)prop(env, o, "bits", 4);
+        d[i].x_kind = (int)prop(env, o, "xKind", G4_KIND_F16);
+        d[i].out_kind = (int)prop(env, o, "outKind", G4_KIND_I8);
+        d[i].k = (int)prop(env, o, "k");
+        d[i].num_rows = (int)prop(env, o, "numRows");
+        d[i].in_scale = (float)prop(env, o, "inScale");
+        d[i].out_scale = (float)prop(env, o, "outScale");
+    }
+    return true;
+}
+
+// qgemvPlanCreate(descs) -> handle; qgemvPlanLaunch(handle); qgemvPlanDestroy(handle).
+napi_value QgemvPlanCreate(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    std::vector<g4_gemv_desc> d;
+    if (a.size() < 1 || !gemv_descs(env, a.v[0], d)) {
+        throw_type(env, "qgemvPlanCreate(descs: object[])");
+        return nullptr;
+    }
+    g4_gemv_plan *plan = nullptr;
+    if (throw_status(env, g4_qgemv_plan_create(d.data(), (int)d.size(), &plan))) return nullptr;
+    return make_num(env, (double)(uintptr_t)plan);
+}
+
+napi_value QgemvPlanLaunch(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    if (throw_status(env, g4_qgemv_plan_launch(reinterpret_cast<const g4_gemv_plan *>(a.ptr(0)),
+                                               nullptr)))
+        return nullptr;
+    return undefined(env);
+}
+
+napi_value QgemvPlanDestroy(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    if (throw_status(env, g4_qgemv_plan_destroy(reinterpret_cast<g4_gemv_plan *>(a.ptr(0)))))
+        return nullptr;
+    return undefined(env);
+}
+
 napi_value QgemvSplit(napi_env env, napi_callback_info info) {
     Args a(env, info, 11);
     int st = g4_qgemv_split(a.i32(0), a.ptr(1), (const float *)a.ptr(2), a.ptr(3), a.i32(4),
@@ -440,7 +493,8 @@ napi_value Init(napi_env env, napi_value exports) {
         {"qgemvSplit", QgemvSplit}, {"qgemvMerge", QgemvMerge},
         {"qgemvExactMerge", QgemvExactMerge}, {"srqQuantize", SrqQuantize},
         {"pleGather", PleGather}, {"pleGatherSplit", PleGatherSplit},
-        {"planTableSplit", PlanTableSplit},
+        {"planTableSplit", PlanTableSplit}, {"qgemvPlanCreate", QgemvPlanCreate},
+        {"qgemvPlanLaunch", QgemvPlanLaunch}, {"qgemvPlanDestroy", QgemvPlanDestroy},
     };
     for (const Fn &f : fns) {
         napi_value v;
