@@ -2,9 +2,9 @@
 // (src/kernels/embedGather.ts:176-261, :435-485), plus one fused launch over every slice of a
 // split table (the reference dispatches once per slice, embedGather.ts:403-419).
 //
-// One thread per 4 bytes of a gathered row: it reads 8 packed codes with one 32-bit load and
-// writes 8 outputs (one 16-byte f16 store, two of f32, one 8-byte of int8), so each load and store
-// instruction of a wave covers one contiguous run of the row. The arithmetic is the reference's: fold the
+// One block per token: each thread reads 8 packed codes with one 32-bit load and writes 8 outputs
+// (one 16-byte f16 store, two of f32, one 8-byte of int8) per run, and the block's threads take
+// consecutive runs, so each load and store instruction covers one contiguous stretch of the row. The arithmetic is the reference's: fold the
 // embed scale 16 into the group scale in f32 (exact, a power of two), then one multiply per
 // element, f32((code - 8) * f32(16 * scale)), rounded to f16 ties-to-even for the f16 output.
 // The scale index follows the shader (embedGather.ts:245-248): group of col = 4 j, so a group
@@ -13,8 +13,8 @@
 
 namespace g4 {
 
-constexpr int kGatherThreads = 256;
 constexpr int kMaxSlices = 16;
+typedef unsigned int u32x2g __attribute__((ext_vector_type(2)));
 
 struct SliceTable {
     const uint8_t *codes[kMaxSlices];
@@ -28,12 +28,18 @@ __device__ __forceinline__ float scale_at(const void *scales, int kind, int64_t 
     return reinterpret_cast<const float *>(scales)[i];
 }
 
-// Writes the 8 outputs of chunk `ch` (codes 8 ch .. 8 ch + 7, one packed u32) of slot `slot`.
-// `src` points at the code word, or is null for an id no slice carries (written as zeros).
-__device__ __forceinline__ void gather_chunk(const uint8_t *src, const void *scales, int scale_kind,
-                                             int64_t row, void *dst, int out_kind, int64_t slot,
-                                             int ch, int cols, int group_size, int groups_per_row) {
-    const uint32_t w = src ? *reinterpret_cast<const uint32_t *>(src) : 0x88888888u;
+// The embed scale of the vec4 starting at column `col` (the group of its first column,
+// embedGather.ts:245-248), times the embed multiplier 16 (exact: a power of two).
+__device__ __forceinline__ float vec4_scale(const void *scales, int scale_kind, int64_t row, int col,
+                                            int group_size, int groups_per_row) {
+    return __fmul_rn(16.0f, scale_at(scales, scale_kind, row * groups_per_row + col / group_size));
+}
+
+// Writes the 8 outputs of chunk `ch` (codes 8 ch .. 8 ch + 7, the packed word `w`) of slot `slot`;
+// s0 / s1 are the folded scales of its two vec4s. A word of 0x88888888 with zero scales writes the
+// zeros of an id no slice carries.
+__device__ __forceinline__ void gather_chunk(uint32_t w, float s0, float s1, void *dst,
+                                             int out_kind, int64_t slot, int ch, int cols) {
     const int col0 = ch * 8;
     const int64_t obase = slot * (int64_t)cols + col0;
     if (out_kind == G4_KIND_I8) {
@@ -44,19 +50,14 @@ __device__ __forceinline__ void gather_chunk(const uint8_t *src, const void *sca
             lo |= (uint32_t)((int)((w >> (4 * q)) & 0xf) - 8 & 0xff) << (8 * q);
             hi |= (uint32_t)((int)((w >> (16 + 4 * q)) & 0xf) - 8 & 0xff) << (8 * q);
         }
-        *reinterpret_cast<uint2 *>(reinterpret_cast<int8_t *>(dst) + obase) = make_uint2(lo, hi);
+        __builtin_nontemporal_store(
+            (u32x2g){lo, hi}, reinterpret_cast<u32x2g *>(reinterpret_cast<int8_t *>(dst) + obase));
         return;
     }
     float out[8];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-        // One scale per vec4 of output, the group of its first column (embedGather.ts:245-248).
-        float scale = 0.0f;
-        if (src) {
-            const int col = col0 + 4 * q;
-            scale = __fmul_rn(16.0f, scale_at(scales, scale_kind,
-                                              row * groups_per_row + col / group_size));
-        }
+        const float scale = q == 0 ? s0 : s1;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int i = 4 * q + e;
@@ -72,53 +73,86 @@ __device__ __forceinline__ void gather_chunk(const uint8_t *src, const void *sca
             const unsigned short hi = __half_as_ushort(__float2half_rn(out[2 * i + 1]));
             h[i] = (uint32_t)lo | ((uint32_t)hi << 16);
         }
-        *reinterpret_cast<uint4 *>(reinterpret_cast<__half *>(dst) + obase) =
-            make_uint4(h[0], h[1], h[2], h[3]);
+        __builtin_nontemporal_store(
+            u32x4{h[0], h[1], h[2], h[3]},
+            reinterpret_cast<u32x4 *>(reinterpret_cast<__half *>(dst) + obase));
     } else {
-        float4 *d = reinterpret_cast<float4 *>(reinterpret_cast<float *>(dst) + obase);
-        d[0] = make_float4(out[0], out[1], out[2], out[3]);
-        d[1] = make_float4(out[4], out[5], out[6], out[7]);
+        u32x4 *d = reinterpret_cast<u32x4 *>(reinterpret_cast<float *>(dst) + obase);
+        __builtin_nontemporal_store(u32x4{__float_as_uint(out[0]), __float_as_uint(out[1]),
+                                          __float_as_uint(out[2]), __float_as_uint(out[3])}, d);
+        __builtin_nontemporal_store(u32x4{__float_as_uint(out[4]), __float_as_uint(out[5]),
+                                          __float_as_uint(out[6]), __float_as_uint(out[7])}, d + 1);
+    }
+}
+
+// One block per token slot (the id, the slice lookup and the row base are uniform scalars). A
+// thread covers the 8-code runs tid, tid + T, tid + 2T, ... of the row (T = threads of the block),
+// so every load instruction reads one contiguous run of codes and every store instruction writes
+// one contiguous run of the output row; outputs are written non-temporally (they are not re-read
+// by this launch).
+constexpr int kRunsPerThread = 4;
+
+__device__ __forceinline__ void gather_row(const uint8_t *row_codes, const void *scales,
+                                           int scale_kind, int64_t row, void *dst, int out_kind,
+                                           int64_t slot, int cols, int group_size,
+                                           int groups_per_row) {
+    const int runs = cols >> 3;
+    const int T = blockDim.x;
+    for (int base = threadIdx.x; base < runs; base += kRunsPerThread * T) {
+        // All of this thread's code words and scales are requested before any is converted.
+        uint32_t w[kRunsPerThread];
+        float s0[kRunsPerThread], s1[kRunsPerThread];
+#pragma unroll
+        for (int u = 0; u < kRunsPerThread; ++u) {
+            const int ch = base + u * T;
+            const bool live = row_codes && ch < runs;
+            w[u] = live ? *reinterpret_cast<const uint32_t *>(row_codes + (int64_t)ch * 4)
+                        : 0x88888888u;
+            s0[u] = live ? vec4_scale(scales, scale_kind, row, ch * 8, group_size, groups_per_row) : 0.0f;
+            s1[u] = live ? vec4_scale(scales, scale_kind, row, ch * 8 + 4, group_size, groups_per_row)
+                         : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kRunsPerThread; ++u) {
+            const int ch = base + u * T;
+            if (ch < runs) gather_chunk(w[u], s0[u], s1[u], dst, out_kind, slot, ch, cols);
+        }
     }
 }
 
 // One slice (or the whole table with start 0 and count = rows): ids outside the slice are left
 // untouched when `sliced`, and written as zeros when not (an id the table does not hold).
-__global__ __launch_bounds__(kGatherThreads) void ple_gather_kernel(
+__global__ __launch_bounds__(1024) void ple_gather_kernel(
     const uint8_t *codes, const void *scales, int scale_kind, const int32_t *ids, void *dst,
     int out_kind, int slots, int cols, int group_size, int groups_per_row, int sliced,
     int64_t start, int64_t count) {
-    const int chunks = cols >> 3;
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= (int64_t)slots * chunks) return;
-    const int64_t slot = t / chunks;
-    const int ch = (int)(t - slot * chunks);
+    const int64_t slot = blockIdx.x;
     const int64_t row = (int64_t)(uint32_t)ids[slot];
     const bool inside = row >= start && row - start < count;
-    if (!inside && sliced) return;
-    const uint8_t *src =
-        inside ? codes + (row - start) * (int64_t)(cols >> 1) + (int64_t)ch * 4 : nullptr;
-    gather_chunk(src, scales, scale_kind, row, dst, out_kind, slot, ch, cols, group_size,
-                 groups_per_row);
+    if (!inside && sliced) return;  // uniform
+    gather_row(inside ? codes + (row - start) * (int64_t)(cols >> 1) : nullptr, scales, scale_kind,
+               row, dst, out_kind, slot, cols, group_size, groups_per_row);
 }
 
 // Every slice of a split table in one launch: each slot finds the slice that carries its id.
-__global__ __launch_bounds__(kGatherThreads) void ple_gather_split_kernel(
+__global__ __launch_bounds__(1024) void ple_gather_split_kernel(
     SliceTable tab, const void *scales, int scale_kind, const int32_t *ids, void *dst, int out_kind,
     int slots, int cols, int group_size, int groups_per_row) {
-    const int chunks = cols >> 3;
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= (int64_t)slots * chunks) return;
-    const int64_t slot = t / chunks;
-    const int ch = (int)(t - slot * chunks);
+    const int64_t slot = blockIdx.x;
     const int64_t row = (int64_t)(uint32_t)ids[slot];
     const uint8_t *src = nullptr;
-#pragma unroll
-    for (int s = 0; s < kMaxSlices; ++s) {
-        if (s < tab.n && row >= tab.start[s] && row - tab.start[s] < tab.count[s])
-            src = tab.codes[s] + (row - tab.start[s]) * (int64_t)(cols >> 1) + (int64_t)ch * 4;
-    }
-    gather_chunk(src, scales, scale_kind, row, dst, out_kind, slot, ch, cols, group_size,
-                 groups_per_row);
+    for (int s = 0; s < tab.n; ++s)
+        if (row >= tab.start[s] && row - tab.start[s] < tab.count[s])
+            src = tab.codes[s] + (row - tab.start[s]) * (int64_t)(cols >> 1);
+    gather_row(src, scales, scale_kind, row, dst, out_kind, slot, cols, group_size, groups_per_row);
+}
+
+// Threads per block: enough for kRunsPerThread 8-code runs each, whole waves, at most 1024.
+static int gather_threads(int cols) {
+    const int runs = cols >> 3;
+    int t = (runs + kRunsPerThread - 1) / kRunsPerThread;
+    t = ((t + 63) / 64) * 64;
+    return t < 64 ? 64 : (t > 1024 ? 1024 : t);
 }
 
 static int check_gather(const void *scales, int scale_kind, const int32_t *ids, void *dst,
@@ -169,9 +203,7 @@ int g4_ple_gather(const void *codes, const void *scales, int scale_kind, const i
         return set_error(G4_ERR_INVALID, "ple-gather-4bit: an unsliced table starts at row 0");
     if (reinterpret_cast<uintptr_t>(codes) & 3)
         return set_error(G4_ERR_INVALID, "%s: codes must be 4-byte aligned", who);
-    const int64_t threads = (int64_t)slots * (cols / 8);
-    const int64_t blocks = (threads + kGatherThreads - 1) / kGatherThreads;
-    hipLaunchKernelGGL(ple_gather_kernel, dim3((unsigned)blocks), dim3(kGatherThreads), 0,
+    hipLaunchKernelGGL(ple_gather_kernel, dim3((unsigned)slots), dim3(gather_threads(cols)), 0,
                        as_stream(stream), reinterpret_cast<const uint8_t *>(codes), scales,
                        scale_kind, ids, dst, out_kind, slots, cols, group_size, groups_per_row,
                        sliced ? 1 : 0, slice_start_row, slice_row_count);
@@ -202,9 +234,7 @@ int g4_ple_gather_split(const void *const *slice_codes, const int64_t *slice_sta
         tab.start[s] = slice_starts[s];
         tab.count[s] = slice_counts[s];
     }
-    const int64_t threads = (int64_t)slots * (cols / 8);
-    const int64_t blocks = (threads + kGatherThreads - 1) / kGatherThreads;
-    hipLaunchKernelGGL(ple_gather_split_kernel, dim3((unsigned)blocks), dim3(kGatherThreads), 0,
+    hipLaunchKernelGGL(ple_gather_split_kernel, dim3((unsigned)slots), dim3(gather_threads(cols)), 0,
                        as_stream(stream), tab, scales, scale_kind, ids, dst, out_kind, slots, cols,
                        group_size, groups_per_row);
     G4_LAUNCHED("ple_gather_split_kernel");
