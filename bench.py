@@ -130,6 +130,71 @@ def bench_gemm(h, m=512, reps=50):
             "note": "f16_in includes the activation snap; int8_in takes codes already snapped"}
 
 
+def bench_gemm_sweep(h, ms=(4, 8, 16, 128, 512, 2048), reps=30):
+    """Config 2: the gate projection (K=1536, N=6144, int4) at every BASELINE M, int8 codes in
+    (the activation snap is timed separately in bench_gemm). Bytes are weights + scales + x + out."""
+    n, k = syn.FFN, syn.HIDDEN
+    w = g4.DeviceBuffer.from_array(syn.int4_weights("c2", "gate", n, k))
+    s = g4.DeviceBuffer.from_array(syn.row_scales("c2", "gate", n))
+    rows = []
+    for m in ms:
+        x = g4.DeviceBuffer.from_array(syn.activations("c2", f"x{m}", m, k, outlier_frac=0.01))
+        codes = g4.DeviceBuffer.empty((m, k), np.int8)
+        g4.srq_quantize(x, codes, m * k, syn.IN_SCALE, stream=h)
+        d = g4.DeviceBuffer.empty((m, n), np.int8)
+        ms_ = timed(h, lambda: g4.qgemm(4, w, s, codes, d, k, n, m, syn.IN_SCALE, syn.OUT_SCALE,
+                                        stream=h), reps, 5)
+        by = n * k // 2 + 4 * n + m * k + m * n
+        rows.append({"m": m, "kernel": g4.kernel_for_shape(4, m, n, k), "us": round(ms_ * 1e3, 3),
+                     "tops": round(2.0 * m * n * k / (ms_ * 1e-3) / 1e12, 2),
+                     "gbs": round(by / (ms_ * 1e-3) / 1e9, 2)})
+    return rows
+
+
+def bench_int8_down(h, reps=50):
+    """Config 1's int8-weight variant of down (6144 -> 1536, I8 codes U[-127,127]) at M=1."""
+    n, k = syn.HIDDEN, syn.FFN
+    w = g4.DeviceBuffer.from_array(syn.int8_weights("c1", "down8", n, k))
+    s = g4.DeviceBuffer.from_array(syn.row_scales("c1", "down8", n))
+    x = g4.DeviceBuffer.from_array(syn.activations("c1", "down8", 1, k)[0])
+    d = g4.DeviceBuffer.empty((n,), np.int8)
+    ms_ = timed(h, lambda: g4.qgemv(8, w, s, x, d, k, n, 1, syn.IN_SCALE, syn.OUT_SCALE, stream=h),
+                reps, 5)
+    return {"n": n, "k": k, "kernel": g4.kernel_for_shape(8, 1, n, k), "us": round(ms_ * 1e3, 3),
+            "gbs": round(proj_bytes(n, k, 8) / (ms_ * 1e-3) / 1e9, 2)}
+
+
+def cpu_extra(seconds=4.0):
+    """The oracle on the host cores for the other rows (bounded samples): the config-2 GEMM at
+    M=16 and the config-3 gather at 64 tokens."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle  # the checker's C restatement, used here only as the timed CPU baseline
+
+    n, k, m = syn.FFN, syn.HIDDEN, 16
+    w = syn.int4_weights("c2", "gate", n, k)
+    s = syn.row_scales("c2", "gate", n)
+    x = syn.activations("c2", f"x{m}", m, k, outlier_frac=0.01).astype(np.float32)
+    done, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        oracle.qgemm(4, w, s, x, n, k, m, syn.IN_SCALE, syn.OUT_SCALE)
+        done += 1
+    el = time.perf_counter() - t0
+    gemm = {"tops": round(2.0 * m * n * k * done / el / 1e12, 4), "sample": f"{done} x M=16 gate GEMM, {el:.1f} s"}
+    rows, cols, tokens = 4096, syn.PLE_COLS, 64
+    codes = syn.ple_codes("c3cpu", rows)
+    scales = syn.ple_scales("c3cpu", rows)
+    ids = (syn.zipf_ids("c3", tokens) % rows).astype(np.int32)
+    done, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        oracle.embed_gather(codes, scales, ids, cols, 256, out_kind="f16")
+        done += 1
+    el = time.perf_counter() - t0
+    per_token = cols // 2 + 2 * (cols // 256) + 4 + 2 * cols
+    gather = {"gbs": round(per_token * tokens * done / el / 1e9, 3),
+              "sample": f"{done} x 64-token gather over a 4096-row table, {el:.1f} s"}
+    return {"cores": oracle.num_threads(), "kind": "port", "gemm_m16": gemm, "ple_gather": gather}
+
+
 def bench_gather(h, tokens=2048, reps=20):
     rows, cols = syn.PLE_ROWS, syn.PLE_COLS
     codes = syn.ple_codes("c3", rows)
@@ -287,6 +352,9 @@ def main():
         gm = bench_gemm(h)
         log("config 3 split PLE gather")
         ga = bench_gather(h)
+        log("config 2 sweep over M, config 1 int8 down")
+        sweep = bench_gemm_sweep(h)
+        down8 = bench_int8_down(h)
         result["extra"] = {
             "per_layer_grouped": {"launches_per_step": LAYERS, "ms_per_step": round(ms_layer, 6),
                                   "gbs": round(step_bytes / (ms_layer * 1e-3) / 1e9, 2)},
@@ -296,11 +364,15 @@ def main():
                                     "gbs": round(proj_bytes(1536, 1536) / (ms_c0 * 1e-3) / 1e9, 2),
                                     "kernel": g4.kernel_for_shape(4, 1, 1536, 1536)},
             "int8_gemm_m512": gm,
+            "gemm_sweep_config2": sweep,
+            "config1_int8_down": down8,
             "ple_gather": ga,
         }
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle on host cores)")
         result["cpu_baseline"] = cpu_baseline()
+        if not args.no_extra:
+            result.setdefault("extra", {})["cpu_other_rows"] = cpu_extra()
     result["config"]["wall_s_after_timing"] = round(time.perf_counter() - t_wall, 3)
     plan.close()
     print(json.dumps(result), flush=True)
