@@ -15,8 +15,8 @@
 //
 // Kernels by M (chosen per shape, see pick_kernel):
 //   M <= 2         the GEMV family (qgemv.hip): bit-identical, cheaper than any tile at this M.
-//   3 <= M <= 32   qgemm_skinny_kernel: 16 weight rows per block, the 4 waves split K, the weight
-//                  stream is read once with 16-byte lane loads, an LDS fold of the 4 partials.
+//   3 <= M <= 32   qgemm_small_kernel: one launch with the snap fused (codes in LDS), 16 weight
+//                  rows per block, the 4 waves split K, an LDS fold of the 4 partials.
 //   M > 32         qgemm_mfma_kernel: 64 x 96 output tiles, activation codes straight to registers,
 //                  weights expanded to int8 in double-buffered LDS, XCD-aware tile order.
 #include "g4_internal.h"
@@ -130,17 +130,26 @@ __device__ __forceinline__ void store_tile_out(void *dst, int m, int n, int N, i
     store_linear_out(dst, (int64_t)m * N + n, out_kind, y, acc, out_scale);
 }
 
-// ---- skinny: M <= MT token rows, 16 weight rows per block, K split over the 4 waves ---------
-// Lane (j = lane % 16, g = lane / 16) owns weight row n0 + j. Per 128-code step kb it loads 16
-// bytes of that row: 4-bit codes kb*128 + g*32 .. +32 (8-bit: kb*128 + g*32 .. +16 per half
-// step). MFMA half-step s in {0,1} takes codes g*32 + s*16 .. +16 of the step from both operands.
+// ---- small M: M <= MT token rows, 16 weight rows per block, K split over the 4 waves ----------
+// The activation snap is fused: the block snaps its MT token rows into LDS as int8 codes (the
+// 4-bit interleave per 8-code group) one K chunk at a time, so a draft-verify or small prefill
+// call is one launch. The 4-bit zero point needs sum(xq) per token row: one more MFMA per step
+// against an all-ones B operand gives it exactly, folded with the partials like the products. Lane (j = lane % 16, g = lane / 16)
+// owns weight row n0 + j; per 128-code stage it loads 16 bytes of that row (8-bit: 32), and MFMA
+// half-step s takes codes g*32 + s*16 .. +16 of the stage from both operands. The LDS rows are
+// padded by 16 bytes so the 16 token rows of one A read fall on distinct banks.
 template <int BITS, int MT>
-__global__ __launch_bounds__(256) void qgemm_skinny_kernel(
-    const int8_t *__restrict__ A, const int *__restrict__ row_sums, const uint8_t *__restrict__ W,
-    const float *__restrict__ scales, void *dst, int M, int N, int K, int kp, float in_scale,
+__global__ __launch_bounds__(256) void qgemm_small_kernel(
+    const void *__restrict__ x, int x_kind, const uint8_t *__restrict__ W,
+    const float *__restrict__ scales, void *dst, int M, int N, int K, float in_scale,
     float out_scale, int out_kind) {
     constexpr int TM = MT / 16;
-    __shared__ v4i red[3][TM][64];
+    constexpr int KC = 32768 / MT;     // codes of a row per LDS chunk
+    constexpr int XSTR = KC + 16;      // LDS bytes per token row
+    constexpr int BATCH = 4;
+    constexpr int NACC = BITS == 4 ? 2 * TM : TM;  // products, then (4-bit) the row sums
+    __shared__ __align__(16) int8_t xs[MT * XSTR];
+    __shared__ v4i red[3][NACC][64];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -150,56 +159,96 @@ __global__ __launch_bounds__(256) void qgemm_skinny_kernel(
     const int m0 = blockIdx.y * MT;
     const int n = min(n0 + j, N - 1);
     const int row_bytes = BITS == 4 ? (K >> 1) : K;
-    const int ksteps = K / kTileBK;
     const uint8_t *wrow = W + (int64_t)n * row_bytes;
-
-    v4i acc[TM];
+    bool r_ok;
+    const float rcp = srq_recip(in_scale, r_ok);
+    v4i acc[NACC];
 #pragma unroll
-    for (int t = 0; t < TM; ++t) acc[t] = v4i{0, 0, 0, 0};
+    for (int t = 0; t < NACC; ++t) acc[t] = v4i{0, 0, 0, 0};
+    const v4i ones = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};
 
-    const int8_t *arow[TM];
+    for (int kc0 = 0; kc0 < K; kc0 += KC) {
+        const int kcn = min(KC, K - kc0);
+        const int gpr = kcn >> 3;  // 8-code groups per row in this chunk
+        lds_barrier();  // the previous chunk's codes are no longer read
+        for (int q = tid; q < MT * gpr; q += 256) {
+            const int r = q / gpr, gi = q - r * gpr;
+            const int m = m0 + r;
+            int c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (m < M) {
+                const int64_t e = (int64_t)m * K + kc0 + gi * 8;
+                if (x_kind == G4_KIND_I8) {
+                    const uint2 v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const int8_t *>(x) + e);
 #pragma unroll
-    for (int t = 0; t < TM; ++t) arow[t] = A + (int64_t)min(m0 + t * 16 + j, M - 1) * kp;
-
-    constexpr int BATCH = 4;
-    for (int kb0 = wave; kb0 < ksteps; kb0 += 4 * BATCH) {
-        u32x4 bw[BATCH][BITS == 4 ? 1 : 2];
-        u32x4 av[BATCH][TM][2];
+                    for (int i = 0; i < 4; ++i) {
+                        c[i] = (int)(int8_t)((v.x >> (8 * i)) & 0xff);
+                        c[4 + i] = (int)(int8_t)((v.y >> (8 * i)) & 0xff);
+                    }
+                } else if (x_kind == G4_KIND_F16) {
+                    const u32x4 v = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const __half *>(x) + e);
+                    const uint32_t h[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int u = 0; u < BATCH; ++u) {
-            const int kb = kb0 + 4 * u;
-            if (kb < ksteps) {
-                if (BITS == 4) {
-                    bw[u][0] = *reinterpret_cast<const u32x4 *>(wrow + kb * 64 + g * 16);
+                    for (int i = 0; i < 4; ++i) {
+                        c[2 * i] = (int)srq_code_fast(
+                            __half2float(__ushort_as_half((unsigned short)(h[i] & 0xffff))), in_scale, rcp, r_ok);
+                        c[2 * i + 1] = (int)srq_code_fast(
+                            __half2float(__ushort_as_half((unsigned short)(h[i] >> 16))), in_scale, rcp, r_ok);
+                    }
                 } else {
-                    bw[u][0] = *reinterpret_cast<const u32x4 *>(wrow + kb * 128 + g * 32);
-                    bw[u][BITS == 4 ? 0 : 1] =
-                        *reinterpret_cast<const u32x4 *>(wrow + kb * 128 + g * 32 + 16);
-                }
+                    const float4 *p4 = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(x) + e);
+                    const float4 v0 = p4[0], v1 = p4[1];
+                    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
-                for (int t = 0; t < TM; ++t) {
-                    const u32x4 *ap = reinterpret_cast<const u32x4 *>(arow[t] + kb * 128 + g * 32);
-                    av[u][t][0] = ap[0];
-                    av[u][t][1] = ap[1];
+                    for (int i = 0; i < 8; ++i) c[i] = (int)srq_code_fast(v[i], in_scale, rcp, r_ok);
                 }
             }
+            uint2 packed;
+            if (BITS == 4) {
+                packed.x = pack4b(c[0], c[2], c[4], c[6]);
+                packed.y = pack4b(c[1], c[3], c[5], c[7]);
+            } else {
+                packed.x = pack4b(c[0], c[1], c[2], c[3]);
+                packed.y = pack4b(c[4], c[5], c[6], c[7]);
+            }
+            *reinterpret_cast<uint2 *>(&xs[r * XSTR + gi * 8]) = packed;
         }
+        lds_barrier();
+        const int ksteps = kcn / kTileBK;
+        const int kbase = kc0 / kTileBK;
+        for (int kb0 = wave; kb0 < ksteps; kb0 += 4 * BATCH) {
+            u32x4 bw[BATCH][BITS == 4 ? 1 : 2];
 #pragma unroll
-        for (int u = 0; u < BATCH; ++u) {
-            const int kb = kb0 + 4 * u;
-            if (kb < ksteps) {
+            for (int u = 0; u < BATCH; ++u) {
+                const int kb = min(kb0 + 4 * u, ksteps - 1);  // clamped: every load is valid
+                if (BITS == 4) {
+                    bw[u][0] = *reinterpret_cast<const u32x4 *>(wrow + (kbase + kb) * 64 + g * 16);
+                } else {
+                    bw[u][0] = *reinterpret_cast<const u32x4 *>(wrow + (kbase + kb) * 128 + g * 32);
+                    bw[u][BITS == 4 ? 0 : 1] =
+                        *reinterpret_cast<const u32x4 *>(wrow + (kbase + kb) * 128 + g * 32 + 16);
+                }
+            }
 #pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    v4i b;
-                    if (BITS == 4) {
-                        b = b_operand<4>(bw[u][0].x, bw[u][0].y, bw[u][0].z, bw[u][0].w, s);
-                    } else {
-                        b = __builtin_bit_cast(v4i, bw[u][BITS == 4 ? 0 : s]);
-                    }
+            for (int u = 0; u < BATCH; ++u) {
+                const int kb = kb0 + 4 * u;
+                if (kb < ksteps) {
 #pragma unroll
-                    for (int t = 0; t < TM; ++t) {
-                        const v4i a = __builtin_bit_cast(v4i, av[u][t][s]);
-                        acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[t], 0, 0, 0);
+                    for (int s = 0; s < 2; ++s) {
+                        v4i b;
+                        if (BITS == 4)
+                            b = b_operand<4>(bw[u][0].x, bw[u][0].y, bw[u][0].z, bw[u][0].w, s);
+                        else
+                            b = __builtin_bit_cast(v4i, bw[u][BITS == 4 ? 0 : s]);
+#pragma unroll
+                        for (int t = 0; t < TM; ++t) {
+                            const v4i a = *reinterpret_cast<const v4i *>(
+                                &xs[(t * 16 + j) * XSTR + kb * kTileBK + g * 32 + s * 16]);
+                            acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[t], 0, 0, 0);
+                            if (BITS == 4 && s == 0)  // each code counted once: both halves
+                                acc[TM + t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, ones, acc[TM + t], 0, 0, 0);
+                            if (BITS == 4 && s == 1)
+                                acc[TM + t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, ones, acc[TM + t], 0, 0, 0);
+                        }
                     }
                 }
             }
@@ -208,26 +257,43 @@ __global__ __launch_bounds__(256) void qgemm_skinny_kernel(
     // Fold the four waves' partial tiles through LDS, then wave 0 writes.
     if (wave > 0) {
 #pragma unroll
-        for (int t = 0; t < TM; ++t) red[wave - 1][t][lane] = acc[t];
+        for (int t = 0; t < NACC; ++t) red[wave - 1][t][lane] = acc[t];
     }
     __syncthreads();
     if (wave == 0) {
+        bool o_ok;
+        const float orcp = srq_recip(out_scale, o_ok);
+        const int nn = n0 + j;
+        if (nn < N) {
+            const float rs = __fmul_rn(in_scale, scales[nn]);
 #pragma unroll
-        for (int t = 0; t < TM; ++t) {
-            v4i a = acc[t];
+            for (int t = 0; t < TM; ++t) {
+                v4i a = acc[t];
+                v4i rsum = BITS == 4 ? acc[TM + t] : v4i{0, 0, 0, 0};
 #pragma unroll
-            for (int w = 0; w < 3; ++w) a += red[w][t][lane];
-            // D layout: lane l, register r -> row 4 * (l / 16) + r of A, column l % 16 of B.
-            const int nn = n0 + j;
-            if (nn < N) {
-                const float scale = scales[nn];
+                for (int w = 0; w < 3; ++w) {
+                    a += red[w][t][lane];
+                    if (BITS == 4) rsum += red[w][TM + t][lane];
+                }
+                // D layout: lane l, register r -> row 4 (l / 16) + r of A, column l % 16 of B.
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int m = m0 + t * 16 + 4 * g + r;
+                    const int lr = t * 16 + 4 * g + r;
+                    const int m = m0 + lr;
                     if (m < M) {
                         int v = a[r];
-                        if (BITS == 4) v -= 8 * row_sums[m];
-                        store_tile_out(dst, m, nn, N, out_kind, v, in_scale, scale, out_scale);
+                        if (BITS == 4) v -= 8 * rsum[r];  // the ones product: sum(xq) of row lr
+                        const float yv = __fmul_rn(rs, (float)v);
+                        const int64_t o = (int64_t)m * N + nn;
+                        if (out_kind == G4_KIND_I8) {
+                            reinterpret_cast<int8_t *>(dst)[o] = (int8_t)srq_code_fast(yv, out_scale, orcp, o_ok);
+                        } else if (out_kind == G4_KIND_I32) {
+                            reinterpret_cast<int32_t *>(dst)[o] = v;
+                        } else {
+                            float f = yv;
+                            if (out_scale != 0.0f) f = __fmul_rn(srq_code_fast(yv, out_scale, orcp, o_ok), out_scale);
+                            reinterpret_cast<float *>(dst)[o] = f;
+                        }
                     }
                 }
             }
@@ -462,8 +528,8 @@ static KernelChoice pick_kernel(int bits, int m, int n, int k, float in_scale) {
 static const char *choice_name(KernelChoice c, int bits) {
     switch (c) {
         case K_GEMV: return bits == 4 ? "qgemv-4bit" : "qgemv-8bit";
-        case K_SKINNY16: return bits == 4 ? "qgemm-4bit-mfma-skinny16" : "qmatmul-8bit-mfma-skinny16";
-        case K_SKINNY32: return bits == 4 ? "qgemm-4bit-mfma-skinny32" : "qmatmul-8bit-mfma-skinny32";
+        case K_SKINNY16: return bits == 4 ? "qgemm-4bit-mfma-small16" : "qmatmul-8bit-mfma-small16";
+        case K_SKINNY32: return bits == 4 ? "qgemm-4bit-mfma-small32" : "qmatmul-8bit-mfma-small32";
         case K_TILE128: return bits == 4 ? "qgemm-4bit-mfma-tile" : "qmatmul-8bit-mfma-tile";
         case K_GEMV_F32: return bits == 4 ? "qgemv-4bit-f32" : "qgemv-8bit-f32";
         default: return bits == 4 ? "qgemv-4bit-columns" : "qgemv-8bit-columns";
@@ -474,18 +540,6 @@ template <int BITS>
 static int launch_mfma(KernelChoice c, const int8_t *codes, const int *sums, const uint8_t *w,
                        const float *scales, void *dst, int m, int n, int k, int kp,
                        float in_scale, float out_scale, int out_kind, hipStream_t stream) {
-    if (c == K_SKINNY16 || c == K_SKINNY32) {
-        const int mt = c == K_SKINNY16 ? 16 : 32;
-        dim3 grid((n + 15) / 16, (m + mt - 1) / mt);
-        if (c == K_SKINNY16)
-            hipLaunchKernelGGL((qgemm_skinny_kernel<BITS, 16>), grid, dim3(256), 0, stream, codes,
-                               sums, w, scales, dst, m, n, k, kp, in_scale, out_scale, out_kind);
-        else
-            hipLaunchKernelGGL((qgemm_skinny_kernel<BITS, 32>), grid, dim3(256), 0, stream, codes,
-                               sums, w, scales, dst, m, n, k, kp, in_scale, out_scale, out_kind);
-        G4_LAUNCHED("qgemm_skinny_kernel");
-        return G4_OK;
-    }
     const int tiles_m = (m + kMfmaBM - 1) / kMfmaBM;
     const int tiles_n = (n + kMfmaBN - 1) / kMfmaBN;
     const int blocks = tiles_m * ((tiles_n + 7) / 8) * 8;  // XCD-aware order: whole groups of 8
@@ -529,6 +583,22 @@ static int run_linear(int bits, const void *wq, const float *scales, const void 
                             out_scale, stream, who);
     if (k > 16384)
         return set_error(G4_ERR_INVALID, "%s: K %d exceeds 16384 (the exact int32/f32 bound)", who, k);
+    if (c == K_SKINNY16 || c == K_SKINNY32) {
+        // One launch: the activation snap is fused into the small-M kernel.
+        const int mt = c == K_SKINNY16 ? 16 : 32;
+        dim3 grid((n + 15) / 16, (m + mt - 1) / mt);
+        const uint8_t *w = reinterpret_cast<const uint8_t *>(wq);
+#define G4_SMALL(B, T)                                                                           \
+    hipLaunchKernelGGL((qgemm_small_kernel<B, T>), grid, dim3(256), 0, stream, x, x_kind, w, scales, \
+                       dst, m, n, k, in_scale, out_scale, out_kind)
+        if (bits == 4 && mt == 16) G4_SMALL(4, 16);
+        else if (bits == 4) G4_SMALL(4, 32);
+        else if (mt == 16) G4_SMALL(8, 16);
+        else G4_SMALL(8, 32);
+#undef G4_SMALL
+        G4_LAUNCHED("qgemm_small_kernel");
+        return G4_OK;
+    }
     const int kp = k;  // k % 128 == 0 on the MFMA kernels
     const size_t code_bytes = (size_t)m * kp;
     const size_t sum_off = (code_bytes + 255) & ~(size_t)255;

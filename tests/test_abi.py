@@ -84,9 +84,9 @@ def test_kernel_choice_per_shape(g4):
     assert g4.kernel_for_shape(8, 1, 1536, 6144) == "qgemv-8bit-stream"
     assert g4.kernel_for_shape(4, 1, 16, 1280) == "qgemv-4bit"  # 40 chunks: no streaming class
     assert g4.kernel_for_shape(4, 2, 6144, 1536) == "qgemv-4bit"
-    assert g4.kernel_for_shape(4, 8, 6144, 1536) == "qgemm-4bit-mfma-skinny16"
+    assert g4.kernel_for_shape(4, 8, 6144, 1536) == "qgemm-4bit-mfma-small16"
     assert g4.kernel_for_shape(4, 512, 6144, 1536) == "qgemm-4bit-mfma-tile"
-    assert g4.kernel_for_shape(8, 4, 1536, 6144) == "qmatmul-8bit-mfma-skinny16"
+    assert g4.kernel_for_shape(8, 4, 1536, 6144) == "qmatmul-8bit-mfma-small16"
 
 
 class _Fake:
