@@ -265,6 +265,21 @@ def traffic_probe(plan, h):
     log(f"traffic probe done: copy {n} B x3, plan x5")
 
 
+def gemm_probe(h):
+    """Launches for rocprofv3 --kernel-trace --stats: the config-2 gate GEMM with f16 activations
+    (activation snap + tile kernel) 50 times at M=512 and 20 times at M=2048."""
+    n, k = syn.FFN, syn.HIDDEN
+    w = g4.DeviceBuffer.from_array(syn.int4_weights("c2", "gate", n, k))
+    s = g4.DeviceBuffer.from_array(syn.row_scales("c2", "gate", n))
+    for m, reps in ((512, 50), (2048, 20)):
+        x = g4.DeviceBuffer.from_array(syn.activations("c2", f"x{m}", m, k, outlier_frac=0.01))
+        d = g4.DeviceBuffer.empty((m, n), np.int8)
+        for _ in range(reps):
+            g4.qgemm(4, w, s, x, d, k, n, m, syn.IN_SCALE, syn.OUT_SCALE, stream=h)
+        g4.synchronize()
+        log(f"gemm probe M={m}: {reps} launches")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -273,6 +288,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true")
+    ap.add_argument("--gemm-probe", action="store_true",
+                    help="only the config-2 GEMM launches (M=512 and M=2048, f16 in), for rocprofv3")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this path is measured on one GPU; --gpus {args.gpus} is not supported "
@@ -284,6 +301,9 @@ def main():
     g4.lib().g4_set_device(0)
     stream = g4.Stream()
     h = stream.handle
+    if args.gemm_probe:
+        gemm_probe(h)
+        return
     log("building 35 layers of config-1 weights (623.6 MB)")
     layers = build_layers()
     items = [L[name] for L in layers for name, _, _ in syn.LAYER_PROJECTIONS]

@@ -2,23 +2,21 @@
 // qmatmul-8bit (src/kernels/pleMatmul.ts), plus the shape routing of src/execute.ts:372-430.
 //
 // Pipeline of one call (calibrated path):
-//  1. quantize_rows_kernel snaps x [M][K] once into int8 codes (the SRQ input prologue), written
-//     to a per-stream workspace with each 8-code group interleaved [x0 x2 x4 x6 x1 x3 x5 x7] for
-//     4-bit weights (so a weight word's low and high nibble lanes line up with the codes without
-//     a shuffle), and sum(xq) per row for the 4-bit zero point.
-//  2. An MFMA kernel contracts codes x weights with v_mfma_i32_16x16x64_i8. The 4-bit weights are
-//     unpacked to unsigned nibbles (w & 0x0F0F0F0F, (w >> 4) & 0x0F0F0F0F) and the zero point comes
-//     off once per output as -8 * sum(xq[m]). The int32 accumulators are exact, so the k order the
-//     MFMA uses internally is irrelevant; only the A and B operands have to agree on it, and they
-//     do because both are filled with the same (lane group, byte) -> k assignment.
+//  1. The activation snap (the SRQ input prologue) runs once per row: quantize_rows_kernel writes
+//     int8 codes to a per-stream workspace, each 8-code group interleaved [x0 x2 x4 x6 x1 x3 x5 x7]
+//     for 4-bit weights so a weight word's even and odd nibble lanes line up with the codes.
+//     (M <= 32 fuses the snap into its kernel instead.)
+//  2. An MFMA kernel contracts codes x weights with v_mfma_i32_16x16x64_i8 in exact int32. The
+//     int32 sums are exact, so the k order the MFMA uses internally is irrelevant; only the A and
+//     B operands have to agree on it, and they do by construction.
 //  3. The epilogue is the reference's f32(f32(inScale * scale[n]) * f32(acc)) and output snap.
 //
 // Kernels by M (chosen per shape, see pick_kernel):
 //   M <= 2         the GEMV family (qgemv.hip): bit-identical, cheaper than any tile at this M.
 //   3 <= M <= 32   qgemm_small_kernel: one launch with the snap fused (codes in LDS), 16 weight
 //                  rows per block, the 4 waves split K, an LDS fold of the 4 partials.
-//   M > 32         qgemm_mfma_kernel: 64 x 96 output tiles, activation codes straight to registers,
-//                  weights expanded to int8 in double-buffered LDS, XCD-aware tile order.
+//   M > 32         qgemm_tile_kernel: 64 x 96 output tiles, activation codes and weights streamed
+//                  global -> LDS by direct loads through a 3-4 stage ring, XCD-aware tile order.
 #include "g4_internal.h"
 
 #include <algorithm>
@@ -41,17 +39,13 @@ __device__ __forceinline__ uint32_t pack4b(int a, int b, int c, int d) {
            ((uint32_t)(d & 0xff) << 24);
 }
 
-// One block per token row: snap K activations into codes (interleaved when PERM), zero the pad to
-// kp, and write sum(codes) for the row.
+// One block per token row: snap K activations into codes (interleaved per 8-code group when PERM)
+// and zero the pad up to kp.
 template <bool PERM>
 __global__ __launch_bounds__(kQuantThreads) void quantize_rows_kernel(
-    const void *x, int x_kind, int k, int kp, float scale, int8_t *codes, int *row_sums) {
-    __shared__ int s_sum;
+    const void *x, int x_kind, int k, int kp, float scale, int8_t *codes) {
     const int m = blockIdx.x;
     const int tid = threadIdx.x;
-    if (tid == 0) s_sum = 0;
-    __syncthreads();
-    int local = 0;
     const int groups = kp >> 3;
     const int live = k >> 3;
     bool r_ok;
@@ -82,12 +76,7 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_rows_kernel(
             out.y = pack4b(c[4], c[5], c[6], c[7]);
         }
         *reinterpret_cast<uint2 *>(codes + (int64_t)m * kp + (int64_t)g * 8) = out;
-        local += c[0] + c[1] + c[2] + c[3] + c[4] + c[5] + c[6] + c[7];
     }
-    local = row16_sum_i32(local);
-    if ((tid & 15) == 0 && local != 0) atomicAdd(&s_sum, local);
-    __syncthreads();
-    if (tid == 0) row_sums[m] = s_sum;
 }
 
 // srqCodes as a kernel (quant.ts:309-334), natural order.
@@ -301,182 +290,311 @@ __global__ __launch_bounds__(256) void qgemm_small_kernel(
     }
 }
 
-// ---- tile: 64 x 96 outputs per block, K in 128-code stages ---------------------------------------
-// Block = 4 waves stacked along M; wave w owns rows m0 + 16 w .. +16 and all 96 columns (6 MFMA
-// column tiles). Two blocks share a CU (two waves per SIMD), so one wave's MFMAs cover the other's
-// LDS and barrier latency.
-//  A (activation codes) goes straight from global memory into registers: lane (j = lane % 16,
-//    g = lane / 16) loads bytes s * 64 + g * 16 .. +16 of its row for MFMA half-step s, so one
-//    load instruction covers 16 rows x 64 contiguous bytes. No LDS traffic for A.
-//  B (weights) is staged through double-buffered LDS once per block, expanded to int8 codes on the
-//    way (4-bit: nibbles into the activation interleave [k0 k2 k4 k6 k1 k3 k5 k7]; 8-bit: as is),
-//    so the inner loop is LDS reads plus MFMAs. Column stride 144 bytes keeps the 16-lane reads on
-//    distinct banks.
-//  Loads run D stages ahead through a register ring written out with compile-time slots, so the
-//  wait counts stay partial (a load behind a branch would drain them).
-// The integer sums are exact; A and B agree on the k assignment inside every MFMA, so the order
-// the matrix core sums in does not matter.
-constexpr int kMfmaBN = 96;
-constexpr int kMfmaBM = 64;
+// ---- tile: 64 x 96 outputs per block, both operands streamed through an LDS ring ---------------
+// Each K stage is 128 codes. Stage st of the tile is
+//   A: 64 rows x 128 bytes of activation codes (8 KB),
+//   B: 96 columns x 64 bytes of packed int4 weights (6 KB), or 96 x 128 bytes of int8 weights.
+// Both go global -> LDS by direct loads (global_load_lds_dwordx4: no VGPRs, no ds_write), NS stages
+// deep. Four waves in a 2 x 2 layout own 32 x 48 outputs each (2 x 3 MFMA tiles of 16 x 16).
+// Per stage a wave waits for its own loads of stage st+1, joins the block barrier, reads the
+// operands of stage st+1 into registers (so their LDS latency hides under the MFMAs), refills the
+// buffer stage st-1 used with stage st+NS-1, and runs stage st's 12 v_mfma_i32_16x16x64_i8.
+// Every wave issues the same number of loads per stage (the weight remainder re-loads a chunk
+// another wave also loads, to the same LDS bytes): with a per-wave count the compiler splits the
+// loop into branches and then drains the LDS reads before each stage's first MFMA.
+//
+// Operand layouts (the k assignment inside an MFMA is free as long as A and B agree, because the
+// int32 sums are exact):
+//   lane (j = lane % 16, g = lane / 16), half-step s takes codes 32 g + 16 s .. +16 of the stage.
+//   A is the per-8 interleaved code row [x0 x2 x4 x6 x1 x3 x5 x7] (4-bit) or natural (8-bit).
+//   4-bit B: a lane's 16 bytes of column j are codes 32 g .. 32 g + 31; with w' = w ^ 0x88888888,
+//   (w' << 4) & 0xF0F0F0F0 holds 16 * (even codes) and w' & 0xF0F0F0F0 16 * (odd codes) as signed
+//   bytes, so the accumulator is 16 * sum(code * x), exact (|sum| <= 2^31 / 16 for K <= 16384),
+//   and no zero-point sums are needed.
+// LDS rows are XOR-swizzled so that any 16 consecutive lanes of a b128 read (and any 8) hit
+// distinct banks: A row r (128 B) keeps chunk c at position c ^ ((r & 7) ^ ((r >> 3) & 1)); 4-bit B
+// column c (64 B) keeps chunk g at g ^ (((c >> 1) ^ (c >> 3)) & 3).
+constexpr int kTileBM = 64;
+constexpr int kTileBN = 96;
+constexpr int kTileEpiStride = kTileBN + 4;  // int32 words per staged output row (bank spread)
 
-template <int BITS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void qgemm_mfma_kernel(
-    const int8_t *__restrict__ A, const int *__restrict__ row_sums, const uint8_t *__restrict__ W,
-    const float *__restrict__ scales, void *dst, int M, int N, int K, int kp, float in_scale,
-    float out_scale, int out_kind, int tiles_m, int tiles_n) {
-    constexpr int BN = kMfmaBN, TN = BN / 16, D = 2;
+// 16 bytes per lane from global memory into LDS at lds + 16 * lane. Issued through asm: when the
+// compiler sees an LDS DMA it waits for every outstanding load (vmcnt(0)) before the next LDS
+// read, which would empty the ring at every stage; here the waits are explicit (tile_wait). M0
+// carries the wave-uniform LDS address; nothing else in these kernels uses M0.
+__device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(src) : "memory", "m0");
+}
+
+// At most N of this wave's vector-memory operations still in flight (its loads of the awaited
+// stage have landed), its LDS reads drained, then the block barrier: afterwards every wave's data
+// for that stage is in LDS and every wave has finished reading the buffer the next refill
+// overwrites. The LDS drain is the builtin so the compiler's own wait bookkeeping sees it.
+template <int N> __device__ __forceinline__ void tile_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt and expcnt unconstrained
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int DPS> __device__ __forceinline__ void tile_wait_stages(int later) {
+    switch (later) {
+        case 0: tile_wait<0>(); break;
+        case 1: tile_wait<1 * DPS>(); break;
+        case 2: tile_wait<2 * DPS>(); break;
+        case 3: tile_wait<3 * DPS>(); break;
+        default: tile_wait<0>(); break;
+    }
+}
+
+__device__ __forceinline__ uint32_t nib_even16(uint32_t w) { return ((w ^ 0x88888888u) << 4) & 0xF0F0F0F0u; }
+__device__ __forceinline__ uint32_t nib_odd16(uint32_t w) { return (w ^ 0x88888888u) & 0xF0F0F0F0u; }
+
+template <int BITS, int NS>
+__global__ __launch_bounds__(256) void qgemm_tile_kernel(
+    const int8_t *__restrict__ A, const uint8_t *__restrict__ W, const float *__restrict__ scales,
+    void *dst, int M, int N, int K, float in_scale, float out_scale, int out_kind, int tiles_m,
+    int tiles_n) {
+    constexpr int BM = kTileBM, BN = kTileBN, TM = 2, TN = 3;
     constexpr int BROW = BITS == 4 ? 64 : 128;  // weight bytes of one column per stage
-    constexpr int BSTR = 144;                   // LDS bytes per column: 128 codes + 16 pad
-    constexpr int B_CHUNKS = BN * BROW / 16;
-    constexpr int B_CH = (B_CHUNKS + 255) / 256;
-    constexpr int CPC = BROW / 16;              // 16-byte weight chunks per column per stage
-    __shared__ __align__(16) uint8_t sB[2][BN * BSTR];
+    constexpr int A_BYTES = BM * 128, B_BYTES = BN * BROW, SB = A_BYTES + B_BYTES;
+    constexpr int A_PW = A_BYTES / 1024 / 4;                   // loads per wave per stage
+    constexpr int B_INS = B_BYTES / 1024, B_PW = (B_INS + 3) / 4;
+    constexpr int DPS = A_PW + B_PW;
+    constexpr int ESTR = kTileEpiStride;
+    static_assert(NS >= 3 && NS <= 5, "ring depth");
+    static_assert(NS * SB >= BM * ESTR * 4 + BN * 4, "the epilogue staging fits the ring");
+    __shared__ __align__(1024) uint8_t smem[NS * SB];
 
+    // Blocks go to the 8 XCDs round robin; one XCD gets every M tile of a run of N tiles, so its L2
+    // fetches those weight columns once.
     const int b = blockIdx.x;
-    // Blocks are dealt to the 8 XCDs round robin: give one XCD every M tile of a run of N tiles,
-    // so its L2 fetches those weight columns once.
     const int xcd = b & 7, idx = b >> 3;
     const int tm = idx % tiles_m;
     const int tn = (idx / tiles_m) * 8 + xcd;
-    if (tn >= tiles_n) return;
-    const int m0 = tm * kMfmaBM, n0 = tn * BN;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tn >= tiles_n) return;  // whole block, before any barrier
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 15, g = lane >> 4;
-    const int ksteps = K / 128;
-    const int row_bytes = BITS == 4 ? K / 2 : K;
-    const int8_t *arow = A + (int64_t)min(m0 + wave * 16 + j, M - 1) * kp + g * 16;
-    const uint8_t *bsrc[B_CH];
-    int bdst[B_CH];
+    const int wm = wave >> 1, wn = wave & 1;
+    const int row_bytes = BITS == 4 ? K >> 1 : K;
+    const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+
+    // Direct-load sources. A load q covers tile rows 8 q .. 8 q + 7; lane i fills row 8 q + i / 8,
+    // position i % 8, with the chunk the swizzle puts there. Rows and columns past the matrix are
+    // clamped to the last one (their products land in outputs that are not stored).
+    const int8_t *asrc[A_PW];
+    uint32_t adst[A_PW];
 #pragma unroll
-    for (int i = 0; i < B_CH; ++i) {
-        const int q = min(tid + 256 * i, B_CHUNKS - 1);
-        const int col = q / CPC, c = q % CPC;
-        bsrc[i] = W + (int64_t)min(n0 + col, N - 1) * row_bytes + c * 16;
-        bdst[i] = col * BSTR + c * (BITS == 4 ? 32 : 16);
+    for (int i = 0; i < A_PW; ++i) {
+        const int q = wave + 4 * i;
+        const int r = 8 * q + (lane >> 3);
+        const int c = (lane & 7) ^ (((lane >> 3) & 7) ^ (q & 1));
+        asrc[i] = A + (int64_t)min(m0 + r, M - 1) * K + 16 * c;
+        adst[i] = q * 1024;
     }
-    // The epilogue's per-row zero-point sums and per-column scales, requested before the K loop so
-    // their latency is not added after it.
-    int rsum[4];
+    const uint8_t *bsrc[B_PW];
+    uint32_t bdst[B_PW];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-        rsum[r] = BITS == 4 ? 8 * row_sums[min(m0 + wave * 16 + 4 * g + r, M - 1)] : 0;
-    float col_scale[TN];
+    for (int i = 0; i < B_PW; ++i) {
+        const int q = min(wave + 4 * i, B_INS - 1);
+        int col, c;
+        if (BITS == 4) {  // load q: columns 16 q .. +15, 4 chunks each
+            const int cl = lane >> 2;
+            col = 16 * q + cl;
+            c = (lane & 3) ^ (((cl >> 1) ^ (cl >> 3)) & 3);
+        } else {  // load q: columns 8 q .. +7, 8 chunks each (the A swizzle)
+            col = 8 * q + (lane >> 3);
+            c = (lane & 7) ^ (((lane >> 3) & 7) ^ (q & 1));
+        }
+        bsrc[i] = W + (int64_t)min(n0 + col, N - 1) * row_bytes + 16 * c;
+        bdst[i] = A_BYTES + q * 1024;
+    }
+    auto issue = [&](int st, int buf) {
+        const uint32_t base = sbase + buf * SB;
 #pragma unroll
-    for (int y = 0; y < TN; ++y) col_scale[y] = __fmul_rn(in_scale, scales[min(n0 + y * 16 + j, N - 1)]);
-    v4i acc[TN];
+        for (int i = 0; i < A_PW; ++i) lds_dma16(asrc[i] + st * 128, base + adst[i]);
 #pragma unroll
-    for (int y = 0; y < TN; ++y) acc[y] = v4i{0, 0, 0, 0};
-    u32x4 ra[D][2];
-    u32x4 rb[D][B_CH];
-    auto load = [&](u32x4 (&xa)[2], u32x4 (&xb)[B_CH], int st) {
-        const int s_ = min(st, ksteps - 1);  // past the end: re-read the last stage, unguarded
-        xa[0] = *reinterpret_cast<const u32x4 *>(arow + s_ * 128);
-        xa[1] = *reinterpret_cast<const u32x4 *>(arow + s_ * 128 + 64);
-#pragma unroll
-        for (int i = 0; i < B_CH; ++i) xb[i] = *reinterpret_cast<const u32x4 *>(bsrc[i] + s_ * BROW);
+        for (int i = 0; i < B_PW; ++i) lds_dma16(bsrc[i] + st * BROW, base + bdst[i]);
     };
-    // Threads past the last chunk hold a copy of it (clamped index) and store it to the same place.
-    auto store_b = [&](const u32x4 (&xb)[B_CH], int buf) {
+    // LDS byte offsets of this lane's operands inside a stage buffer.
+    const int sig = (j & 7) ^ ((j >> 3) & 1);
+    uint32_t aoff[2], boff[2];
 #pragma unroll
-        for (int i = 0; i < B_CH; ++i) {
-            const u32x4 w = xb[i];
+    for (int s = 0; s < 2; ++s) {
+        aoff[s] = (wm * 32 / 8 + (j >> 3)) * 1024 + (j & 7) * 128 + 16 * ((2 * g + s) ^ sig);
+        boff[s] = A_BYTES + (wn * 48 / 8 + (j >> 3)) * 1024 + (j & 7) * 128 + 16 * ((2 * g + s) ^ sig);
+    }
+    const uint32_t boff4 = A_BYTES + (wn * 48 + j) * 64 + 16 * (g ^ (((j >> 1) ^ (j >> 3)) & 3));
+
+    v4i acc[TM][TN];
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int u = 0; u < TN; ++u) acc[t][u] = v4i{0, 0, 0, 0};
+    constexpr int BR = BITS == 4 ? 1 : 2;  // b128 weight reads per column tile per stage
+    v4i ra[2][TM][2];
+    u32x4 rb[2][TN][BR];
+    auto read_ops = [&](int buf, v4i (&a)[TM][2], u32x4 (&bw)[TN][BR]) {
+        const uint8_t *sa = smem + buf * SB;
+#pragma unroll
+        for (int t = 0; t < TM; ++t)
+#pragma unroll
+            for (int s = 0; s < 2; ++s) a[t][s] = *reinterpret_cast<const v4i *>(sa + aoff[s] + t * 2048);
+#pragma unroll
+        for (int u = 0; u < TN; ++u) {
             if (BITS == 4) {
-                const u32x4 e0{w.x & 0x0F0F0F0Fu, (w.x >> 4) & 0x0F0F0F0Fu, w.y & 0x0F0F0F0Fu,
-                               (w.y >> 4) & 0x0F0F0F0Fu};
-                const u32x4 e1{w.z & 0x0F0F0F0Fu, (w.z >> 4) & 0x0F0F0F0Fu, w.w & 0x0F0F0F0Fu,
-                               (w.w >> 4) & 0x0F0F0F0Fu};
-                *reinterpret_cast<u32x4 *>(&sB[buf][bdst[i]]) = e0;
-                *reinterpret_cast<u32x4 *>(&sB[buf][bdst[i] + 16]) = e1;
+                bw[u][0] = *reinterpret_cast<const u32x4 *>(sa + boff4 + u * 1024);
             } else {
-                *reinterpret_cast<u32x4 *>(&sB[buf][bdst[i]]) = w;
+#pragma unroll
+                for (int s = 0; s < BR; ++s) bw[u][s] = *reinterpret_cast<const u32x4 *>(sa + boff[s] + u * 2048);
             }
         }
     };
+    auto compute = [&](const v4i (&a)[TM][2], const u32x4 (&bw)[TN][BR]) {
+        v4i bo[2][TN];
 #pragma unroll
-    for (int i = 0; i < D; ++i) load(ra[i], rb[i], i);
-    store_b(rb[0], 0);
-    lds_barrier();
-    // Stage st consumes ring slot st % D and refills it with stage st + D. Whole groups of D stages
-    // run unguarded (a branch around the loads would make the wait counts drain at the loop head);
-    // a final odd stage is peeled.
-    auto stage = [&](u32x4 (&xa)[2], u32x4 (&xb)[B_CH], const u32x4 (&xb_next)[B_CH], int st) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            v4i bo[TN];
-#pragma unroll
-            for (int y = 0; y < TN; ++y)
-                bo[y] = *reinterpret_cast<const v4i *>(
-                    &sB[st & 1][(y * 16 + j) * BSTR + (s * 4 + g) * 16]);
-#pragma unroll
-            for (int y = 0; y < TN; ++y)
-                acc[y] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, xa[s]), bo[y],
-                                                               acc[y], 0, 0, 0);
+        for (int u = 0; u < TN; ++u) {
+            if (BITS == 4) {
+                const u32x4 w = bw[u][0];
+                bo[0][u] = v4i{(int)nib_even16(w.x), (int)nib_odd16(w.x), (int)nib_even16(w.y), (int)nib_odd16(w.y)};
+                bo[1][u] = v4i{(int)nib_even16(w.z), (int)nib_odd16(w.z), (int)nib_even16(w.w), (int)nib_odd16(w.w)};
+            } else {
+                bo[0][u] = __builtin_bit_cast(v4i, bw[u][0]);
+                bo[1][u] = __builtin_bit_cast(v4i, bw[u][BR - 1]);
+            }
         }
-        store_b(xb_next, (st + 1) & 1);
-        load(xa, xb, st + D);
-        lds_barrier();
+        // all six accumulators of one half-step before the next: consecutive MFMAs are independent
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int u = 0; u < TN; ++u)
+#pragma unroll
+                for (int t = 0; t < TM; ++t)
+                    acc[t][u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t][s], bo[s][u], acc[t][u], 0, 0, 0);
     };
-    static_assert(D == 2, "the ring below is written out for two slots");
-    int st = 0;
-    for (; st + 2 <= ksteps; st += 2) {
-        stage(ra[0], rb[0], rb[1], st);
-        stage(ra[1], rb[1], rb[0], st + 1);
+
+    // nk >= NS - 1 (the host picks NS). Stages 0 .. NS-2 in flight, then stage 0's operands.
+    const int nk = K >> 7;
+#pragma unroll
+    for (int st = 0; st < NS - 1; ++st) issue(st, st);
+    tile_wait_stages<DPS>(NS - 2);
+    read_ops(0, ra[0], rb[0]);
+    // Stage st: stage st+1 landed; read its operands, refill the buffer of stage st-1 with stage
+    // st+NS-1, then stage st's MFMAs. Pairs of stages keep the register double buffer static.
+    int s0 = 0;
+    for (; s0 + NS + 1 <= nk; s0 += 2) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int st = s0 + h;
+            tile_wait_stages<DPS>(NS - 3);  // stages issued after st+1: st+2 .. st+NS-2
+            read_ops((st + 1) % NS, ra[h ^ 1], rb[h ^ 1]);
+            issue(st + NS - 1, (st + NS - 1) % NS);
+            __builtin_amdgcn_sched_barrier(0);  // operand reads and loads go out before the MFMAs
+            compute(ra[h], rb[h]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
-    if (st < ksteps) stage(ra[0], rb[0], rb[1], st);
-    // D layout of a 16 x 16 MFMA tile: lane l, register r -> row 4 (l / 16) + r, column l % 16.
-    // The outputs go through LDS so each row of the tile leaves as whole 16-byte stores (scattered
-    // byte stores of 16-byte runs cost more than the contraction). Edge tiles and rows whose start
-    // is not 16-byte aligned keep per-element stores.
+    // The remaining stages (nothing or fewer loads left to issue), also in register pairs.
+    for (; s0 < nk; s0 += 2) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int st = s0 + h;
+            if (st >= nk) break;
+            if (st + 1 < nk) {
+                const int last = min(nk - 1, st + NS - 2);  // the last stage issued so far
+                tile_wait_stages<DPS>(last - (st + 1));
+                read_ops((st + 1) % NS, ra[h ^ 1], rb[h ^ 1]);
+                if (st + NS - 1 < nk) issue(st + NS - 1, (st + NS - 1) % NS);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            compute(ra[h], rb[h]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // Epilogue. The int32 sums go to LDS (rows of ESTR words), then each thread takes runs of 8
+    // columns of one row: one column-scale multiply, the snap, and one store per run.
+    tile_wait<0>();  // every wave is done with the ring
+    int32_t *sacc = reinterpret_cast<int32_t *>(smem);
+    float *sscale = reinterpret_cast<float *>(smem + BM * ESTR * 4);
+    if (tid < BN) sscale[tid] = __fmul_rn(in_scale, scales[min(n0 + tid, N - 1)]);
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int u = 0; u < TN; ++u)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)  // D layout: lane l, register r -> row 4 (l / 16) + r, column l % 16
+                sacc[(wm * 32 + t * 16 + 4 * g + r) * ESTR + wn * 48 + u * 16 + j] =
+                    BITS == 4 ? acc[t][u][r] >> 4 : acc[t][u][r];
+    __syncthreads();
     bool r_ok;
     const float rcp = srq_recip(out_scale, r_ok);
-    const int esz = out_kind == G4_KIND_I8 ? 1 : 4;
-    const bool full = m0 + kMfmaBM <= M && n0 + BN <= N && ((int64_t)N * esz) % 16 == 0;
-    lds_barrier();  // every wave is done reading the last stage's weights
-    uint8_t *stile = &sB[0][0];  // 64 x 96 outputs: 6 KB (int8) or 24 KB (f32 / int32) of LDS
-    static_assert(2 * BN * BSTR >= kMfmaBM * BN * 4, "the output tile fits the weight buffers");
+    constexpr int RC = BN / 8;
+    for (int q = tid; q < BM * RC; q += 256) {
+        const int lr = q / RC, c = q - lr * RC;
+        const int m = m0 + lr, n = n0 + c * 8;
+        if (m >= M || n >= N) continue;
+        const v4i x0 = *reinterpret_cast<const v4i *>(sacc + lr * ESTR + c * 8);
+        const v4i x1 = *reinterpret_cast<const v4i *>(sacc + lr * ESTR + c * 8 + 4);
+        const int v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const int live = min(8, N - n);
+        const int64_t o = (int64_t)m * N + n;
+        if (out_kind == G4_KIND_I32) {
+            int32_t *d = reinterpret_cast<int32_t *>(dst) + o;
+            if (live == 8 && (o & 3) == 0) {
+                reinterpret_cast<v4i *>(d)[0] = x0;
+                reinterpret_cast<v4i *>(d)[1] = x1;
+            } else {
+                for (int e = 0; e < live; ++e) d[e] = v[e];
+            }
+            continue;
+        }
+        float y[8], code[8];
+        bool near = !r_ok;
 #pragma unroll
-    for (int y = 0; y < TN; ++y) {
-        const int n = n0 + y * 16 + j;
-        const float rs = col_scale[y];
+        for (int e = 0; e < 8; ++e) {
+            y[e] = __fmul_rn(sscale[c * 8 + e], (float)v[e]);  // the reference's epilogue order
+            const float t = __fmul_rn(y[e], rcp);
+            code[e] = rintf(t);
+            // |fl(y * fl(1/s)) - fl(y / s)| < 2^-13 while |y / s| <= 256 (beyond, both clamp), so a
+            // quotient farther than that from a half integer rounds to the same code either way.
+            near |= fabsf(t - code[e]) >= 0.5f - 0x1p-13f;
+        }
+        if (near) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int lr = wave * 16 + 4 * g + r;
-            const int m = m0 + lr;
-            const int v = acc[y][r] - rsum[r];
-            const float yv = __fmul_rn(rs, (float)v);
-            if (full) {
-                const int o = lr * BN + y * 16 + j;
-                if (out_kind == G4_KIND_I8) {
-                    stile[o] = (uint8_t)(int8_t)srq_code_fast(yv, out_scale, rcp, r_ok);
-                } else if (out_kind == G4_KIND_I32) {
-                    reinterpret_cast<int32_t *>(stile)[o] = v;
-                } else {
-                    float f = yv;
-                    if (out_scale != 0.0f) f = __fmul_rn(srq_code_fast(yv, out_scale, rcp, r_ok), out_scale);
-                    reinterpret_cast<float *>(stile)[o] = f;
-                }
-            } else if (m < M && n < N) {
-                const int64_t o = (int64_t)m * N + n;
-                if (out_kind == G4_KIND_I8) {
-                    reinterpret_cast<int8_t *>(dst)[o] = (int8_t)srq_code_fast(yv, out_scale, rcp, r_ok);
-                } else if (out_kind == G4_KIND_I32) {
-                    reinterpret_cast<int32_t *>(dst)[o] = v;
-                } else {
-                    float f = yv;
-                    if (out_scale != 0.0f) f = __fmul_rn(srq_code_fast(yv, out_scale, rcp, r_ok), out_scale);
-                    reinterpret_cast<float *>(dst)[o] = f;
-                }
+            for (int e = 0; e < 8; ++e) code[e] = rintf(__fdiv_rn(y[e], out_scale));
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) code[e] = fminf(fmaxf(code[e], -128.0f), 127.0f);
+        if (out_kind == G4_KIND_I8) {
+            uint32_t p0 = 0, p1 = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                p0 |= ((uint32_t)(int)code[e] & 0xffu) << (8 * e);
+                p1 |= ((uint32_t)(int)code[e + 4] & 0xffu) << (8 * e);
+            }
+            int8_t *d = reinterpret_cast<int8_t *>(dst) + o;
+            if (live == 8 && (o & 7) == 0) {
+                *reinterpret_cast<uint2 *>(d) = make_uint2(p0, p1);
+            } else {
+                for (int e = 0; e < live; ++e) d[e] = (int8_t)(int)code[e];
+            }
+        } else {  // f32: q * outScale, or y itself when outScale is 0 (no output snap)
+            float f[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = out_scale != 0.0f ? __fmul_rn(code[e], out_scale) : y[e];
+            float *d = reinterpret_cast<float *>(dst) + o;
+            if (live == 8 && (o & 3) == 0) {
+                reinterpret_cast<float4 *>(d)[0] = make_float4(f[0], f[1], f[2], f[3]);
+                reinterpret_cast<float4 *>(d)[1] = make_float4(f[4], f[5], f[6], f[7]);
+            } else {
+                for (int e = 0; e < live; ++e) d[e] = f[e];
             }
         }
-    }
-    if (!full) return;  // uniform
-    lds_barrier();
-    const int row_chunks = BN * esz / 16;  // 6 (int8) or 24 (f32 / int32)
-    for (int q = tid; q < kMfmaBM * row_chunks; q += 256) {
-        const int lr = q / row_chunks, c = q - lr * row_chunks;
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(stile + lr * BN * esz + c * 16);
-        *reinterpret_cast<u32x4 *>(reinterpret_cast<uint8_t *>(dst) +
-                                   ((int64_t)(m0 + lr) * N + n0) * esz + c * 16) = v;
     }
 }
 
@@ -520,7 +638,7 @@ static KernelChoice pick_kernel(int bits, int m, int n, int k, float in_scale) {
     if (m <= 2) return K_GEMV;
     if (k % kTileBK != 0) return K_GEMV_COLS;
     if (m <= 16) return K_SKINNY16;
-    if (m <= 32) return K_SKINNY32;
+    if (m <= 32 || k < 2 * kTileBK) return K_SKINNY32;  // the tile ring needs two K stages
     (void)bits;
     return K_TILE128;
 }
@@ -537,15 +655,20 @@ static const char *choice_name(KernelChoice c, int bits) {
 }
 
 template <int BITS>
-static int launch_mfma(KernelChoice c, const int8_t *codes, const int *sums, const uint8_t *w,
-                       const float *scales, void *dst, int m, int n, int k, int kp,
-                       float in_scale, float out_scale, int out_kind, hipStream_t stream) {
-    const int tiles_m = (m + kMfmaBM - 1) / kMfmaBM;
-    const int tiles_n = (n + kMfmaBN - 1) / kMfmaBN;
+static int launch_tile(const int8_t *codes, const uint8_t *w, const float *scales, void *dst, int m,
+                       int n, int k, float in_scale, float out_scale, int out_kind,
+                       hipStream_t stream) {
+    const int tiles_m = (m + kTileBM - 1) / kTileBM;
+    const int tiles_n = (n + kTileBN - 1) / kTileBN;
     const int blocks = tiles_m * ((tiles_n + 7) / 8) * 8;  // XCD-aware order: whole groups of 8
-    hipLaunchKernelGGL((qgemm_mfma_kernel<BITS>), dim3(blocks), dim3(256), 0, stream, codes, sums,
-                       w, scales, dst, m, n, k, kp, in_scale, out_scale, out_kind, tiles_m, tiles_n);
-    G4_LAUNCHED("qgemm_mfma_kernel");
+    const int nk = k / kTileBK;  // >= 2 (k % 128 == 0 and k >= 256 here)
+    if (nk >= 3)
+        hipLaunchKernelGGL((qgemm_tile_kernel<BITS, 4>), dim3(blocks), dim3(256), 0, stream, codes,
+                           w, scales, dst, m, n, k, in_scale, out_scale, out_kind, tiles_m, tiles_n);
+    else
+        hipLaunchKernelGGL((qgemm_tile_kernel<BITS, 3>), dim3(blocks), dim3(256), 0, stream, codes,
+                           w, scales, dst, m, n, k, in_scale, out_scale, out_kind, tiles_m, tiles_n);
+    G4_LAUNCHED("qgemm_tile_kernel");
     return G4_OK;
 }
 
@@ -600,26 +723,21 @@ static int run_linear(int bits, const void *wq, const float *scales, const void 
         return G4_OK;
     }
     const int kp = k;  // k % 128 == 0 on the MFMA kernels
-    const size_t code_bytes = (size_t)m * kp;
-    const size_t sum_off = (code_bytes + 255) & ~(size_t)255;
     void *ws = nullptr;
-    int rc = workspace(stream, sum_off + (size_t)m * sizeof(int), &ws);
+    int rc = workspace(stream, (size_t)m * kp, &ws);
     if (rc) return rc;
     int8_t *codes = reinterpret_cast<int8_t *>(ws);
-    int *sums = reinterpret_cast<int *>(reinterpret_cast<uint8_t *>(ws) + sum_off);
     if (bits == 4)
         hipLaunchKernelGGL(quantize_rows_kernel<true>, dim3(m), dim3(kQuantThreads), 0, stream, x,
-                           x_kind, k, kp, in_scale, codes, sums);
+                           x_kind, k, kp, in_scale, codes);
     else
         hipLaunchKernelGGL(quantize_rows_kernel<false>, dim3(m), dim3(kQuantThreads), 0, stream, x,
-                           x_kind, k, kp, in_scale, codes, sums);
+                           x_kind, k, kp, in_scale, codes);
     G4_LAUNCHED("quantize_rows_kernel");
     const uint8_t *w = reinterpret_cast<const uint8_t *>(wq);
     if (bits == 4)
-        return launch_mfma<4>(c, codes, sums, w, scales, dst, m, n, k, kp, in_scale, out_scale,
-                              out_kind, stream);
-    return launch_mfma<8>(c, codes, sums, w, scales, dst, m, n, k, kp, in_scale, out_scale,
-                          out_kind, stream);
+        return launch_tile<4>(codes, w, scales, dst, m, n, k, in_scale, out_scale, out_kind, stream);
+    return launch_tile<8>(codes, w, scales, dst, m, n, k, in_scale, out_scale, out_kind, stream);
 }
 
 }  // namespace g4

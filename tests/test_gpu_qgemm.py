@@ -126,3 +126,54 @@ def test_uncalibrated_gemm_grid_exact(gpu, oracle):
     of = out_buf(gpu, (5, 64), np.float32)
     gpu.qgemm(4, dev(gpu, w), dev(gpu, s), dev(gpu, x), of, 512, 64, 5, 0.0, 0.0625)
     assert f32_equal(of.download(), want)
+
+
+@pytest.mark.parametrize("out_kind", ["f32", "i8", "i32"])
+def test_tile_epilogue_kinds_m96(gpu, oracle, gate, out_kind):
+    # The tile kernel's epilogue for every output kind, over a ragged last M tile (96 = 64 + 32)
+    # and every column of the gate shape.
+    n, k, w, s, wb, sb = gate
+    m = 96
+    x = syn.activations("c2", "epi96", m, k, outlier_frac=0.01)
+    want, acc, codes = oracle.qgemm(4, w, s, x.astype(np.float32), n, k, m, syn.IN_SCALE,
+                                    syn.OUT_SCALE)
+    dt = {"f32": np.float32, "i8": np.int8, "i32": np.int32}[out_kind]
+    o = out_buf(gpu, (m, n), dt)
+    gpu.qgemm(4, wb, sb, dev(gpu, x), o, k, n, m, syn.IN_SCALE, syn.OUT_SCALE)
+    got = o.download()
+    if out_kind == "f32":
+        assert f32_equal(got, want)
+    elif out_kind == "i8":
+        assert np.array_equal(got, codes)
+    else:
+        assert np.array_equal(got, acc)
+
+
+def test_tile_int8_codes_in(gpu, oracle, gate):
+    # Activation codes already snapped (x_kind int8) through the tile path equal the f16 path.
+    n, k, w, s, wb, sb = gate
+    m = 200
+    x = syn.activations("c2", "codes200", m, k, outlier_frac=0.01)
+    _, _, codes = oracle.qgemm(4, w, s, x.astype(np.float32), n, k, m, syn.IN_SCALE, syn.OUT_SCALE)
+    xq = np.clip(np.rint(x.astype(np.float32) / np.float32(syn.IN_SCALE)), -128, 127).astype(np.int8)
+    o8 = out_buf(gpu, (m, n), np.int8)
+    gpu.qgemm(4, wb, sb, dev(gpu, xq), o8, k, n, m, syn.IN_SCALE, syn.OUT_SCALE)
+    assert np.array_equal(o8.download(), codes)
+
+
+@pytest.mark.parametrize("bits,m,n,k", [(4, 100, 333, 256), (8, 70, 1001, 128), (8, 65, 77, 384)])
+def test_short_k_and_odd_n(gpu, oracle, bits, m, n, k):
+    # K of one or two 128-code stages (routed to the small-M kernel or the 3-stage ring) and
+    # column counts that are not a multiple of the 8-wide output runs.
+    w = syn.weights("shortk", f"{bits}-{m}x{n}x{k}", n, k, bits)
+    s = syn.row_scales("shortk", f"{bits}-{m}x{n}x{k}", n)
+    x = syn.activations("shortk", f"{bits}-{m}x{n}x{k}", m, k)
+    print(f"short k bits={bits} m={m} n={n} k={k} kernel={gpu.kernel_for_shape(bits, m, n, k)}",
+          flush=True)
+    _, acc, codes = oracle.qgemm(bits, w, s, x.astype(np.float32), n, k, m, 0.05, 0.1)
+    o8 = out_buf(gpu, (m, n), np.int8)
+    gpu.qgemm(bits, dev(gpu, w), dev(gpu, s), dev(gpu, x), o8, k, n, m, 0.05, 0.1)
+    assert np.array_equal(o8.download(), codes)
+    o32 = out_buf(gpu, (m, n), np.int32)
+    gpu.qgemm(bits, dev(gpu, w), dev(gpu, s), dev(gpu, x), o32, k, n, m, 0.05, 0.1)
+    assert np.array_equal(o32.download(), acc)
