@@ -265,6 +265,82 @@ def traffic_probe(plan, h):
     log(f"traffic probe done: copy {n} B x3, plan x5")
 
 
+def decode_step_bytes(shape, pos):
+    """Algorithmic HBM bytes of one E2B-shape decode step at `pos` for `batch` rows: every weight
+    byte and row scale the step reads once (35 layers of q/k/v/o/gate/up/down int4 and the int8
+    per-layer gate and projection, the per-layer model projection, the tied head), plus per row
+    the KV each layer's attention reads (f32 K and V over its window) and writes (producers), the
+    PLE row (4480 B of codes + 35 f32 scales) and the embedding row. Activations between kernels
+    (a few KB per row per layer) are not counted."""
+    s = shape
+    H, F, QW, P, hd = s.hidden, s.ffn, s.q_heads * s.head_dim, s.ple_dim, s.head_dim
+
+    def lin(n, k, bits):
+        return n * k * bits // 8 + 4 * n
+
+    w = 0
+    for l in range(s.layers):
+        prod = l < s.kv_producers
+        w += lin(QW, H, 4) + lin(H, QW, 4) + 2 * lin(F, H, 4) + lin(H, F, 4)
+        w += lin(P, H, 8) + lin(H, P, 8)
+        if prod:
+            w += 2 * lin(hd, H, 4)
+    w += lin(s.layers * P, H, 4) + lin(s.vocab, H, 4)
+    per_row = 0
+    for l in range(s.layers):
+        span = pos + 1 if s.is_global(l) else min(pos + 1, s.sliding_window)
+        per_row += span * hd * 4 * 2
+        if l < s.kv_producers:
+            per_row += hd * 4 * 2
+    per_row += s.layers * P // 2 + 4 * s.layers + H // 2 + 4 + 4 * s.vocab  # PLE row, embed row, logits
+    return w + s.batch * per_row
+
+
+def bench_decode(h, batch, steps=20, warmup=3, probe=False):
+    """one E2B-shape decode step (35 layers, KV capacity 4096, position 4095, so
+    global layers attend over 4096 positions and sliding ones over 512), greedy over 262144 rows,
+    as one captured graph replayed per token; and the same step launched eagerly."""
+    import g4decode as gd
+    shape = gd.Shape(batch=batch, kv_capacity=4096)
+    model = gd.SyntheticModel(shape, seed=4, stream=h)
+    dec = gd.Decoder(shape, model)
+    dec.fill_kv_history(stream=h)
+    pos = shape.kv_capacity - 1
+    dec.set_position(pos)
+    toks = g4.DeviceBuffer.from_array(np.arange(batch, dtype=np.int32) * 7919 % shape.vocab)
+    nxt = g4.DeviceBuffer.empty((batch,), np.int32)
+    g4.synchronize()
+    stream = g4.Stream()
+    sh = stream.handle
+    dec.step(toks, nxt, sh)
+    stream.synchronize()
+    graph = g4.Graph(stream, lambda: dec.step(toks, nxt, sh))
+    if probe:
+        for _ in range(steps):
+            graph.launch()
+        stream.synchronize()
+        log(f"decode probe batch {batch}: {steps} graph replays")
+        graph.close()
+        dec.close()
+        return None
+    ms_graph = timed(sh, graph.launch, steps, warmup)
+    ms_eager = timed(sh, lambda: dec.step(toks, nxt, sh), max(3, steps // 4), 1)
+    nb = decode_step_bytes(shape, pos)
+    out = {
+        "batch": batch, "kv_positions": pos + 1, "ms_per_step_graph": round(ms_graph, 4),
+        "tok_per_s": round(batch / (ms_graph * 1e-3), 1),
+        "ms_per_step_eager": round(ms_eager, 4), "bytes_per_step": nb,
+        "gbs": round(nb / (ms_graph * 1e-3) / 1e9, 1),
+        "pct_hbm_peak": round(100 * nb / (ms_graph * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+        "next_tokens_head": [int(t) for t in nxt.download()[:4]],
+        "model_bytes": model.nbytes(),
+    }
+    graph.close()
+    dec.close()
+    stream.close()
+    return out
+
+
 def gemm_probe(h):
     """Launches for rocprofv3 --kernel-trace --stats: the config-2 gate GEMM with f16 activations
     (activation snap + tile kernel) 50 times at M=512 and 20 times at M=2048."""
@@ -290,6 +366,8 @@ def main():
     ap.add_argument("--traffic-probe", action="store_true")
     ap.add_argument("--gemm-probe", action="store_true",
                     help="only the config-2 GEMM launches (M=512 and M=2048, f16 in), for rocprofv3")
+    ap.add_argument("--decode-probe", type=int, default=0, metavar="BATCH",
+                    help="only config-4 decode steps at this batch (graph replays), for rocprofv3")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this path is measured on one GPU; --gpus {args.gpus} is not supported "
@@ -303,6 +381,9 @@ def main():
     h = stream.handle
     if args.gemm_probe:
         gemm_probe(h)
+        return
+    if args.decode_probe:
+        bench_decode(h, args.decode_probe, steps=10, probe=True)
         return
     log("building 35 layers of config-1 weights (623.6 MB)")
     layers = build_layers()
@@ -375,7 +456,11 @@ def main():
         log("config 2 sweep over M, config 1 int8 down")
         sweep = bench_gemm_sweep(h)
         down8 = bench_int8_down(h)
+        log("config 4 decode step, batch 1 and 32")
+        dec1 = bench_decode(h, 1)
+        dec32 = bench_decode(h, 32)
         result["extra"] = {
+            "decode_step_config4": {"batch1": dec1, "batch32": dec32},
             "per_layer_grouped": {"launches_per_step": LAYERS, "ms_per_step": round(ms_layer, 6),
                                   "gbs": round(step_bytes / (ms_layer * 1e-3) / 1e9, 2)},
             "decode_shaped": {"launches_per_step": 4 * LAYERS, "ms_per_step": round(ms_dec, 6),

@@ -1,0 +1,666 @@
+// The decode-step glue around the quantized projections (the E2B-shape step of BASELINE config 4):
+// RMS norm and its residual joins, q/k norm + RoPE + KV store, split attention decode and merge,
+// gelu * up, the token embedding, the per-layer-input combine, logit softcap and argmax.
+//
+// Reference kernels (Ar5en1c/gemma4-webgpu-engine): rmsNorm.ts:131-180 (rms-norm),
+// mlpEpilogue.ts:196-230 (norm-residual), blockJoin.ts:160-175 (norm-residual-norm),
+// attnPrologue.ts:268-329 (q-norm-rope, kv-norm-rope-store), rope.ts:240-258 (split half form),
+// attention.ts:858-918 (attention decode, scale 1.0, sliding window), geluMul.ts:101-116 (gelu),
+// embedGather.ts:93-113 (embed scale folded once), plan.ts:670-690 (per-layer inputs),
+// logitSoftcap.ts:104-124 and argmax.ts:267-300 (first strict maximum).
+//
+// The arithmetic is fixed so the CPU oracle (oracle/g4_decode_oracle.c) can state it exactly:
+//  - every reduction is 256 lane-strided partial sums (lane l takes elements l, l+256, ...
+//    ascending) followed by a pairwise tree (stride 128 down to 1, lane l adds lane l + stride);
+//  - 1/sqrt is the IEEE square root then the IEEE divide;
+//  - exp and tanh are d_expf / d_tanhf: Cody-Waite reduction, a degree-6 Taylor polynomial and
+//    ldexp (tanh of small arguments through the same polynomial as expm1), every step separately
+//    rounded;
+//  - attention runs in chunks of 256 positions, merged in ascending chunk order.
+// The projections between these kernels are the library's GEMV/GEMM entry points, which take and
+// give int8 codes: every kernel here that feeds a projection emits its input snap directly.
+#include "g4_internal.h"
+#include "../../include/g4decode.h"
+
+namespace g4 {
+
+constexpr int kDecThreads = 256;
+constexpr int kAttnChunk = 256;
+
+// ---- the exact-arithmetic building blocks ---------------------------------------------------------
+
+__device__ __forceinline__ float d_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.7f) return __int_as_float(0x7f800000);
+    if (x < -87.0f) return 0.0f;
+    const float n = rintf(__fmul_rn(x, 0x1.715476p+0f));             // round(x * log2 e)
+    float r = __fsub_rn(x, __fmul_rn(n, 0x1.62e4p-1f));              // x - n * ln2_hi (15-bit)
+    r = __fsub_rn(r, __fmul_rn(n, 0x1.7f7d1cp-20f));                 // - n * ln2_lo
+    float p = 0x1.6c16c2p-10f;                                       // 1/720
+    p = __fadd_rn(__fmul_rn(p, r), 0x1.111112p-7f);                  // 1/120
+    p = __fadd_rn(__fmul_rn(p, r), 0x1.555556p-5f);                  // 1/24
+    p = __fadd_rn(__fmul_rn(p, r), 0x1.555556p-3f);                  // 1/6
+    p = __fadd_rn(__fmul_rn(p, r), 0.5f);
+    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
+    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
+    return ldexpf(p, (int)n);
+}
+
+// exp(y) - 1 for |y| <= 0.35: d_expf's Taylor chain stopped before its final + 1, times y.
+__device__ __forceinline__ float d_expm1_small(float y) {
+    float p = 0x1.6c16c2p-10f;
+    p = __fadd_rn(__fmul_rn(p, y), 0x1.111112p-7f);
+    p = __fadd_rn(__fmul_rn(p, y), 0x1.555556p-5f);
+    p = __fadd_rn(__fmul_rn(p, y), 0x1.555556p-3f);
+    p = __fadd_rn(__fmul_rn(p, y), 0.5f);
+    p = __fadd_rn(__fmul_rn(p, y), 1.0f);
+    return __fmul_rn(p, y);
+}
+
+// Below 0.171875 the form -em / (2 + em), em = expm1(-2|x|), avoids the cancellation of 1 - t.
+__device__ __forceinline__ float d_tanhf(float x) {
+    const float ax = fabsf(x);
+    if (ax < 0x1p-12f) return x;
+    float r;
+    if (ax < 0.171875f) {
+        const float em = d_expm1_small(-2.0f * ax);
+        r = __fdiv_rn(-em, __fadd_rn(2.0f, em));
+    } else {
+        const float t = d_expf(-2.0f * ax);
+        r = __fdiv_rn(__fsub_rn(1.0f, t), __fadd_rn(1.0f, t));
+    }
+    return copysignf(r, x);
+}
+
+// geluMul.ts:101-116 in the shader's order.
+__device__ __forceinline__ float d_gelu(float x) {
+    const float cube = __fmul_rn(__fmul_rn(x, x), x);
+    float inner = __fmul_rn(0x1.988454p-1f, __fadd_rn(x, __fmul_rn(0x1.6e4e26p-5f, cube)));
+    inner = fminf(fmaxf(inner, -10.0f), 10.0f);
+    return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, d_tanhf(inner)));
+}
+
+// The pairwise tree over 256 lanes (every thread of the block calls it, returns the total).
+__device__ float block_tree_sum(float part, float *lds) {
+    const int t = threadIdx.x;
+    lds[t] = part;
+    __syncthreads();
+    for (int stride = kDecThreads / 2; stride >= 1; stride >>= 1) {
+        if (t < stride) lds[t] = __fadd_rn(lds[t], lds[t + stride]);
+        __syncthreads();
+    }
+    const float total = lds[0];
+    __syncthreads();
+    return total;
+}
+
+__device__ float block_max(float v, float *lds) {
+    const int t = threadIdx.x;
+    lds[t] = v;
+    __syncthreads();
+    for (int stride = kDecThreads / 2; stride >= 1; stride >>= 1) {
+        if (t < stride) lds[t] = fmaxf(lds[t], lds[t + stride]);
+        __syncthreads();
+    }
+    const float m = lds[0];
+    __syncthreads();
+    return m;
+}
+
+// sqrtf, not __fsqrt_rn: on this toolchain __fsqrt_rn is the native (approximate) v_sqrt_f32
+// unless OCML_BASIC_ROUNDED_OPERATIONS is defined, while sqrtf lowers to v_sqrt_f32 plus the
+// neighbour test that makes it correctly rounded.
+__device__ __forceinline__ float inv_rms(float sumsq, int width, float eps) {
+    return __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(sumsq, (float)width), eps)));
+}
+
+__device__ __forceinline__ float load_val(const void *src, int kind, float scale, int64_t i) {
+    if (kind == G4_KIND_I8) return __fmul_rn((float)reinterpret_cast<const int8_t *>(src)[i], scale);
+    return reinterpret_cast<const float *>(src)[i];
+}
+
+__device__ __forceinline__ int8_t snap_code(float v, float s) { return (int8_t)srq_code_i(v, s); }
+
+// ---- rms-norm / norm-residual / norm-residual-norm --------------------------------------------------
+
+constexpr int kJoinMaxPer = 8;  // width <= 2048
+
+// One block per row. y = (src * inv) * gain (gain null: weightless); with a residual,
+// hidden = resid + y, times alpha when alpha != 1. Outputs: hidden (f32), and codes of either the
+// second norm of hidden (gain2 given) or of hidden itself, snapped on in_scale.
+__global__ __launch_bounds__(kDecThreads) void join_kernel(
+    const void *src, int src_kind, float src_scale, const float *gain, const float *resid,
+    float alpha, const float *gain2, int width, float eps, float in_scale, float *hidden,
+    int8_t *codes) {
+    __shared__ float lds[kDecThreads];
+    const int t = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const int64_t base = row * width;
+    float v[kJoinMaxPer];
+    float part = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kJoinMaxPer; ++e) {
+        const int i = t + e * kDecThreads;
+        v[e] = i < width ? load_val(src, src_kind, src_scale, base + i) : 0.0f;
+        if (i < width) part = __fadd_rn(part, __fmul_rn(v[e], v[e]));
+    }
+    const float inv = inv_rms(block_tree_sum(part, lds), width, eps);
+    float part2 = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kJoinMaxPer; ++e) {
+        const int i = t + e * kDecThreads;
+        if (i >= width) continue;
+        float y = __fmul_rn(v[e], inv);
+        if (gain) y = __fmul_rn(y, gain[i]);
+        if (resid) {
+            y = __fadd_rn(resid[base + i], y);
+            if (alpha != 1.0f) y = __fmul_rn(y, alpha);
+        }
+        v[e] = y;
+        if (hidden) hidden[base + i] = y;
+        if (gain2) part2 = __fadd_rn(part2, __fmul_rn(y, y));
+    }
+    if (!codes) return;
+    if (gain2) {
+        const float inv2 = inv_rms(block_tree_sum(part2, lds), width, eps);
+#pragma unroll
+        for (int e = 0; e < kJoinMaxPer; ++e) {
+            const int i = t + e * kDecThreads;
+            if (i < width) codes[base + i] = snap_code(__fmul_rn(__fmul_rn(v[e], inv2), gain2[i]), in_scale);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < kJoinMaxPer; ++e) {
+            const int i = t + e * kDecThreads;
+            if (i < width) codes[base + i] = snap_code(v[e], in_scale);
+        }
+    }
+}
+
+// ---- q-norm-rope and kv-norm-rope-store ----------------------------------------------------------
+
+// The position a step works on: the device word when the step is replayed from a captured graph,
+// clamped to [0, pos_host] (then the largest position the caches and the split grid were sized
+// for, so no value of the word reaches outside them), else the host value.
+__device__ __forceinline__ int step_pos(int pos_host, const int32_t *pos_dev) {
+    return pos_dev ? min(max(*pos_dev, 0), pos_host) : pos_host;
+}
+
+// Grid (heads [+ 2 on a producer layer], rows); 256 threads = one head_dim 256 row. Blocks below
+// `heads` norm + rotate a query head into q_out [row][heads][256]; block `heads` norms + rotates
+// k into the K cache at the position, block heads + 1 norms v (weightless) into the V cache there.
+// cos_tab / sin_tab: [positions][128] tables, read at the position's row.
+__global__ __launch_bounds__(kDecThreads) void attn_prologue_kernel(
+    const int8_t *q_codes, float q_scale, const int8_t *k_codes, float k_scale,
+    const int8_t *v_codes, float v_scale, const float *q_gain, const float *k_gain,
+    const float *cos_tab, const float *sin_tab, int heads, float eps, float *q_out, float *k_cache,
+    float *v_cache, int64_t cache_row_stride, int pos_host, const int32_t *pos_dev) {
+    __shared__ float lds[kDecThreads];
+    __shared__ float xs[kDecThreads];
+    const int t = threadIdx.x;
+    const int h = blockIdx.x;
+    const int64_t row = blockIdx.y;
+    const int pos = step_pos(pos_host, pos_dev);
+    const float *cos_row = cos_tab + (int64_t)pos * (kDecThreads / 2);
+    const float *sin_row = sin_tab + (int64_t)pos * (kDecThreads / 2);
+    const int8_t *src;
+    float scale;
+    const float *gain;
+    float *dst;
+    bool rotate = true;
+    if (h < heads) {
+        src = q_codes + (row * heads + h) * kDecThreads;
+        scale = q_scale;
+        gain = q_gain;
+        dst = q_out + (row * heads + h) * kDecThreads;
+    } else if (h == heads) {
+        src = k_codes + row * kDecThreads;
+        scale = k_scale;
+        gain = k_gain;
+        dst = k_cache + row * cache_row_stride + (int64_t)pos * kDecThreads;
+    } else {
+        src = v_codes + row * kDecThreads;
+        scale = v_scale;
+        gain = nullptr;
+        dst = v_cache + row * cache_row_stride + (int64_t)pos * kDecThreads;
+        rotate = false;
+    }
+    const float x = __fmul_rn((float)src[t], scale);
+    const float inv = inv_rms(block_tree_sum(__fmul_rn(x, x), lds), kDecThreads, eps);
+    float y = __fmul_rn(x, inv);
+    if (gain) y = __fmul_rn(y, gain[t]);
+    if (!rotate) {
+        dst[t] = y;
+        return;
+    }
+    xs[t] = y;
+    __syncthreads();
+    constexpr int P = kDecThreads / 2;
+    const int i = t < P ? t : t - P;
+    const float lo = xs[i], hi = xs[i + P], c = cos_row[i], s = sin_row[i];
+    dst[t] = t < P ? __fsub_rn(__fmul_rn(lo, c), __fmul_rn(hi, s))
+                   : __fadd_rn(__fmul_rn(hi, c), __fmul_rn(lo, s));
+}
+
+// ---- attention decode: split partials, then the ordered merge -------------------------------------
+
+// Grid (max chunks, heads, rows). Chunk c covers positions lo + 256 c .. min(+256, pos + 1).
+// Thread t scores position start + t against the query (sequential dot over the 256 dims), the
+// block takes the max, e = exp(s - m), l = tree sum of e, and thread d accumulates
+// sum over positions (ascending) of e * v[d]. Writes (m, l) and o[256] per (row, head, chunk).
+__global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
+    const float *q, const float *k_cache, const float *v_cache, int64_t cache_row_stride, int heads,
+    int pos_host, const int32_t *pos_dev, int window, float *part_ml, float *part_o, int max_chunks) {
+    __shared__ float lds[kDecThreads];
+    __shared__ float qs[kDecThreads];
+    __shared__ float es[kAttnChunk];
+    const int t = threadIdx.x;
+    const int c = blockIdx.x, h = blockIdx.y;
+    const int64_t row = blockIdx.z;
+    const int pos = step_pos(pos_host, pos_dev);
+    const int lo = window > 0 ? max(0, pos - window + 1) : 0;
+    const int chunks = (pos - lo + 1 + kAttnChunk - 1) / kAttnChunk;
+    if (c >= chunks) return;  // whole block
+    const int start = lo + c * kAttnChunk;
+    const int cnt = min(kAttnChunk, pos + 1 - start);
+    const float *kb = k_cache + row * cache_row_stride;
+    const float *vb = v_cache + row * cache_row_stride;
+    qs[t] = q[(row * heads + h) * kDecThreads + t];
+    __syncthreads();
+    float score = -__int_as_float(0x7f800000);
+    if (t < cnt) {
+        const float4 *kr = reinterpret_cast<const float4 *>(kb + (int64_t)(start + t) * kDecThreads);
+        float d = 0.0f;
+        for (int i = 0; i < kDecThreads / 4; ++i) {
+            const float4 kv = kr[i];
+            d = __fadd_rn(d, __fmul_rn(qs[4 * i], kv.x));
+            d = __fadd_rn(d, __fmul_rn(qs[4 * i + 1], kv.y));
+            d = __fadd_rn(d, __fmul_rn(qs[4 * i + 2], kv.z));
+            d = __fadd_rn(d, __fmul_rn(qs[4 * i + 3], kv.w));
+        }
+        score = d;
+    }
+    const float m = block_max(score, lds);
+    const float e = t < cnt ? d_expf(__fsub_rn(score, m)) : 0.0f;
+    es[t] = e;
+    const float l = block_tree_sum(e, lds);  // also orders the es writes before the reads below
+    float o = 0.0f;
+    for (int j = 0; j < cnt; ++j) o = __fadd_rn(o, __fmul_rn(es[j], vb[(int64_t)(start + j) * kDecThreads + t]));
+    const int64_t slot = (row * heads + h) * max_chunks + c;
+    part_o[slot * kDecThreads + t] = o;
+    if (t == 0) {
+        part_ml[slot * 2] = m;
+        part_ml[slot * 2 + 1] = l;
+    }
+}
+
+// Grid (heads, rows); thread d merges dim d: M = max m_c, w_c = exp(m_c - M),
+// L = sum l_c w_c, O = sum o_c w_c (ascending c), out = O / L, then the o_proj input snap.
+__global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(
+    const float *part_ml, const float *part_o, int heads, int pos_host, const int32_t *pos_dev,
+    int window, int max_chunks, float in_scale, int8_t *codes, float *out_f32) {
+    const int t = threadIdx.x, h = blockIdx.x;
+    const int64_t row = blockIdx.y;
+    const int pos = step_pos(pos_host, pos_dev);
+    const int lo = window > 0 ? max(0, pos - window + 1) : 0;
+    const int chunks = (pos - lo + 1 + kAttnChunk - 1) / kAttnChunk;
+    const int64_t slot0 = (row * heads + h) * max_chunks;
+    float M = -__int_as_float(0x7f800000);
+    for (int c = 0; c < chunks; ++c) M = fmaxf(M, part_ml[(slot0 + c) * 2]);
+    float L = 0.0f, O = 0.0f;
+    for (int c = 0; c < chunks; ++c) {
+        const float w = d_expf(__fsub_rn(part_ml[(slot0 + c) * 2], M));
+        L = __fadd_rn(L, __fmul_rn(part_ml[(slot0 + c) * 2 + 1], w));
+        O = __fadd_rn(O, __fmul_rn(part_o[(slot0 + c) * kDecThreads + t], w));
+    }
+    const float y = __fdiv_rn(O, L);
+    const int64_t o = (row * heads + h) * kDecThreads + t;
+    if (out_f32) out_f32[o] = y;
+    if (codes) codes[o] = snap_code(y, in_scale);
+}
+
+// ---- gelu * up with the consumer's snap ------------------------------------------------------------
+
+// rows x n: codes = srq(gelu(g * gs) * u, in_scale) with u = up codes * us, or (up_f32 given) the
+// f32 value at up_f32[row * up_stride + i] (the per-layer-input form).
+__global__ void gelu_mul_kernel(const int8_t *g, float gs, const int8_t *u, float us,
+                                const float *up_f32, int64_t up_stride, int n, float in_scale,
+                                int8_t *codes) {
+    const int64_t row = blockIdx.y;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const float gv = __fmul_rn((float)g[row * n + i], gs);
+        const float uv = up_f32 ? up_f32[row * up_stride + i] : __fmul_rn((float)u[row * n + i], us);
+        codes[row * n + i] = snap_code(__fmul_rn(d_gelu(gv), uv), in_scale);
+    }
+}
+
+// ---- the token embedding (tied int4 table) -----------------------------------------------------------
+
+// One block per row: x = (code - 8) * f32(scale[id] * embed_scale); also the codes of x snapped on
+// in_scale (the input of the per-layer model projection). An id outside [0, vocab) (argmax's -1
+// over an all-NaN row, or a caller's bad token) reads nothing and gives a zero row.
+__global__ __launch_bounds__(kDecThreads) void embed_kernel(
+    const uint8_t *table, const float *row_scales, const int32_t *ids, int64_t vocab, int cols,
+    float embed_scale, float in_scale, float *x, int8_t *codes) {
+    const int64_t row = blockIdx.x;
+    const int64_t id = ids[row];
+    if (id < 0 || id >= vocab) {
+        for (int i = threadIdx.x; i < cols; i += kDecThreads) {
+            x[row * cols + i] = 0.0f;
+            if (codes) codes[row * cols + i] = 0;
+        }
+        return;
+    }
+    const float s = __fmul_rn(row_scales[id], embed_scale);
+    const uint8_t *src = table + id * (int64_t)(cols / 2);
+    for (int i = threadIdx.x; i < cols; i += kDecThreads) {
+        const int code = (int)((src[i >> 1] >> (4 * (i & 1))) & 0xF) - 8;
+        const float v = __fmul_rn((float)code, s);
+        x[row * cols + i] = v;
+        if (codes) codes[row * cols + i] = snap_code(v, in_scale);
+    }
+}
+
+// ---- per-layer inputs: projection norm, add the gathered identity, scale by 2^-0.5 -----------------
+
+// Grid (groups, rows), 256 threads = one group of 256.
+__global__ __launch_bounds__(kDecThreads) void ple_combine_kernel(
+    const int8_t *proj_codes, float proj_scale, float alpha, const float *gain,
+    const float *identity, int groups, float eps, float *out) {
+    __shared__ float lds[kDecThreads];
+    const int t = threadIdx.x;
+    const int64_t o = ((int64_t)blockIdx.y * groups + blockIdx.x) * kDecThreads + t;
+    const float x = __fmul_rn(__fmul_rn((float)proj_codes[o], proj_scale), alpha);
+    const float inv = inv_rms(block_tree_sum(__fmul_rn(x, x), lds), kDecThreads, eps);
+    const float y = __fmul_rn(__fmul_rn(x, inv), gain[t]);
+    out[o] = __fmul_rn(__fadd_rn(y, identity[o]), 0x1.6a09e6p-1f);
+}
+
+// ---- logit softcap and the two-stage argmax ------------------------------------------------------
+
+constexpr int kArgmaxSpan = 4096;  // logits per partial block
+
+// argmax.ts:267-300's strict rule: a value wins only above the best so far, starting from -inf,
+// so -inf and NaN never win and an empty winner stays (-inf, -1). Equal values above -inf (two
+// partial winners) resolve to the lower index.
+__device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
+    if (v > bv || (v == bv && v > -__int_as_float(0x7f800000) && (unsigned)i < (unsigned)bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+// Grid (ceil(vocab / 4096), rows). capped = tanh(x / cap) * cap (cap 0: x), optionally stored;
+// each block leaves its first strict maximum (value, index).
+__global__ __launch_bounds__(kDecThreads) void softcap_argmax_partial_kernel(
+    const float *logits, int64_t vocab, float cap, float *capped, float *part_v, int *part_i) {
+    __shared__ float sv[kDecThreads];
+    __shared__ int si[kDecThreads];
+    const int t = threadIdx.x;
+    const int64_t row = blockIdx.y;
+    const int64_t b0 = (int64_t)blockIdx.x * kArgmaxSpan;
+    float bv = -__int_as_float(0x7f800000);
+    int bi = -1;
+    for (int64_t i = b0 + t; i < min(b0 + kArgmaxSpan, vocab); i += kDecThreads) {
+        const float x = logits[row * vocab + i];
+        const float y = cap != 0.0f ? __fmul_rn(d_tanhf(__fdiv_rn(x, cap)), cap) : x;
+        if (capped) capped[row * vocab + i] = y;
+        better(bv, bi, y, (int)i);
+    }
+    sv[t] = bv;
+    si[t] = bi;
+    __syncthreads();
+    for (int stride = kDecThreads / 2; stride >= 1; stride >>= 1) {
+        if (t < stride) {
+            float v = sv[t];
+            int i = si[t];
+            better(v, i, sv[t + stride], si[t + stride]);
+            sv[t] = v;
+            si[t] = i;
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        part_v[row * gridDim.x + blockIdx.x] = sv[0];
+        part_i[row * gridDim.x + blockIdx.x] = si[0];
+    }
+}
+
+// One block per row over its `parts` partials: the winning index goes to tokens[row].
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float *part_v, const int *part_i,
+                                                          int parts, int32_t *tokens) {
+    __shared__ float sv[64];
+    __shared__ int si[64];
+    const int t = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    float bv = -__int_as_float(0x7f800000);
+    int bi = -1;
+    for (int p = t; p < parts; p += 64) better(bv, bi, part_v[row * parts + p], part_i[row * parts + p]);
+    sv[t] = bv;
+    si[t] = bi;
+    __syncthreads();
+    for (int stride = 32; stride >= 1; stride >>= 1) {
+        if (t < stride) {
+            float v = sv[t];
+            int i = si[t];
+            better(v, i, sv[t + stride], si[t + stride]);
+            sv[t] = v;
+            si[t] = i;
+        }
+        __syncthreads();
+    }
+    if (t == 0) tokens[row] = si[0];
+}
+
+// ---- seeded fills (synthetic KV histories without a host round trip) ------------------------------
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// out[i] = lo + u * span with u = (splitmix64(seed + i) >> 40) * 2^-24, in [0, 1); each step one
+// f32 rounding. The same stream in numpy reproduces it bit for bit.
+__global__ void fill_hash_f32_kernel(float *out, int64_t n, uint64_t seed, float lo, float span) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float u = (float)(splitmix64(seed + (uint64_t)i) >> 40) * 0x1p-24f;
+        out[i] = __fadd_rn(lo, __fmul_rn(u, span));
+    }
+}
+
+// out[i] = the top byte of splitmix64(seed + i): uniform int4 pairs or int8 codes.
+__global__ void fill_hash_u8_kernel(uint8_t *out, int64_t n, uint64_t seed) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = (uint8_t)(splitmix64(seed + (uint64_t)i) >> 56);
+}
+
+}  // namespace g4
+
+
+using namespace g4;
+
+static int grid_1d(int64_t n, int threads) {
+    int64_t b = (n + threads - 1) / threads;
+    return (int)(b < 1 ? 1 : (b > 65536 ? 65536 : b));
+}
+
+static int attn_chunks(int pos, int window) {
+    const int lo = window > 0 ? (pos - window + 1 > 0 ? pos - window + 1 : 0) : 0;
+    return (pos - lo + 1 + kAttnChunk - 1) / kAttnChunk;
+}
+
+extern "C" {
+
+int g4_rms_join(const void *src, int src_kind, float src_scale, const float *gain,
+                const float *resid, float alpha, const float *gain2, int rows, int width,
+                float eps, float in_scale, float *hidden, int8_t *codes, void *stream) {
+    if (!src || rows <= 0 || width <= 0)
+        return set_error(G4_ERR_INVALID, "rms-norm needs params.rows and params.width and input src");
+    if (width > kJoinMaxPer * kDecThreads)
+        return set_error(G4_ERR_UNSUPPORTED, "rms-norm: width %d exceeds %d", width,
+                         kJoinMaxPer * kDecThreads);
+    if (src_kind != G4_KIND_F32 && src_kind != G4_KIND_I8)
+        return set_error(G4_ERR_INVALID, "rms-norm: src_kind must be f32 or int8 codes");
+    if (!hidden && !codes) return set_error(G4_ERR_INVALID, "rms-norm: no output");
+    if (codes && in_scale == 0.0f)
+        return set_error(G4_ERR_INVALID, "rms-norm: int8 codes need the consumer's inScale");
+    if (gain2 && !codes) return set_error(G4_ERR_INVALID, "norm-residual-norm: gain2 without codes");
+    hipLaunchKernelGGL(join_kernel, dim3(rows), dim3(kDecThreads), 0, as_stream(stream), src,
+                       src_kind, src_scale, gain, resid, alpha, gain2, width, eps, in_scale,
+                       hidden, codes);
+    G4_LAUNCHED("join_kernel");
+    return G4_OK;
+}
+
+int g4_attn_prologue(const int8_t *q_codes, float q_scale, const int8_t *k_codes, float k_scale,
+                     const int8_t *v_codes, float v_scale, const float *q_gain,
+                     const float *k_gain, const float *cos_tab, const float *sin_tab, int rows,
+                     int heads, int head_dim, float eps, float *q_out, float *k_cache,
+                     float *v_cache, int64_t cache_row_stride, int pos, const int32_t *pos_dev,
+                     void *stream) {
+    if (head_dim != kDecThreads)
+        return set_error(G4_ERR_UNSUPPORTED, "q-norm-rope: head_dim %d (this build serves 256)",
+                         head_dim);
+    if (!q_codes || !q_gain || !cos_tab || !sin_tab || !q_out || rows <= 0 || heads <= 0)
+        return set_error(G4_ERR_INVALID, "q-norm-rope needs inputs q, gain, cosTab, sinTab");
+    if (pos < 0) return set_error(G4_ERR_INVALID, "q-norm-rope: position %d", pos);
+    const bool producer = k_codes != nullptr;
+    if (producer && (!v_codes || !k_gain || !k_cache || !v_cache))
+        return set_error(G4_ERR_INVALID, "kv-norm-rope-store needs k, v, k gain and both caches");
+    hipLaunchKernelGGL(attn_prologue_kernel, dim3(heads + (producer ? 2 : 0), rows),
+                       dim3(kDecThreads), 0, as_stream(stream), q_codes, q_scale, k_codes, k_scale,
+                       v_codes, v_scale, q_gain, k_gain, cos_tab, sin_tab, heads, eps, q_out,
+                       k_cache, v_cache, cache_row_stride, pos, pos_dev);
+    G4_LAUNCHED("attn_prologue_kernel");
+    return G4_OK;
+}
+
+size_t g4_attention_workspace_bytes(int rows, int heads, int pos, int window) {
+    if (rows <= 0 || heads <= 0 || pos < 0 || window < 0) return 0;
+    return (size_t)rows * heads * attn_chunks(pos, window) * (2 + kDecThreads) * sizeof(float);
+}
+
+int g4_attention_decode(const float *q, const float *k_cache, const float *v_cache,
+                        int64_t cache_row_stride, int rows, int heads, int head_dim, int pos,
+                        const int32_t *pos_dev, int window, float *workspace,
+                        size_t workspace_bytes, float in_scale, int8_t *codes, float *out_f32,
+                        void *stream) {
+    if (head_dim != kDecThreads)
+        return set_error(G4_ERR_UNSUPPORTED, "attention-decode: head_dim %d (this build serves 256)",
+                         head_dim);
+    if (!q || !k_cache || !v_cache || !workspace || rows <= 0 || heads <= 0 || pos < 0 ||
+        window < 0)
+        return set_error(G4_ERR_INVALID, "attention-decode needs q, k, v, a workspace and pos >= 0");
+    if (!codes && !out_f32) return set_error(G4_ERR_INVALID, "attention-decode: no output");
+    if (codes && in_scale == 0.0f)
+        return set_error(G4_ERR_INVALID, "attention-decode: int8 codes need the o_proj inScale");
+    const int chunks = attn_chunks(pos, window);
+    const size_t need = g4_attention_workspace_bytes(rows, heads, pos, window);
+    if (workspace_bytes < need)
+        return set_error(G4_ERR_INVALID, "attention-decode: workspace %zu B < %zu B",
+                         workspace_bytes, need);
+    float *part_ml = workspace;
+    float *part_o = workspace + (size_t)rows * heads * chunks * 2;
+    hipLaunchKernelGGL(attn_split_kernel, dim3(chunks, heads, rows), dim3(kDecThreads), 0,
+                       as_stream(stream), q, k_cache, v_cache, cache_row_stride, heads, pos,
+                       pos_dev, window, part_ml, part_o, chunks);
+    G4_LAUNCHED("attn_split_kernel");
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(heads, rows), dim3(kDecThreads), 0,
+                       as_stream(stream), part_ml, part_o, heads, pos, pos_dev, window, chunks,
+                       in_scale, codes, out_f32);
+    G4_LAUNCHED("attn_merge_kernel");
+    return G4_OK;
+}
+
+int g4_gelu_mul(const int8_t *g_codes, float g_scale, const int8_t *u_codes, float u_scale,
+                const float *up_f32, int64_t up_stride, int rows, int n, float in_scale,
+                int8_t *codes, void *stream) {
+    if (!g_codes || !codes || (!u_codes && !up_f32) || rows <= 0 || n <= 0)
+        return set_error(G4_ERR_INVALID, "gelu-mul needs inputs gate and up and an output");
+    if (in_scale == 0.0f)
+        return set_error(G4_ERR_INVALID, "gelu-mul: codes need the consumer's inScale");
+    if (up_f32 && up_stride < n) return set_error(G4_ERR_INVALID, "gelu-mul: up stride < n");
+    const int bx = grid_1d(n, kDecThreads);
+    hipLaunchKernelGGL(gelu_mul_kernel, dim3(bx, rows), dim3(kDecThreads), 0, as_stream(stream),
+                       g_codes, g_scale, u_codes, u_scale, up_f32, up_stride, n, in_scale, codes);
+    G4_LAUNCHED("gelu_mul_kernel");
+    return G4_OK;
+}
+
+int g4_embed_tokens(const void *table, const float *row_scales, const int32_t *ids, int rows,
+                    int64_t vocab, int cols, float embed_scale, float in_scale, float *x,
+                    int8_t *codes, void *stream) {
+    if (!table || !row_scales || !ids || !x || rows <= 0 || vocab <= 0 || cols <= 0 || (cols & 1))
+        return set_error(G4_ERR_INVALID, "embed-gather needs codes, scales, ids, the row count "
+                                         "and an even width");
+    if (codes && in_scale == 0.0f)
+        return set_error(G4_ERR_INVALID, "embed-gather: codes need inScale");
+    hipLaunchKernelGGL(embed_kernel, dim3(rows), dim3(kDecThreads), 0, as_stream(stream),
+                       reinterpret_cast<const uint8_t *>(table), row_scales, ids, vocab, cols,
+                       embed_scale, in_scale, x, codes);
+    G4_LAUNCHED("embed_kernel");
+    return G4_OK;
+}
+
+int g4_ple_combine(const int8_t *proj_codes, float proj_scale, float alpha, const float *gain,
+                   const float *identity, int rows, int groups, int group, float eps, float *out,
+                   void *stream) {
+    if (group != kDecThreads)
+        return set_error(G4_ERR_UNSUPPORTED, "per-layer inputs: group %d (serves 256)", group);
+    if (!proj_codes || !gain || !identity || !out || rows <= 0 || groups <= 0)
+        return set_error(G4_ERR_INVALID,
+                         "per-layer inputs need the projection, gain and identity rows");
+    hipLaunchKernelGGL(ple_combine_kernel, dim3(groups, rows), dim3(kDecThreads), 0,
+                       as_stream(stream), proj_codes, proj_scale, alpha, gain, identity, groups,
+                       eps, out);
+    G4_LAUNCHED("ple_combine_kernel");
+    return G4_OK;
+}
+
+size_t g4_argmax_workspace_bytes(int rows, int64_t vocab) {
+    if (rows <= 0 || vocab <= 0) return 0;
+    return (size_t)rows * (size_t)((vocab + kArgmaxSpan - 1) / kArgmaxSpan) * 8;
+}
+
+int g4_softcap_argmax(const float *logits, int rows, int64_t vocab, float cap, float *capped,
+                      void *workspace, size_t workspace_bytes, int32_t *tokens, void *stream) {
+    if (!logits || !tokens || !workspace || rows <= 0 || vocab <= 0 || vocab > INT32_MAX)
+        return set_error(G4_ERR_INVALID, "argmax needs logits, a workspace and tokens");
+    if (workspace_bytes < g4_argmax_workspace_bytes(rows, vocab))
+        return set_error(G4_ERR_INVALID, "argmax: workspace %zu B < %zu B", workspace_bytes,
+                         g4_argmax_workspace_bytes(rows, vocab));
+    const int parts = (int)((vocab + kArgmaxSpan - 1) / kArgmaxSpan);
+    float *pv = reinterpret_cast<float *>(workspace);
+    int *pi = reinterpret_cast<int *>(pv + (size_t)rows * parts);
+    hipLaunchKernelGGL(softcap_argmax_partial_kernel, dim3(parts, rows), dim3(kDecThreads), 0,
+                       as_stream(stream), logits, vocab, cap, capped, pv, pi);
+    G4_LAUNCHED("softcap_argmax_partial_kernel");
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, as_stream(stream), pv, pi,
+                       parts, tokens);
+    G4_LAUNCHED("argmax_final_kernel");
+    return G4_OK;
+}
+
+int g4_fill_hash_f32(float *out, int64_t n, uint64_t seed, float lo, float hi, void *stream) {
+    if (!out || n < 0) return set_error(G4_ERR_INVALID, "fill: bad arguments");
+    if (n == 0) return G4_OK;
+    hipLaunchKernelGGL(fill_hash_f32_kernel, dim3(grid_1d(n, 256)), dim3(256), 0,
+                       as_stream(stream), out, n, seed, lo, hi - lo);
+    G4_LAUNCHED("fill_hash_f32_kernel");
+    return G4_OK;
+}
+
+int g4_fill_hash_u8(void *out, int64_t n, uint64_t seed, void *stream) {
+    if (!out || n < 0) return set_error(G4_ERR_INVALID, "fill: bad arguments");
+    if (n == 0) return G4_OK;
+    hipLaunchKernelGGL(fill_hash_u8_kernel, dim3(grid_1d(n, 256)), dim3(256), 0,
+                       as_stream(stream), reinterpret_cast<uint8_t *>(out), n, seed);
+    G4_LAUNCHED("fill_hash_u8_kernel");
+    return G4_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,430 @@
+// The native decode-step runner: one E2B-shape decode step for `batch` sequences as a fixed list of
+// launches on one stream (the dispatch walk of plan.ts:780-792 planDecodeStep, executed as
+// execute.ts does, without the per-dispatch bind work: every buffer and GEMV plan is built once in
+// g4_decode_create). The step reads its position from a device word, so a captured graph of one
+// step replays every later token unchanged.
+//
+// Per layer (plan.ts:487-665, with the synthetic config's uniform FFN and head_dim):
+//   [layer 0: input_layernorm, from the embedding phase]
+//   q (+ k, v on a producer) GEMV        -> int8 codes on out_scale
+//   q-norm-rope (+ kv-norm-rope-store)   -> q f32; K, V rows at the position
+//   attention decode over the layer's cache (own, or the last producer of its kind) -> o input snap
+//   o GEMV; norm-residual-norm (post_attention_layernorm, residual, pre_feedforward_layernorm)
+//   gate, up GEMV; gelu-mul (down's snap); down GEMV
+//   norm-residual (post_feedforward_layernorm, residual), snapped for per_layer_input_gate
+//   per_layer_input_gate (int8 GEMV); gelu times the layer's per-layer input row (the projection's
+//   snap); per_layer_projection (int8 GEMV)
+//   norm-residual-norm (post_per_layer_input_norm, residual, layer_scalar, then the next layer's
+//   input_layernorm, or the final norm on the last layer)
+// Embedding phase (plan.ts:720-729): tied int4 embed gather (x sqrt(hidden) folded), PLE gather,
+// per_layer_model_projection (int4 GEMV, then hidden^-0.5), per_layer_projection_norm, + identity,
+// x 2^-0.5. Head (plan.ts:768-777): tied int4 GEMV to f32 logits, softcap, two-stage argmax.
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "g4_internal.h"
+#include "../../include/g4decode.h"
+
+namespace {
+
+using namespace g4;
+
+struct Plan {
+    g4_gemv_plan *p = nullptr;
+};
+
+struct DeviceAlloc {
+    std::vector<void *> ptrs;
+    int get(void **out, size_t bytes) {
+        void *p = nullptr;
+        if (hipMalloc(&p, bytes < 256 ? 256 : bytes) != hipSuccess)
+            return set_error(G4_ERR_HIP, "decode: hipMalloc of %zu bytes failed", bytes);
+        ptrs.push_back(p);
+        *out = p;
+        return G4_OK;
+    }
+    ~DeviceAlloc() {
+        for (void *p : ptrs) (void)hipFree(p);
+    }
+};
+
+}  // namespace
+
+struct g4_decode {
+    g4_decode_shape s{};
+    g4_decode_weights w{};
+    std::vector<g4_decode_layer> layers;
+    DeviceAlloc mem;
+    int32_t *pos = nullptr;
+    float *identity = nullptr, *per_layer = nullptr, *hidden = nullptr;
+    float *q = nullptr, *attn_ws = nullptr, *logits = nullptr;
+    size_t attn_ws_bytes = 0, argmax_ws_bytes = 0;
+    void *argmax_ws = nullptr;
+    int8_t *embed_codes = nullptr, *ple_codes = nullptr, *xcodes = nullptr, *qc = nullptr,
+           *kc = nullptr, *vc = nullptr, *attn_codes = nullptr, *oc = nullptr, *gc = nullptr,
+           *uc = nullptr, *act = nullptr, *dc = nullptr, *pgc = nullptr, *pac = nullptr,
+           *ppc = nullptr, *head_codes = nullptr;
+    std::vector<float *> kv;  // per producer: [batch][2][capacity][head_dim]
+    int stop = -1;
+    // M = 1 GEMV plans per layer: qkv (or q), o, gate+up, down, ple gate, ple projection.
+    std::vector<Plan> plans;
+    Plan ple_model_plan, head_plan;
+    ~g4_decode() {
+        for (Plan &p : plans)
+            if (p.p) g4_qgemv_plan_destroy(p.p);
+        if (ple_model_plan.p) g4_qgemv_plan_destroy(ple_model_plan.p);
+        if (head_plan.p) g4_qgemv_plan_destroy(head_plan.p);
+    }
+};
+
+namespace {
+
+enum { P_QKV = 0, P_O, P_GATEUP, P_DOWN, P_PLE_GATE, P_PLE_PROJ, P_PER_LAYER };
+
+bool is_global(const g4_decode_shape &s, int l) { return l % s.global_period == s.global_period - 1; }
+
+// kv.ts:76-93: producers read their own cache; consumers the last producer of their own kind.
+int kv_source(const g4_decode_shape &s, int l) {
+    if (l < s.kv_producers) return l;
+    int last = -1;
+    for (int p = 0; p < s.kv_producers; ++p)
+        if (is_global(s, p) == is_global(s, l)) last = p;
+    return last;
+}
+
+g4_gemv_desc desc(const void *w, const float *sc, const void *x, void *dst, int bits, int k, int n,
+                  int out_kind, float in_scale, float out_scale) {
+    g4_gemv_desc d{};
+    d.wq = w;
+    d.scales = sc;
+    d.x = x;
+    d.dst = dst;
+    d.bits = bits;
+    d.x_kind = G4_KIND_I8;
+    d.out_kind = out_kind;
+    d.k = k;
+    d.num_rows = n;
+    d.in_scale = in_scale;
+    d.out_scale = out_scale;
+    return d;
+}
+
+// One linear of `batch` int8-coded rows: the prebuilt M = 1 plan when there is one (batch 1 and a
+// streaming shape class), else the library's routing (GEMV columns, small-M MFMA up to 32 rows).
+int run_linear_rows(const g4_decode &d, const Plan &plan, const g4_gemv_desc &one, void *stream) {
+    if (d.s.batch == 1 && plan.p) return g4_qgemv_plan_launch(plan.p, stream);
+    return g4_linear(one.bits, one.wq, one.scales, one.x, G4_KIND_I8, one.dst, one.out_kind, one.k,
+                     one.num_rows, d.s.batch, one.in_scale, one.out_scale, stream);
+}
+
+#define G4_TRY(call)             \
+    do {                         \
+        int rc_ = (call);        \
+        if (rc_ != G4_OK) return rc_; \
+    } while (0)
+
+int check_shape(const g4_decode_shape &s) {
+    if (s.layers <= 0 || s.layers > 64 || s.kv_producers <= 0 || s.kv_producers > s.layers)
+        return set_error(G4_ERR_INVALID, "decode: layers %d / kv_producers %d", s.layers,
+                         s.kv_producers);
+    if (s.head_dim != 256 || s.ple_dim != 256)
+        return set_error(G4_ERR_UNSUPPORTED, "decode: head_dim and ple_dim must be 256");
+    if (s.hidden <= 0 || s.hidden % 256 || s.hidden > 2048)
+        return set_error(G4_ERR_UNSUPPORTED, "decode: hidden %d (a multiple of 256, at most 2048)",
+                         s.hidden);
+    if (s.ffn <= 0 || s.ffn % 256 || s.ffn > 16384)
+        return set_error(G4_ERR_UNSUPPORTED, "decode: ffn %d (a multiple of 256, at most 16384)", s.ffn);
+    if (s.q_heads <= 0 || (s.q_heads * s.head_dim) % 256 || s.q_heads * s.head_dim > 16384)
+        return set_error(G4_ERR_UNSUPPORTED, "decode: q_heads %d", s.q_heads);
+    if (s.global_period <= 0 || s.sliding_window <= 0)
+        return set_error(G4_ERR_INVALID, "decode: global_period and sliding_window must be positive");
+    if (s.kv_capacity <= 0 || s.kv_capacity > (1 << 20))
+        return set_error(G4_ERR_INVALID, "decode: kv_capacity %d", s.kv_capacity);
+    if (s.batch <= 0 || s.batch > 64) return set_error(G4_ERR_INVALID, "decode: batch %d (1..64)", s.batch);
+    if (s.vocab <= 0 || s.vocab > (int64_t)1 << 30)
+        return set_error(G4_ERR_INVALID, "decode: vocab %lld", (long long)s.vocab);
+    if (s.in_scale <= 0.0f || s.out_scale <= 0.0f)
+        return set_error(G4_ERR_INVALID, "decode: the static scales must be calibrated (non-zero)");
+    for (int l = 0; l < s.layers; ++l)
+        if (kv_source(s, l) < 0)
+            return set_error(G4_ERR_INVALID, "decode: layer %d has no producer of its kind", l);
+    return G4_OK;
+}
+
+int check_weights(const g4_decode_shape &s, const g4_decode_weights &w) {
+    if (!w.embed || !w.embed_s || !w.ple_table || !w.ple_table_s || !w.ple_model_proj ||
+        !w.ple_model_proj_s || !w.ple_proj_norm || !w.final_norm || !w.rope_local_cos ||
+        !w.rope_local_sin || !w.rope_global_cos || !w.rope_global_sin || !w.layer)
+        return set_error(G4_ERR_INVALID, "decode: a model-level weight is missing");
+    for (int l = 0; l < s.layers; ++l) {
+        const g4_decode_layer &L = w.layer[l];
+        const bool prod = l < s.kv_producers;
+        if (!L.q || !L.o || !L.gate || !L.up || !L.down || !L.ple_gate || !L.ple_proj || !L.q_s ||
+            !L.o_s || !L.gate_s || !L.up_s || !L.down_s || !L.ple_gate_s || !L.ple_proj_s ||
+            !L.input_norm || !L.post_attn_norm || !L.pre_ffn_norm || !L.post_ffn_norm ||
+            !L.post_ple_norm || !L.q_norm)
+            return set_error(G4_ERR_INVALID, "decode: layer %d misses a weight", l);
+        if (prod && (!L.k || !L.v || !L.k_s || !L.v_s || !L.k_norm))
+            return set_error(G4_ERR_INVALID, "decode: producer layer %d misses k, v or k_norm", l);
+    }
+    return G4_OK;
+}
+
+// A grouped M = 1 plan, or none when a shape has no streaming class (the runner then launches
+// each projection through g4_linear).
+int try_plan(const g4_gemv_desc *descs, int count, Plan &out) {
+    const int rc = g4_qgemv_plan_create(descs, count, &out.p);
+    if (rc == G4_ERR_UNSUPPORTED) {
+        out.p = nullptr;
+        clear_error();
+        return G4_OK;
+    }
+    return rc;
+}
+
+int build(g4_decode &d) {
+    const g4_decode_shape &s = d.s;
+    const int B = s.batch, H = s.hidden, F = s.ffn, QW = s.q_heads * s.head_dim;
+    const int PL = s.layers * s.ple_dim;
+    DeviceAlloc &m = d.mem;
+    auto f32 = [&](float **p, size_t n) { return m.get((void **)p, n * sizeof(float)); };
+    auto i8 = [&](int8_t **p, size_t n) { return m.get((void **)p, n); };
+    G4_TRY(m.get((void **)&d.pos, sizeof(int32_t)));
+    G4_HIP(hipMemset(d.pos, 0, sizeof(int32_t)));
+    G4_TRY(f32(&d.identity, (size_t)B * PL));
+    G4_TRY(f32(&d.per_layer, (size_t)B * PL));
+    G4_TRY(f32(&d.hidden, (size_t)B * H));
+    G4_TRY(f32(&d.q, (size_t)B * QW));
+    G4_TRY(f32(&d.logits, (size_t)B * s.vocab));
+    d.attn_ws_bytes = g4_attention_workspace_bytes(B, s.q_heads, s.kv_capacity - 1, 0);
+    G4_TRY(m.get((void **)&d.attn_ws, d.attn_ws_bytes));
+    d.argmax_ws_bytes = g4_argmax_workspace_bytes(B, s.vocab);
+    G4_TRY(m.get(&d.argmax_ws, d.argmax_ws_bytes));
+    G4_TRY(i8(&d.embed_codes, (size_t)B * H));
+    G4_TRY(i8(&d.ple_codes, (size_t)B * PL));
+    G4_TRY(i8(&d.xcodes, (size_t)B * H));
+    G4_TRY(i8(&d.qc, (size_t)B * QW));
+    G4_TRY(i8(&d.kc, (size_t)B * s.head_dim));
+    G4_TRY(i8(&d.vc, (size_t)B * s.head_dim));
+    G4_TRY(i8(&d.attn_codes, (size_t)B * QW));
+    G4_TRY(i8(&d.oc, (size_t)B * H));
+    G4_TRY(i8(&d.gc, (size_t)B * F));
+    G4_TRY(i8(&d.uc, (size_t)B * F));
+    G4_TRY(i8(&d.act, (size_t)B * F));
+    G4_TRY(i8(&d.dc, (size_t)B * H));
+    G4_TRY(i8(&d.pgc, (size_t)B * s.ple_dim));
+    G4_TRY(i8(&d.pac, (size_t)B * s.ple_dim));
+    G4_TRY(i8(&d.ppc, (size_t)B * H));
+    G4_TRY(i8(&d.head_codes, (size_t)B * H));
+    const size_t cache = (size_t)B * 2 * s.kv_capacity * s.head_dim;
+    d.kv.assign(s.kv_producers, nullptr);
+    for (int p = 0; p < s.kv_producers; ++p) {
+        G4_TRY(f32(&d.kv[p], cache));
+        G4_HIP(hipMemset(d.kv[p], 0, cache * sizeof(float)));
+    }
+    if (B != 1) return G4_OK;
+    // M = 1: one grouped-GEMV plan per launch group.
+    const float in = s.in_scale, out = s.out_scale;
+    d.plans.assign((size_t)s.layers * P_PER_LAYER, Plan{});
+    for (int l = 0; l < s.layers; ++l) {
+        const g4_decode_layer &L = d.layers[l];
+        Plan *P = &d.plans[(size_t)l * P_PER_LAYER];
+        std::vector<g4_gemv_desc> g{desc(L.q, L.q_s, d.xcodes, d.qc, 4, H, QW, G4_KIND_I8, in, out)};
+        if (l < s.kv_producers) {
+            g.push_back(desc(L.k, L.k_s, d.xcodes, d.kc, 4, H, s.head_dim, G4_KIND_I8, in, out));
+            g.push_back(desc(L.v, L.v_s, d.xcodes, d.vc, 4, H, s.head_dim, G4_KIND_I8, in, out));
+        }
+        G4_TRY(try_plan(g.data(), (int)g.size(), P[P_QKV]));
+        g4_gemv_desc o = desc(L.o, L.o_s, d.attn_codes, d.oc, 4, QW, H, G4_KIND_I8, in, out);
+        G4_TRY(try_plan(&o, 1, P[P_O]));
+        g4_gemv_desc gu[2] = {desc(L.gate, L.gate_s, d.xcodes, d.gc, 4, H, F, G4_KIND_I8, in, out),
+                              desc(L.up, L.up_s, d.xcodes, d.uc, 4, H, F, G4_KIND_I8, in, out)};
+        G4_TRY(try_plan(gu, 2, P[P_GATEUP]));
+        g4_gemv_desc dn = desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out);
+        G4_TRY(try_plan(&dn, 1, P[P_DOWN]));
+        g4_gemv_desc pg = desc(L.ple_gate, L.ple_gate_s, d.xcodes, d.pgc, 8, H, s.ple_dim,
+                               G4_KIND_I8, in, out);
+        G4_TRY(try_plan(&pg, 1, P[P_PLE_GATE]));
+        g4_gemv_desc pp = desc(L.ple_proj, L.ple_proj_s, d.pac, d.ppc, 8, s.ple_dim, H, G4_KIND_I8,
+                               in, out);
+        G4_TRY(try_plan(&pp, 1, P[P_PLE_PROJ]));
+    }
+    g4_gemv_desc pm = desc(d.w.ple_model_proj, d.w.ple_model_proj_s, d.embed_codes, d.ple_codes, 4,
+                           H, PL, G4_KIND_I8, in, out);
+    G4_TRY(try_plan(&pm, 1, d.ple_model_plan));
+    g4_gemv_desc hd = desc(d.w.embed, d.w.embed_s, d.head_codes, d.logits, 4, H, (int)s.vocab,
+                           G4_KIND_F32, in, 0.0f);
+    G4_TRY(try_plan(&hd, 1, d.head_plan));
+    return G4_OK;
+}
+
+int run_layer(g4_decode &d, int l, void *st) {
+    const g4_decode_shape &s = d.s;
+    const g4_decode_layer &L = d.layers[l];
+    const int B = s.batch, H = s.hidden, F = s.ffn, QW = s.q_heads * s.head_dim;
+    const float in = s.in_scale, out = s.out_scale;
+    const bool prod = l < s.kv_producers, glob = is_global(s, l);
+    const Plan *P = d.plans.empty() ? nullptr : &d.plans[(size_t)l * P_PER_LAYER];
+    static const Plan none;
+    auto plan = [&](int i) -> const Plan & { return P ? P[i] : none; };
+
+    // attention block
+    G4_TRY(run_linear_rows(d, plan(P_QKV), desc(L.q, L.q_s, d.xcodes, d.qc, 4, H, QW, G4_KIND_I8, in, out), st));
+    if (prod && !plan(P_QKV).p) {
+        G4_TRY(run_linear_rows(d, none, desc(L.k, L.k_s, d.xcodes, d.kc, 4, H, s.head_dim, G4_KIND_I8, in, out), st));
+        G4_TRY(run_linear_rows(d, none, desc(L.v, L.v_s, d.xcodes, d.vc, 4, H, s.head_dim, G4_KIND_I8, in, out), st));
+    }
+    const int src = kv_source(s, l);
+    float *kb = d.kv[src];
+    float *vb = kb + (size_t)s.kv_capacity * s.head_dim;
+    const int64_t row_stride = (int64_t)2 * s.kv_capacity * s.head_dim;
+    const float *cos_tab = glob ? d.w.rope_global_cos : d.w.rope_local_cos;
+    const float *sin_tab = glob ? d.w.rope_global_sin : d.w.rope_local_sin;
+    G4_TRY(g4_attn_prologue(d.qc, out, prod ? d.kc : nullptr, out, prod ? d.vc : nullptr, out,
+                            L.q_norm, prod ? L.k_norm : nullptr, cos_tab, sin_tab, B, s.q_heads,
+                            s.head_dim, s.eps, d.q, prod ? kb : nullptr, prod ? vb : nullptr,
+                            row_stride, s.kv_capacity - 1, d.pos, st));
+    G4_TRY(g4_attention_decode(d.q, kb, vb, row_stride, B, s.q_heads, s.head_dim,
+                               s.kv_capacity - 1, d.pos, glob ? 0 : s.sliding_window, d.attn_ws,
+                               d.attn_ws_bytes, in, d.attn_codes, nullptr, st));
+    G4_TRY(run_linear_rows(d, plan(P_O), desc(L.o, L.o_s, d.attn_codes, d.oc, 4, QW, H, G4_KIND_I8, in, out), st));
+    G4_TRY(g4_rms_join(d.oc, G4_KIND_I8, out, L.post_attn_norm, d.hidden, 1.0f, L.pre_ffn_norm, B,
+                       H, s.eps, in, d.hidden, d.xcodes, st));
+    // MLP block
+    G4_TRY(run_linear_rows(d, plan(P_GATEUP), desc(L.gate, L.gate_s, d.xcodes, d.gc, 4, H, F, G4_KIND_I8, in, out), st));
+    if (!plan(P_GATEUP).p)
+        G4_TRY(run_linear_rows(d, none, desc(L.up, L.up_s, d.xcodes, d.uc, 4, H, F, G4_KIND_I8, in, out), st));
+    G4_TRY(g4_gelu_mul(d.gc, out, d.uc, out, nullptr, 0, B, F, in, d.act, st));
+    G4_TRY(run_linear_rows(d, plan(P_DOWN), desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out), st));
+    G4_TRY(g4_rms_join(d.dc, G4_KIND_I8, out, L.post_ffn_norm, d.hidden, 1.0f, nullptr, B, H,
+                       s.eps, in, d.hidden, d.xcodes, st));
+    // per-layer-input block
+    G4_TRY(run_linear_rows(d, plan(P_PLE_GATE), desc(L.ple_gate, L.ple_gate_s, d.xcodes, d.pgc, 8, H, s.ple_dim, G4_KIND_I8, in, out), st));
+    G4_TRY(g4_gelu_mul(d.pgc, out, nullptr, 0.0f, d.per_layer + (size_t)l * s.ple_dim,
+                       (int64_t)s.layers * s.ple_dim, B, s.ple_dim, in, d.pac, st));
+    G4_TRY(run_linear_rows(d, plan(P_PLE_PROJ), desc(L.ple_proj, L.ple_proj_s, d.pac, d.ppc, 8, s.ple_dim, H, G4_KIND_I8, in, out), st));
+    // the tail join: residual, layer scalar, then the next input norm (or the final norm)
+    const bool last = l + 1 == s.layers;
+    const float *next_norm = last ? d.w.final_norm : d.layers[l + 1].input_norm;
+    G4_TRY(g4_rms_join(d.ppc, G4_KIND_I8, out, L.post_ple_norm, d.hidden, L.layer_scalar,
+                       next_norm, B, H, s.eps, in, d.hidden, last ? d.head_codes : d.xcodes, st));
+    return G4_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int g4_decode_create(const g4_decode_shape *shape, const g4_decode_weights *weights,
+                     g4_decode **out) {
+    if (!shape || !weights || !out) return set_error(G4_ERR_INVALID, "decode: null argument");
+    *out = nullptr;
+    G4_TRY(check_shape(*shape));
+    G4_TRY(check_weights(*shape, *weights));
+    g4_decode *d = new (std::nothrow) g4_decode();
+    if (!d) return set_error(G4_ERR_INVALID, "decode: out of host memory");
+    d->s = *shape;
+    d->w = *weights;
+    d->layers.assign(weights->layer, weights->layer + shape->layers);
+    d->w.layer = d->layers.data();
+    int rc = build(*d);
+    if (rc != G4_OK) {
+        delete d;
+        return rc;
+    }
+    *out = d;
+    return G4_OK;
+}
+
+int g4_decode_destroy(g4_decode *d) {
+    if (d) {
+        (void)hipDeviceSynchronize();
+        delete d;
+    }
+    return G4_OK;
+}
+
+int g4_decode_kv(g4_decode *d, int layer, float **k, float **v, int64_t *row_stride) {
+    if (!d || layer < 0 || layer >= d->s.kv_producers)
+        return set_error(G4_ERR_INVALID, "decode: layer %d owns no KV cache", layer);
+    if (k) *k = d->kv[layer];
+    if (v) *v = d->kv[layer] + (size_t)d->s.kv_capacity * d->s.head_dim;
+    if (row_stride) *row_stride = (int64_t)2 * d->s.kv_capacity * d->s.head_dim;
+    return G4_OK;
+}
+
+int g4_decode_position(g4_decode *d, int32_t **pos) {
+    if (!d || !pos) return set_error(G4_ERR_INVALID, "decode: null argument");
+    *pos = d->pos;
+    return G4_OK;
+}
+
+int g4_decode_set_stop(g4_decode *d, int last_layer) {
+    if (!d || last_layer < -1 || last_layer >= d->s.layers)
+        return set_error(G4_ERR_INVALID, "decode: stop layer %d", last_layer);
+    d->stop = last_layer;
+    return G4_OK;
+}
+
+int g4_decode_buffer(g4_decode *d, const char *name, void **ptr, size_t *bytes) {
+    if (!d || !name || !ptr) return set_error(G4_ERR_INVALID, "decode: null argument");
+    const g4_decode_shape &s = d->s;
+    const size_t B = (size_t)s.batch;
+    struct Named {
+        const char *n;
+        void *p;
+        size_t b;
+    } all[] = {
+        {"hidden", d->hidden, B * s.hidden * 4},
+        {"logits", d->logits, B * (size_t)s.vocab * 4},
+        {"per_layer", d->per_layer, B * s.layers * s.ple_dim * 4},
+        {"head_codes", d->head_codes, B * s.hidden},
+        {"codes", d->xcodes, B * s.hidden},
+    };
+    for (const Named &n : all)
+        if (std::strcmp(n.n, name) == 0) {
+            *ptr = n.p;
+            if (bytes) *bytes = n.b;
+            return G4_OK;
+        }
+    return set_error(G4_ERR_INVALID, "decode: no buffer named '%s'", name);
+}
+
+int g4_decode_step(g4_decode *d, const int32_t *tokens, int32_t *next_tokens, void *stream) {
+    if (!d || !tokens || !next_tokens) return set_error(G4_ERR_INVALID, "decode: null argument");
+    const g4_decode_shape &s = d->s;
+    const int B = s.batch, H = s.hidden, PL = s.layers * s.ple_dim;
+    const float in = s.in_scale, out = s.out_scale;
+    // embedding phase: the residual stream starts at the scaled embedding
+    const float embed_scale = (float)std::sqrt((double)H);
+    G4_TRY(g4_embed_tokens(d->w.embed, d->w.embed_s, tokens, B, s.vocab, H, embed_scale, in,
+                           d->hidden, d->embed_codes, stream));
+    // the unsliced gather over all `vocab` rows: an id outside them gives a zero row
+    G4_TRY(g4_ple_gather(d->w.ple_table, d->w.ple_table_s, 0, tokens, d->identity, G4_KIND_F32,
+                         B, PL, s.ple_dim, s.layers, 0, 0, s.vocab, stream));
+    G4_TRY(run_linear_rows(*d, d->ple_model_plan,
+                           desc(d->w.ple_model_proj, d->w.ple_model_proj_s, d->embed_codes,
+                                d->ple_codes, 4, H, PL, G4_KIND_I8, in, out),
+                           stream));
+    const float alpha = (float)std::pow((double)H, -0.5);
+    G4_TRY(g4_ple_combine(d->ple_codes, out, alpha, d->w.ple_proj_norm, d->identity, B, s.layers,
+                          s.ple_dim, s.eps, d->per_layer, stream));
+    G4_TRY(g4_rms_join(d->hidden, G4_KIND_F32, 1.0f, d->layers[0].input_norm, nullptr, 1.0f,
+                       nullptr, B, H, s.eps, in, nullptr, d->xcodes, stream));
+    const int last = d->stop >= 0 ? d->stop : s.layers - 1;
+    for (int l = 0; l <= last; ++l) G4_TRY(run_layer(*d, l, stream));
+    if (last != s.layers - 1) return G4_OK;
+    // head: tied int4 GEMV to f32 logits, softcap in place, argmax
+    G4_TRY(run_linear_rows(*d, d->head_plan,
+                           desc(d->w.embed, d->w.embed_s, d->head_codes, d->logits, 4, H,
+                                (int)s.vocab, G4_KIND_F32, in, 0.0f),
+                           stream));
+    G4_TRY(g4_softcap_argmax(d->logits, B, s.vocab, s.final_softcap, d->logits, d->argmax_ws,
+                             d->argmax_ws_bytes, next_tokens, stream));
+    return G4_OK;
+}
+
+}  // extern "C"

@@ -57,7 +57,42 @@ class TableSplitPlan(ctypes.Structure):
                 ("binding_budget", _i64), ("dispatches_per_gather", _i64)]
 
 
-# Every symbol include/g4w8a8.h declares, with its ctypes signature (restype, argtypes).
+class DecodeShape(ctypes.Structure):
+    """include/g4decode.h g4_decode_shape."""
+    _fields_ = [(n, _c_int) for n in ("layers", "kv_producers", "hidden", "ffn", "q_heads",
+                                      "head_dim", "ple_dim", "global_period", "sliding_window",
+                                      "kv_capacity", "batch")] + [
+        ("vocab", _i64), ("eps", _c_float), ("final_softcap", _c_float), ("in_scale", _c_float),
+        ("out_scale", _c_float)]
+
+
+DECODE_LAYER_FIELDS = ("q", "k", "v", "o", "gate", "up", "down", "ple_gate", "ple_proj",
+                       "q_s", "k_s", "v_s", "o_s", "gate_s", "up_s", "down_s", "ple_gate_s",
+                       "ple_proj_s", "input_norm", "post_attn_norm", "pre_ffn_norm",
+                       "post_ffn_norm", "post_ple_norm", "q_norm", "k_norm")
+
+
+class DecodeLayer(ctypes.Structure):
+    """include/g4decode.h g4_decode_layer (device pointers plus the layer scalar)."""
+    _fields_ = [(n, _vp) for n in DECODE_LAYER_FIELDS] + [("layer_scalar", _c_float)]
+
+
+DECODE_MODEL_FIELDS = ("embed", "embed_s", "ple_table", "ple_table_s", "ple_model_proj",
+                       "ple_model_proj_s", "ple_proj_norm", "final_norm", "rope_local_cos",
+                       "rope_local_sin", "rope_global_cos", "rope_global_sin")
+
+
+class DecodeWeights(ctypes.Structure):
+    """include/g4decode.h g4_decode_weights."""
+    _fields_ = [(n, _vp) for n in DECODE_MODEL_FIELDS] + [("layer", ctypes.POINTER(DecodeLayer))]
+
+
+_u64 = ctypes.c_uint64
+_sz = ctypes.c_size_t
+_i32p = ctypes.POINTER(ctypes.c_int32)
+
+# Every symbol include/g4w8a8.h and include/g4decode.h declare, with its ctypes signature
+# (restype, argtypes).
 SIGNATURES = {
     "g4_abi_version": (_c_int, []),
     "g4_last_error": (ctypes.c_char_p, []),
@@ -114,6 +149,35 @@ SIGNATURES = {
                                      ctypes.POINTER(TableSplitPlan), ctypes.POINTER(TableSlice),
                                      _i64]),
     "g4_slice_for_row": (_i64, [ctypes.POINTER(TableSlice), _i64, _i64]),
+    # include/g4decode.h
+    "g4_rms_join": (_c_int, [_vp, _c_int, _c_float, _vp, _vp, _c_float, _vp, _c_int, _c_int,
+                             _c_float, _c_float, _vp, _vp, _vp]),
+    "g4_attn_prologue": (_c_int, [_vp, _c_float, _vp, _c_float, _vp, _c_float, _vp, _vp, _vp, _vp,
+                                  _c_int, _c_int, _c_int, _c_float, _vp, _vp, _vp, _i64, _c_int,
+                                  _vp, _vp]),
+    "g4_attention_decode": (_c_int, [_vp, _vp, _vp, _i64, _c_int, _c_int, _c_int, _c_int, _vp,
+                                     _c_int, _vp, _sz, _c_float, _vp, _vp, _vp]),
+    "g4_attention_workspace_bytes": (_sz, [_c_int, _c_int, _c_int, _c_int]),
+    "g4_gelu_mul": (_c_int, [_vp, _c_float, _vp, _c_float, _vp, _i64, _c_int, _c_int, _c_float,
+                             _vp, _vp]),
+    "g4_embed_tokens": (_c_int, [_vp, _vp, _vp, _c_int, _i64, _c_int, _c_float, _c_float, _vp,
+                                 _vp, _vp]),
+    "g4_ple_combine": (_c_int, [_vp, _c_float, _c_float, _vp, _vp, _c_int, _c_int, _c_int,
+                                _c_float, _vp, _vp]),
+    "g4_softcap_argmax": (_c_int, [_vp, _c_int, _i64, _c_float, _vp, _vp, _sz, _vp, _vp]),
+    "g4_argmax_workspace_bytes": (_sz, [_c_int, _i64]),
+    "g4_fill_hash_f32": (_c_int, [_vp, _i64, _u64, _c_float, _c_float, _vp]),
+    "g4_fill_hash_u8": (_c_int, [_vp, _i64, _u64, _vp]),
+    "g4_decode_create": (_c_int, [ctypes.POINTER(DecodeShape), ctypes.POINTER(DecodeWeights),
+                                  ctypes.POINTER(_vp)]),
+    "g4_decode_destroy": (_c_int, [_vp]),
+    "g4_decode_kv": (_c_int, [_vp, _c_int, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+                              ctypes.POINTER(_i64)]),
+    "g4_decode_position": (_c_int, [_vp, ctypes.POINTER(_vp)]),
+    "g4_decode_step": (_c_int, [_vp, _vp, _vp, _vp]),
+    "g4_decode_buffer": (_c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp),
+                                  ctypes.POINTER(_sz)]),
+    "g4_decode_set_stop": (_c_int, [_vp, _c_int]),
 }
 
 _lib = None

@@ -1,4 +1,4 @@
-"""The C ABI library loads and exports every symbol include/g4w8a8.h declares, and refuses bad
+"""The C ABI library loads and exports every symbol include/*.h declares, and refuses bad
 arguments with the reference's messages before touching a device (no compute calls here)."""
 import os
 import re
@@ -9,7 +9,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def header_symbols():
-    text = open(os.path.join(ROOT, "include", "g4w8a8.h")).read()
+    text = "".join(open(os.path.join(ROOT, "include", h)).read()
+                   for h in sorted(os.listdir(os.path.join(ROOT, "include"))) if h.endswith(".h"))
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(g4_[a-z0-9_]+)\s*\(", text)))
 
@@ -92,3 +93,30 @@ def test_kernel_choice_per_shape(g4):
 class _Fake:
     ptr = 0x1000
     kind = 2
+
+
+def test_struct_layouts_match_the_headers(g4, tmp_path):
+    """ctypes mirrors of the C structs: sizes and every field offset, as gcc lays them out."""
+    import ctypes
+    import subprocess
+    structs = {"g4_decode_shape": g4.DecodeShape, "g4_decode_layer": g4.DecodeLayer,
+               "g4_decode_weights": g4.DecodeWeights, "g4_gemv_desc": g4.GemvDesc,
+               "g4_table_split_input": g4.TableSplitInput, "g4_table_slice": g4.TableSlice,
+               "g4_table_split_plan": g4.TableSplitPlan}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "g4decode.h"', 'int main(void){']
+    for cname, py in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in py._fields_:
+            lines.append(f'printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("return 0;}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)],
+                   check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {tuple(l.split()[:2]): int(l.split()[2]) for l in out if l}
+    for cname, py in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for f, _ in py._fields_:
+            assert got[(cname, f)] == getattr(py, f).offset, (cname, f)
