@@ -16,7 +16,8 @@
 //  - exp and tanh are d_expf / d_tanhf: Cody-Waite reduction, a degree-6 Taylor polynomial and
 //    ldexp (tanh of small arguments through the same polynomial as expm1), every step separately
 //    rounded;
-//  - attention runs in chunks of 256 positions, merged in ascending chunk order.
+//  - attention runs in chunks of 32 positions, merged in ascending chunk order; a score is eight
+//    sequential 32-dim dot products combined by a pairwise tree.
 // The projections between these kernels are the library's GEMV/GEMM entry points, which take and
 // give int8 codes: every kernel here that feeds a projection emits its input snap directly.
 #include "g4_internal.h"
@@ -25,60 +26,11 @@
 namespace g4 {
 
 constexpr int kDecThreads = 256;
-constexpr int kAttnChunk = 256;
+constexpr int kAttnChunk = 32;
+constexpr int kAttnMaxHeads = 8;
 
-// ---- the exact-arithmetic building blocks ---------------------------------------------------------
-
-__device__ __forceinline__ float d_expf(float x) {
-    if (x != x) return x;
-    if (x > 88.7f) return __int_as_float(0x7f800000);
-    if (x < -87.0f) return 0.0f;
-    const float n = rintf(__fmul_rn(x, 0x1.715476p+0f));             // round(x * log2 e)
-    float r = __fsub_rn(x, __fmul_rn(n, 0x1.62e4p-1f));              // x - n * ln2_hi (15-bit)
-    r = __fsub_rn(r, __fmul_rn(n, 0x1.7f7d1cp-20f));                 // - n * ln2_lo
-    float p = 0x1.6c16c2p-10f;                                       // 1/720
-    p = __fadd_rn(__fmul_rn(p, r), 0x1.111112p-7f);                  // 1/120
-    p = __fadd_rn(__fmul_rn(p, r), 0x1.555556p-5f);                  // 1/24
-    p = __fadd_rn(__fmul_rn(p, r), 0x1.555556p-3f);                  // 1/6
-    p = __fadd_rn(__fmul_rn(p, r), 0.5f);
-    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
-    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
-    return ldexpf(p, (int)n);
-}
-
-// exp(y) - 1 for |y| <= 0.35: d_expf's Taylor chain stopped before its final + 1, times y.
-__device__ __forceinline__ float d_expm1_small(float y) {
-    float p = 0x1.6c16c2p-10f;
-    p = __fadd_rn(__fmul_rn(p, y), 0x1.111112p-7f);
-    p = __fadd_rn(__fmul_rn(p, y), 0x1.555556p-5f);
-    p = __fadd_rn(__fmul_rn(p, y), 0x1.555556p-3f);
-    p = __fadd_rn(__fmul_rn(p, y), 0.5f);
-    p = __fadd_rn(__fmul_rn(p, y), 1.0f);
-    return __fmul_rn(p, y);
-}
-
-// Below 0.171875 the form -em / (2 + em), em = expm1(-2|x|), avoids the cancellation of 1 - t.
-__device__ __forceinline__ float d_tanhf(float x) {
-    const float ax = fabsf(x);
-    if (ax < 0x1p-12f) return x;
-    float r;
-    if (ax < 0.171875f) {
-        const float em = d_expm1_small(-2.0f * ax);
-        r = __fdiv_rn(-em, __fadd_rn(2.0f, em));
-    } else {
-        const float t = d_expf(-2.0f * ax);
-        r = __fdiv_rn(__fsub_rn(1.0f, t), __fadd_rn(1.0f, t));
-    }
-    return copysignf(r, x);
-}
-
-// geluMul.ts:101-116 in the shader's order.
-__device__ __forceinline__ float d_gelu(float x) {
-    const float cube = __fmul_rn(__fmul_rn(x, x), x);
-    float inner = __fmul_rn(0x1.988454p-1f, __fadd_rn(x, __fmul_rn(0x1.6e4e26p-5f, cube)));
-    inner = fminf(fmaxf(inner, -10.0f), 10.0f);
-    return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, d_tanhf(inner)));
-}
+// d_expf, d_tanhf and d_gelu (the deterministic exp / tanh / gelu) live in g4_internal.h, shared
+// with the GEMV gelu prologues.
 
 // The pairwise tree over 256 lanes (every thread of the block calls it, returns the total).
 __device__ float block_tree_sum(float part, float *lds) {
@@ -244,19 +196,22 @@ __global__ __launch_bounds__(kDecThreads) void attn_prologue_kernel(
 
 // ---- attention decode: split partials, then the ordered merge -------------------------------------
 
-// Grid (max chunks, heads, rows). Chunk c covers positions lo + 256 c .. min(+256, pos + 1).
-// Thread t scores position start + t against the query (sequential dot over the 256 dims), the
-// block takes the max, e = exp(s - m), l = tree sum of e, and thread d accumulates
+// Grid (max chunks, rows), 256 threads. Chunk c covers positions lo + 32 c .. min(+32, pos + 1), for
+// every query head of the row at once (heads <= 8 share the one KV head), so each K and V row of
+// the chunk is read once. Scores: thread t takes eighth t & 7 (32 dims, sequential) of position
+// t >> 3 against every head, and the position's eight lanes combine by the pairwise tree
+// ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)) (an xor butterfly: IEEE addition commutes, so
+// every lane ends with the tree's value). Per head (one 32-lane half-wave each): m = max,
+// e = exp(s - m), l = the 32-lane pairwise tree of e. Then thread d accumulates, for every head,
 // sum over positions (ascending) of e * v[d]. Writes (m, l) and o[256] per (row, head, chunk).
 __global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
     const float *q, const float *k_cache, const float *v_cache, int64_t cache_row_stride, int heads,
     int pos_host, const int32_t *pos_dev, int window, float *part_ml, float *part_o, int max_chunks) {
-    __shared__ float lds[kDecThreads];
-    __shared__ float qs[kDecThreads];
-    __shared__ float es[kAttnChunk];
+    __shared__ __align__(16) float qs[kAttnMaxHeads * kDecThreads];
+    __shared__ __align__(16) float es[kAttnMaxHeads * kAttnChunk];
     const int t = threadIdx.x;
-    const int c = blockIdx.x, h = blockIdx.y;
-    const int64_t row = blockIdx.z;
+    const int c = blockIdx.x;
+    const int64_t row = blockIdx.y;
     const int pos = step_pos(pos_host, pos_dev);
     const int lo = window > 0 ? max(0, pos - window + 1) : 0;
     const int chunks = (pos - lo + 1 + kAttnChunk - 1) / kAttnChunk;
@@ -265,53 +220,123 @@ __global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
     const int cnt = min(kAttnChunk, pos + 1 - start);
     const float *kb = k_cache + row * cache_row_stride;
     const float *vb = v_cache + row * cache_row_stride;
-    qs[t] = q[(row * heads + h) * kDecThreads + t];
+    // the chunk's K segment and V rows are requested before the q staging so the loads overlap it
+    const int j = t >> 3, sg = t & 7;
+    const float4 *kr = reinterpret_cast<const float4 *>(
+        kb + (int64_t)(start + min(j, cnt - 1)) * kDecThreads + sg * 32);
+    float4 kq[8];
+#pragma unroll
+    for (int i4 = 0; i4 < 8; ++i4) kq[i4] = kr[i4];
+    float vv[kAttnChunk];
+#pragma unroll
+    for (int u = 0; u < kAttnChunk; ++u)
+        vv[u] = vb[(int64_t)(start + min(u, cnt - 1)) * kDecThreads + t];
+    for (int i = t; i < heads * kDecThreads; i += kDecThreads)
+        qs[i] = q[row * heads * kDecThreads + i];
     __syncthreads();
-    float score = -__int_as_float(0x7f800000);
-    if (t < cnt) {
-        const float4 *kr = reinterpret_cast<const float4 *>(kb + (int64_t)(start + t) * kDecThreads);
-        float d = 0.0f;
-        for (int i = 0; i < kDecThreads / 4; ++i) {
-            const float4 kv = kr[i];
-            d = __fadd_rn(d, __fmul_rn(qs[4 * i], kv.x));
-            d = __fadd_rn(d, __fmul_rn(qs[4 * i + 1], kv.y));
-            d = __fadd_rn(d, __fmul_rn(qs[4 * i + 2], kv.z));
-            d = __fadd_rn(d, __fmul_rn(qs[4 * i + 3], kv.w));
+
+    // scores
+    float sc[kAttnMaxHeads];
+#pragma unroll
+    for (int h = 0; h < kAttnMaxHeads; ++h) {
+        float a = 0.0f;
+        if (h < heads) {
+            const float *qh = qs + h * kDecThreads + sg * 32;
+#pragma unroll
+            for (int i4 = 0; i4 < 8; ++i4) {
+                const float4 qv = *reinterpret_cast<const float4 *>(qh + 4 * i4);
+                const float4 kv = kq[i4];
+                a = __fadd_rn(a, __fmul_rn(qv.x, kv.x));
+                a = __fadd_rn(a, __fmul_rn(qv.y, kv.y));
+                a = __fadd_rn(a, __fmul_rn(qv.z, kv.z));
+                a = __fadd_rn(a, __fmul_rn(qv.w, kv.w));
+            }
         }
-        score = d;
+        a = __fadd_rn(a, __shfl_xor(a, 1));
+        a = __fadd_rn(a, __shfl_xor(a, 2));
+        sc[h] = __fadd_rn(a, __shfl_xor(a, 4));
     }
-    const float m = block_max(score, lds);
-    const float e = t < cnt ? d_expf(__fsub_rn(score, m)) : 0.0f;
-    es[t] = e;
-    const float l = block_tree_sum(e, lds);  // also orders the es writes before the reads below
-    float o = 0.0f;
-    for (int j = 0; j < cnt; ++j) o = __fadd_rn(o, __fmul_rn(es[j], vb[(int64_t)(start + j) * kDecThreads + t]));
-    const int64_t slot = (row * heads + h) * max_chunks + c;
-    part_o[slot * kDecThreads + t] = o;
-    if (t == 0) {
-        part_ml[slot * 2] = m;
-        part_ml[slot * 2 + 1] = l;
+    if (sg == 0) {
+#pragma unroll
+        for (int h = 0; h < kAttnMaxHeads; ++h)
+            if (h < heads) es[h * kAttnChunk + j] = j < cnt ? sc[h] : -__int_as_float(0x7f800000);
+    }
+    __syncthreads();
+
+    // per head, uniform within its 32-lane half-wave: max, exp, the pairwise sum
+    const int hh = t >> 5, p = t & 31;
+    if (hh < heads) {
+        const float x = es[hh * kAttnChunk + p];
+        float m = x;
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 32));
+        const float e = p < cnt ? d_expf(__fsub_rn(x, m)) : 0.0f;
+        float l = e;
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) l = __fadd_rn(l, __shfl_down(l, off, 32));
+        es[hh * kAttnChunk + p] = e;
+        if (p == 0) {
+            const int64_t slot = (row * heads + hh) * max_chunks + c;
+            part_ml[slot * 2] = m;
+            part_ml[slot * 2 + 1] = l;
+        }
+    }
+    __syncthreads();
+
+    // o[h][d] = sum over positions (ascending) of e[h][j] * v[j][d]
+#pragma unroll
+    for (int h = 0; h < kAttnMaxHeads; ++h) {
+        if (h < heads) {
+            float o = 0.0f;
+#pragma unroll
+            for (int u = 0; u < kAttnChunk; ++u)
+                if (u < cnt) o = __fadd_rn(o, __fmul_rn(es[h * kAttnChunk + u], vv[u]));
+            part_o[((row * heads + h) * max_chunks + c) * kDecThreads + t] = o;
+        }
     }
 }
 
-// Grid (heads, rows); thread d merges dim d: M = max m_c, w_c = exp(m_c - M),
-// L = sum l_c w_c, O = sum o_c w_c (ascending c), out = O / L, then the o_proj input snap.
+// Grid (heads, rows); thread d merges dim d over the chunks in ascending order: M = max m_c,
+// w_c = exp(m_c - M) (once per chunk, staged in LDS), L = sum l_c w_c, O = sum o_c w_c,
+// out = O / L, then the o_proj input snap.
 __global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(
     const float *part_ml, const float *part_o, int heads, int pos_host, const int32_t *pos_dev,
     int window, int max_chunks, float in_scale, int8_t *codes, float *out_f32) {
+    __shared__ float red[kDecThreads];
+    __shared__ float ws[kDecThreads];
+    __shared__ float ls[kDecThreads];
     const int t = threadIdx.x, h = blockIdx.x;
     const int64_t row = blockIdx.y;
     const int pos = step_pos(pos_host, pos_dev);
     const int lo = window > 0 ? max(0, pos - window + 1) : 0;
     const int chunks = (pos - lo + 1 + kAttnChunk - 1) / kAttnChunk;
     const int64_t slot0 = (row * heads + h) * max_chunks;
-    float M = -__int_as_float(0x7f800000);
-    for (int c = 0; c < chunks; ++c) M = fmaxf(M, part_ml[(slot0 + c) * 2]);
+    float m = -__int_as_float(0x7f800000);
+    for (int c = t; c < chunks; c += kDecThreads) m = fmaxf(m, part_ml[(slot0 + c) * 2]);
+    const float M = block_max(m, red);
     float L = 0.0f, O = 0.0f;
-    for (int c = 0; c < chunks; ++c) {
-        const float w = d_expf(__fsub_rn(part_ml[(slot0 + c) * 2], M));
-        L = __fadd_rn(L, __fmul_rn(part_ml[(slot0 + c) * 2 + 1], w));
-        O = __fadd_rn(O, __fmul_rn(part_o[(slot0 + c) * kDecThreads + t], w));
+    for (int c0 = 0; c0 < chunks; c0 += kDecThreads) {
+        const int n = min(kDecThreads, chunks - c0);
+        if (t < n) {
+            ws[t] = d_expf(__fsub_rn(part_ml[(slot0 + c0 + t) * 2], M));
+            ls[t] = part_ml[(slot0 + c0 + t) * 2 + 1];
+        }
+        __syncthreads();
+        constexpr int kB = 16;  // partials loaded together (indices clamped, so all valid)
+        for (int u0 = 0; u0 < n; u0 += kB) {
+            float oo[kB];
+#pragma unroll
+            for (int u = 0; u < kB; ++u)
+                oo[u] = part_o[(slot0 + c0 + min(u0 + u, n - 1)) * kDecThreads + t];
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                if (u0 + u < n) {
+                    L = __fadd_rn(L, __fmul_rn(ls[u0 + u], ws[u0 + u]));
+                    O = __fadd_rn(O, __fmul_rn(oo[u], ws[u0 + u]));
+                }
+            }
+        }
+        __syncthreads();
     }
     const float y = __fdiv_rn(O, L);
     const int64_t o = (row * heads + h) * kDecThreads + t;
@@ -555,6 +580,9 @@ int g4_attention_decode(const float *q, const float *k_cache, const float *v_cac
     if (!q || !k_cache || !v_cache || !workspace || rows <= 0 || heads <= 0 || pos < 0 ||
         window < 0)
         return set_error(G4_ERR_INVALID, "attention-decode needs q, k, v, a workspace and pos >= 0");
+    if (heads > kAttnMaxHeads)
+        return set_error(G4_ERR_UNSUPPORTED, "attention-decode: %d query heads per KV head (at most %d)",
+                         heads, kAttnMaxHeads);
     if (!codes && !out_f32) return set_error(G4_ERR_INVALID, "attention-decode: no output");
     if (codes && in_scale == 0.0f)
         return set_error(G4_ERR_INVALID, "attention-decode: int8 codes need the o_proj inScale");
@@ -565,7 +593,7 @@ int g4_attention_decode(const float *q, const float *k_cache, const float *v_cac
                          workspace_bytes, need);
     float *part_ml = workspace;
     float *part_o = workspace + (size_t)rows * heads * chunks * 2;
-    hipLaunchKernelGGL(attn_split_kernel, dim3(chunks, heads, rows), dim3(kDecThreads), 0,
+    hipLaunchKernelGGL(attn_split_kernel, dim3(chunks, rows), dim3(kDecThreads), 0,
                        as_stream(stream), q, k_cache, v_cache, cache_row_stride, heads, pos,
                        pos_dev, window, part_ml, part_o, chunks);
     G4_LAUNCHED("attn_split_kernel");

@@ -10,10 +10,11 @@
 //   q-norm-rope (+ kv-norm-rope-store)   -> q f32; K, V rows at the position
 //   attention decode over the layer's cache (own, or the last producer of its kind) -> o input snap
 //   o GEMV; norm-residual-norm (post_attention_layernorm, residual, pre_feedforward_layernorm)
-//   gate, up GEMV; gelu-mul (down's snap); down GEMV
+//   gate, up GEMV; down GEMV reading gelu(gate) * up through its fused prologue (batch 1), or the
+//   gelu-mul pass then the GEMV
 //   norm-residual (post_feedforward_layernorm, residual), snapped for per_layer_input_gate
-//   per_layer_input_gate (int8 GEMV); gelu times the layer's per-layer input row (the projection's
-//   snap); per_layer_projection (int8 GEMV)
+//   per_layer_input_gate (int8 GEMV); per_layer_projection (int8 GEMV) reading gelu(gate) times the
+//   layer's per-layer-input row through the same prologue (or the gelu-mul pass, then the GEMV)
 //   norm-residual-norm (post_per_layer_input_norm, residual, layer_scalar, then the next layer's
 //   input_layernorm, or the final norm on the last layer)
 // Embedding phase (plan.ts:720-729): tied int4 embed gather (x sqrt(hidden) folded), PLE gather,
@@ -175,8 +176,8 @@ int check_weights(const g4_decode_shape &s, const g4_decode_weights &w) {
 
 // A grouped M = 1 plan, or none when a shape has no streaming class (the runner then launches
 // each projection through g4_linear).
-int try_plan(const g4_gemv_desc *descs, int count, Plan &out) {
-    const int rc = g4_qgemv_plan_create(descs, count, &out.p);
+int try_plan(const g4_gemv_desc *descs, int count, Plan &out, const g4_gelu_act *acts = nullptr) {
+    const int rc = g4_qgemv_plan_create_gelu(descs, acts, count, &out.p);
     if (rc == G4_ERR_UNSUPPORTED) {
         out.p = nullptr;
         clear_error();
@@ -243,14 +244,19 @@ int build(g4_decode &d) {
         g4_gemv_desc gu[2] = {desc(L.gate, L.gate_s, d.xcodes, d.gc, 4, H, F, G4_KIND_I8, in, out),
                               desc(L.up, L.up_s, d.xcodes, d.uc, 4, H, F, G4_KIND_I8, in, out)};
         G4_TRY(try_plan(gu, 2, P[P_GATEUP]));
-        g4_gemv_desc dn = desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out);
-        G4_TRY(try_plan(&dn, 1, P[P_DOWN]));
+        // down_proj reads gelu(gate) * up through the fused prologue (qgemv-4bit-gelu)
+        g4_gemv_desc dn = desc(L.down, L.down_s, d.gc, d.dc, 4, F, H, G4_KIND_I8, in, out);
+        const g4_gelu_act dna{d.uc, G4_KIND_I8, out, out, 0};
+        G4_TRY(try_plan(&dn, 1, P[P_DOWN], &dna));
         g4_gemv_desc pg = desc(L.ple_gate, L.ple_gate_s, d.xcodes, d.pgc, 8, H, s.ple_dim,
                                G4_KIND_I8, in, out);
         G4_TRY(try_plan(&pg, 1, P[P_PLE_GATE]));
-        g4_gemv_desc pp = desc(L.ple_proj, L.ple_proj_s, d.pac, d.ppc, 8, s.ple_dim, H, G4_KIND_I8,
+        // per_layer_projection reads gelu(gate) * the layer's per-layer-input row (qgemv-8bit-gelu
+        // with upOffset = layer * ple_dim)
+        g4_gemv_desc pp = desc(L.ple_proj, L.ple_proj_s, d.pgc, d.ppc, 8, s.ple_dim, H, G4_KIND_I8,
                                in, out);
-        G4_TRY(try_plan(&pp, 1, P[P_PLE_PROJ]));
+        const g4_gelu_act ppa{d.per_layer, G4_KIND_F32, out, 0.0f, (int64_t)l * s.ple_dim};
+        G4_TRY(try_plan(&pp, 1, P[P_PLE_PROJ], &ppa));
     }
     g4_gemv_desc pm = desc(d.w.ple_model_proj, d.w.ple_model_proj_s, d.embed_codes, d.ple_codes, 4,
                            H, PL, G4_KIND_I8, in, out);
@@ -297,15 +303,23 @@ int run_layer(g4_decode &d, int l, void *st) {
     G4_TRY(run_linear_rows(d, plan(P_GATEUP), desc(L.gate, L.gate_s, d.xcodes, d.gc, 4, H, F, G4_KIND_I8, in, out), st));
     if (!plan(P_GATEUP).p)
         G4_TRY(run_linear_rows(d, none, desc(L.up, L.up_s, d.xcodes, d.uc, 4, H, F, G4_KIND_I8, in, out), st));
-    G4_TRY(g4_gelu_mul(d.gc, out, d.uc, out, nullptr, 0, B, F, in, d.act, st));
-    G4_TRY(run_linear_rows(d, plan(P_DOWN), desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out), st));
+    if (plan(P_DOWN).p) {
+        G4_TRY(g4_qgemv_plan_launch(plan(P_DOWN).p, st));  // gelu prologue fused
+    } else {
+        G4_TRY(g4_gelu_mul(d.gc, out, d.uc, out, nullptr, 0, B, F, in, d.act, st));
+        G4_TRY(run_linear_rows(d, none, desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out), st));
+    }
     G4_TRY(g4_rms_join(d.dc, G4_KIND_I8, out, L.post_ffn_norm, d.hidden, 1.0f, nullptr, B, H,
                        s.eps, in, d.hidden, d.xcodes, st));
     // per-layer-input block
     G4_TRY(run_linear_rows(d, plan(P_PLE_GATE), desc(L.ple_gate, L.ple_gate_s, d.xcodes, d.pgc, 8, H, s.ple_dim, G4_KIND_I8, in, out), st));
-    G4_TRY(g4_gelu_mul(d.pgc, out, nullptr, 0.0f, d.per_layer + (size_t)l * s.ple_dim,
-                       (int64_t)s.layers * s.ple_dim, B, s.ple_dim, in, d.pac, st));
-    G4_TRY(run_linear_rows(d, plan(P_PLE_PROJ), desc(L.ple_proj, L.ple_proj_s, d.pac, d.ppc, 8, s.ple_dim, H, G4_KIND_I8, in, out), st));
+    if (plan(P_PLE_PROJ).p) {
+        G4_TRY(g4_qgemv_plan_launch(plan(P_PLE_PROJ).p, st));  // gelu prologue fused
+    } else {
+        G4_TRY(g4_gelu_mul(d.pgc, out, nullptr, 0.0f, d.per_layer + (size_t)l * s.ple_dim,
+                           (int64_t)s.layers * s.ple_dim, B, s.ple_dim, in, d.pac, st));
+        G4_TRY(run_linear_rows(d, none, desc(L.ple_proj, L.ple_proj_s, d.pac, d.ppc, 8, s.ple_dim, H, G4_KIND_I8, in, out), st));
+    }
     // the tail join: residual, layer scalar, then the next input norm (or the final norm)
     const bool last = l + 1 == s.layers;
     const float *next_norm = last ? d.w.final_norm : d.layers[l + 1].input_norm;

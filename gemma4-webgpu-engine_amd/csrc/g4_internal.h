@@ -41,12 +41,28 @@ inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s);
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 
-// Validates one GEMV descriptor against what the GEMV kernels assume (qgemv.hip).
-int check_job_desc(const g4_gemv_desc &d, const char *who);
+// The gelu activation prologue of one GEMV job (qgemv.ts:359-400): the job's x is the gate, and
+// the GEMV reads gelu_tanh(gate[i]) * up[i] in place of x[i]. `up` already carries the offset;
+// null means no prologue. gate codes (x_kind int8) are times g_scale, up codes times u_scale.
+struct GeluAct {
+    const void *up = nullptr;
+    float g_scale = 0.0f;
+    float u_scale = 0.0f;
+    int up_kind = G4_KIND_F32;
+};
+
+// The internal form of a public g4_gelu_act (NULL or a NULL up: no prologue).
+GeluAct gelu_act_of(const g4_gelu_act *a);
+
+// Validates one GEMV descriptor (and its prologue, when act.up is set) against what the GEMV
+// kernels assume (qgemv.hip).
+int check_job_desc(const g4_gemv_desc &d, const GeluAct &act, const char *who);
 
 // Launches calibrated M = 1 GEMVs on the streaming kernel when every one has a compiled shape
-// class (qgemv_stream.hip); otherwise enqueues nothing and sets *launched = false.
-int stream_try_launch(const g4_gemv_desc *descs, int count, hipStream_t stream, bool *launched);
+// class (qgemv_stream.hip); otherwise enqueues nothing and sets *launched = false. acts: one per
+// descriptor, or null for none.
+int stream_try_launch(const g4_gemv_desc *descs, const GeluAct *acts, int count, hipStream_t stream,
+                      bool *launched);
 
 // The streaming shape class of a row of K codes at `bits`, or -1 (qgemv_stream.hip).
 int stream_class_for(int bits, int k);
@@ -84,8 +100,98 @@ __device__ __forceinline__ float srq_recip(float s, bool &ok) {
     return r;
 }
 
+// ---- device: deterministic exp, tanh and gelu (geluMul.ts:101-116) --------------------------------
+// Every step is one IEEE f32 rounding (no FMA), so a CPU restatement (oracle/g4_decode_oracle.c)
+// reproduces them bit for bit. exp: Cody-Waite reduction by ln 2 (15-bit high part), a degree-6
+// Taylor polynomial on |r| <= ln2 / 2, ldexp; within 3 ulp of exp. tanh: x below 2^-12, the exact
+// form -em / (2 + em) with em = expm1(-2|x|) below 0.171875, else (1 - t) / (1 + t) with
+// t = exp(-2|x|); within 8 ulp of tanh. gelu: the tanh form in the shader's operation order.
+
+__device__ __forceinline__ float d_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.7f) return __int_as_float(0x7f800000);
+    if (x < -87.0f) return 0.0f;
+    const float n = rintf(__fmul_rn(x, 0x1.715476p+0f));             // round(x * log2 e)
+    float r = __fsub_rn(x, __fmul_rn(n, 0x1.62e4p-1f));              // x - n * ln2_hi (15-bit)
+    r = __fsub_rn(r, __fmul_rn(n, 0x1.7f7d1cp-20f));                 // - n * ln2_lo
+    float p = 0x1.6c16c2p-10f;                                       // 1/720
+    p = __fadd_rn(__fmul_rn(p, r), 0x1.111112p-7f);                  // 1/120
+    p = __fadd_rn(__fmul_rn(p, r), 0x1.555556p-5f);                  // 1/24
+    p = __fadd_rn(__fmul_rn(p, r), 0x1.555556p-3f);                  // 1/6
+    p = __fadd_rn(__fmul_rn(p, r), 0.5f);
+    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
+    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
+    return ldexpf(p, (int)n);
+}
+
+// exp(y) - 1 for |y| <= 0.35: d_expf's Taylor chain stopped before its final + 1, times y.
+__device__ __forceinline__ float d_expm1_small(float y) {
+    float p = 0x1.6c16c2p-10f;
+    p = __fadd_rn(__fmul_rn(p, y), 0x1.111112p-7f);
+    p = __fadd_rn(__fmul_rn(p, y), 0x1.555556p-5f);
+    p = __fadd_rn(__fmul_rn(p, y), 0x1.555556p-3f);
+    p = __fadd_rn(__fmul_rn(p, y), 0.5f);
+    p = __fadd_rn(__fmul_rn(p, y), 1.0f);
+    return __fmul_rn(p, y);
+}
+
+// Below 0.171875 the form -em / (2 + em), em = expm1(-2|x|), avoids the cancellation of 1 - t.
+__device__ __forceinline__ float d_tanhf(float x) {
+    const float ax = fabsf(x);
+    if (ax < 0x1p-12f) return x;
+    float r;
+    if (ax < 0.171875f) {
+        const float em = d_expm1_small(-2.0f * ax);
+        r = __fdiv_rn(-em, __fadd_rn(2.0f, em));
+    } else {
+        const float t = d_expf(-2.0f * ax);
+        r = __fdiv_rn(__fsub_rn(1.0f, t), __fadd_rn(1.0f, t));
+    }
+    return copysignf(r, x);
+}
+
+// geluMul.ts:101-116 in the shader's order.
+__device__ __forceinline__ float d_gelu(float x) {
+    const float cube = __fmul_rn(__fmul_rn(x, x), x);
+    float inner = __fmul_rn(0x1.988454p-1f, __fadd_rn(x, __fmul_rn(0x1.6e4e26p-5f, cube)));
+    inner = fminf(fmaxf(inner, -10.0f), 10.0f);
+    return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, d_tanhf(inner)));
+}
+
+
 // The closing expression of every quantized linear (qgemv.ts:1168-1172, :680-686), in its order:
 // one f32 multiply folds the input scale into the row scale, one more multiplies the reduced sum.
+// Eight activation values e .. e + 7 of an f32 vector, or of int8 codes times `scale`.
+__device__ __forceinline__ void act_vals8(const void *p, int kind, float scale, int64_t e,
+                                          float v[8]) {
+    if (kind == G4_KIND_I8) {
+        const uint2 w = *reinterpret_cast<const uint2 *>(reinterpret_cast<const int8_t *>(p) + e);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = __fmul_rn((float)(int8_t)((w.x >> (8 * i)) & 0xff), scale);
+            v[4 + i] = __fmul_rn((float)(int8_t)((w.y >> (8 * i)) & 0xff), scale);
+        }
+    } else {
+        const float4 *q = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(p) + e);
+        const float4 a = q[0], b = q[1];
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w;
+        v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    }
+}
+
+// The gelu prologue's codes for activations e .. e + 7: srq(gelu_tanh(gate) * up) on s, the
+// gelu-mul kernel's expression and snap (geluMul.ts:101-116), so the fused GEMV reads exactly the
+// codes the separate pass would have written.
+__device__ __forceinline__ void gelu_codes8(const void *gate, int g_kind, float gs, const void *up,
+                                            int u_kind, float us, int64_t e, float s, float r,
+                                            bool r_ok, int c[8]) {
+    float g[8], u[8];
+    act_vals8(gate, g_kind, gs, e, g);
+    act_vals8(up, u_kind, us, e, u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = (int)srq_code_fast(__fmul_rn(d_gelu(g[i]), u[i]), s, r, r_ok);
+}
+
 __device__ __forceinline__ float linear_epilogue(float in_scale, float row_scale, float sum) {
     return __fmul_rn(__fmul_rn(in_scale, row_scale), sum);
 }

@@ -46,6 +46,7 @@ struct GemvJob {
     int wg_begin;
     int passes;
     int kwaves;  // waves splitting K inside a block: 1, 2 or 4
+    GeluAct act; // the gelu prologue (act.up set): x is the gate
 };
 
 struct GemvLaunch {
@@ -244,7 +245,11 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_int_kernel(GemvLaunch L) {
             const int gi = COLS == 1 ? g : g - col * groups;
             int c[8];
             const int64_t e = (int64_t)col * k + c_lo + gi * 8;
-            load_codes8(J.x, J.x_kind, e, J.in_scale, r, r_ok, c);
+            if (J.act.up)
+                gelu_codes8(J.x, J.x_kind, J.act.g_scale, J.act.up, J.act.up_kind, J.act.u_scale, e,
+                            J.in_scale, r, r_ok, c);
+            else
+                load_codes8(J.x, J.x_kind, e, J.in_scale, r, r_ok, c);
             uint2 packed;
             if (bits == 4) {
                 packed.x = pack4(c[0], c[2], c[4], c[6]);
@@ -437,7 +442,37 @@ int check_job(const GemvJob &J, int cols, const char *who) {
     if (!aligned16(J.w) || !aligned16(J.x))
         return set_error(G4_ERR_INVALID, "%s: wq and x must be 16-byte aligned", who);
     if (cols < 1 || cols > 2) return set_error(G4_ERR_INVALID, "%s: cols %d not in 1..2", who, cols);
+    if (J.act.up) {
+        // qgemv.ts:359-400: the prologue binds gate and up in place of x
+        if (J.in_scale == 0.0f)
+            return set_error(G4_ERR_UNSUPPORTED,
+                             "%s: the fused gelu prologue runs calibrated sites (inScale != 0); run "
+                             "g4_gelu_mul then the GEMV", who);
+        if (cols != 1) return set_error(G4_ERR_INVALID, "%s: the gelu prologue is single-column", who);
+        if (J.x_kind != G4_KIND_F32 && J.x_kind != G4_KIND_I8)
+            return set_error(G4_ERR_INVALID, "%s: gate must be f32 or int8 codes", who);
+        if (J.act.up_kind != G4_KIND_F32 && J.act.up_kind != G4_KIND_I8)
+            return set_error(G4_ERR_INVALID, "%s: up must be f32 or int8 codes", who);
+        const uintptr_t need_up = J.act.up_kind == G4_KIND_F32 ? 15 : 7;
+        if (reinterpret_cast<uintptr_t>(J.act.up) & need_up)
+            return set_error(G4_ERR_INVALID, "%s: up (after upOffset) must be %d-byte aligned", who,
+                             (int)need_up + 1);
+        if ((J.x_kind == G4_KIND_I8 && !std::isfinite(J.act.g_scale)) ||
+            (J.act.up_kind == G4_KIND_I8 && !std::isfinite(J.act.u_scale)))
+            return set_error(G4_ERR_INVALID, "%s: gate and up scales must be finite", who);
+    }
     return G4_OK;
+}
+
+GeluAct gelu_act_of(const g4_gelu_act *a) {
+    GeluAct g;
+    if (!a || !a->up) return g;
+    const size_t elem = a->up_kind == G4_KIND_I8 ? 1 : 4;
+    g.up = reinterpret_cast<const uint8_t *>(a->up) + (size_t)a->up_offset * elem;
+    g.up_kind = a->up_kind;
+    g.g_scale = a->gate_scale;
+    g.u_scale = a->up_scale;
+    return g;
 }
 
 static g4_gemv_desc desc_of(const GemvJob &J) {
@@ -472,15 +507,23 @@ static GemvJob job_of(const g4_gemv_desc &d) {
     return J;
 }
 
-int check_job_desc(const g4_gemv_desc &d, const char *who) { return check_job(job_of(d), 1, who); }
+int check_job_desc(const g4_gemv_desc &d, const GeluAct &act, const char *who) {
+    GemvJob J = job_of(d);
+    J.act = act;
+    return check_job(J, 1, who);
+}
 
 // Single-column launches of calibrated jobs go to the streaming kernel when their shapes allow.
 static int try_stream(const GemvLaunch &L, int cols, hipStream_t stream, bool *launched) {
     *launched = false;
     if (cols != 1 || L.splits > 1) return G4_OK;
     g4_gemv_desc d[G4_MAX_GROUP];
-    for (int i = 0; i < L.count; ++i) d[i] = desc_of(L.job[i]);
-    return stream_try_launch(d, L.count, stream, launched);
+    GeluAct a[G4_MAX_GROUP];
+    for (int i = 0; i < L.count; ++i) {
+        d[i] = desc_of(L.job[i]);
+        a[i] = L.job[i].act;
+    }
+    return stream_try_launch(d, a, L.count, stream, launched);
 }
 
 // Waves splitting K in a block: long rows split so every block streams about the same bytes.
@@ -719,6 +762,64 @@ int g4_qgemv_split(int bits, const void *wq, const float *scales, const void *x,
     int rc = check_job(J, 1, bits == 4 ? "qgemv-4bit-split" : "qgemv-8bit-split");
     if (rc) return rc;
     return launch_gemv(L, 1, as_stream(stream));
+}
+
+// qgemv-4bit-gelu / qgemv-8bit-gelu and the gelu exact split (qgemv.ts:359-400, 1668-1696;
+// exactSplit.ts:19-31): the GEMV or split build with the prologue reading gate and up.
+static int gelu_gemv(int bits, const void *wq, const float *scales, const void *gate,
+                     int gate_kind, const g4_gelu_act *act, void *dst, int out_kind, int k,
+                     int num_rows, int k_splits, int exact, float in_scale, float out_scale,
+                     void *stream) {
+    const bool split = k_splits > 0;
+    char who[40];
+    snprintf(who, sizeof who, "qgemv-%dbit-gelu%s", bits, split ? (exact ? "-exact-split" : "-split") : "");
+    if (!act || !act->up) return set_error(G4_ERR_INVALID, "%s needs inputs named gate and up", who);
+    if (bits != 4 && bits != 8) return set_error(G4_ERR_INVALID, "%s: bits must be 4 or 8", who);
+    if (k <= 0 || num_rows <= 0) return set_error(G4_ERR_INVALID, "%s needs params.k and params.numRows", who);
+    const int span = bits == 4 ? 256 : 128;
+    if (k % span != 0)
+        return set_error(G4_ERR_INVALID, "%s needs K a multiple of %d, got %d", who, span, k);
+    if (act->up_offset < 0) return set_error(G4_ERR_INVALID, "%s: upOffset must be >= 0", who);
+    if (split && k_splits != 1 && k_splits != 2 && k_splits != 4 && k_splits != 8)
+        return set_error(G4_ERR_INVALID, "gemv geometry: kSplits must be 1, 2, 4 or 8, got %d", k_splits);
+    if (split && exact && (!(in_scale > 0.0f) || k > 16384))
+        return set_error(G4_ERR_INVALID, "exact split needs calibrated int8 input and K <= 16384");
+    GemvLaunch L{};
+    L.count = 1;
+    L.splits = split ? k_splits : 1;
+    L.split_exact = split && exact ? 1 : 0;
+    GemvJob &J = L.job[0];
+    J.w = reinterpret_cast<const uint8_t *>(wq);
+    J.scales = scales;
+    J.x = gate;
+    J.dst = dst;
+    J.bits = bits;
+    J.x_kind = gate_kind;
+    J.out_kind = split ? G4_KIND_F32 : out_kind;
+    J.k = k;
+    J.rows = num_rows;
+    J.in_scale = in_scale;
+    J.out_scale = split ? 0.0f : out_scale;
+    J.act = gelu_act_of(act);
+    int rc = check_job(J, 1, who);
+    if (rc) return rc;
+    return launch_gemv(L, 1, as_stream(stream));
+}
+
+int g4_qgemv_gelu(int bits, const void *wq, const float *scales, const void *gate, int gate_kind,
+                  const g4_gelu_act *act, void *dst, int out_kind, int k, int num_rows,
+                  float in_scale, float out_scale, void *stream) {
+    return gelu_gemv(bits, wq, scales, gate, gate_kind, act, dst, out_kind, k, num_rows, 0, 0,
+                     in_scale, out_scale, stream);
+}
+
+int g4_qgemv_gelu_split(int bits, const void *wq, const float *scales, const void *gate,
+                        int gate_kind, const g4_gelu_act *act, float *partials, int k,
+                        int num_rows, int k_splits, int exact, float in_scale, void *stream) {
+    if (k_splits < 1)
+        return set_error(G4_ERR_INVALID, "gemv geometry: kSplits must be 1, 2, 4 or 8, got %d", k_splits);
+    return gelu_gemv(bits, wq, scales, gate, gate_kind, act, partials, G4_KIND_F32, k, num_rows,
+                     k_splits, exact, in_scale, 0.0f, stream);
 }
 
 static int merge_common(const float *partials, const float *scales, void *dst, int out_kind,

@@ -36,25 +36,30 @@ constexpr int kBlocksPerCu = 8;
 
 #define G4_GLOBAL __attribute__((address_space(1)))
 
-// One projection of a streaming launch (64 bytes).
+// One projection of a streaming launch (80 bytes). With the gelu prologue (up set) x is the gate
+// and the block snaps gelu_tanh(gate) * up instead of x.
 struct StreamJob {
     const uint8_t *w;
     const float *scales;
     const void *x;
     void *dst;
+    const void *up;
     int k;
     int rows;
     int tile_begin;
     int tiles;
     float in_scale;
     float out_scale;
+    float g_scale;
+    float u_scale;
     int8_t bits;
     int8_t x_kind;
     int8_t out_kind;
     int8_t cls;
-    int pad;
+    int8_t up_kind;
+    int8_t pad[3];
 };
-static_assert(sizeof(StreamJob) == 64, "StreamJob is one 64-byte record");
+static_assert(sizeof(StreamJob) == 80, "StreamJob is one 80-byte record");
 
 struct StreamArgs {
     const StreamJob *table;  // device table (plan launches); null for kernel-argument jobs
@@ -204,12 +209,39 @@ __device__ __forceinline__ int snap_kind(const StreamJob &J, uint8_t *xs, int ti
     return local;
 }
 
+// The gelu prologue's snap: codes of gelu_tanh(gate) * up for the job's K activations.
+__device__ __forceinline__ int snap_gelu(const StreamJob &J, uint8_t *xs, int tid) {
+    bool r_ok;
+    const float s = J.in_scale;
+    const float rcp = srq_recip(s, r_ok);
+    const int groups = J.k >> 3;
+    int local = 0;
+    for (int g = tid; g < groups; g += kStreamThreads) {
+        int c[8];
+        gelu_codes8(J.x, J.x_kind, J.g_scale, J.up, J.up_kind, J.u_scale, (int64_t)g * 8, s, rcp,
+                    r_ok, c);
+        uint2 packed;
+        if (J.bits == 4) {
+            packed.x = pack_bytes(c[0], c[2], c[4], c[6]);
+            packed.y = pack_bytes(c[1], c[3], c[5], c[7]);
+        } else {
+            packed.x = pack_bytes(c[0], c[1], c[2], c[3]);
+            packed.y = pack_bytes(c[4], c[5], c[6], c[7]);
+        }
+        *reinterpret_cast<uint2 *>(xs + g * 8) = packed;
+        local += c[0] + c[1] + c[2] + c[3] + c[4] + c[5] + c[6] + c[7];
+    }
+    return local;
+}
+
 // Snaps the K activations of job J into int8 codes in LDS (4-bit jobs: each 8-code group stored
 // as [x0 x2 x4 x6 | x1 x3 x5 x7] so a weight word's low and high nibbles each dot one half) and
 // returns sum(xq) over the whole vector, which takes the 4-bit zero point off once per row.
 __device__ __forceinline__ int snap_activations(const StreamJob &J, uint8_t *xs, int *s_sum, int tid) {
     int local;
-    if (J.x_kind == G4_KIND_F16)
+    if (J.up)
+        local = snap_gelu(J, xs, tid);
+    else if (J.x_kind == G4_KIND_F16)
         local = snap_kind<G4_KIND_F16>(J, xs, tid);
     else if (J.x_kind == G4_KIND_F32)
         local = snap_kind<G4_KIND_F32>(J, xs, tid);
@@ -332,8 +364,8 @@ void qgemv_stream_kernel(StreamArgs A) {
     }
 }
 
-// Fills a StreamJob from a validated descriptor; returns false when no class fits.
-bool stream_job_from(const g4_gemv_desc &d, StreamJob &J) {
+// Fills a StreamJob from a validated descriptor and prologue; returns false when no class fits.
+bool stream_job_from(const g4_gemv_desc &d, const GeluAct &act, StreamJob &J) {
     const int cls = stream_class_for(d.bits, d.k);
     if (cls < 0 || d.in_scale == 0.0f) return false;
     J = StreamJob{};
@@ -349,6 +381,10 @@ bool stream_job_from(const g4_gemv_desc &d, StreamJob &J) {
     J.x_kind = (int8_t)d.x_kind;
     J.out_kind = (int8_t)d.out_kind;
     J.cls = (int8_t)cls;
+    J.up = act.up;
+    J.up_kind = (int8_t)act.up_kind;
+    J.g_scale = act.g_scale;
+    J.u_scale = act.u_scale;
     return true;
 }
 
@@ -388,12 +424,13 @@ int launch_stream_karg(StreamJob *jobs, int count, hipStream_t stream) {
 
 // Launches the jobs on the streaming kernel when every one of them is calibrated and has a shape
 // class; otherwise enqueues nothing and reports *launched = false.
-int stream_try_launch(const g4_gemv_desc *descs, int count, hipStream_t stream, bool *launched) {
+int stream_try_launch(const g4_gemv_desc *descs, const GeluAct *acts, int count, hipStream_t stream,
+                      bool *launched) {
     *launched = false;
     if (count < 1 || count > kMaxKargJobs) return G4_OK;
     StreamJob jobs[kMaxKargJobs];
     for (int i = 0; i < count; ++i)
-        if (!stream_job_from(descs[i], jobs[i])) return G4_OK;
+        if (!stream_job_from(descs[i], acts ? acts[i] : GeluAct{}, jobs[i])) return G4_OK;
     int rc = launch_stream_karg(jobs, count, stream);
     if (rc == G4_OK) *launched = true;
     return rc;
@@ -418,15 +455,23 @@ struct g4_gemv_plan {
 extern "C" {
 
 int g4_qgemv_plan_create(const g4_gemv_desc *descs, int count, g4_gemv_plan **out) {
+    return g4_qgemv_plan_create_gelu(descs, nullptr, count, out);
+}
+
+int g4_qgemv_plan_create_gelu(const g4_gemv_desc *descs, const g4_gelu_act *acts, int count,
+                              g4_gemv_plan **out) {
     if (!out) return set_error(G4_ERR_INVALID, "g4_qgemv_plan_create: plan is NULL");
     *out = nullptr;
     if (!descs || count < 1)
         return set_error(G4_ERR_INVALID, "g4_qgemv_plan_create: needs at least one descriptor");
     std::vector<StreamJob> jobs(count);
     for (int i = 0; i < count; ++i) {
-        int rc = check_job_desc(descs[i], "GEMV plan");
+        if (acts && acts[i].up && acts[i].up_offset < 0)
+            return set_error(G4_ERR_INVALID, "GEMV plan: projection %d has a negative upOffset", i);
+        const GeluAct act = gelu_act_of(acts ? &acts[i] : nullptr);
+        int rc = check_job_desc(descs[i], act, "GEMV plan");
         if (rc) return rc;
-        if (!stream_job_from(descs[i], jobs[i]))
+        if (!stream_job_from(descs[i], act, jobs[i]))
             return set_error(G4_ERR_UNSUPPORTED,
                              "GEMV plan: projection %d (bits %d, K %d, inScale %g) has no streaming "
                              "shape class; run it through g4_qgemv",

@@ -39,6 +39,12 @@ class GemvDesc(ctypes.Structure):
                 ("in_scale", _c_float), ("out_scale", _c_float)]
 
 
+class GeluAct(ctypes.Structure):
+    """include/g4w8a8.h g4_gelu_act: the fused gelu prologue's up operand."""
+    _fields_ = [("up", _vp), ("up_kind", _c_int), ("gate_scale", _c_float),
+                ("up_scale", _c_float), ("up_offset", _i64)]
+
+
 class TableSplitInput(ctypes.Structure):
     _fields_ = [("rows", _i64), ("row_bytes", _i64), ("max_storage_buffer_binding_size", _i64),
                 ("max_buffer_size", _i64), ("max_storage_buffers_per_shader_stage", _i64),
@@ -139,6 +145,12 @@ SIGNATURES = {
     "g4_qgemv_merge": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_float, _vp]),
     "g4_qgemv_exact_merge": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_float, _c_float,
                                       _vp]),
+    "g4_qgemv_gelu": (_c_int, [_c_int, _vp, _vp, _vp, _c_int, ctypes.POINTER(GeluAct), _vp, _c_int,
+                               _c_int, _c_int, _c_float, _c_float, _vp]),
+    "g4_qgemv_gelu_split": (_c_int, [_c_int, _vp, _vp, _vp, _c_int, ctypes.POINTER(GeluAct), _vp,
+                                     _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
+    "g4_qgemv_plan_create_gelu": (_c_int, [ctypes.POINTER(GemvDesc), ctypes.POINTER(GeluAct),
+                                           _c_int, ctypes.POINTER(_vp)]),
     "g4_srq_quantize": (_c_int, [_vp, _c_int, _vp, _i64, _c_float, _vp]),
     "g4_ple_gather": (_c_int, [_vp, _vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                _c_int, _i64, _i64, _vp]),
@@ -410,14 +422,26 @@ def qgemv_grouped(items_or_array, stream=None):
     _check(lib().g4_qgemv_grouped(arr, len(arr), stream))
 
 
-class GemvPlan:
-    """A device-resident grouped GEMV over any number of projections (g4_qgemv_plan_*)."""
+def gelu_act(up, up_kind=None, gate_scale=0.0, up_scale=0.0, up_offset=0) -> GeluAct:
+    """The fused gelu prologue's up operand (g4_gelu_act); up_kind defaults to the buffer's."""
+    kind = up.kind if up_kind is None else up_kind
+    return GeluAct(_ptr(up), kind, float(gate_scale), float(up_scale), int(up_offset))
 
-    def __init__(self, items):
+
+class GemvPlan:
+    """A device-resident grouped GEMV over any number of projections (g4_qgemv_plan_*). acts: an
+    optional list (one per item, None for no prologue) of gelu_act(...) prologues."""
+
+    def __init__(self, items, acts=None):
         self._arr = make_group(items)
         self._items = list(items)  # keeps the buffers the plan points at alive
         h = _vp()
-        _check(lib().g4_qgemv_plan_create(self._arr, len(self._arr), ctypes.byref(h)))
+        if acts is None:
+            _check(lib().g4_qgemv_plan_create(self._arr, len(self._arr), ctypes.byref(h)))
+        else:
+            self._acts = (GeluAct * len(items))(*[a if a is not None else GeluAct() for a in acts])
+            _check(lib().g4_qgemv_plan_create_gelu(self._arr, self._acts, len(self._arr),
+                                                   ctypes.byref(h)))
         self.handle = h.value
 
     def launch(self, stream=None):
@@ -438,6 +462,24 @@ class GemvPlan:
             self.close()
         except Exception:
             pass
+
+
+def qgemv_gelu(bits, wq, scales, gate, act: GeluAct, dst, k, num_rows, in_scale, out_scale,
+               gate_kind=None, out_kind=None, stream=None):
+    """qgemv-4bit-gelu / qgemv-8bit-gelu: gelu(gate) * up read in place of x."""
+    _check(lib().g4_qgemv_gelu(bits, _ptr(wq), _ptr(scales), _ptr(gate),
+                               gate.kind if gate_kind is None else gate_kind, ctypes.byref(act),
+                               _ptr(dst), dst.kind if out_kind is None else out_kind, k, num_rows,
+                               float(in_scale), float(out_scale), stream))
+
+
+def qgemv_gelu_split(bits, wq, scales, gate, act: GeluAct, partials, k, num_rows, k_splits, exact,
+                     in_scale, gate_kind=None, stream=None):
+    """qgemv-4bit-gelu-exact-split (exact) or the scaled split over the gelu prologue's codes."""
+    _check(lib().g4_qgemv_gelu_split(bits, _ptr(wq), _ptr(scales), _ptr(gate),
+                                     gate.kind if gate_kind is None else gate_kind,
+                                     ctypes.byref(act), _ptr(partials), k, num_rows, k_splits,
+                                     1 if exact else 0, float(in_scale), stream))
 
 
 def qgemv_split(bits, wq, scales, x, partials, k, num_rows, k_splits, exact, in_scale,

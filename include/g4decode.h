@@ -10,9 +10,9 @@
  * stream, launches only (no host synchronisation), so every call can be graph-captured.
  *
  * The arithmetic is fixed (256-lane strided partial sums then a pairwise tree for every reduction,
- * IEEE sqrt then divide for 1/sqrt, one exp/tanh restatement, attention in splits of 256
- * positions merged in ascending order), so the results are bit-reproducible and a CPU restatement
- * states them exactly. Every kernel that feeds a projection emits that projection's int8 input
+ * IEEE sqrt then divide for 1/sqrt, one exp/tanh restatement, attention in splits of 32 positions
+ * merged in ascending order with segment-wise score dot products), so the results are
+ * bit-reproducible and a CPU restatement states them exactly. Every kernel that feeds a projection emits that projection's int8 input
  * snap (quant.ts:309-334 srqCodes) directly.
  */
 #ifndef G4DECODE_H
@@ -62,7 +62,8 @@ int g4_attn_prologue(const int8_t *q_codes, float q_scale, const int8_t *k_codes
  * attention-decode-split + attention-decode-merge (src/kernels/attention.ts:858-918; the split
  * form of plan.ts:562-570): one query position per row, `heads` query heads sharing the single KV
  * head, scale 1.0 (plan.ts:518-519), window > 0 = the last `window` positions inclusive, 0 =
- * unwindowed. Output: the o_proj input codes on in_scale (codes) and/or the f32 rows (out_f32),
+ * unwindowed; heads <= 8. Output: the o_proj input codes on in_scale (codes) and/or the f32 rows
+ * (out_f32),
  * [rows][heads][256]. With pos_dev, `pos` is the largest position the device word may hold (it
  * sizes the split grid and the workspace; the word is clamped to [0, pos]).
  * workspace: g4_attention_workspace_bytes(...) bytes.

@@ -189,6 +189,41 @@ int g4_qgemv_exact_merge(const float *partials, const float *scales, void *dst, 
                          int num_rows, int k_splits, float in_scale, float out_scale,
                          void *stream);
 
+/*
+ * The fused gelu prologue (GemvPrologue 'gelu', src/kernels/qgemv.ts:359-400): the GEMV reads
+ * x[i] = gelu_tanh(gate[i]) * up[up_offset + i] in place of x, the gelu-mul kernel's expression
+ * (geluMul.ts:101-116), snapped on inScale. The gate is passed where x goes (f32, the reference's
+ * gate output, or int8 codes times gate_scale); `up` is f32 or int8 codes times up_scale. On a
+ * calibrated site the result is bit for bit the unfused gelu-mul + GEMV chain (qgemv.ts:362-368).
+ * Calibrated (inScale != 0), single column only. f32 operands need 16-byte alignment (after the
+ * offset), int8 codes 8-byte.
+ */
+typedef struct g4_gelu_act {
+    const void *up;    /* NULL in a plan entry: that projection has no prologue */
+    int up_kind;       /* G4_KIND_F32 or G4_KIND_I8 */
+    float gate_scale;  /* the gate's int8 codes (x_kind G4_KIND_I8) times this */
+    float up_scale;    /* up_kind G4_KIND_I8: the codes times this */
+    int64_t up_offset; /* elements, the reference's params.upOffset (the per-layer-input slice) */
+} g4_gelu_act;
+
+/* qgemv-4bit-gelu / qgemv-8bit-gelu (registry src/kernels/qgemv.ts:1668-1696, bindGemv(bits,
+ * 'gelu')): the down_proj of a decode MLP and the per_layer_projection. */
+int g4_qgemv_gelu(int bits, const void *wq, const float *scales, const void *gate, int gate_kind,
+                  const g4_gelu_act *act, void *dst, int out_kind, int k, int num_rows,
+                  float in_scale, float out_scale, void *stream);
+
+/* qgemv-4bit-gelu-exact-split (src/kernels/exactSplit.ts:19-31 with the gelu prologue; plan.ts
+ * :594-597 producer down exact partials): the split-K partials of g4_qgemv_split over the gelu
+ * prologue's codes; fold them with g4_qgemv_exact_merge (exact = 1) or g4_qgemv_merge. */
+int g4_qgemv_gelu_split(int bits, const void *wq, const float *scales, const void *gate,
+                        int gate_kind, const g4_gelu_act *act, float *partials, int k,
+                        int num_rows, int k_splits, int exact, float in_scale, void *stream);
+
+/* g4_qgemv_plan_create with a prologue per projection: acts[i] (acts may be NULL) gives
+ * projection i the gelu prologue when acts[i].up is set; descs[i].x is then the gate. */
+int g4_qgemv_plan_create_gelu(const g4_gemv_desc *descs, const g4_gelu_act *acts, int count,
+                              g4_gemv_plan **plan);
+
 /* quant.ts:309-334 srqCodes as a kernel: n activations (f32 or f16) to int8 codes on scale. */
 int g4_srq_quantize(const void *x, int x_kind, int8_t *codes, int64_t n, float scale,
                     void *stream);

@@ -19,7 +19,7 @@ _i64 = ctypes.c_int64
 _f = ctypes.c_float
 
 THREADS = 256
-ATTN_CHUNK = 256
+ATTN_CHUNK = 32
 
 _ready = False
 
@@ -45,6 +45,7 @@ def lib():
                                         _f32p]),
             "g4d_attention_decode": (None, [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _f32p]),
             "g4d_gelu_mul_codes": (None, [_i8p, _f, _i8p, _f, _f32p, _i64, _f, _i8p]),
+            "g4d_gelu_mul_f32_codes": (None, [_f32p, _f32p, _i64, _f, _i8p]),
             "g4d_embed_row": (None, [_u8p, _f, _i64, _f, _f32p]),
             "g4d_ple_combine": (None, [_i8p, _f, _f, _f32p, _f32p, _i64, _i64, _f, _f32p]),
             "g4d_softcap": (None, [_f32p, _i64, _f, _f32p]),
@@ -187,6 +188,15 @@ def gelu_mul_codes(g_codes, g_scale, u_codes, u_scale, in_scale, up_f32=None) ->
     codes = np.empty(g_codes.shape, dtype=np.int8)
     lib().g4d_gelu_mul_codes(_p(g_codes, _i8p), f32(g_scale), _p(u, _i8p), f32(u_scale),
                              _p(up, _f32p), g_codes.size, f32(in_scale), _p(codes, _i8p))
+    return codes
+
+
+# geluMul.ts:219-233 on f32 operands (the reference's gate and up buffers)
+def gelu_mul_f32_codes(g, u, in_scale) -> np.ndarray:
+    g, u = _f32(g), _f32(u)
+    codes = np.empty(g.shape, dtype=np.int8)
+    lib().g4d_gelu_mul_f32_codes(_p(g, _f32p), _p(u, _f32p), g.size, f32(in_scale),
+                                 _p(codes, _i8p))
     return codes
 
 

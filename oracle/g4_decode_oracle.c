@@ -187,6 +187,17 @@ void g4d_kv_norm_rope(const int8_t *k_codes, float k_scale, const int8_t *v_code
     free(tmp);
 }
 
+float g4d_score(const float *q, const float *k, int64_t head_dim) {
+    const int64_t seg = head_dim / 8;
+    float s[8];
+    for (int g = 0; g < 8; ++g) {
+        float acc = 0.0f;
+        for (int64_t i = g * seg; i < (g + 1) * seg; ++i) acc = acc + q[i] * k[i];
+        s[g] = acc;
+    }
+    return ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+}
+
 void g4d_attention_decode(const float *q, const float *k, const float *v, int64_t heads,
                           int64_t head_dim, int64_t p, int64_t window, float *out) {
     const int64_t lo = window > 0 ? (p - window + 1 > 0 ? p - window + 1 : 0) : 0;
@@ -204,9 +215,7 @@ void g4d_attention_decode(const float *q, const float *k, const float *v, int64_
             const int64_t cnt = end - start;
             float mx = -INFINITY;
             for (int64_t j = 0; j < cnt; ++j) {
-                const float *kj = k + (start + j) * head_dim;
-                float d = 0.0f;
-                for (int64_t i = 0; i < head_dim; ++i) d = d + qh[i] * kj[i];
+                const float d = g4d_score(qh, k + (start + j) * head_dim, head_dim);
                 e[j] = d;
                 if (d > mx) mx = d;
             }
@@ -241,6 +250,11 @@ void g4d_gelu_mul_codes(const int8_t *g_codes, float g_scale, const int8_t *u_co
         const float u = up_f32 ? up_f32[i] : (float)u_codes[i] * u_scale;
         codes[i] = or_srq_code(g4d_gelu_tanh(g) * u, in_scale);
     }
+}
+
+void g4d_gelu_mul_f32_codes(const float *g, const float *u, int64_t n, float in_scale,
+                            int8_t *codes) {
+    for (int64_t i = 0; i < n; ++i) codes[i] = or_srq_code(g4d_gelu_tanh(g[i]) * u[i], in_scale);
 }
 
 void g4d_embed_row(const uint8_t *row_codes, float row_scale, int64_t cols, float embed_scale,

@@ -29,7 +29,7 @@ extern "C" {
 #endif
 
 #define G4D_THREADS 256     /* lanes of every reduction */
-#define G4D_ATTN_CHUNK 256  /* positions per attention split */
+#define G4D_ATTN_CHUNK 32   /* positions per attention split */
 
 /* exp(x) in f32 (returns 0 below -87, +inf above 88.7). */
 float g4d_expf(float x);
@@ -88,9 +88,15 @@ void g4d_kv_norm_rope(const int8_t *k_codes, float k_scale, const int8_t *v_code
  * Split form: positions lo .. p in chunks of G4D_ATTN_CHUNK; per chunk m = max score,
  * e = g4d_expf(s - m), l = fixed-order sum of e, o[d] = sum over positions ascending of e * v[d];
  * merge in ascending chunk order with w_c = g4d_expf(m_c - M): L = sum l_c * w_c,
- * O[d] = sum o_c[d] * w_c, out = O / L. Scores are sequential f32 dot products over d.
+ * O[d] = sum o_c[d] * w_c, out = O / L. A score is eight sequential f32 dot products over the
+ * eighths of d, combined by a pairwise tree ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7))
+ * (g4d_score).
  * q: [heads][head_dim]; k, v: [positions][head_dim]; out: [heads][head_dim].
  */
+/* The attention score q . k over head_dim (a multiple of 8): sequential sums over each eighth,
+ * then the pairwise tree ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)). */
+float g4d_score(const float *q, const float *k, int64_t head_dim);
+
 void g4d_attention_decode(const float *q, const float *k, const float *v, int64_t heads,
                           int64_t head_dim, int64_t p, int64_t window, float *out);
 
@@ -98,6 +104,10 @@ void g4d_attention_decode(const float *q, const float *k, const float *v, int64_
  * where g, u are int8 codes; up_f32 (when non NULL) replaces u*su (the per-layer-input form). */
 void g4d_gelu_mul_codes(const int8_t *g_codes, float g_scale, const int8_t *u_codes, float u_scale,
                         const float *up_f32, int64_t n, float in_scale, int8_t *codes);
+
+/* The same with f32 operands (the reference's gate and up buffers): codes = srq(gelu(g) * u). */
+void g4d_gelu_mul_f32_codes(const float *g, const float *u, int64_t n, float in_scale,
+                            int8_t *codes);
 
 /* embedGather.ts:93-113 token embedding with the embed scale folded once:
  * x = (code - 8) * f32(scale[row] * f32(sqrt(1536))) for an int4 row of `cols` codes. */

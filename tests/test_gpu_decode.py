@@ -382,3 +382,43 @@ def test_decode_graph_replay(gpu):
     for (te, le), (tg, lg) in zip(eager, graph):
         assert te == tg
         assert same(le, lg)
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_decode_step_e2b_full(gpu, batch):
+    """BASELINE config 4 at its real shape: 35 layers (15 KV producers), hidden 1536, FFN 6144,
+    8 query heads over one KV head of 256, tied int4 head over 262144 rows, a 4096-position seeded
+    KV, decoding position 4095 (global layers attend over all 4096 positions, sliding ones over
+    512). Every output of the step is compared bit for bit: next tokens, capped logits, the final
+    residual row, the per-layer inputs and each producer's KV row at the position."""
+    import decode_ref as ref
+    import g4decode as gd
+    print(f"decode e2b full batch={batch}", flush=True)
+    shape = gd.Shape(batch=batch, kv_capacity=4096)
+    model = gd.SyntheticModel(shape, seed=4)
+    dec = gd.Decoder(shape, model)
+    dec.fill_kv_history()
+    gpu.synchronize()
+    pos = 4095
+    kv = {}
+    for p in range(shape.kv_producers):
+        k, v = dec.download_kv(p)
+        kv[p] = (k.copy(), v.copy())
+    toks = [1234, 262143, 7][:batch]
+    nxt = gpu.DeviceBuffer.empty((batch,), np.int32)
+    dec.set_position(pos)
+    dec.step(dev(gpu, np.array(toks, np.int32)), nxt)
+    gpu.synchronize()
+    got = {"next": nxt.download(), "logits": dec.download("logits", np.float32),
+           "hidden": dec.download("hidden", np.float32),
+           "per_layer": dec.download("per_layer", np.float32),
+           "head_codes": dec.download("head_codes", np.int8)}
+    dkv = {p: dec.download_kv(p) for p in range(shape.kv_producers)}
+    dec.close()
+    print("device step done; running the CPU composition", flush=True)
+    want = ref.step(shape, ref.Weights(model), kv, toks, pos)
+    print("next tokens", got["next"], want["next"], flush=True)
+    for key in got:
+        assert same(got[key], want[key]), key
+    for p in kv:
+        assert same(dkv[p][0][:, pos], kv[p][0][:, pos]) and same(dkv[p][1][:, pos], kv[p][1][:, pos]), p
