@@ -32,17 +32,25 @@ constexpr int kAttnMaxHeads = 8;
 // d_expf, d_tanhf and d_gelu (the deterministic exp / tanh / gelu) live in g4_internal.h, shared
 // with the GEMV gelu prologues.
 
-// The pairwise tree over 256 lanes (every thread of the block calls it, returns the total).
+// The pairwise tree over 256 lanes: level s adds lane l + s into lane l for l < s, s = 128 .. 1
+// (every thread of the block calls it; returns the total). The two cross-wave levels go through
+// LDS, the six in-wave levels through lane shuffles, so the same tree costs three barriers.
 __device__ float block_tree_sum(float part, float *lds) {
-    const int t = threadIdx.x;
-    lds[t] = part;
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+    if (w >= 2) lds[t - 128] = part;
     __syncthreads();
-    for (int stride = kDecThreads / 2; stride >= 1; stride >>= 1) {
-        if (t < stride) lds[t] = __fadd_rn(lds[t], lds[t + stride]);
-        __syncthreads();
+    if (w < 2) part = __fadd_rn(part, lds[t]);           // s = 128
+    if (w == 1) lds[128 + lane] = part;
+    __syncthreads();
+    if (w == 0) {
+        part = __fadd_rn(part, lds[128 + lane]);         // s = 64
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, __shfl_down(part, off));
+        if (lane == 0) lds[192] = part;
     }
-    const float total = lds[0];
     __syncthreads();
+    const float total = lds[192];
+    __syncthreads();  // the caller may reuse lds at once
     return total;
 }
 
@@ -88,14 +96,22 @@ __global__ __launch_bounds__(kDecThreads) void join_kernel(
     const int t = threadIdx.x;
     const int64_t row = blockIdx.x;
     const int64_t base = row * width;
-    float v[kJoinMaxPer];
-    float part = 0.0f;
+    // every operand is loaded before the first barrier (a barrier also fences the compiler's
+    // load scheduling, so later loads would each cost a memory latency of their own)
+    float v[kJoinMaxPer], ga[kJoinMaxPer], re[kJoinMaxPer], g2[kJoinMaxPer];
 #pragma unroll
     for (int e = 0; e < kJoinMaxPer; ++e) {
         const int i = t + e * kDecThreads;
-        v[e] = i < width ? load_val(src, src_kind, src_scale, base + i) : 0.0f;
-        if (i < width) part = __fadd_rn(part, __fmul_rn(v[e], v[e]));
+        const bool in = i < width;
+        v[e] = in ? load_val(src, src_kind, src_scale, base + i) : 0.0f;
+        ga[e] = in && gain ? gain[i] : 1.0f;
+        re[e] = in && resid ? resid[base + i] : 0.0f;
+        g2[e] = in && gain2 ? gain2[i] : 0.0f;
     }
+    float part = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kJoinMaxPer; ++e)
+        if (t + e * kDecThreads < width) part = __fadd_rn(part, __fmul_rn(v[e], v[e]));
     const float inv = inv_rms(block_tree_sum(part, lds), width, eps);
     float part2 = 0.0f;
 #pragma unroll
@@ -103,9 +119,9 @@ __global__ __launch_bounds__(kDecThreads) void join_kernel(
         const int i = t + e * kDecThreads;
         if (i >= width) continue;
         float y = __fmul_rn(v[e], inv);
-        if (gain) y = __fmul_rn(y, gain[i]);
+        if (gain) y = __fmul_rn(y, ga[e]);
         if (resid) {
-            y = __fadd_rn(resid[base + i], y);
+            y = __fadd_rn(re[e], y);
             if (alpha != 1.0f) y = __fmul_rn(y, alpha);
         }
         v[e] = y;
@@ -118,7 +134,7 @@ __global__ __launch_bounds__(kDecThreads) void join_kernel(
 #pragma unroll
         for (int e = 0; e < kJoinMaxPer; ++e) {
             const int i = t + e * kDecThreads;
-            if (i < width) codes[base + i] = snap_code(__fmul_rn(__fmul_rn(v[e], inv2), gain2[i]), in_scale);
+            if (i < width) codes[base + i] = snap_code(__fmul_rn(__fmul_rn(v[e], inv2), g2[e]), in_scale);
         }
     } else {
 #pragma unroll
@@ -177,19 +193,21 @@ __global__ __launch_bounds__(kDecThreads) void attn_prologue_kernel(
         dst = v_cache + row * cache_row_stride + (int64_t)pos * kDecThreads;
         rotate = false;
     }
+    constexpr int P = kDecThreads / 2;
+    const int i = t < P ? t : t - P;
     const float x = __fmul_rn((float)src[t], scale);
+    const float gt = gain ? gain[t] : 1.0f;
+    const float c = cos_row[i], s = sin_row[i];  // loaded before the barriers, like the rest
     const float inv = inv_rms(block_tree_sum(__fmul_rn(x, x), lds), kDecThreads, eps);
     float y = __fmul_rn(x, inv);
-    if (gain) y = __fmul_rn(y, gain[t]);
+    if (gain) y = __fmul_rn(y, gt);
     if (!rotate) {
         dst[t] = y;
         return;
     }
     xs[t] = y;
     __syncthreads();
-    constexpr int P = kDecThreads / 2;
-    const int i = t < P ? t : t - P;
-    const float lo = xs[i], hi = xs[i + P], c = cos_row[i], s = sin_row[i];
+    const float lo = xs[i], hi = xs[i + P];
     dst[t] = t < P ? __fsub_rn(__fmul_rn(lo, c), __fmul_rn(hi, s))
                    : __fadd_rn(__fmul_rn(hi, c), __fmul_rn(lo, s));
 }
@@ -396,9 +414,10 @@ __global__ __launch_bounds__(kDecThreads) void ple_combine_kernel(
     const int t = threadIdx.x;
     const int64_t o = ((int64_t)blockIdx.y * groups + blockIdx.x) * kDecThreads + t;
     const float x = __fmul_rn(__fmul_rn((float)proj_codes[o], proj_scale), alpha);
+    const float gt = gain[t], id = identity[o];  // loaded before the barriers
     const float inv = inv_rms(block_tree_sum(__fmul_rn(x, x), lds), kDecThreads, eps);
-    const float y = __fmul_rn(__fmul_rn(x, inv), gain[t]);
-    out[o] = __fmul_rn(__fadd_rn(y, identity[o]), 0x1.6a09e6p-1f);
+    const float y = __fmul_rn(__fmul_rn(x, inv), gt);
+    out[o] = __fmul_rn(__fadd_rn(y, id), 0x1.6a09e6p-1f);
 }
 
 // ---- logit softcap and the two-stage argmax ------------------------------------------------------

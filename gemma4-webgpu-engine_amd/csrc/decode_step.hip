@@ -10,11 +10,11 @@
 //   q-norm-rope (+ kv-norm-rope-store)   -> q f32; K, V rows at the position
 //   attention decode over the layer's cache (own, or the last producer of its kind) -> o input snap
 //   o GEMV; norm-residual-norm (post_attention_layernorm, residual, pre_feedforward_layernorm)
-//   gate, up GEMV; down GEMV reading gelu(gate) * up through its fused prologue (batch 1), or the
-//   gelu-mul pass then the GEMV
+//   gate and up GEMV with the gelu-mul pass in their epilogue (batch 1: one paired launch), or the
+//   two GEMVs then the gelu-mul pass; down GEMV
 //   norm-residual (post_feedforward_layernorm, residual), snapped for per_layer_input_gate
-//   per_layer_input_gate (int8 GEMV); per_layer_projection (int8 GEMV) reading gelu(gate) times the
-//   layer's per-layer-input row through the same prologue (or the gelu-mul pass, then the GEMV)
+//   per_layer_input_gate (int8 GEMV) with gelu(gate) times the layer's per-layer-input row in its
+//   epilogue (or the gelu-mul pass after it); per_layer_projection (int8 GEMV)
 //   norm-residual-norm (post_per_layer_input_norm, residual, layer_scalar, then the next layer's
 //   input_layernorm, or the final norm on the last layer)
 // Embedding phase (plan.ts:720-729): tied int4 embed gather (x sqrt(hidden) folded), PLE gather,
@@ -35,6 +35,7 @@ using namespace g4;
 
 struct Plan {
     g4_gemv_plan *p = nullptr;
+    bool gelu = false;  // the gelu-mul pass is folded into this plan's epilogue
 };
 
 struct DeviceAlloc {
@@ -176,13 +177,26 @@ int check_weights(const g4_decode_shape &s, const g4_decode_weights &w) {
 
 // A grouped M = 1 plan, or none when a shape has no streaming class (the runner then launches
 // each projection through g4_linear).
-int try_plan(const g4_gemv_desc *descs, int count, Plan &out, const g4_gelu_act *acts = nullptr) {
-    const int rc = g4_qgemv_plan_create_gelu(descs, acts, count, &out.p);
+int try_plan(const g4_gemv_desc *descs, int count, Plan &out) {
+    const int rc = g4_qgemv_plan_create(descs, count, &out.p);
     if (rc == G4_ERR_UNSUPPORTED) {
         out.p = nullptr;
         clear_error();
         return G4_OK;
     }
+    return rc;
+}
+
+// A plan with the gelu-mul pass in the gate's epilogue; none when a shape has no streaming class
+// (the runner then launches the unfused chain).
+int try_gelu_plan(const g4_gemv_desc &gate, const GeluEpilogue &epi, Plan &out) {
+    const int rc = gemv_plan_create_epilogue(&gate, &epi, 1, &out.p);
+    if (rc == G4_ERR_UNSUPPORTED) {
+        out.p = nullptr;
+        clear_error();
+        return G4_OK;
+    }
+    out.gelu = rc == G4_OK;
     return rc;
 }
 
@@ -241,22 +255,36 @@ int build(g4_decode &d) {
         G4_TRY(try_plan(g.data(), (int)g.size(), P[P_QKV]));
         g4_gemv_desc o = desc(L.o, L.o_s, d.attn_codes, d.oc, 4, QW, H, G4_KIND_I8, in, out);
         G4_TRY(try_plan(&o, 1, P[P_O]));
-        g4_gemv_desc gu[2] = {desc(L.gate, L.gate_s, d.xcodes, d.gc, 4, H, F, G4_KIND_I8, in, out),
-                              desc(L.up, L.up_s, d.xcodes, d.uc, 4, H, F, G4_KIND_I8, in, out)};
-        G4_TRY(try_plan(gu, 2, P[P_GATEUP]));
-        // down_proj reads gelu(gate) * up through the fused prologue (qgemv-4bit-gelu)
-        g4_gemv_desc dn = desc(L.down, L.down_s, d.gc, d.dc, 4, F, H, G4_KIND_I8, in, out);
-        const g4_gelu_act dna{d.uc, G4_KIND_I8, out, out, 0};
-        G4_TRY(try_plan(&dn, 1, P[P_DOWN], &dna));
-        g4_gemv_desc pg = desc(L.ple_gate, L.ple_gate_s, d.xcodes, d.pgc, 8, H, s.ple_dim,
-                               G4_KIND_I8, in, out);
-        G4_TRY(try_plan(&pg, 1, P[P_PLE_GATE]));
-        // per_layer_projection reads gelu(gate) * the layer's per-layer-input row (qgemv-8bit-gelu
-        // with upOffset = layer * ple_dim)
-        g4_gemv_desc pp = desc(L.ple_proj, L.ple_proj_s, d.pgc, d.ppc, 8, s.ple_dim, H, G4_KIND_I8,
+        // gate and up rows stream through one paired tile whose epilogue is the gelu-mul pass:
+        // act = srq(gelu(gate code * out) * (up code * out), in), the codes down_proj reads
+        GeluEpilogue gue;
+        gue.w_up = L.up;
+        gue.s_up = L.up_s;
+        gue.act_scale = in;
+        G4_TRY(try_gelu_plan(desc(L.gate, L.gate_s, d.xcodes, d.act, 4, H, F, G4_KIND_I8, in, out),
+                             gue, P[P_GATEUP]));
+        if (!P[P_GATEUP].p) {
+            g4_gemv_desc gu[2] = {desc(L.gate, L.gate_s, d.xcodes, d.gc, 4, H, F, G4_KIND_I8, in, out),
+                                  desc(L.up, L.up_s, d.xcodes, d.uc, 4, H, F, G4_KIND_I8, in, out)};
+            G4_TRY(try_plan(gu, 2, P[P_GATEUP]));
+        }
+        g4_gemv_desc dn = desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out);
+        G4_TRY(try_plan(&dn, 1, P[P_DOWN]));
+        // per_layer_input_gate's epilogue multiplies gelu(gate) by the layer's per-layer-input row
+        GeluEpilogue pge;
+        pge.up_vec = d.per_layer + (size_t)l * s.ple_dim;
+        pge.act_scale = in;
+        G4_TRY(try_gelu_plan(desc(L.ple_gate, L.ple_gate_s, d.xcodes, d.pac, 8, H, s.ple_dim,
+                                  G4_KIND_I8, in, out),
+                             pge, P[P_PLE_GATE]));
+        if (!P[P_PLE_GATE].p) {
+            g4_gemv_desc pg = desc(L.ple_gate, L.ple_gate_s, d.xcodes, d.pgc, 8, H, s.ple_dim,
+                                   G4_KIND_I8, in, out);
+            G4_TRY(try_plan(&pg, 1, P[P_PLE_GATE]));
+        }
+        g4_gemv_desc pp = desc(L.ple_proj, L.ple_proj_s, d.pac, d.ppc, 8, s.ple_dim, H, G4_KIND_I8,
                                in, out);
-        const g4_gelu_act ppa{d.per_layer, G4_KIND_F32, out, 0.0f, (int64_t)l * s.ple_dim};
-        G4_TRY(try_plan(&pp, 1, P[P_PLE_PROJ], &ppa));
+        G4_TRY(try_plan(&pp, 1, P[P_PLE_PROJ]));
     }
     g4_gemv_desc pm = desc(d.w.ple_model_proj, d.w.ple_model_proj_s, d.embed_codes, d.ple_codes, 4,
                            H, PL, G4_KIND_I8, in, out);
@@ -299,27 +327,28 @@ int run_layer(g4_decode &d, int l, void *st) {
     G4_TRY(run_linear_rows(d, plan(P_O), desc(L.o, L.o_s, d.attn_codes, d.oc, 4, QW, H, G4_KIND_I8, in, out), st));
     G4_TRY(g4_rms_join(d.oc, G4_KIND_I8, out, L.post_attn_norm, d.hidden, 1.0f, L.pre_ffn_norm, B,
                        H, s.eps, in, d.hidden, d.xcodes, st));
-    // MLP block
-    G4_TRY(run_linear_rows(d, plan(P_GATEUP), desc(L.gate, L.gate_s, d.xcodes, d.gc, 4, H, F, G4_KIND_I8, in, out), st));
-    if (!plan(P_GATEUP).p)
-        G4_TRY(run_linear_rows(d, none, desc(L.up, L.up_s, d.xcodes, d.uc, 4, H, F, G4_KIND_I8, in, out), st));
-    if (plan(P_DOWN).p) {
-        G4_TRY(g4_qgemv_plan_launch(plan(P_DOWN).p, st));  // gelu prologue fused
+    // MLP block: gate, up and the gelu-mul pass (one paired launch when folded), then down
+    if (plan(P_GATEUP).gelu) {
+        G4_TRY(g4_qgemv_plan_launch(plan(P_GATEUP).p, st));
     } else {
+        G4_TRY(run_linear_rows(d, plan(P_GATEUP), desc(L.gate, L.gate_s, d.xcodes, d.gc, 4, H, F, G4_KIND_I8, in, out), st));
+        if (!plan(P_GATEUP).p)
+            G4_TRY(run_linear_rows(d, none, desc(L.up, L.up_s, d.xcodes, d.uc, 4, H, F, G4_KIND_I8, in, out), st));
         G4_TRY(g4_gelu_mul(d.gc, out, d.uc, out, nullptr, 0, B, F, in, d.act, st));
-        G4_TRY(run_linear_rows(d, none, desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out), st));
     }
+    G4_TRY(run_linear_rows(d, plan(P_DOWN), desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out), st));
     G4_TRY(g4_rms_join(d.dc, G4_KIND_I8, out, L.post_ffn_norm, d.hidden, 1.0f, nullptr, B, H,
                        s.eps, in, d.hidden, d.xcodes, st));
-    // per-layer-input block
-    G4_TRY(run_linear_rows(d, plan(P_PLE_GATE), desc(L.ple_gate, L.ple_gate_s, d.xcodes, d.pgc, 8, H, s.ple_dim, G4_KIND_I8, in, out), st));
-    if (plan(P_PLE_PROJ).p) {
-        G4_TRY(g4_qgemv_plan_launch(plan(P_PLE_PROJ).p, st));  // gelu prologue fused
+    // per-layer-input block: the gate (with gelu times the layer's row folded when planned), then
+    // per_layer_projection
+    if (plan(P_PLE_GATE).gelu) {
+        G4_TRY(g4_qgemv_plan_launch(plan(P_PLE_GATE).p, st));
     } else {
+        G4_TRY(run_linear_rows(d, plan(P_PLE_GATE), desc(L.ple_gate, L.ple_gate_s, d.xcodes, d.pgc, 8, H, s.ple_dim, G4_KIND_I8, in, out), st));
         G4_TRY(g4_gelu_mul(d.pgc, out, nullptr, 0.0f, d.per_layer + (size_t)l * s.ple_dim,
                            (int64_t)s.layers * s.ple_dim, B, s.ple_dim, in, d.pac, st));
-        G4_TRY(run_linear_rows(d, none, desc(L.ple_proj, L.ple_proj_s, d.pac, d.ppc, 8, s.ple_dim, H, G4_KIND_I8, in, out), st));
     }
+    G4_TRY(run_linear_rows(d, plan(P_PLE_PROJ), desc(L.ple_proj, L.ple_proj_s, d.pac, d.ppc, 8, s.ple_dim, H, G4_KIND_I8, in, out), st));
     // the tail join: residual, layer scalar, then the next input norm (or the final norm)
     const bool last = l + 1 == s.layers;
     const float *next_norm = last ? d.w.final_norm : d.layers[l + 1].input_norm;

@@ -51,6 +51,21 @@ struct GeluAct {
     int up_kind = G4_KIND_F32;
 };
 
+// The gelu-mul pass folded into the gate's GEMV epilogue (the decode runner's form, no reference
+// counterpart): the job's rows are the gate, its output codes go back on out_scale, and dst
+// receives srq(gelu(gate) * up, act_scale) with up the same row of a paired 4-bit up projection
+// (w_up, s_up) or up_vec[row] (f32). act_scale 0: no epilogue.
+struct GeluEpilogue {
+    const void *w_up = nullptr;
+    const float *s_up = nullptr;
+    const float *up_vec = nullptr;
+    float act_scale = 0.0f;
+};
+
+// A GEMV plan whose projections may carry a gelu epilogue (qgemv_stream.hip).
+int gemv_plan_create_epilogue(const g4_gemv_desc *descs, const GeluEpilogue *epis, int count,
+                              g4_gemv_plan **out);
+
 // The internal form of a public g4_gelu_act (NULL or a NULL up: no prologue).
 GeluAct gelu_act_of(const g4_gelu_act *a);
 

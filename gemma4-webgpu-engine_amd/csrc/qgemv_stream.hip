@@ -36,14 +36,19 @@ constexpr int kBlocksPerCu = 8;
 
 #define G4_GLOBAL __attribute__((address_space(1)))
 
-// One projection of a streaming launch (80 bytes). With the gelu prologue (up set) x is the gate
-// and the block snaps gelu_tanh(gate) * up instead of x.
+// One projection of a streaming launch (112 bytes). With the gelu prologue (up set) x is the gate
+// and the block snaps gelu_tanh(gate) * up instead of x. With a gelu epilogue (epi != 0) the job's
+// rows are the gate and dst receives srq(gelu(gate code * out_scale) * u, act_scale), where u is
+// the same row of a paired up projection (epi 1: aux / aux_scales are its weights and scales) or
+// aux[row] of an f32 vector (epi 2): the gelu-mul pass folded into the producer.
 struct StreamJob {
     const uint8_t *w;
     const float *scales;
     const void *x;
     void *dst;
     const void *up;
+    const void *aux;
+    const float *aux_scales;
     int k;
     int rows;
     int tile_begin;
@@ -52,14 +57,16 @@ struct StreamJob {
     float out_scale;
     float g_scale;
     float u_scale;
+    float act_scale;
     int8_t bits;
     int8_t x_kind;
     int8_t out_kind;
     int8_t cls;
     int8_t up_kind;
-    int8_t pad[3];
+    int8_t epi;
+    int8_t pad[14];
 };
-static_assert(sizeof(StreamJob) == 80, "StreamJob is one 80-byte record");
+static_assert(sizeof(StreamJob) == 112, "StreamJob is one 112-byte record");
 
 struct StreamArgs {
     const StreamJob *table;  // device table (plan launches); null for kernel-argument jobs
@@ -269,10 +276,53 @@ __device__ __forceinline__ void stream_store(const StreamJob &J, int row, int s,
     }
 }
 
+// The dot of one 16-byte weight chunk against its LDS codes.
+template <int BITS>
+__device__ __forceinline__ int chunk_dot(const u32x4 &w, const uint8_t *xs, int ch, int acc) {
+    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+    if (BITS == 4) {
+        const u32x4 xa = *reinterpret_cast<const u32x4 *>(xs + ch * 32);
+        const u32x4 xb = *reinterpret_cast<const u32x4 *>(xs + ch * 32 + 16);
+        const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc = __builtin_amdgcn_sdot4((int)(wv[i] & 0x0F0F0F0Fu), (int)xv[2 * i], acc, false);
+            acc = __builtin_amdgcn_sdot4((int)((wv[i] >> 4) & 0x0F0F0F0Fu), (int)xv[2 * i + 1], acc,
+                                         false);
+        }
+    } else {
+        const u32x4 xa = *reinterpret_cast<const u32x4 *>(xs + ch * 16);
+        acc = __builtin_amdgcn_sdot4((int)wv[0], (int)xa.x, acc, false);
+        acc = __builtin_amdgcn_sdot4((int)wv[1], (int)xa.y, acc, false);
+        acc = __builtin_amdgcn_sdot4((int)wv[2], (int)xa.z, acc, false);
+        acc = __builtin_amdgcn_sdot4((int)wv[3], (int)xa.w, acc, false);
+    }
+    return acc;
+}
+
+template <int LPR>
+__device__ __forceinline__ int row_reduce(int acc) {
+    acc = row16_sum_i32(acc);
+    if (LPR >= 32) acc += __shfl_xor(acc, 16);
+    if (LPR >= 64) acc += __shfl_xor(acc, 32);
+    return acc;
+}
+
+// The gelu epilogue of a gate row (epi != 0): the gate's int8 code back on out_scale, the up value
+// (a paired row's code on out_scale, or the f32 vector entry), and the snap of gelu(g) * u on
+// act_scale: the gelu-mul pass (geluMul.ts:101-116) on exactly the values it would have read.
+__device__ __forceinline__ void stream_store_gelu(const StreamJob &J, int row, float y_gate,
+                                                  float u) {
+    const float g = __fmul_rn(srq_code_f(y_gate, J.out_scale), J.out_scale);
+    gstore<int8_t>(reinterpret_cast<int8_t *>(J.dst) + row,
+                   (int8_t)srq_code_i(__fmul_rn(d_gelu(g), u), J.act_scale));
+}
+
 // One tile of one job for class <BITS, LPR, CPL>: this lane's CPL 16-byte chunks of its row
 // (row index clamped, so every load is valid) and the row scale, the dot against the LDS codes,
 // the fixed reduction over the row's LPR lanes (exact int32), and the row's output from one lane.
-template <int BITS, int LPR, int CPL>
+// PAIR: the same rows of the paired up projection stream beside the gate's, for the gelu epilogue.
+template <int BITS, int LPR, int CPL, bool PAIR>
 __device__ __forceinline__ void stream_tile(const StreamJob &J, int t, const uint8_t *xs, int sx,
                                             int wave, int lane) {
     constexpr int RPW = 64 / LPR;
@@ -284,42 +334,61 @@ __device__ __forceinline__ void stream_tile(const StreamJob &J, int t, const uin
     u32x4 w[CPL];
 #pragma unroll
     for (int u = 0; u < CPL; ++u) w[u] = load_w16(base + u * LPR * 16);
-    const float scale = gload<float>(J.scales + rc);
-    int acc = 0;
+    u32x4 w2[PAIR ? CPL : 1];
+    if (PAIR) {
+        const uint8_t *base2 = reinterpret_cast<const uint8_t *>(J.aux) + (int64_t)rc * ROW_BYTES + lr * 16;
 #pragma unroll
-    for (int u = 0; u < CPL; ++u) {
-        const int ch = lr + u * LPR;
-        const uint32_t wv[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-        if (BITS == 4) {
-            const u32x4 xa = *reinterpret_cast<const u32x4 *>(xs + ch * 32);
-            const u32x4 xb = *reinterpret_cast<const u32x4 *>(xs + ch * 32 + 16);
-            const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                acc = __builtin_amdgcn_sdot4((int)(wv[i] & 0x0F0F0F0Fu), (int)xv[2 * i], acc, false);
-                acc = __builtin_amdgcn_sdot4((int)((wv[i] >> 4) & 0x0F0F0F0Fu), (int)xv[2 * i + 1],
-                                             acc, false);
-            }
-        } else {
-            const u32x4 xa = *reinterpret_cast<const u32x4 *>(xs + ch * 16);
-            acc = __builtin_amdgcn_sdot4((int)wv[0], (int)xa.x, acc, false);
-            acc = __builtin_amdgcn_sdot4((int)wv[1], (int)xa.y, acc, false);
-            acc = __builtin_amdgcn_sdot4((int)wv[2], (int)xa.z, acc, false);
-            acc = __builtin_amdgcn_sdot4((int)wv[3], (int)xa.w, acc, false);
-        }
+        for (int u = 0; u < CPL; ++u) w2[u] = load_w16(base2 + u * LPR * 16);
     }
-    acc = row16_sum_i32(acc);
-    if (LPR >= 32) acc += __shfl_xor(acc, 16);
-    if (LPR >= 64) acc += __shfl_xor(acc, 32);
-    if (lr == 0 && row < J.rows) stream_store(J, row, BITS == 4 ? acc - 8 * sx : acc, scale);
+    const float scale = gload<float>(J.scales + rc);
+    const float scale2 = PAIR ? gload<float>(J.aux_scales + rc) : 0.0f;
+    int acc = 0, acc2 = 0;
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) acc = chunk_dot<BITS>(w[u], xs, lr + u * LPR, acc);
+    if (PAIR) {
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) acc2 = chunk_dot<BITS>(w2[u], xs, lr + u * LPR, acc2);
+    }
+    acc = row_reduce<LPR>(acc);
+    if (PAIR) acc2 = row_reduce<LPR>(acc2);
+    if (lr != 0 || row >= J.rows) return;
+    const int a = BITS == 4 ? acc - 8 * sx : acc;
+    if (J.epi == 0) {
+        stream_store(J, row, a, scale);
+    } else if (PAIR) {
+        const int a2 = BITS == 4 ? acc2 - 8 * sx : acc2;
+        const float yu = linear_epilogue(J.in_scale, scale2, (float)a2);
+        stream_store_gelu(J, row, linear_epilogue(J.in_scale, scale, (float)a),
+                          __fmul_rn(srq_code_f(yu, J.out_scale), J.out_scale));
+    } else {
+        stream_store_gelu(J, row, linear_epilogue(J.in_scale, scale, (float)a),
+                          gload<float>(reinterpret_cast<const float *>(J.aux) + row));
+    }
 }
 
+template <bool PAIR>
 __device__ __forceinline__ void stream_dispatch(const StreamJob &J, int t, const uint8_t *xs,
                                                 int sx, int wave, int lane) {
+    if (PAIR && J.epi == 1) {
+        // paired gate/up rows: the 4-bit classes only (the host refuses others)
+        switch (J.cls) {
+#define G4_CASE(i)                                                                               \
+    case i:                                                                                      \
+        stream_tile<kClasses[i].bits, kClasses[i].lpr, kClasses[i].cpl, true>(J, t, xs, sx, wave, \
+                                                                              lane);             \
+        break;
+            G4_CASE(0) G4_CASE(1) G4_CASE(2) G4_CASE(3) G4_CASE(4) G4_CASE(5) G4_CASE(6) G4_CASE(7)
+#undef G4_CASE
+            default:
+                break;
+        }
+        return;
+    }
     switch (J.cls) {
-#define G4_CASE(i)                                                                              \
-    case i:                                                                                     \
-        stream_tile<kClasses[i].bits, kClasses[i].lpr, kClasses[i].cpl>(J, t, xs, sx, wave, lane); \
+#define G4_CASE(i)                                                                                \
+    case i:                                                                                       \
+        stream_tile<kClasses[i].bits, kClasses[i].lpr, kClasses[i].cpl, false>(J, t, xs, sx, wave, \
+                                                                               lane);             \
         break;
         G4_CASE(0) G4_CASE(1) G4_CASE(2) G4_CASE(3) G4_CASE(4) G4_CASE(5) G4_CASE(6) G4_CASE(7)
         G4_CASE(8) G4_CASE(9) G4_CASE(10) G4_CASE(11) G4_CASE(12) G4_CASE(13) G4_CASE(14)
@@ -330,12 +399,10 @@ __device__ __forceinline__ void stream_dispatch(const StreamJob &J, int t, const
     }
 }
 static_assert(kNumClasses == 17, "stream_dispatch lists every class");
+static_assert(kClasses[7].bits == 4 && kClasses[8].bits == 8, "classes 0-7 are the 4-bit ones");
 
-template <bool TABLE>
-__global__ __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
-void qgemv_stream_kernel(StreamArgs A) {
-    extern __shared__ __align__(16) uint8_t xs[];
-    __shared__ int s_sum;
+template <bool TABLE, bool PAIR>
+__device__ __forceinline__ void stream_body(const StreamArgs &A, uint8_t *xs, int *s_sum) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const unsigned G = gridDim.x, b = blockIdx.x;
@@ -352,16 +419,33 @@ void qgemv_stream_kernel(StreamArgs A) {
             if (i < A.njobs && t0 >= A.job[i].tile_begin) j = i;
     }
     StreamJob J = TABLE ? A.table[j] : A.job[j];
-    int sx = snap_activations(J, xs, &s_sum, tid);
+    int sx = snap_activations(J, xs, s_sum, tid);
     for (int t = t0; t < t1; ++t) {
         if (t >= J.tile_begin + J.tiles) {
             ++j;
             J = TABLE ? A.table[j] : A.job[j];
             __syncthreads();  // every wave is done with the previous job's codes
-            sx = snap_activations(J, xs, &s_sum, tid);
+            sx = snap_activations(J, xs, s_sum, tid);
         }
-        stream_dispatch(J, t, xs, sx, wave, lane);
+        stream_dispatch<PAIR>(J, t, xs, sx, wave, lane);
     }
+}
+
+template <bool TABLE>
+__global__ __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void qgemv_stream_kernel(StreamArgs A) {
+    extern __shared__ __align__(16) uint8_t xs[];
+    __shared__ int s_sum;
+    stream_body<TABLE, false>(A, xs, &s_sum);
+}
+
+// The same with paired gate/up jobs: twice the weight registers, so half the waves per SIMD.
+template <bool TABLE>
+__global__ __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(4, 8)))
+void qgemv_stream_pair_kernel(StreamArgs A) {
+    extern __shared__ __align__(16) uint8_t xs[];
+    __shared__ int s_sum;
+    stream_body<TABLE, true>(A, xs, &s_sum);
 }
 
 // Fills a StreamJob from a validated descriptor and prologue; returns false when no class fits.
@@ -450,7 +534,82 @@ struct g4_gemv_plan {
     int grid = 0;
     int max_k = 0;
     int device = 0;
+    bool paired = false;  // launches qgemv_stream_pair_kernel
 };
+
+namespace g4 {
+
+// Uploads a validated job list as a plan.
+static int plan_from_jobs(std::vector<StreamJob> &jobs, g4_gemv_plan **out) {
+    const int count = (int)jobs.size();
+    int max_k = 0;
+    const int tiles = layout_tiles(jobs.data(), count, max_k);
+    const int grid = grid_for(tiles);
+    std::vector<int> block_job(grid);
+    for (int b = 0, j = 0; b < grid; ++b) {
+        const int tb = (int)(((uint64_t)b * (unsigned)tiles) / (unsigned)grid);
+        while (j + 1 < count && jobs[j + 1].tile_begin <= tb) ++j;
+        block_job[b] = j;
+    }
+    g4_gemv_plan *p = new g4_gemv_plan();
+    p->njobs = count;
+    p->total_tiles = tiles;
+    p->grid = grid;
+    p->max_k = max_k;
+    for (const StreamJob &J : jobs) p->paired |= J.epi == 1;
+    hipError_t err = hipGetDevice(&p->device);
+    if (err == hipSuccess) err = hipMalloc(&p->table, sizeof(StreamJob) * count);
+    if (err == hipSuccess) err = hipMalloc(&p->block_job, sizeof(int) * grid);
+    if (err == hipSuccess)
+        err = hipMemcpy(p->table, jobs.data(), sizeof(StreamJob) * count, hipMemcpyHostToDevice);
+    if (err == hipSuccess)
+        err = hipMemcpy(p->block_job, block_job.data(), sizeof(int) * grid, hipMemcpyHostToDevice);
+    if (err != hipSuccess) {
+        (void)hipFree(p->table);
+        (void)hipFree(p->block_job);
+        delete p;
+        return hip_status(err, "GEMV plan");
+    }
+    *out = p;
+    return G4_OK;
+}
+
+int gemv_plan_create_epilogue(const g4_gemv_desc *descs, const GeluEpilogue *epis, int count,
+                              g4_gemv_plan **out) {
+    if (!out || !descs || count < 1) return set_error(G4_ERR_INVALID, "GEMV plan: no projections");
+    *out = nullptr;
+    std::vector<StreamJob> jobs(count);
+    for (int i = 0; i < count; ++i) {
+        int rc = check_job_desc(descs[i], GeluAct{}, "GEMV plan");
+        if (rc) return rc;
+        if (!stream_job_from(descs[i], GeluAct{}, jobs[i]))
+            return set_error(G4_ERR_UNSUPPORTED, "GEMV plan: projection %d has no streaming class", i);
+        const GeluEpilogue *e = epis ? &epis[i] : nullptr;
+        if (!e || e->act_scale == 0.0f) continue;
+        if (descs[i].out_kind != G4_KIND_I8 || descs[i].out_scale == 0.0f)
+            return set_error(G4_ERR_INVALID, "GEMV plan: a gelu epilogue needs int8 gate codes");
+        StreamJob &J = jobs[i];
+        J.act_scale = e->act_scale;
+        if (e->w_up) {
+            if (descs[i].bits != 4)
+                return set_error(G4_ERR_UNSUPPORTED, "GEMV plan: paired gate/up rows are 4-bit only");
+            if (!e->s_up || (reinterpret_cast<uintptr_t>(e->w_up) & 15))
+                return set_error(G4_ERR_INVALID,
+                                 "GEMV plan: paired up weights need scales and 16-byte alignment");
+            J.epi = 1;
+            J.aux = e->w_up;
+            J.aux_scales = e->s_up;
+        } else {
+            if (!e->up_vec)
+                return set_error(G4_ERR_INVALID, "GEMV plan: a gelu epilogue needs an up operand");
+            J.epi = 2;
+            J.aux = e->up_vec;
+        }
+    }
+    return plan_from_jobs(jobs, out);
+}
+
+}  // namespace g4
 
 extern "C" {
 
@@ -477,35 +636,7 @@ int g4_qgemv_plan_create_gelu(const g4_gemv_desc *descs, const g4_gelu_act *acts
                              "shape class; run it through g4_qgemv",
                              i, descs[i].bits, descs[i].k, (double)descs[i].in_scale);
     }
-    int max_k = 0;
-    const int tiles = layout_tiles(jobs.data(), count, max_k);
-    const int grid = grid_for(tiles);
-    std::vector<int> block_job(grid);
-    for (int b = 0, j = 0; b < grid; ++b) {
-        const int tb = (int)(((uint64_t)b * (unsigned)tiles) / (unsigned)grid);
-        while (j + 1 < count && jobs[j + 1].tile_begin <= tb) ++j;
-        block_job[b] = j;
-    }
-    g4_gemv_plan *p = new g4_gemv_plan();
-    p->njobs = count;
-    p->total_tiles = tiles;
-    p->grid = grid;
-    p->max_k = max_k;
-    hipGetDevice(&p->device);
-    hipError_t err = hipMalloc(&p->table, sizeof(StreamJob) * count);
-    if (err == hipSuccess) err = hipMalloc(&p->block_job, sizeof(int) * grid);
-    if (err == hipSuccess)
-        err = hipMemcpy(p->table, jobs.data(), sizeof(StreamJob) * count, hipMemcpyHostToDevice);
-    if (err == hipSuccess)
-        err = hipMemcpy(p->block_job, block_job.data(), sizeof(int) * grid, hipMemcpyHostToDevice);
-    if (err != hipSuccess) {
-        hipFree(p->table);
-        hipFree(p->block_job);
-        delete p;
-        return hip_status(err, "g4_qgemv_plan_create");
-    }
-    *out = p;
-    return G4_OK;
+    return plan_from_jobs(jobs, out);
 }
 
 int g4_qgemv_plan_launch(const g4_gemv_plan *p, void *stream) {
@@ -515,8 +646,12 @@ int g4_qgemv_plan_launch(const g4_gemv_plan *p, void *stream) {
     A.block_job = p->block_job;
     A.njobs = p->njobs;
     A.total_tiles = p->total_tiles;
-    hipLaunchKernelGGL(qgemv_stream_kernel<true>, dim3(p->grid), dim3(kStreamThreads),
-                       (size_t)((p->max_k + 15) & ~15), as_stream(stream), A);
+    if (p->paired)
+        hipLaunchKernelGGL(qgemv_stream_pair_kernel<true>, dim3(p->grid), dim3(kStreamThreads),
+                           (size_t)((p->max_k + 15) & ~15), as_stream(stream), A);
+    else
+        hipLaunchKernelGGL(qgemv_stream_kernel<true>, dim3(p->grid), dim3(kStreamThreads),
+                           (size_t)((p->max_k + 15) & ~15), as_stream(stream), A);
     G4_LAUNCHED("qgemv_stream_kernel");
     return G4_OK;
 }
