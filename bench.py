@@ -296,7 +296,27 @@ def decode_step_bytes(shape, pos):
     return w + s.batch * per_row
 
 
-def bench_decode(h, batch, steps=20, warmup=3, probe=False):
+def cpu_decode_step(shape, model, dec, pos, tokens):
+    """The CPU composition of one decode step (oracle/decode_ref.py, C oracle kernels with OpenMP
+    over the host cores) on the same model, KV and tokens: the weights are copied to the host
+    before the timed region."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import decode_ref as ref
+    import oracle as o
+    W = ref.Weights(model)
+    for name in model.buffers:
+        if name != "ple_table":
+            W[name]
+    kv = {p: tuple(a.copy() for a in dec.download_kv(p)) for p in range(shape.kv_producers)}
+    t0 = time.perf_counter()
+    out = ref.step(shape, W, kv, list(tokens), pos)
+    secs = time.perf_counter() - t0
+    return {"value": round(len(tokens) / secs, 3), "unit": "tok/s", "cores": o.num_threads(),
+            "kind": "port", "sample": f"one decode step at batch {len(tokens)} (position {pos})",
+            "seconds": round(secs, 3), "next_tokens": [int(t) for t in out["next"]]}
+
+
+def bench_decode(h, batch, steps=20, warmup=3, probe=False, cpu=False):
     """one E2B-shape decode step (35 layers, KV capacity 4096, position 4095, so
     global layers attend over 4096 positions and sliding ones over 512), greedy over 262144 rows,
     as one captured graph replayed per token; and the same step launched eagerly."""
@@ -335,6 +355,14 @@ def bench_decode(h, batch, steps=20, warmup=3, probe=False):
         "next_tokens_head": [int(t) for t in nxt.download()[:4]],
         "model_bytes": model.nbytes(),
     }
+    if cpu:
+        log(f"config 4 CPU composition, batch {batch}")
+        toks_host = [int(t) for t in toks.download()]
+        dec.fill_kv_history()  # the timed replays rewrote the position's rows; restore the history
+        g4.synchronize()
+        c = cpu_decode_step(shape, model, dec, pos, toks_host)
+        c["matches_gpu_next_tokens"] = c["next_tokens"] == out["next_tokens_head"][:batch]
+        out["cpu"] = c
     graph.close()
     dec.close()
     stream.close()
@@ -457,7 +485,7 @@ def main():
         sweep = bench_gemm_sweep(h)
         down8 = bench_int8_down(h)
         log("config 4 decode step, batch 1 and 32")
-        dec1 = bench_decode(h, 1)
+        dec1 = bench_decode(h, 1, cpu=not args.no_cpu_baseline)
         dec32 = bench_decode(h, 32)
         result["extra"] = {
             "decode_step_config4": {"batch1": dec1, "batch32": dec32},

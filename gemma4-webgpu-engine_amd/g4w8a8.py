@@ -613,6 +613,28 @@ def _bind_exact_merge(inputs, output, params, stream=None):
                       _p(params, "outScale", 0.0), stream=stream)
 
 
+def _bind_gelu(bits, split):
+    """qgemv-4bit-gelu / qgemv-8bit-gelu and the gelu exact split: gate and up in place of x
+    (qgemv.ts:359-400, 1668-1696; exactSplit.ts:19-31). gate/up are f32 buffers (the reference's)
+    or int8 codes with params gateScale / upScale."""
+    who = f"qgemv-{bits}bit-gelu-exact-split" if split else f"qgemv-{bits}bit-gelu"
+
+    def run(inputs, output, params, stream=None):
+        _need(inputs, ["wq", "scales", "gate", "up"], who)
+        act = gelu_act(inputs["up"], gate_scale=_p(params, "gateScale", 0.0),
+                       up_scale=_p(params, "upScale", 0.0), up_offset=int(_p(params, "upOffset", 0)))
+        if split:
+            qgemv_gelu_split(bits, inputs["wq"], inputs["scales"], inputs["gate"], act, output,
+                             int(_p(params, "k", 0)), int(_p(params, "numRows", 0)),
+                             int(_p(params, "kSplits", 1)), True, _p(params, "inScale", 0.0),
+                             stream=stream)
+        else:
+            qgemv_gelu(bits, inputs["wq"], inputs["scales"], inputs["gate"], act, output,
+                       int(_p(params, "k", 0)), int(_p(params, "numRows", 0)),
+                       _p(params, "inScale", 0.0), _p(params, "outScale", 0.0), stream=stream)
+    return run
+
+
 PLE_COLS, PLE_GROUP_SIZE = 8960, 256  # PLE_ROW_VALUES and PLE_GROUP_SIZE (quant.ts:35-37)
 
 
@@ -646,6 +668,9 @@ KERNELS = {
     "qmatmul-8bit": _bind_gemm(8),
     "qkv-batch-4bit": _bind_batch(3),
     "gate-up-batch-4bit": _bind_batch(2),
+    "qgemv-4bit-gelu": _bind_gelu(4, False),
+    "qgemv-8bit-gelu": _bind_gelu(8, False),
+    "qgemv-4bit-gelu-exact-split": _bind_gelu(4, True),
     "qgemv-4bit-split": _bind_split(4),
     "qgemv-8bit-split": _bind_split(8),
     "qgemv-merge": _bind_merge,

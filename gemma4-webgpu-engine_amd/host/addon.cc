@@ -365,6 +365,30 @@ napi_value QgemvSplit(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// qgemv-4bit-gelu / qgemv-8bit-gelu: (bits, wq, scales, gate, gateKind, up, upKind, upOffset,
+// dst, outKind, k, numRows, inScale, outScale[, gateScale, upScale])
+napi_value QgemvGelu(napi_env env, napi_callback_info info) {
+    Args a(env, info, 16);
+    g4_gelu_act act{a.ptr(5), a.i32(6), (float)a.num(14), (float)a.num(15), (int64_t)a.num(7)};
+    int st = g4_qgemv_gelu(a.i32(0), a.ptr(1), (const float *)a.ptr(2), a.ptr(3), a.i32(4), &act,
+                           a.ptr(8), a.i32(9), a.i32(10), a.i32(11), (float)a.num(12),
+                           (float)a.num(13), nullptr);
+    if (throw_status(env, st)) return nullptr;
+    return undefined(env);
+}
+
+// qgemv-4bit-gelu-exact-split: (bits, wq, scales, gate, gateKind, up, upKind, upOffset, partials,
+// k, numRows, kSplits, exact, inScale[, gateScale, upScale])
+napi_value QgemvGeluSplit(napi_env env, napi_callback_info info) {
+    Args a(env, info, 16);
+    g4_gelu_act act{a.ptr(5), a.i32(6), (float)a.num(14), (float)a.num(15), (int64_t)a.num(7)};
+    int st = g4_qgemv_gelu_split(a.i32(0), a.ptr(1), (const float *)a.ptr(2), a.ptr(3), a.i32(4),
+                                 &act, (float *)a.ptr(8), a.i32(9), a.i32(10), a.i32(11),
+                                 a.i32(12), (float)a.num(13), nullptr);
+    if (throw_status(env, st)) return nullptr;
+    return undefined(env);
+}
+
 napi_value QgemvMerge(napi_env env, napi_callback_info info) {
     Args a(env, info, 6);
     int st = g4_qgemv_merge((const float *)a.ptr(0), a.ptr(1), a.i32(2), a.i32(3), a.i32(4),
@@ -491,6 +515,7 @@ napi_value Init(napi_env env, napi_value exports) {
         {"qgemm", Qgemm}, {"linear", Linear}, {"kernelForShape", KernelForShape},
         {"projectionBatch", ProjectionBatch}, {"qgemvGrouped", QgemvGrouped},
         {"qgemvSplit", QgemvSplit}, {"qgemvMerge", QgemvMerge},
+        {"qgemvGelu", QgemvGelu}, {"qgemvGeluSplit", QgemvGeluSplit},
         {"qgemvExactMerge", QgemvExactMerge}, {"srqQuantize", SrqQuantize},
         {"pleGather", PleGather}, {"pleGatherSplit", PleGatherSplit},
         {"planTableSplit", PlanTableSplit}, {"qgemvPlanCreate", QgemvPlanCreate},

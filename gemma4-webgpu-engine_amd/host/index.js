@@ -118,6 +118,25 @@ function splitKernel(bits) {
   };
 }
 
+// qgemv-4bit-gelu / qgemv-8bit-gelu (qgemv.ts:1668-1696) and the gelu exact split (exactSplit.ts:
+// 19-31): gate and up bound in place of x, upOffset selecting the per-layer row.
+function geluKernel(bits, split) {
+  const who = split ? `qgemv-${bits}bit-gelu-exact-split` : `qgemv-${bits}bit-gelu`;
+  return ({ inputs, output, params }) => {
+    need(inputs, ['wq', 'scales', 'gate', 'up'], who);
+    const head = [bits, inputs.wq.addr, inputs.scales.addr, inputs.gate.addr, inputs.gate.kind,
+      inputs.up.addr, inputs.up.kind, num(params, 'upOffset', 0), output.addr];
+    const scales = [num(params, 'gateScale', 0), num(params, 'upScale', 0)];
+    if (split) {
+      g4().qgemvGeluSplit(...head, num(params, 'k', 0), num(params, 'numRows', 0),
+        num(params, 'kSplits', 1), 1, num(params, 'inScale', 0), ...scales);
+    } else {
+      g4().qgemvGelu(...head, output.kind, num(params, 'k', 0), num(params, 'numRows', 0),
+        num(params, 'inScale', 0), num(params, 'outScale', 0), ...scales);
+    }
+  };
+}
+
 const PLE_COLS = 8960; // PLE_ROW_VALUES (quant.ts:35-37)
 const PLE_GROUP_SIZE = 256;
 
@@ -153,6 +172,9 @@ const KERNELS = {
   'qmatmul-8bit': gemmKernel(8),
   'qkv-batch-4bit': batchKernel(3),
   'gate-up-batch-4bit': batchKernel(2),
+  'qgemv-4bit-gelu': geluKernel(4, false),
+  'qgemv-8bit-gelu': geluKernel(8, false),
+  'qgemv-4bit-gelu-exact-split': geluKernel(4, true),
   'qgemv-4bit-split': splitKernel(4),
   'qgemv-8bit-split': splitKernel(8),
   'qgemv-merge': ({ inputs, output, params }) => {

@@ -15,7 +15,9 @@ function throwsWith(fn, fragment) {
 // registry
 for (const n of ['qgemv-4bit', 'qgemv-8bit', 'qgemv-4bit-m2', 'qgemm-4bit', 'qmatmul-8bit',
   'qkv-batch-4bit', 'gate-up-batch-4bit', 'qgemv-merge', 'qgemv-exact-merge', 'ple-gather-4bit',
-  'ple-gather-4bit-sliced']) assert.ok(h.kernelNames().includes(n), n);
+  'ple-gather-4bit-sliced', 'qgemv-4bit-gelu', 'qgemv-8bit-gelu', 'qgemv-4bit-gelu-exact-split'])
+  assert.ok(h.kernelNames().includes(n), n);
+throwsWith(() => h.bind('qgemv-4bit-gelu', { inputs: { wq: { addr: 1 } }, output: {}, params: {} }), 'needs inputs named wq, scales, gate, up');
 throwsWith(() => h.bind('qgemv-3bit', { inputs: {}, output: {}, params: {} }), 'no registered kernel named qgemv-3bit');
 throwsWith(() => h.bind('qgemv-4bit', { inputs: { wq: { addr: 1 } }, output: {}, params: {} }), 'needs inputs named wq, scales, x');
 throwsWith(() => h.bind('ple-gather-4bit-sliced', { inputs: { codes: { addr: 1, bytes: 4480 }, scales: { addr: 1 }, ids: { addr: 1 } }, output: { addr: 1 }, params: { slots: 4 } }), 'naming a non empty vocabulary range');

@@ -77,6 +77,26 @@ def test_node_host_gpu_parity(tmp_path, oracle):
                              "ids": {"file": put("ple.i", ids), "kind": "i32"}},
                   "output": {"bytes": slots * cols * 4, "kind": "f32"},
                   "params": {"slots": slots, "sliceStartRow": start, "sliceRowCount": count}})
+    # the down_proj of a decode MLP through qgemv-4bit-gelu: the reference's f32 gate and up, the
+    # up row at an offset (upOffset), against gelu-mul codes fed to the GEMV oracle
+    import decode_oracle as d
+    n3, k3, off = 1536, 6144, 256
+    rng = np.random.default_rng(5)
+    gate = (rng.standard_normal(k3) * 2.0).astype(np.float32)
+    up = (rng.standard_normal(k3 + off) * 1.5).astype(np.float32)
+    w3 = syn.int4_weights("node", "down", n3, k3)
+    s3 = syn.row_scales("node", "down", n3)
+    act = d.gelu_mul_f32_codes(gate, up[off:], syn.IN_SCALE)
+    want["gelu"] = oracle.qgemv(4, w3, s3, act.astype(np.float32) * np.float32(syn.IN_SCALE), n3,
+                                k3, syn.IN_SCALE, syn.OUT_SCALE)[2]
+    cases.append({"name": "gelu", "kernel": "qgemv-4bit-gelu",
+                  "inputs": {"wq": {"file": put("gelu.w", w3), "kind": "i8"},
+                             "scales": {"file": put("gelu.s", s3), "kind": "f32"},
+                             "gate": {"file": put("gelu.g", gate), "kind": "f32"},
+                             "up": {"file": put("gelu.u", up), "kind": "f32"}},
+                  "output": {"bytes": n3, "kind": "i8"},
+                  "params": {"k": k3, "numRows": n3, "inScale": syn.IN_SCALE,
+                             "outScale": syn.OUT_SCALE, "upOffset": off}})
     (tmp_path / "manifest.json").write_text(json.dumps({"cases": cases}))
     print("node gpu parity: running node", flush=True)
     r = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "gpu_parity.js"), str(tmp_path)],
@@ -86,5 +106,6 @@ def test_node_host_gpu_parity(tmp_path, oracle):
     assert np.array_equal(got_c0, want["c0"])
     got_g = np.fromfile(tmp_path / "g.out", np.int8)
     assert np.array_equal(got_g, want["g"])
+    assert np.array_equal(np.fromfile(tmp_path / "gelu.out", np.int8), want["gelu"])
     got_ple = np.fromfile(tmp_path / "ple.out", np.float32)
     assert np.array_equal(got_ple.view(np.uint32), want["ple"].view(np.uint32))
