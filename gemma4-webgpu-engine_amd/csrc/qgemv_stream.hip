@@ -665,8 +665,8 @@ int g4_qgemv_plan_info(const g4_gemv_plan *p, int *tiles, int *grid) {
 
 int g4_qgemv_plan_destroy(g4_gemv_plan *p) {
     if (!p) return G4_OK;
-    hipFree(p->table);
-    hipFree(p->block_job);
+    (void)hipFree(p->table);
+    (void)hipFree(p->block_job);
     delete p;
     return G4_OK;
 }

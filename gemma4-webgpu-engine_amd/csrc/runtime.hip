@@ -196,7 +196,7 @@ int g4_graph_end_capture(void *stream, void **graph_exec) {
     G4_HIP(hipStreamEndCapture(as_stream(stream), &graph));
     hipGraphExec_t exec = nullptr;
     hipError_t err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    hipGraphDestroy(graph);
+    (void)hipGraphDestroy(graph);
     if (err != hipSuccess) return hip_status(err, "hipGraphInstantiate");
     *graph_exec = exec;
     return G4_OK;

@@ -262,6 +262,125 @@ class SyntheticModel:
         return sum(b.nbytes for b in self.buffers.values())
 
 
+# The checkpoint's tensor names for each device tensor of the step (textTensorNames,
+# src/safetensors.ts:930-985; the families of src/quant.ts:546-647).
+CKPT_MODEL = {
+    "embed": "model.language_model.embed_tokens.embedding_quantized",
+    "embed_s": "model.language_model.embed_tokens.embedding_scale",
+    "ple_table": "model.language_model.embed_tokens_per_layer.embedding_quantized",
+    "ple_table_s": "model.language_model.embed_tokens_per_layer.embedding_scale",
+    "ple_model_proj": "model.language_model.per_layer_model_projection.weight",
+    "ple_model_proj_s": "model.language_model.per_layer_model_projection.weight_scale",
+    "ple_proj_norm": "model.language_model.per_layer_projection_norm.weight",
+    "final_norm": "model.language_model.norm.weight",
+}
+CKPT_LINEARS = {"q": "self_attn.q_proj", "k": "self_attn.k_proj", "v": "self_attn.v_proj",
+                "o": "self_attn.o_proj", "gate": "mlp.gate_proj", "up": "mlp.up_proj",
+                "down": "mlp.down_proj", "ple_gate": "per_layer_input_gate",
+                "ple_proj": "per_layer_projection"}
+CKPT_NORMS = {"input_norm": "input_layernorm", "post_attn_norm": "post_attention_layernorm",
+              "pre_ffn_norm": "pre_feedforward_layernorm",
+              "post_ffn_norm": "post_feedforward_layernorm",
+              "post_ple_norm": "post_per_layer_input_norm", "q_norm": "self_attn.q_norm",
+              "k_norm": "self_attn.k_norm"}
+
+
+def ckpt_layer(l: int, part: str) -> str:
+    return f"model.language_model.layers.{l}.{part}"
+
+
+class CheckpointModel:
+    """The step's device tensors read from a local safetensors file in the checkpoint's naming
+    (include/g4ckpt.h), the same interface as SyntheticModel. The lm_head pair resolves to the
+    embed pair through the tie. A linear's family is read from its stored shape: int4 U8 [N, K/2]
+    and int8 I8 [N, K] are served; the 2-bit families and the bf16 dense per-layer projection are
+    not, and neither are activation scales that differ from the shape's one static pair."""
+
+    def __init__(self, shape: Shape, path: str, stream=None):
+        import g4ckpt as ck
+        self.shape = s = shape
+        self.buffers: dict[str, g4.DeviceBuffer] = {}
+        self.families: dict[str, tuple] = {}
+        d = ck.Directory.open(path)
+        self.directory = d
+        d.apply_ties()
+        H, F, QW, P = s.hidden, s.ffn, s.q_heads * s.head_dim, s.ple_dim
+        PL = s.layers * P
+
+        def scalar(name):
+            t = d.find(name)
+            a = d.read(name).reshape(-1)
+            if t.dtype == "BF16":
+                return float((a.astype(np.uint32) << 16).view(np.float32)[0])
+            return float(a.astype(np.float32)[0])
+
+        def linear(key, base, n, k):
+            w = d.find(base + ".weight")
+            bits = {(w.dtype, (n, k // 2)): 4, (w.dtype, (n, k)): 8}.get((w.dtype, tuple(w.shape)))
+            if w.dtype == "U8" and tuple(w.shape) == (n, k // 4):
+                raise ValueError(f"{base}: the 2-bit family is not served by this build")
+            if (w.dtype, bits) not in (("U8", 4), ("I8", 8)):
+                raise ValueError(f"{base}.weight is {w.dtype} {list(w.shape)}; expected U8 "
+                                 f"[{n}, {k // 2}] (int4) or I8 [{n}, {k}] (int8)")
+            self.families[key] = (bits, ck.quant_bits(base))
+            self.buffers[key] = d.upload(base + ".weight", stream=stream)
+            sc = d.find(base + ".weight_scale")
+            if sc.dtype != "F32" or sc.element_count != n:
+                raise ValueError(f"{base}.weight_scale must be F32 with {n} values")
+            self.buffers[key + "_s"] = d.upload(base + ".weight_scale", stream=stream)
+            for which, want in (("input", s.in_scale), ("output", s.out_scale)):
+                name = f"{base}.{which}_activation_scale"
+                if name in d and np.float32(scalar(name)) != np.float32(want):
+                    raise ValueError(f"{name} = {scalar(name)}; the step serves one static "
+                                     f"{which} scale, {want}")
+            return bits
+
+        for key, name in CKPT_MODEL.items():
+            if key.endswith("_s") or key in ("ple_model_proj",):
+                continue
+            if key.endswith("norm"):
+                self.buffers[key] = d.upload_f32(name, stream=stream)
+            else:
+                self.buffers[key] = d.upload(name, stream=stream)
+        if d.find(CKPT_MODEL["ple_model_proj"]).dtype == "BF16":
+            raise ValueError("per_layer_model_projection is the bf16 dense matmul, which this build "
+                             "serves only as an int4 projection")
+        linear("ple_model_proj", "model.language_model.per_layer_model_projection", PL, H)
+        for key in ("embed_s", "ple_table_s"):
+            self.buffers[key] = d.upload(CKPT_MODEL[key], stream=stream)
+        if "lm_head.input_activation_scale" in d and \
+                np.float32(scalar("lm_head.input_activation_scale")) != np.float32(s.in_scale):
+            raise ValueError("lm_head.input_activation_scale differs from the static input scale")
+        for name, a in _rope_all(s).items():
+            self.buffers[name] = g4.DeviceBuffer.from_array(a)
+        self.layer_scalar = np.zeros(s.layers, np.float32)
+        for l in range(s.layers):
+            prod = l < s.kv_producers
+            dims = {"q": (QW, H), "k": (s.head_dim, H), "v": (s.head_dim, H), "o": (H, QW),
+                    "gate": (F, H), "up": (F, H), "down": (H, F), "ple_gate": (P, H),
+                    "ple_proj": (H, P)}
+            for key, part in CKPT_LINEARS.items():
+                if key in ("k", "v") and not prod:
+                    continue
+                bits = linear(f"l{l}.{key}", ckpt_layer(l, part), *dims[key])
+                if (key in ("ple_gate", "ple_proj")) != (bits == 8):
+                    raise ValueError(f"{ckpt_layer(l, part)}: int{bits} where the step runs "
+                                     f"{'int8' if key in ('ple_gate', 'ple_proj') else 'int4'}")
+            for key, part in CKPT_NORMS.items():
+                if key == "k_norm" and not prod:
+                    continue
+                self.buffers[f"l{l}.{key}"] = d.upload_f32(ckpt_layer(l, part + ".weight"),
+                                                           stream=stream)
+            self.layer_scalar[l] = scalar(ckpt_layer(l, "layer_scalar"))
+        self._keep = None
+
+    ptr = SyntheticModel.ptr
+    host = SyntheticModel.host
+    host_rows = SyntheticModel.host_rows
+    weights = SyntheticModel.weights
+    nbytes = SyntheticModel.nbytes
+
+
 class Decoder:
     """The native runner (g4_decode_create / g4_decode_step) over one model."""
 

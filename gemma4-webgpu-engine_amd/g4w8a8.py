@@ -93,6 +93,15 @@ class DecodeWeights(ctypes.Structure):
     _fields_ = [(n, _vp) for n in DECODE_MODEL_FIELDS] + [("layer", ctypes.POINTER(DecodeLayer))]
 
 
+class StTensor(ctypes.Structure):
+    """include/g4ckpt.h g4_st_tensor."""
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_char_p), ("ndim", ctypes.c_int),
+                ("shape", ctypes.c_int64 * 8), ("data_start", ctypes.c_int64),
+                ("data_end", ctypes.c_int64), ("file_start", ctypes.c_int64),
+                ("file_end", ctypes.c_int64), ("byte_length", ctypes.c_int64),
+                ("element_count", ctypes.c_int64)]
+
+
 _u64 = ctypes.c_uint64
 _sz = ctypes.c_size_t
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -190,6 +199,30 @@ SIGNATURES = {
     "g4_decode_buffer": (_c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp),
                                   ctypes.POINTER(_sz)]),
     "g4_decode_set_stop": (_c_int, [_vp, _c_int]),
+    # include/g4ckpt.h
+    "g4_st_parse": (_c_int, [_vp, _sz, _c_int, ctypes.POINTER(_vp)]),
+    "g4_st_open": (_c_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "g4_st_close": (_c_int, [_vp]),
+    "g4_st_info": (_c_int, [_vp, ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                            ctypes.POINTER(_i64)]),
+    "g4_st_count": (_i64, [_vp]),
+    "g4_st_tensor_at": (_c_int, [_vp, _i64, ctypes.POINTER(StTensor)]),
+    "g4_st_find": (_c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(StTensor)]),
+    "g4_st_metadata": (ctypes.c_char_p, [_vp, ctypes.c_char_p]),
+    "g4_st_coverage_gaps": (_i64, [_vp, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _i64]),
+    "g4_st_apply_ties": (_c_int, [_vp]),
+    "g4_st_tie_count": (_c_int, []),
+    "g4_st_tie": (_c_int, [_c_int, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_char_p),
+                           ctypes.POINTER(_i64)]),
+    "g4_st_read": (_c_int, [_vp, ctypes.c_char_p, _i64, _vp, _sz]),
+    "g4_st_upload": (_c_int, [_vp, ctypes.c_char_p, _vp, _sz, _vp]),
+    "g4_st_upload_f32": (_c_int, [_vp, ctypes.c_char_p, _vp, _i64, _vp]),
+    "g4_tie_guard": (_c_int, [_vp, _sz, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _sz]),
+    "g4_sha256_hex": (None, [_vp, _sz, ctypes.c_char_p]),
+    "g4_quant_bits": (_c_int, [ctypes.c_char_p]),
+    "g4_module_path_for_tensor": (_c_int, [ctypes.c_char_p, ctypes.c_char_p, _sz]),
+    "g4_text_tensor_names": (_i64, [_c_int, _c_int, _c_int, ctypes.c_char_p, _sz,
+                                    ctypes.POINTER(_sz)]),
 }
 
 _lib = None

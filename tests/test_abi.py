@@ -102,8 +102,10 @@ def test_struct_layouts_match_the_headers(g4, tmp_path):
     structs = {"g4_decode_shape": g4.DecodeShape, "g4_decode_layer": g4.DecodeLayer,
                "g4_decode_weights": g4.DecodeWeights, "g4_gemv_desc": g4.GemvDesc,
                "g4_table_split_input": g4.TableSplitInput, "g4_table_slice": g4.TableSlice,
-               "g4_table_split_plan": g4.TableSplitPlan, "g4_gelu_act": g4.GeluAct}
-    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "g4decode.h"', 'int main(void){']
+               "g4_table_split_plan": g4.TableSplitPlan, "g4_gelu_act": g4.GeluAct,
+               "g4_st_tensor": g4.StTensor}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "g4decode.h"', '#include "g4ckpt.h"',
+             'int main(void){']
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
         for f, _ in py._fields_:
