@@ -20,7 +20,7 @@
 //    sequential 32-dim dot products combined by a pairwise tree.
 // The projections between these kernels are the library's GEMV/GEMM entry points, which take and
 // give int8 codes: every kernel here that feeds a projection emits its input snap directly.
-#include "g4_internal.h"
+#include "g4_rowops.h"
 #include "../../include/g4decode.h"
 
 namespace g4 {
@@ -30,29 +30,9 @@ constexpr int kAttnChunk = 32;
 constexpr int kAttnMaxHeads = 8;
 
 // d_expf, d_tanhf and d_gelu (the deterministic exp / tanh / gelu) live in g4_internal.h, shared
-// with the GEMV gelu prologues.
-
-// The pairwise tree over 256 lanes: level s adds lane l + s into lane l for l < s, s = 128 .. 1
-// (every thread of the block calls it; returns the total). The two cross-wave levels go through
-// LDS, the six in-wave levels through lane shuffles, so the same tree costs three barriers.
-__device__ float block_tree_sum(float part, float *lds) {
-    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-    if (w >= 2) lds[t - 128] = part;
-    __syncthreads();
-    if (w < 2) part = __fadd_rn(part, lds[t]);           // s = 128
-    if (w == 1) lds[128 + lane] = part;
-    __syncthreads();
-    if (w == 0) {
-        part = __fadd_rn(part, lds[128 + lane]);         // s = 64
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, __shfl_down(part, off));
-        if (lane == 0) lds[192] = part;
-    }
-    __syncthreads();
-    const float total = lds[192];
-    __syncthreads();  // the caller may reuse lds at once
-    return total;
-}
+// with the GEMV gelu prologues; block_tree_sum, inv_rms and the RMS join row in g4_rowops.h, shared
+// with the GEMV whose last block runs a join.
+static_assert(kDecThreads == kRowThreads, "the glue kernels run the shared 256-lane row operations");
 
 __device__ float block_max(float v, float *lds) {
     const int t = threadIdx.x;
@@ -67,82 +47,12 @@ __device__ float block_max(float v, float *lds) {
     return m;
 }
 
-// sqrtf, not __fsqrt_rn: on this toolchain __fsqrt_rn is the native (approximate) v_sqrt_f32
-// unless OCML_BASIC_ROUNDED_OPERATIONS is defined, while sqrtf lowers to v_sqrt_f32 plus the
-// neighbour test that makes it correctly rounded.
-__device__ __forceinline__ float inv_rms(float sumsq, int width, float eps) {
-    return __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(sumsq, (float)width), eps)));
-}
-
-__device__ __forceinline__ float load_val(const void *src, int kind, float scale, int64_t i) {
-    if (kind == G4_KIND_I8) return __fmul_rn((float)reinterpret_cast<const int8_t *>(src)[i], scale);
-    return reinterpret_cast<const float *>(src)[i];
-}
-
-__device__ __forceinline__ int8_t snap_code(float v, float s) { return (int8_t)srq_code_i(v, s); }
-
 // ---- rms-norm / norm-residual / norm-residual-norm --------------------------------------------------
 
-constexpr int kJoinMaxPer = 8;  // width <= 2048
-
-// One block per row. y = (src * inv) * gain (gain null: weightless); with a residual,
-// hidden = resid + y, times alpha when alpha != 1. Outputs: hidden (f32), and codes of either the
-// second norm of hidden (gain2 given) or of hidden itself, snapped on in_scale.
-__global__ __launch_bounds__(kDecThreads) void join_kernel(
-    const void *src, int src_kind, float src_scale, const float *gain, const float *resid,
-    float alpha, const float *gain2, int width, float eps, float in_scale, float *hidden,
-    int8_t *codes) {
+// One block per row (rms_join_row).
+__global__ __launch_bounds__(kDecThreads) void join_kernel(JoinTail J) {
     __shared__ float lds[kDecThreads];
-    const int t = threadIdx.x;
-    const int64_t row = blockIdx.x;
-    const int64_t base = row * width;
-    // every operand is loaded before the first barrier (a barrier also fences the compiler's
-    // load scheduling, so later loads would each cost a memory latency of their own)
-    float v[kJoinMaxPer], ga[kJoinMaxPer], re[kJoinMaxPer], g2[kJoinMaxPer];
-#pragma unroll
-    for (int e = 0; e < kJoinMaxPer; ++e) {
-        const int i = t + e * kDecThreads;
-        const bool in = i < width;
-        v[e] = in ? load_val(src, src_kind, src_scale, base + i) : 0.0f;
-        ga[e] = in && gain ? gain[i] : 1.0f;
-        re[e] = in && resid ? resid[base + i] : 0.0f;
-        g2[e] = in && gain2 ? gain2[i] : 0.0f;
-    }
-    float part = 0.0f;
-#pragma unroll
-    for (int e = 0; e < kJoinMaxPer; ++e)
-        if (t + e * kDecThreads < width) part = __fadd_rn(part, __fmul_rn(v[e], v[e]));
-    const float inv = inv_rms(block_tree_sum(part, lds), width, eps);
-    float part2 = 0.0f;
-#pragma unroll
-    for (int e = 0; e < kJoinMaxPer; ++e) {
-        const int i = t + e * kDecThreads;
-        if (i >= width) continue;
-        float y = __fmul_rn(v[e], inv);
-        if (gain) y = __fmul_rn(y, ga[e]);
-        if (resid) {
-            y = __fadd_rn(re[e], y);
-            if (alpha != 1.0f) y = __fmul_rn(y, alpha);
-        }
-        v[e] = y;
-        if (hidden) hidden[base + i] = y;
-        if (gain2) part2 = __fadd_rn(part2, __fmul_rn(y, y));
-    }
-    if (!codes) return;
-    if (gain2) {
-        const float inv2 = inv_rms(block_tree_sum(part2, lds), width, eps);
-#pragma unroll
-        for (int e = 0; e < kJoinMaxPer; ++e) {
-            const int i = t + e * kDecThreads;
-            if (i < width) codes[base + i] = snap_code(__fmul_rn(__fmul_rn(v[e], inv2), g2[e]), in_scale);
-        }
-    } else {
-#pragma unroll
-        for (int e = 0; e < kJoinMaxPer; ++e) {
-            const int i = t + e * kDecThreads;
-            if (i < width) codes[base + i] = snap_code(v[e], in_scale);
-        }
-    }
+    rms_join_row(J, blockIdx.x, lds);
 }
 
 // ---- q-norm-rope and kv-norm-rope-store ----------------------------------------------------------
@@ -553,9 +463,20 @@ int g4_rms_join(const void *src, int src_kind, float src_scale, const float *gai
     if (codes && in_scale == 0.0f)
         return set_error(G4_ERR_INVALID, "rms-norm: int8 codes need the consumer's inScale");
     if (gain2 && !codes) return set_error(G4_ERR_INVALID, "norm-residual-norm: gain2 without codes");
-    hipLaunchKernelGGL(join_kernel, dim3(rows), dim3(kDecThreads), 0, as_stream(stream), src,
-                       src_kind, src_scale, gain, resid, alpha, gain2, width, eps, in_scale,
-                       hidden, codes);
+    JoinTail J;
+    J.src = src;
+    J.src_kind = src_kind;
+    J.src_scale = src_scale;
+    J.gain = gain;
+    J.resid = resid;
+    J.alpha = alpha;
+    J.gain2 = gain2;
+    J.width = width;
+    J.eps = eps;
+    J.in_scale = in_scale;
+    J.hidden = hidden;
+    J.codes = codes;
+    hipLaunchKernelGGL(join_kernel, dim3(rows), dim3(kDecThreads), 0, as_stream(stream), J);
     G4_LAUNCHED("join_kernel");
     return G4_OK;
 }

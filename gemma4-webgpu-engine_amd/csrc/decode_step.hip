@@ -17,6 +17,11 @@
 //   epilogue (or the gelu-mul pass after it); per_layer_projection (int8 GEMV)
 //   norm-residual-norm (post_per_layer_input_norm, residual, layer_scalar, then the next layer's
 //   input_layernorm, or the final norm on the last layer)
+// The residual stream alternates between two rows: a join reads one and writes the other. At
+// batch 1 every join is the prologue of the projection plan that reads its codes (the layer's
+// gate/up, per_layer_input_gate, the next layer's q/k/v, or the head), computed by each of that
+// plan's blocks in place of its activation snap, so it costs no launch of its own; block 0 writes
+// the new residual row, which the other blocks never read.
 // Embedding phase (plan.ts:720-729): tied int4 embed gather (x sqrt(hidden) folded), PLE gather,
 // per_layer_model_projection (int4 GEMV, then hidden^-0.5), per_layer_projection_norm, + identity,
 // x 2^-0.5. Head (plan.ts:768-777): tied int4 GEMV to f32 logits, softcap, two-stage argmax.
@@ -61,7 +66,8 @@ struct g4_decode {
     std::vector<g4_decode_layer> layers;
     DeviceAlloc mem;
     int32_t *pos = nullptr;
-    float *identity = nullptr, *per_layer = nullptr, *hidden = nullptr;
+    float *identity = nullptr, *per_layer = nullptr;
+    float *hbuf[2] = {nullptr, nullptr};  // the residual stream's two rows (a join reads one, writes the other)
     float *q = nullptr, *attn_ws = nullptr, *logits = nullptr;
     size_t attn_ws_bytes = 0, argmax_ws_bytes = 0;
     void *argmax_ws = nullptr;
@@ -74,6 +80,10 @@ struct g4_decode {
     // M = 1 GEMV plans per layer: qkv (or q), o, gate+up, down, ple gate, ple projection.
     std::vector<Plan> plans;
     Plan ple_model_plan, head_plan;
+    // the step's RMS joins in order: the layer-0 input norm, then three per layer; each either the
+    // prologue of the plan that reads its codes (carried) or a g4_rms_join launch
+    std::vector<JoinTail> joins;
+    std::vector<char> carried;
     ~g4_decode() {
         for (Plan &p : plans)
             if (p.p) g4_qgemv_plan_destroy(p.p);
@@ -200,6 +210,70 @@ int try_gelu_plan(const g4_gemv_desc &gate, const GeluEpilogue &epi, Plan &out) 
     return rc;
 }
 
+// The joins of a step: index 0 the layer-0 input norm (no residual), then for layer l the three at
+// 1 + 3 l + {0, 1, 2}: post-attention (+ pre-feedforward norm), post-feedforward, and the
+// per-layer-input tail (+ layer scalar, the next input norm or the final norm). Join k > 0 reads
+// the residual row hbuf[(k - 1) & 1] and writes hbuf[k & 1].
+int join_index(int layer, int which) { return 1 + 3 * layer + which; }
+
+float *join_resid(g4_decode &d, int k) { return d.hbuf[(k - 1) & 1]; }
+float *join_out(g4_decode &d, int k) { return d.hbuf[k & 1]; }
+
+JoinTail make_join(g4_decode &d, int k, const void *src, int src_kind, float src_scale,
+                   const float *gain, float alpha, const float *gain2, int8_t *codes) {
+    const g4_decode_shape &s = d.s;
+    JoinTail j;
+    j.src = src;
+    j.src_kind = src_kind;
+    j.src_scale = src_scale;
+    j.gain = gain;
+    j.resid = k > 0 ? join_resid(d, k) : nullptr;
+    j.alpha = alpha;
+    j.gain2 = gain2;
+    j.width = s.hidden;
+    j.eps = s.eps;
+    j.in_scale = s.in_scale;
+    j.hidden = k > 0 ? join_out(d, k) : nullptr;
+    j.codes = codes;
+    return j;
+}
+
+void build_joins(g4_decode &d) {
+    const g4_decode_shape &s = d.s;
+    const float out = s.out_scale;
+    d.joins.clear();
+    d.joins.push_back(make_join(d, 0, d.hbuf[0], G4_KIND_F32, 1.0f, d.layers[0].input_norm, 1.0f,
+                                nullptr, d.xcodes));
+    for (int l = 0; l < s.layers; ++l) {
+        const g4_decode_layer &L = d.layers[l];
+        const bool last = l + 1 == s.layers;
+        d.joins.push_back(make_join(d, join_index(l, 0), d.oc, G4_KIND_I8, out, L.post_attn_norm,
+                                    1.0f, L.pre_ffn_norm, d.xcodes));
+        d.joins.push_back(make_join(d, join_index(l, 1), d.dc, G4_KIND_I8, out, L.post_ffn_norm,
+                                    1.0f, nullptr, d.xcodes));
+        d.joins.push_back(make_join(d, join_index(l, 2), d.ppc, G4_KIND_I8, out, L.post_ple_norm,
+                                    L.layer_scalar, last ? d.w.final_norm : d.layers[l + 1].input_norm,
+                                    last ? d.head_codes : d.xcodes));
+    }
+    d.carried.assign(d.joins.size(), 0);
+}
+
+// Makes join k the prologue of `plan` when the plan exists.
+int carry_join(g4_decode &d, int k, const Plan &plan) {
+    if (!plan.p) return G4_OK;
+    G4_TRY(gemv_plan_set_prologue_join(plan.p, d.joins[k]));
+    d.carried[k] = 1;
+    return G4_OK;
+}
+
+// Join k for the step's `batch` rows, unless a plan carries it.
+int run_join(g4_decode &d, int k, void *st) {
+    if (d.carried[k]) return G4_OK;
+    const JoinTail &j = d.joins[k];
+    return g4_rms_join(j.src, j.src_kind, j.src_scale, j.gain, j.resid, j.alpha, j.gain2, d.s.batch,
+                       j.width, j.eps, j.in_scale, j.hidden, j.codes, st);
+}
+
 int build(g4_decode &d) {
     const g4_decode_shape &s = d.s;
     const int B = s.batch, H = s.hidden, F = s.ffn, QW = s.q_heads * s.head_dim;
@@ -211,7 +285,8 @@ int build(g4_decode &d) {
     G4_HIP(hipMemset(d.pos, 0, sizeof(int32_t)));
     G4_TRY(f32(&d.identity, (size_t)B * PL));
     G4_TRY(f32(&d.per_layer, (size_t)B * PL));
-    G4_TRY(f32(&d.hidden, (size_t)B * H));
+    G4_TRY(f32(&d.hbuf[0], (size_t)B * H));
+    G4_TRY(f32(&d.hbuf[1], (size_t)B * H));
     G4_TRY(f32(&d.q, (size_t)B * QW));
     G4_TRY(f32(&d.logits, (size_t)B * s.vocab));
     d.attn_ws_bytes = g4_attention_workspace_bytes(B, s.q_heads, s.kv_capacity - 1, 0);
@@ -240,6 +315,7 @@ int build(g4_decode &d) {
         G4_TRY(f32(&d.kv[p], cache));
         G4_HIP(hipMemset(d.kv[p], 0, cache * sizeof(float)));
     }
+    build_joins(d);
     if (B != 1) return G4_OK;
     // M = 1: one grouped-GEMV plan per launch group.
     const float in = s.in_scale, out = s.out_scale;
@@ -292,6 +368,16 @@ int build(g4_decode &d) {
     g4_gemv_desc hd = desc(d.w.embed, d.w.embed_s, d.head_codes, d.logits, 4, H, (int)s.vocab,
                            G4_KIND_F32, in, 0.0f);
     G4_TRY(try_plan(&hd, 1, d.head_plan));
+    // each join rides in the plan that reads its codes
+    G4_TRY(carry_join(d, 0, d.plans[P_QKV]));
+    for (int l = 0; l < s.layers; ++l) {
+        const Plan *P = &d.plans[(size_t)l * P_PER_LAYER];
+        const bool last = l + 1 == s.layers;
+        G4_TRY(carry_join(d, join_index(l, 0), P[P_GATEUP]));
+        G4_TRY(carry_join(d, join_index(l, 1), P[P_PLE_GATE]));
+        G4_TRY(carry_join(d, join_index(l, 2),
+                          last ? d.head_plan : d.plans[(size_t)(l + 1) * P_PER_LAYER + P_QKV]));
+    }
     return G4_OK;
 }
 
@@ -325,8 +411,7 @@ int run_layer(g4_decode &d, int l, void *st) {
                                s.kv_capacity - 1, d.pos, glob ? 0 : s.sliding_window, d.attn_ws,
                                d.attn_ws_bytes, in, d.attn_codes, nullptr, st));
     G4_TRY(run_linear_rows(d, plan(P_O), desc(L.o, L.o_s, d.attn_codes, d.oc, 4, QW, H, G4_KIND_I8, in, out), st));
-    G4_TRY(g4_rms_join(d.oc, G4_KIND_I8, out, L.post_attn_norm, d.hidden, 1.0f, L.pre_ffn_norm, B,
-                       H, s.eps, in, d.hidden, d.xcodes, st));
+    G4_TRY(run_join(d, join_index(l, 0), st));
     // MLP block: gate, up and the gelu-mul pass (one paired launch when folded), then down
     if (plan(P_GATEUP).gelu) {
         G4_TRY(g4_qgemv_plan_launch(plan(P_GATEUP).p, st));
@@ -337,8 +422,7 @@ int run_layer(g4_decode &d, int l, void *st) {
         G4_TRY(g4_gelu_mul(d.gc, out, d.uc, out, nullptr, 0, B, F, in, d.act, st));
     }
     G4_TRY(run_linear_rows(d, plan(P_DOWN), desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out), st));
-    G4_TRY(g4_rms_join(d.dc, G4_KIND_I8, out, L.post_ffn_norm, d.hidden, 1.0f, nullptr, B, H,
-                       s.eps, in, d.hidden, d.xcodes, st));
+    G4_TRY(run_join(d, join_index(l, 1), st));
     // per-layer-input block: the gate (with gelu times the layer's row folded when planned), then
     // per_layer_projection
     if (plan(P_PLE_GATE).gelu) {
@@ -350,11 +434,22 @@ int run_layer(g4_decode &d, int l, void *st) {
     }
     G4_TRY(run_linear_rows(d, plan(P_PLE_PROJ), desc(L.ple_proj, L.ple_proj_s, d.pac, d.ppc, 8, s.ple_dim, H, G4_KIND_I8, in, out), st));
     // the tail join: residual, layer scalar, then the next input norm (or the final norm)
-    const bool last = l + 1 == s.layers;
-    const float *next_norm = last ? d.w.final_norm : d.layers[l + 1].input_norm;
-    G4_TRY(g4_rms_join(d.ppc, G4_KIND_I8, out, L.post_ple_norm, d.hidden, L.layer_scalar,
-                       next_norm, B, H, s.eps, in, d.hidden, last ? d.head_codes : d.xcodes, st));
+    // the tail join: residual, layer scalar, then the next input norm (or the final norm); a step
+    // that stops here launches it even when the next layer's plan would carry it
+    const int k = join_index(l, 2);
+    if (!d.carried[k] || (l == d.stop && l + 1 < s.layers)) {
+        const JoinTail &j = d.joins[k];
+        G4_TRY(g4_rms_join(j.src, j.src_kind, j.src_scale, j.gain, j.resid, j.alpha, j.gain2, B,
+                           j.width, j.eps, j.in_scale, j.hidden, j.codes, st));
+    }
     return G4_OK;
+}
+
+// The index of the step's last join (its row is the final residual): the tail join of the last
+// layer run.
+int last_join(const g4_decode &d) {
+    const int last = d.stop >= 0 ? d.stop : d.s.layers - 1;
+    return join_index(last, 2);
 }
 
 }  // namespace
@@ -421,7 +516,7 @@ int g4_decode_buffer(g4_decode *d, const char *name, void **ptr, size_t *bytes) 
         void *p;
         size_t b;
     } all[] = {
-        {"hidden", d->hidden, B * s.hidden * 4},
+        {"hidden", d->hbuf[last_join(*d) & 1], B * s.hidden * 4},
         {"logits", d->logits, B * (size_t)s.vocab * 4},
         {"per_layer", d->per_layer, B * s.layers * s.ple_dim * 4},
         {"head_codes", d->head_codes, B * s.hidden},
@@ -444,7 +539,7 @@ int g4_decode_step(g4_decode *d, const int32_t *tokens, int32_t *next_tokens, vo
     // embedding phase: the residual stream starts at the scaled embedding
     const float embed_scale = (float)std::sqrt((double)H);
     G4_TRY(g4_embed_tokens(d->w.embed, d->w.embed_s, tokens, B, s.vocab, H, embed_scale, in,
-                           d->hidden, d->embed_codes, stream));
+                           d->hbuf[0], d->embed_codes, stream));
     // the unsliced gather over all `vocab` rows: an id outside them gives a zero row
     G4_TRY(g4_ple_gather(d->w.ple_table, d->w.ple_table_s, 0, tokens, d->identity, G4_KIND_F32,
                          B, PL, s.ple_dim, s.layers, 0, 0, s.vocab, stream));
@@ -455,8 +550,7 @@ int g4_decode_step(g4_decode *d, const int32_t *tokens, int32_t *next_tokens, vo
     const float alpha = (float)std::pow((double)H, -0.5);
     G4_TRY(g4_ple_combine(d->ple_codes, out, alpha, d->w.ple_proj_norm, d->identity, B, s.layers,
                           s.ple_dim, s.eps, d->per_layer, stream));
-    G4_TRY(g4_rms_join(d->hidden, G4_KIND_F32, 1.0f, d->layers[0].input_norm, nullptr, 1.0f,
-                       nullptr, B, H, s.eps, in, nullptr, d->xcodes, stream));
+    G4_TRY(run_join(*d, 0, stream));
     const int last = d->stop >= 0 ? d->stop : s.layers - 1;
     for (int l = 0; l <= last; ++l) G4_TRY(run_layer(*d, l, stream));
     if (last != s.layers - 1) return G4_OK;

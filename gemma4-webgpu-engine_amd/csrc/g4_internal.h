@@ -66,6 +66,28 @@ struct GeluEpilogue {
 int gemv_plan_create_epilogue(const g4_gemv_desc *descs, const GeluEpilogue *epis, int count,
                               g4_gemv_plan **out);
 
+// One row's RMS join, the arguments of g4_rms_join for rows = 1 (g4_rowops.h rms_join_row).
+struct JoinTail {
+    const void *src = nullptr;
+    int src_kind = G4_KIND_F32;
+    float src_scale = 1.0f;
+    const float *gain = nullptr;
+    const float *resid = nullptr;
+    float alpha = 1.0f;
+    const float *gain2 = nullptr;
+    int width = 0;
+    float eps = 0.0f;
+    float in_scale = 0.0f;
+    float *hidden = nullptr;
+    int8_t *codes = nullptr;
+};
+
+// Makes the RMS join `j` the prologue of a plan (the decode runner's launch fold, no reference
+// counterpart): every projection of the plan reads j.codes (at one bit width), and takes them
+// from the join, which every block computes in place of its snap; block 0 also stores j.hidden and
+// j.codes. j.hidden must not alias j.resid (blocks still read the residual while block 0 writes).
+int gemv_plan_set_prologue_join(g4_gemv_plan *p, const JoinTail &j);
+
 // The internal form of a public g4_gelu_act (NULL or a NULL up: no prologue).
 GeluAct gelu_act_of(const g4_gelu_act *a);
 

@@ -1,0 +1,123 @@
+// Row operations of the decode glue shared by their own kernels (decode.hip) and by the streaming
+// GEMV, whose blocks can run the RMS join that produces their activation row in place of its snap
+// (qgemv_stream.hip).
+//
+// Arithmetic (the CPU restatement oracle/g4_decode_oracle.c states the same steps): a reduction is
+// 256 lane-strided partial sums (lane l takes elements l, l + 256, ... ascending) followed by a
+// pairwise tree (stride 128 down to 1, lane l adds lane l + stride); 1/sqrt is the IEEE square
+// root then the IEEE divide. Every function here expects a block of exactly 256 threads.
+#pragma once
+
+#include "g4_internal.h"
+
+namespace g4 {
+
+constexpr int kRowThreads = 256;
+constexpr int kJoinMaxPer = 8;  // an RMS join serves widths up to 8 * 256
+
+// The pairwise tree over 256 lanes: level s adds lane l + s into lane l for l < s, s = 128 .. 1
+// (every thread of the block calls it; returns the total). The two cross-wave levels go through
+// LDS, the six in-wave levels through lane shuffles, so the same tree costs three barriers.
+// lds: at least 193 floats.
+__device__ __forceinline__ float block_tree_sum(float part, float *lds) {
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+    if (w >= 2) lds[t - 128] = part;
+    __syncthreads();
+    if (w < 2) part = __fadd_rn(part, lds[t]);           // s = 128
+    if (w == 1) lds[128 + lane] = part;
+    __syncthreads();
+    if (w == 0) {
+        part = __fadd_rn(part, lds[128 + lane]);         // s = 64
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, __shfl_down(part, off));
+        if (lane == 0) lds[192] = part;
+    }
+    __syncthreads();
+    const float total = lds[192];
+    __syncthreads();  // the caller may reuse lds at once
+    return total;
+}
+
+// sqrtf, not __fsqrt_rn: on this toolchain __fsqrt_rn is the native (approximate) v_sqrt_f32
+// unless OCML_BASIC_ROUNDED_OPERATIONS is defined, while sqrtf lowers to v_sqrt_f32 plus the
+// neighbour test that makes it correctly rounded.
+__device__ __forceinline__ float inv_rms(float sumsq, int width, float eps) {
+    return __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(sumsq, (float)width), eps)));
+}
+
+__device__ __forceinline__ float load_val(const void *src, int kind, float scale, int64_t i) {
+    if (kind == G4_KIND_I8) return __fmul_rn((float)reinterpret_cast<const int8_t *>(src)[i], scale);
+    return reinterpret_cast<const float *>(src)[i];
+}
+
+__device__ __forceinline__ int8_t snap_code(float v, float s) { return (int8_t)srq_code_i(v, s); }
+
+// rms-norm / norm-residual / norm-residual-norm of one row (rmsNorm.ts:131-180,
+// mlpEpilogue.ts:196-230, blockJoin.ts:160-175): y = (src * inv) * gain (gain null: weightless);
+// with a residual, hidden = resid + y, times alpha when alpha != 1. Outputs: hidden (f32, when
+// J.hidden is set), and emit(i, code) for every element i < width with the code of either the
+// second norm of hidden (gain2 given) or of hidden itself, snapped on in_scale (when J.codes is
+// set). lds: at least 193 floats.
+template <typename Emit>
+__device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row, float *lds,
+                                                  Emit emit) {
+    const int t = threadIdx.x;
+    const int width = J.width;
+    const int64_t base = row * width;
+    // every operand is loaded before the first barrier (a barrier also fences the compiler's
+    // load scheduling, so later loads would each cost a memory latency of their own)
+    float v[kJoinMaxPer], ga[kJoinMaxPer], re[kJoinMaxPer], g2[kJoinMaxPer];
+#pragma unroll
+    for (int e = 0; e < kJoinMaxPer; ++e) {
+        const int i = t + e * kRowThreads;
+        const bool in = i < width;
+        v[e] = in ? load_val(J.src, J.src_kind, J.src_scale, base + i) : 0.0f;
+        ga[e] = in && J.gain ? J.gain[i] : 1.0f;
+        re[e] = in && J.resid ? J.resid[base + i] : 0.0f;
+        g2[e] = in && J.gain2 ? J.gain2[i] : 0.0f;
+    }
+    float part = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kJoinMaxPer; ++e)
+        if (t + e * kRowThreads < width) part = __fadd_rn(part, __fmul_rn(v[e], v[e]));
+    const float inv = inv_rms(block_tree_sum(part, lds), width, J.eps);
+    float part2 = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kJoinMaxPer; ++e) {
+        const int i = t + e * kRowThreads;
+        if (i >= width) continue;
+        float y = __fmul_rn(v[e], inv);
+        if (J.gain) y = __fmul_rn(y, ga[e]);
+        if (J.resid) {
+            y = __fadd_rn(re[e], y);
+            if (J.alpha != 1.0f) y = __fmul_rn(y, J.alpha);
+        }
+        v[e] = y;
+        if (J.hidden) J.hidden[base + i] = y;
+        if (J.gain2) part2 = __fadd_rn(part2, __fmul_rn(y, y));
+    }
+    if (!J.codes) return;
+    if (J.gain2) {
+        const float inv2 = inv_rms(block_tree_sum(part2, lds), width, J.eps);
+#pragma unroll
+        for (int e = 0; e < kJoinMaxPer; ++e) {
+            const int i = t + e * kRowThreads;
+            if (i < width) emit(i, snap_code(__fmul_rn(__fmul_rn(v[e], inv2), g2[e]), J.in_scale));
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < kJoinMaxPer; ++e) {
+            const int i = t + e * kRowThreads;
+            if (i < width) emit(i, snap_code(v[e], J.in_scale));
+        }
+    }
+}
+
+// The join kernel's form: codes to J.codes[row][i].
+__device__ __forceinline__ void rms_join_row(const JoinTail &J, int64_t row, float *lds) {
+    int8_t *codes = J.codes;
+    const int64_t base = row * J.width;
+    rms_join_row_emit(J, row, lds, [=](int i, int8_t c) { codes[base + i] = c; });
+}
+
+}  // namespace g4

@@ -22,7 +22,7 @@
 // Job descriptors travel in the kernel arguments (up to kMaxKargJobs, the per-call entry points)
 // or in a device table built once by g4_qgemv_plan_create (any count, the decode-step form: the
 // reference caches its per-token bind the same way, runtime.ts:702-767).
-#include "g4_internal.h"
+#include "g4_rowops.h"
 
 #include <algorithm>
 #include <vector>
@@ -33,6 +33,7 @@ constexpr int kStreamThreads = 256;
 constexpr int kMaxKargJobs = 16;
 constexpr int kStreamMaxK = 16384;
 constexpr int kBlocksPerCu = 8;
+static_assert(kStreamThreads == kRowThreads, "a prologue join runs on the GEMV's block");
 
 #define G4_GLOBAL __attribute__((address_space(1)))
 
@@ -64,7 +65,8 @@ struct StreamJob {
     int8_t cls;
     int8_t up_kind;
     int8_t epi;
-    int8_t pad[14];
+    int8_t pre;  // x is the codes of the plan's prologue join, computed by every block (no snap)
+    int8_t pad[13];
 };
 static_assert(sizeof(StreamJob) == 112, "StreamJob is one 112-byte record");
 
@@ -73,6 +75,7 @@ struct StreamArgs {
     const int *block_job;    // plan launches: the job of each block's first tile
     int njobs;
     int total_tiles;
+    const JoinTail *pre;     // plan launches: the RMS join whose codes the `pre` jobs read; or null
     StreamJob job[kMaxKargJobs];
 };
 
@@ -241,6 +244,37 @@ __device__ __forceinline__ int snap_gelu(const StreamJob &J, uint8_t *xs, int ti
     return local;
 }
 
+// The block's sum of its threads' code sums (after the snap's LDS stores).
+__device__ __forceinline__ int block_code_sum(int local, int *s_sum, int tid) {
+    if (tid == 0) *s_sum = 0;
+    lds_barrier();
+    local = row16_sum_i32(local);
+    if ((tid & 15) == 0 && local != 0) atomicAdd(s_sum, local);
+    lds_barrier();
+    return *s_sum;
+}
+
+// The prologue join's snap: every block runs the RMS join that produces the job's activation row
+// (the same arithmetic as the join kernel, so the same codes) and stores its codes in the snap
+// layout; block 0 also stores the join's outputs (the new residual row and the codes) for the
+// kernels after this one. Replaces a join launch between the producer GEMV and this one.
+__device__ __forceinline__ int snap_join(const JoinTail *pre, int four, uint8_t *xs) {
+    JoinTail T = *pre;
+    // the reduction tree sits in the dynamic LDS after the codes (the launch sizes it so); a
+    // static array would shift every code address of the tile loop by its size
+    float *red = reinterpret_cast<float *>(xs + ((T.width + 15) & ~15));
+    int8_t *codes = blockIdx.x == 0 ? T.codes : nullptr;
+    if (blockIdx.x != 0) T.hidden = nullptr;
+    int local = 0;
+    rms_join_row_emit(T, 0, red, [&](int i, int8_t c) {
+        const int j = i & 7;
+        xs[four ? (i & ~7) + (j & 1 ? 4 : 0) + (j >> 1) : i] = (uint8_t)c;
+        if (codes) gstore<int8_t>(codes + i, c);
+        local += c;
+    });
+    return local;
+}
+
 // Snaps the K activations of job J into int8 codes in LDS (4-bit jobs: each 8-code group stored
 // as [x0 x2 x4 x6 | x1 x3 x5 x7] so a weight word's low and high nibbles each dot one half) and
 // returns sum(xq) over the whole vector, which takes the 4-bit zero point off once per row.
@@ -254,12 +288,13 @@ __device__ __forceinline__ int snap_activations(const StreamJob &J, uint8_t *xs,
         local = snap_kind<G4_KIND_F32>(J, xs, tid);
     else
         local = snap_kind<G4_KIND_I8>(J, xs, tid);
-    if (tid == 0) *s_sum = 0;
-    lds_barrier();
-    local = row16_sum_i32(local);
-    if ((tid & 15) == 0 && local != 0) atomicAdd(s_sum, local);
-    lds_barrier();
-    return *s_sum;
+    return block_code_sum(local, s_sum, tid);
+}
+
+// The codes of a prologue join in the snap layout, and their sum.
+__device__ __forceinline__ int snap_join_codes(const JoinTail *pre, bool four, uint8_t *xs,
+                                               int *s_sum, int tid) {
+    return block_code_sum(snap_join(pre, four, xs), s_sum, tid);
 }
 
 // One output element of job J at row `row` (the reference's epilogue, qgemv.ts:680-686).
@@ -401,7 +436,10 @@ __device__ __forceinline__ void stream_dispatch(const StreamJob &J, int t, const
 static_assert(kNumClasses == 17, "stream_dispatch lists every class");
 static_assert(kClasses[7].bits == 4 && kClasses[8].bits == 8, "classes 0-7 are the 4-bit ones");
 
-template <bool TABLE, bool PAIR>
+// JOIN (plan launches whose jobs all read a prologue join's codes): the block's codes come from
+// the join, computed before the job is loaded for the tile loop (so the job's fields are not live
+// across the join, whose registers would push them to scratch), and stay for every job.
+template <bool TABLE, bool PAIR, bool JOIN>
 __device__ __forceinline__ void stream_body(const StreamArgs &A, uint8_t *xs, int *s_sum) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -418,34 +456,43 @@ __device__ __forceinline__ void stream_body(const StreamArgs &A, uint8_t *xs, in
         for (int i = 1; i < kMaxKargJobs; ++i)
             if (i < A.njobs && t0 >= A.job[i].tile_begin) j = i;
     }
-    StreamJob J = TABLE ? A.table[j] : A.job[j];
-    int sx = snap_activations(J, xs, s_sum, tid);
+    int sx;
+    StreamJob J;
+    if (JOIN) {
+        sx = snap_join_codes(A.pre, A.table[j].bits == 4, xs, s_sum, tid);
+        J = A.table[j];
+    } else {
+        J = TABLE ? A.table[j] : A.job[j];
+        sx = snap_activations(J, xs, s_sum, tid);
+    }
     for (int t = t0; t < t1; ++t) {
         if (t >= J.tile_begin + J.tiles) {
             ++j;
             J = TABLE ? A.table[j] : A.job[j];
-            __syncthreads();  // every wave is done with the previous job's codes
-            sx = snap_activations(J, xs, s_sum, tid);
+            if (!JOIN) {
+                __syncthreads();  // every wave is done with the previous job's codes
+                sx = snap_activations(J, xs, s_sum, tid);
+            }
         }
         stream_dispatch<PAIR>(J, t, xs, sx, wave, lane);
     }
 }
 
-template <bool TABLE>
+template <bool TABLE, bool JOIN>
 __global__ __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void qgemv_stream_kernel(StreamArgs A) {
     extern __shared__ __align__(16) uint8_t xs[];
     __shared__ int s_sum;
-    stream_body<TABLE, false>(A, xs, &s_sum);
+    stream_body<TABLE, false, JOIN>(A, xs, &s_sum);
 }
 
 // The same with paired gate/up jobs: twice the weight registers, so half the waves per SIMD.
-template <bool TABLE>
+template <bool TABLE, bool JOIN>
 __global__ __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(4, 8)))
 void qgemv_stream_pair_kernel(StreamArgs A) {
     extern __shared__ __align__(16) uint8_t xs[];
     __shared__ int s_sum;
-    stream_body<TABLE, true>(A, xs, &s_sum);
+    stream_body<TABLE, true, JOIN>(A, xs, &s_sum);
 }
 
 // Fills a StreamJob from a validated descriptor and prologue; returns false when no class fits.
@@ -500,7 +547,7 @@ int launch_stream_karg(StreamJob *jobs, int count, hipStream_t stream) {
     A.njobs = count;
     for (int i = 0; i < count; ++i) A.job[i] = jobs[i];
     const int grid = grid_for(A.total_tiles);
-    hipLaunchKernelGGL(qgemv_stream_kernel<false>, dim3(grid), dim3(kStreamThreads),
+    hipLaunchKernelGGL((qgemv_stream_kernel<false, false>), dim3(grid), dim3(kStreamThreads),
                        (size_t)((max_k + 15) & ~15), stream, A);
     G4_LAUNCHED("qgemv_stream_kernel");
     return G4_OK;
@@ -535,6 +582,7 @@ struct g4_gemv_plan {
     int max_k = 0;
     int device = 0;
     bool paired = false;  // launches qgemv_stream_pair_kernel
+    JoinTail *pre = nullptr;  // device copy of the prologue join, or null
 };
 
 namespace g4 {
@@ -609,6 +657,38 @@ int gemv_plan_create_epilogue(const g4_gemv_desc *descs, const GeluEpilogue *epi
     return plan_from_jobs(jobs, out);
 }
 
+int gemv_plan_set_prologue_join(g4_gemv_plan *p, const JoinTail &j) {
+    if (!p) return set_error(G4_ERR_INVALID, "GEMV plan join: plan is NULL");
+    if (!j.src || j.width <= 0 || j.width > kJoinMaxPer * kRowThreads || (j.width & 7))
+        return set_error(G4_ERR_INVALID, "GEMV plan join: width %d (a multiple of 8, at most %d)",
+                         j.width, kJoinMaxPer * kRowThreads);
+    if (j.src_kind != G4_KIND_F32 && j.src_kind != G4_KIND_I8)
+        return set_error(G4_ERR_INVALID, "GEMV plan join: src_kind must be f32 or int8 codes");
+    if (!j.codes || j.in_scale == 0.0f)
+        return set_error(G4_ERR_INVALID, "GEMV plan join: needs its codes and the consumer's inScale");
+    if (j.resid && j.hidden == j.resid)
+        return set_error(G4_ERR_INVALID,
+                         "GEMV plan join: every block reads the residual, so the new row needs "
+                         "its own buffer");
+    // the projections read the join's codes from the join
+    std::vector<StreamJob> jobs(p->njobs);
+    G4_HIP(hipMemcpy(jobs.data(), p->table, sizeof(StreamJob) * p->njobs, hipMemcpyDeviceToHost));
+    // (every job, with one bit width: a block snaps once, at its first tile)
+    for (StreamJob &J : jobs) {
+        if (J.x != j.codes || J.x_kind != G4_KIND_I8 || J.up || J.k != j.width ||
+            J.in_scale != j.in_scale || J.bits != jobs[0].bits)
+            return set_error(G4_ERR_INVALID,
+                             "GEMV plan join: every projection of the plan must read the join's %d "
+                             "int8 codes on its inScale, at one bit width, without a gelu prologue",
+                             j.width);
+        J.pre = 1;
+    }
+    G4_HIP(hipMemcpy(p->table, jobs.data(), sizeof(StreamJob) * p->njobs, hipMemcpyHostToDevice));
+    if (!p->pre) G4_HIP(hipMalloc(&p->pre, sizeof(JoinTail)));
+    G4_HIP(hipMemcpy(p->pre, &j, sizeof(JoinTail), hipMemcpyHostToDevice));
+    return G4_OK;
+}
+
 }  // namespace g4
 
 extern "C" {
@@ -646,12 +726,19 @@ int g4_qgemv_plan_launch(const g4_gemv_plan *p, void *stream) {
     A.block_job = p->block_job;
     A.njobs = p->njobs;
     A.total_tiles = p->total_tiles;
-    if (p->paired)
-        hipLaunchKernelGGL(qgemv_stream_pair_kernel<true>, dim3(p->grid), dim3(kStreamThreads),
-                           (size_t)((p->max_k + 15) & ~15), as_stream(stream), A);
+    A.pre = p->pre;
+    // with a prologue join, the join's reduction tree follows the codes
+    const size_t lds = (size_t)((p->max_k + 15) & ~15) + (p->pre ? kRowThreads * sizeof(float) : 0);
+    const dim3 grid(p->grid), block(kStreamThreads);
+    const hipStream_t st = as_stream(stream);
+    if (p->paired && p->pre)
+        hipLaunchKernelGGL((qgemv_stream_pair_kernel<true, true>), grid, block, lds, st, A);
+    else if (p->paired)
+        hipLaunchKernelGGL((qgemv_stream_pair_kernel<true, false>), grid, block, lds, st, A);
+    else if (p->pre)
+        hipLaunchKernelGGL((qgemv_stream_kernel<true, true>), grid, block, lds, st, A);
     else
-        hipLaunchKernelGGL(qgemv_stream_kernel<true>, dim3(p->grid), dim3(kStreamThreads),
-                           (size_t)((p->max_k + 15) & ~15), as_stream(stream), A);
+        hipLaunchKernelGGL((qgemv_stream_kernel<true, false>), grid, block, lds, st, A);
     G4_LAUNCHED("qgemv_stream_kernel");
     return G4_OK;
 }
@@ -667,6 +754,7 @@ int g4_qgemv_plan_destroy(g4_gemv_plan *p) {
     if (!p) return G4_OK;
     (void)hipFree(p->table);
     (void)hipFree(p->block_job);
+    (void)hipFree(p->pre);
     delete p;
     return G4_OK;
 }
