@@ -392,10 +392,13 @@ int run_layer(g4_decode &d, int l, void *st) {
     auto plan = [&](int i) -> const Plan & { return P ? P[i] : none; };
 
     // attention block
-    G4_TRY(run_linear_rows(d, plan(P_QKV), desc(L.q, L.q_s, d.xcodes, d.qc, 4, H, QW, G4_KIND_I8, in, out), st));
-    if (prod && !plan(P_QKV).p) {
-        G4_TRY(run_linear_rows(d, none, desc(L.k, L.k_s, d.xcodes, d.kc, 4, H, s.head_dim, G4_KIND_I8, in, out), st));
-        G4_TRY(run_linear_rows(d, none, desc(L.v, L.v_s, d.xcodes, d.vc, 4, H, s.head_dim, G4_KIND_I8, in, out), st));
+    if (plan(P_QKV).p) {
+        G4_TRY(g4_qgemv_plan_launch(plan(P_QKV).p, st));
+    } else {  // q (+ k, v) over the same codes: one grouped launch
+        const LinearOut qkv[3] = {{L.q, L.q_s, d.qc, QW},
+                                  {L.k, L.k_s, d.kc, s.head_dim},
+                                  {L.v, L.v_s, d.vc, s.head_dim}};
+        G4_TRY(linear_grouped(4, d.xcodes, G4_KIND_I8, H, B, in, out, G4_KIND_I8, qkv, prod ? 3 : 1, st));
     }
     const int src = kv_source(s, l);
     float *kb = d.kv[src];
@@ -416,9 +419,12 @@ int run_layer(g4_decode &d, int l, void *st) {
     if (plan(P_GATEUP).gelu) {
         G4_TRY(g4_qgemv_plan_launch(plan(P_GATEUP).p, st));
     } else {
-        G4_TRY(run_linear_rows(d, plan(P_GATEUP), desc(L.gate, L.gate_s, d.xcodes, d.gc, 4, H, F, G4_KIND_I8, in, out), st));
-        if (!plan(P_GATEUP).p)
-            G4_TRY(run_linear_rows(d, none, desc(L.up, L.up_s, d.xcodes, d.uc, 4, H, F, G4_KIND_I8, in, out), st));
+        if (plan(P_GATEUP).p) {
+            G4_TRY(g4_qgemv_plan_launch(plan(P_GATEUP).p, st));
+        } else {  // gate and up over the same codes: one grouped launch
+            const LinearOut gu[2] = {{L.gate, L.gate_s, d.gc, F}, {L.up, L.up_s, d.uc, F}};
+            G4_TRY(linear_grouped(4, d.xcodes, G4_KIND_I8, H, B, in, out, G4_KIND_I8, gu, 2, st));
+        }
         G4_TRY(g4_gelu_mul(d.gc, out, d.uc, out, nullptr, 0, B, F, in, d.act, st));
     }
     G4_TRY(run_linear_rows(d, plan(P_DOWN), desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out), st));

@@ -88,6 +88,20 @@ struct JoinTail {
 // j.codes. j.hidden must not alias j.resid (blocks still read the residual while block 0 writes).
 int gemv_plan_set_prologue_join(g4_gemv_plan *p, const JoinTail &j);
 
+// One output of a grouped linear: weights, row scales, destination and row count.
+struct LinearOut {
+    const void *wq;
+    const float *scales;
+    void *dst;
+    int n;
+};
+
+// Several linears over the same activations x (m rows of k) and scales (qgemm.hip): one launch of
+// the small-M kernel when every output takes it (m 3..32) and there are at most 4, else one
+// library call each. Validated as g4_linear validates each.
+int linear_grouped(int bits, const void *x, int x_kind, int k, int m, float in_scale,
+                   float out_scale, int out_kind, const LinearOut *outs, int count, void *stream);
+
 // The internal form of a public g4_gelu_act (NULL or a NULL up: no prologue).
 GeluAct gelu_act_of(const g4_gelu_act *a);
 

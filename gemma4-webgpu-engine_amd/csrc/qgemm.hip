@@ -14,8 +14,11 @@
 // Kernels by M (chosen per shape, see pick_kernel):
 //   M <= 2         the GEMV family (qgemv.hip): bit-identical, cheaper than any tile at this M.
 //   3 <= M <= 32   qgemm_small_kernel: one launch with the snap fused (codes in LDS), 16 weight
-//                  rows per block, the 4 waves split K, an LDS fold of the 4 partials.
-//   M > 32         qgemm_tile_kernel: 64 x 96 output tiles, activation codes and weights streamed
+//                  rows per block, the block's waves split K (4, or 16 when the grid is no wider
+//                  than the CU count), an LDS fold of the partials; several projections of the
+//                  same x can share one grid (linear_grouped).
+//   M > 32, or over 32768+ rows
+//                  qgemm_tile_kernel: 64 x 96 output tiles, activation codes and weights streamed
 //                  global -> LDS by direct loads through a 3-4 stage ring, XCD-aware tile order.
 #include "g4_internal.h"
 
@@ -119,32 +122,68 @@ __device__ __forceinline__ void store_tile_out(void *dst, int m, int n, int N, i
     store_linear_out(dst, (int64_t)m * N + n, out_kind, y, acc, out_scale);
 }
 
-// ---- small M: M <= MT token rows, 16 weight rows per block, K split over the 4 waves ----------
+// ---- small M: M <= MT token rows, 16 weight rows per block, K split over the block's waves ------
 // The activation snap is fused: the block snaps its MT token rows into LDS as int8 codes (the
 // 4-bit interleave per 8-code group) one K chunk at a time, so a draft-verify or small prefill
 // call is one launch. The 4-bit zero point needs sum(xq) per token row: one more MFMA per step
-// against an all-ones B operand gives it exactly, folded with the partials like the products. Lane (j = lane % 16, g = lane / 16)
-// owns weight row n0 + j; per 128-code stage it loads 16 bytes of that row (8-bit: 32), and MFMA
-// half-step s takes codes g*32 + s*16 .. +16 of the stage from both operands. The LDS rows are
-// padded by 16 bytes so the 16 token rows of one A read fall on distinct banks.
-template <int BITS, int MT>
-__global__ __launch_bounds__(256) void qgemm_small_kernel(
-    const void *__restrict__ x, int x_kind, const uint8_t *__restrict__ W,
-    const float *__restrict__ scales, void *dst, int M, int N, int K, float in_scale,
+// against an all-ones B operand gives it exactly, folded with the partials like the products.
+// Lane (j = lane % 16, g = lane / 16) owns weight row n0 + j; per 128-code stage it loads 16 bytes
+// of that row (8-bit: 32), and MFMA half-step s takes codes g*32 + s*16 .. +16 of the stage from
+// both operands. The LDS rows are padded by 16 bytes so the 16 token rows of one A read fall on
+// distinct banks.
+//
+// WAVES: 4 for wide outputs (many blocks); 16 when the output has too few 16-row blocks to fill
+// the chip (N = 1536 gives 96), so each block walks its K four times faster: a chunk of 128-code
+// steps has one step per wave, and the fold of the 16 partial tiles goes through LDS. The sums are
+// int32 and exact, so the split changes no result.
+//
+// Grouped launches: up to kSmallMaxJobs projections of the same x, K and scales (q, k, v; gate and
+// up) share one grid; block b belongs to the first job whose block_end exceeds it.
+constexpr int kSmallMaxJobs = 4;
+struct SmallJobs {
+    const uint8_t *w[kSmallMaxJobs];
+    const float *scales[kSmallMaxJobs];
+    void *dst[kSmallMaxJobs];
+    int n[kSmallMaxJobs];
+    int block_end[kSmallMaxJobs];  // cumulative 16-row blocks
+    int count;
+};
+
+template <int MT, int WAVES> constexpr int small_kc() { return (WAVES >= 16 ? 65536 : 32768) / MT; }
+
+template <int BITS, int MT, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
+    const void *__restrict__ x, int x_kind, SmallJobs jobs, int M, int K, float in_scale,
     float out_scale, int out_kind) {
+    constexpr int THREADS = WAVES * 64;
     constexpr int TM = MT / 16;
-    constexpr int KC = 32768 / MT;     // codes of a row per LDS chunk
-    constexpr int XSTR = KC + 16;      // LDS bytes per token row
-    constexpr int BATCH = 4;
+    constexpr int KC = small_kc<MT, WAVES>();  // codes of a row per LDS chunk
+    constexpr int XSTR = KC + 16;              // LDS bytes per token row
+    constexpr int BATCH = WAVES >= 16 ? 1 : 4;
     constexpr int NACC = BITS == 4 ? 2 * TM : TM;  // products, then (4-bit) the row sums
     __shared__ __align__(16) int8_t xs[MT * XSTR];
-    __shared__ v4i red[3][NACC][64];
+    __shared__ v4i red[WAVES - 1][NACC][64];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int j = lane & 15;
     const int g = lane >> 4;
-    const int n0 = blockIdx.x * 16;
+    // the block's job (uniform selects, no indexed kernel-argument array)
+    const uint8_t *W = jobs.w[0];
+    const float *scales = jobs.scales[0];
+    void *dst = jobs.dst[0];
+    int N = jobs.n[0], begin = 0;
+#pragma unroll
+    for (int i = 1; i < kSmallMaxJobs; ++i) {
+        if (i < jobs.count && (int)blockIdx.x >= jobs.block_end[i - 1]) {
+            W = jobs.w[i];
+            scales = jobs.scales[i];
+            dst = jobs.dst[i];
+            N = jobs.n[i];
+            begin = jobs.block_end[i - 1];
+        }
+    }
+    const int n0 = ((int)blockIdx.x - begin) * 16;
     const int m0 = blockIdx.y * MT;
     const int n = min(n0 + j, N - 1);
     const int row_bytes = BITS == 4 ? (K >> 1) : K;
@@ -160,55 +199,82 @@ __global__ __launch_bounds__(256) void qgemm_small_kernel(
         const int kcn = min(KC, K - kc0);
         const int gpr = kcn >> 3;  // 8-code groups per row in this chunk
         lds_barrier();  // the previous chunk's codes are no longer read
-        for (int q = tid; q < MT * gpr; q += 256) {
-            const int r = q / gpr, gi = q - r * gpr;
-            const int m = m0 + r;
-            int c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (m < M) {
-                const int64_t e = (int64_t)m * K + kc0 + gi * 8;
+        // the snap: each thread issues the loads of SB groups (indices clamped, so every load is
+        // valid) before converting any, so a chunk costs one memory latency per SB groups. Only
+        // the block's real token rows are snapped: a padding row's LDS codes reach only the
+        // products of its own output row, which is never stored.
+        constexpr int SB = 4;
+        const int total = min(MT, M - m0) * gpr;
+        for (int q0 = tid; q0 < total; q0 += SB * THREADS) {
+            u32x4 raw_a[SB], raw_b[SB];
+            int rr[SB], gg[SB];  // row and group of each load, kept for the stores (one divide)
+#pragma unroll
+            for (int u = 0; u < SB; ++u) {
+                const int q = min(q0 + u * THREADS, total - 1);
+                const int r = q / gpr, gi = q - r * gpr;
+                rr[u] = r;
+                gg[u] = gi;
+                const int64_t e = (int64_t)(m0 + r) * K + kc0 + gi * 8;
                 if (x_kind == G4_KIND_I8) {
                     const uint2 v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const int8_t *>(x) + e);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        c[i] = (int)(int8_t)((v.x >> (8 * i)) & 0xff);
-                        c[4 + i] = (int)(int8_t)((v.y >> (8 * i)) & 0xff);
-                    }
+                    raw_a[u] = u32x4{v.x, v.y, 0u, 0u};
+                    raw_b[u] = u32x4{0u, 0u, 0u, 0u};
                 } else if (x_kind == G4_KIND_F16) {
-                    const u32x4 v = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const __half *>(x) + e);
-                    const uint32_t h[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        c[2 * i] = (int)srq_code_fast(
-                            __half2float(__ushort_as_half((unsigned short)(h[i] & 0xffff))), in_scale, rcp, r_ok);
-                        c[2 * i + 1] = (int)srq_code_fast(
-                            __half2float(__ushort_as_half((unsigned short)(h[i] >> 16))), in_scale, rcp, r_ok);
-                    }
+                    raw_a[u] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const __half *>(x) + e);
+                    raw_b[u] = u32x4{0u, 0u, 0u, 0u};
                 } else {
-                    const float4 *p4 = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(x) + e);
-                    const float4 v0 = p4[0], v1 = p4[1];
-                    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) c[i] = (int)srq_code_fast(v[i], in_scale, rcp, r_ok);
+                    const u32x4 *p4 = reinterpret_cast<const u32x4 *>(reinterpret_cast<const float *>(x) + e);
+                    raw_a[u] = p4[0];
+                    raw_b[u] = p4[1];
                 }
             }
-            uint2 packed;
-            if (BITS == 4) {
-                packed.x = pack4b(c[0], c[2], c[4], c[6]);
-                packed.y = pack4b(c[1], c[3], c[5], c[7]);
-            } else {
-                packed.x = pack4b(c[0], c[1], c[2], c[3]);
-                packed.y = pack4b(c[4], c[5], c[6], c[7]);
+#pragma unroll
+            for (int u = 0; u < SB; ++u) {
+                if (q0 + u * THREADS >= total) break;
+                const int r = rr[u], gi = gg[u];
+                int c[8];
+                {
+                    if (x_kind == G4_KIND_I8) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            c[i] = (int)(int8_t)((raw_a[u].x >> (8 * i)) & 0xff);
+                            c[4 + i] = (int)(int8_t)((raw_a[u].y >> (8 * i)) & 0xff);
+                        }
+                    } else if (x_kind == G4_KIND_F16) {
+                        const uint32_t h[4] = {raw_a[u].x, raw_a[u].y, raw_a[u].z, raw_a[u].w};
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            c[2 * i] = (int)srq_code_fast(
+                                __half2float(__ushort_as_half((unsigned short)(h[i] & 0xffff))), in_scale, rcp, r_ok);
+                            c[2 * i + 1] = (int)srq_code_fast(
+                                __half2float(__ushort_as_half((unsigned short)(h[i] >> 16))), in_scale, rcp, r_ok);
+                        }
+                    } else {
+                        const uint32_t v[8] = {raw_a[u].x, raw_a[u].y, raw_a[u].z, raw_a[u].w,
+                                               raw_b[u].x, raw_b[u].y, raw_b[u].z, raw_b[u].w};
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) c[i] = (int)srq_code_fast(__uint_as_float(v[i]), in_scale, rcp, r_ok);
+                    }
+                }
+                uint2 packed;
+                if (BITS == 4) {
+                    packed.x = pack4b(c[0], c[2], c[4], c[6]);
+                    packed.y = pack4b(c[1], c[3], c[5], c[7]);
+                } else {
+                    packed.x = pack4b(c[0], c[1], c[2], c[3]);
+                    packed.y = pack4b(c[4], c[5], c[6], c[7]);
+                }
+                *reinterpret_cast<uint2 *>(&xs[r * XSTR + gi * 8]) = packed;
             }
-            *reinterpret_cast<uint2 *>(&xs[r * XSTR + gi * 8]) = packed;
         }
         lds_barrier();
         const int ksteps = kcn / kTileBK;
         const int kbase = kc0 / kTileBK;
-        for (int kb0 = wave; kb0 < ksteps; kb0 += 4 * BATCH) {
+        for (int kb0 = wave; kb0 < ksteps; kb0 += WAVES * BATCH) {
             u32x4 bw[BATCH][BITS == 4 ? 1 : 2];
 #pragma unroll
             for (int u = 0; u < BATCH; ++u) {
-                const int kb = min(kb0 + 4 * u, ksteps - 1);  // clamped: every load is valid
+                const int kb = min(kb0 + WAVES * u, ksteps - 1);  // clamped: every load is valid
                 if (BITS == 4) {
                     bw[u][0] = *reinterpret_cast<const u32x4 *>(wrow + (kbase + kb) * 64 + g * 16);
                 } else {
@@ -219,7 +285,7 @@ __global__ __launch_bounds__(256) void qgemm_small_kernel(
             }
 #pragma unroll
             for (int u = 0; u < BATCH; ++u) {
-                const int kb = kb0 + 4 * u;
+                const int kb = kb0 + WAVES * u;
                 if (kb < ksteps) {
 #pragma unroll
                     for (int s = 0; s < 2; ++s) {
@@ -233,9 +299,7 @@ __global__ __launch_bounds__(256) void qgemm_small_kernel(
                             const v4i a = *reinterpret_cast<const v4i *>(
                                 &xs[(t * 16 + j) * XSTR + kb * kTileBK + g * 32 + s * 16]);
                             acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[t], 0, 0, 0);
-                            if (BITS == 4 && s == 0)  // each code counted once: both halves
-                                acc[TM + t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, ones, acc[TM + t], 0, 0, 0);
-                            if (BITS == 4 && s == 1)
+                            if (BITS == 4)  // each code counted once: both halves
                                 acc[TM + t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, ones, acc[TM + t], 0, 0, 0);
                         }
                     }
@@ -243,7 +307,7 @@ __global__ __launch_bounds__(256) void qgemm_small_kernel(
             }
         }
     }
-    // Fold the four waves' partial tiles through LDS, then wave 0 writes.
+    // Fold the waves' partial tiles through LDS, then wave 0 writes.
     if (wave > 0) {
 #pragma unroll
         for (int t = 0; t < NACC; ++t) red[wave - 1][t][lane] = acc[t];
@@ -260,7 +324,7 @@ __global__ __launch_bounds__(256) void qgemm_small_kernel(
                 v4i a = acc[t];
                 v4i rsum = BITS == 4 ? acc[TM + t] : v4i{0, 0, 0, 0};
 #pragma unroll
-                for (int w = 0; w < 3; ++w) {
+                for (int w = 0; w < WAVES - 1; ++w) {
                     a += red[w][t][lane];
                     if (BITS == 4) rsum += red[w][TM + t][lane];
                 }
@@ -633,12 +697,15 @@ static int workspace(void *stream, size_t bytes, void **out) {
 enum KernelChoice { K_GEMV = 0, K_SKINNY16, K_SKINNY32, K_TILE128, K_GEMV_F32, K_GEMV_COLS };
 
 static KernelChoice pick_kernel(int bits, int m, int n, int k, float in_scale) {
-    (void)n;
     if (in_scale == 0.0f) return K_GEMV_F32;
     if (m <= 2) return K_GEMV;
     if (k % kTileBK != 0) return K_GEMV_COLS;
+    // the small kernel snaps all of x in each 16-row block: past 32768 rows (the tied head) the
+    // re-reads outweigh the weights, and the 64-row tile (mostly padding rows) streams faster
+    if (n >= 32768 && k >= 2 * kTileBK) return K_TILE128;
     if (m <= 16) return K_SKINNY16;
-    if (m <= 32 || k < 2 * kTileBK) return K_SKINNY32;  // the tile ring needs two K stages
+    if (k < 2 * kTileBK) return K_SKINNY32;  // the tile ring needs two K stages
+    if (m <= 32) return K_SKINNY32;
     (void)bits;
     return K_TILE128;
 }
@@ -652,6 +719,35 @@ static const char *choice_name(KernelChoice c, int bits) {
         case K_GEMV_F32: return bits == 4 ? "qgemv-4bit-f32" : "qgemv-8bit-f32";
         default: return bits == 4 ? "qgemv-4bit-columns" : "qgemv-8bit-columns";
     }
+}
+
+// The small-M kernel over `jobs` (16-row blocks laid end to end): 16 waves per block when the
+// grid has no more blocks than the device has CUs (each block then walks its K four times
+// faster), else 4.
+template <int BITS, int MT>
+static void launch_small_t(const void *x, int x_kind, const SmallJobs &jobs, int m, int k,
+                           float in_scale, float out_scale, int out_kind, hipStream_t stream) {
+    const dim3 grid(jobs.block_end[jobs.count - 1], (m + MT - 1) / MT);
+    if ((int64_t)grid.x * grid.y <= device_cu_count())
+        hipLaunchKernelGGL((qgemm_small_kernel<BITS, MT, 16>), grid, dim3(1024), 0, stream, x,
+                           x_kind, jobs, m, k, in_scale, out_scale, out_kind);
+    else
+        hipLaunchKernelGGL((qgemm_small_kernel<BITS, MT, 4>), grid, dim3(256), 0, stream, x,
+                           x_kind, jobs, m, k, in_scale, out_scale, out_kind);
+}
+
+static int launch_small(int bits, int mt, const void *x, int x_kind, const SmallJobs &jobs, int m,
+                        int k, float in_scale, float out_scale, int out_kind, hipStream_t stream) {
+    if (bits == 4 && mt == 16)
+        launch_small_t<4, 16>(x, x_kind, jobs, m, k, in_scale, out_scale, out_kind, stream);
+    else if (bits == 4)
+        launch_small_t<4, 32>(x, x_kind, jobs, m, k, in_scale, out_scale, out_kind, stream);
+    else if (mt == 16)
+        launch_small_t<8, 16>(x, x_kind, jobs, m, k, in_scale, out_scale, out_kind, stream);
+    else
+        launch_small_t<8, 32>(x, x_kind, jobs, m, k, in_scale, out_scale, out_kind, stream);
+    G4_LAUNCHED("qgemm_small_kernel");
+    return G4_OK;
 }
 
 template <int BITS>
@@ -708,19 +804,15 @@ static int run_linear(int bits, const void *wq, const float *scales, const void 
         return set_error(G4_ERR_INVALID, "%s: K %d exceeds 16384 (the exact int32/f32 bound)", who, k);
     if (c == K_SKINNY16 || c == K_SKINNY32) {
         // One launch: the activation snap is fused into the small-M kernel.
-        const int mt = c == K_SKINNY16 ? 16 : 32;
-        dim3 grid((n + 15) / 16, (m + mt - 1) / mt);
-        const uint8_t *w = reinterpret_cast<const uint8_t *>(wq);
-#define G4_SMALL(B, T)                                                                           \
-    hipLaunchKernelGGL((qgemm_small_kernel<B, T>), grid, dim3(256), 0, stream, x, x_kind, w, scales, \
-                       dst, m, n, k, in_scale, out_scale, out_kind)
-        if (bits == 4 && mt == 16) G4_SMALL(4, 16);
-        else if (bits == 4) G4_SMALL(4, 32);
-        else if (mt == 16) G4_SMALL(8, 16);
-        else G4_SMALL(8, 32);
-#undef G4_SMALL
-        G4_LAUNCHED("qgemm_small_kernel");
-        return G4_OK;
+        SmallJobs jobs{};
+        jobs.w[0] = reinterpret_cast<const uint8_t *>(wq);
+        jobs.scales[0] = scales;
+        jobs.dst[0] = dst;
+        jobs.n[0] = n;
+        jobs.block_end[0] = (n + 15) / 16;
+        jobs.count = 1;
+        return launch_small(bits, c == K_SKINNY16 ? 16 : 32, x, x_kind, jobs, m, k, in_scale,
+                            out_scale, out_kind, stream);
     }
     const int kp = k;  // k % 128 == 0 on the MFMA kernels
     void *ws = nullptr;
@@ -738,6 +830,42 @@ static int run_linear(int bits, const void *wq, const float *scales, const void 
     if (bits == 4)
         return launch_tile<4>(codes, w, scales, dst, m, n, k, in_scale, out_scale, out_kind, stream);
     return launch_tile<8>(codes, w, scales, dst, m, n, k, in_scale, out_scale, out_kind, stream);
+}
+
+int linear_grouped(int bits, const void *x, int x_kind, int k, int m, float in_scale,
+                   float out_scale, int out_kind, const LinearOut *outs, int count, void *stream) {
+    if (!outs || count < 1) return set_error(G4_ERR_INVALID, "grouped linear: no outputs");
+    const char *who = bits == 4 ? "qgemm-4bit" : "qmatmul-8bit";
+    bool small = count <= kSmallMaxJobs && k <= 16384;
+    for (int i = 0; i < count; ++i) {
+        const LinearOut &o = outs[i];
+        int rc = check_linear(bits, o.wq, o.scales, x, x_kind, o.dst, out_kind, k, o.n, m, in_scale,
+                              out_scale, who);
+        if (rc) return rc;
+        const KernelChoice c = pick_kernel(bits, m, o.n, k, in_scale);
+        small &= c == K_SKINNY16 || c == K_SKINNY32;
+    }
+    if (!small) {  // one call each, through the library's routing
+        for (int i = 0; i < count; ++i) {
+            int rc = run_linear(bits, outs[i].wq, outs[i].scales, x, x_kind, outs[i].dst, out_kind,
+                                k, outs[i].n, m, in_scale, out_scale, as_stream(stream), who);
+            if (rc) return rc;
+        }
+        return G4_OK;
+    }
+    SmallJobs jobs{};
+    int blocks = 0;
+    for (int i = 0; i < count; ++i) {
+        jobs.w[i] = reinterpret_cast<const uint8_t *>(outs[i].wq);
+        jobs.scales[i] = outs[i].scales;
+        jobs.dst[i] = outs[i].dst;
+        jobs.n[i] = outs[i].n;
+        blocks += (outs[i].n + 15) / 16;
+        jobs.block_end[i] = blocks;
+    }
+    jobs.count = count;
+    return launch_small(bits, m <= 16 ? 16 : 32, x, x_kind, jobs, m, k, in_scale, out_scale,
+                        out_kind, as_stream(stream));
 }
 
 }  // namespace g4
