@@ -124,6 +124,49 @@ __global__ __launch_bounds__(kDecThreads) void attn_prologue_kernel(
 
 // ---- attention decode: split partials, then the ordered merge -------------------------------------
 
+// attn_prologue_kernel's arithmetic for one 256-wide head vector on one wave: lane l holds
+// elements l, l + 64, l + 128 and l + 192, so the block tree's levels 128 and 64 are in-lane adds
+// in the same order (x[l]^2 + x[l+128]^2, then + (x[l+64]^2 + x[l+192]^2)) and the rest is the same
+// shuffle tree; the RoPE pairs (i, i + 128) are in-lane too. Writes the four results to out.
+__device__ __forceinline__ void wave_norm_rope(const int8_t *src, float scale, const float *gain,
+                                               const float *cos_row, const float *sin_row,
+                                               bool rotate, float eps, float *out) {
+    const int l = threadIdx.x & 63;
+    float x[4], gt[4], c[2], sn[2];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        x[k] = __fmul_rn((float)src[l + 64 * k], scale);
+        gt[k] = gain ? gain[l + 64 * k] : 1.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        c[k] = rotate ? cos_row[l + 64 * k] : 0.0f;
+        sn[k] = rotate ? sin_row[l + 64 * k] : 0.0f;
+    }
+    float part = __fadd_rn(__fadd_rn(__fmul_rn(x[0], x[0]), __fmul_rn(x[2], x[2])),
+                           __fadd_rn(__fmul_rn(x[1], x[1]), __fmul_rn(x[3], x[3])));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, __shfl_down(part, off));
+    const float inv = inv_rms(__shfl(part, 0), kDecThreads, eps);
+    float y[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        y[k] = __fmul_rn(x[k], inv);
+        if (gain) y[k] = __fmul_rn(y[k], gt[k]);
+    }
+    if (!rotate) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) out[l + 64 * k] = y[k];
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {  // pair (l + 64 k, l + 64 k + 128)
+        const float lo = y[k], hi = y[k + 2];
+        out[l + 64 * k] = __fsub_rn(__fmul_rn(lo, c[k]), __fmul_rn(hi, sn[k]));
+        out[l + 64 * k + 128] = __fadd_rn(__fmul_rn(hi, c[k]), __fmul_rn(lo, sn[k]));
+    }
+}
+
 // Grid (max chunks, rows), 256 threads. Chunk c covers positions lo + 32 c .. min(+32, pos + 1), for
 // every query head of the row at once (heads <= 8 share the one KV head), so each K and V row of
 // the chunk is read once. Scores: thread t takes eighth t & 7 (32 dims, sequential) of position
@@ -132,11 +175,15 @@ __global__ __launch_bounds__(kDecThreads) void attn_prologue_kernel(
 // every lane ends with the tree's value). Per head (one 32-lane half-wave each): m = max,
 // e = exp(s - m), l = the 32-lane pairwise tree of e. Then thread d accumulates, for every head,
 // sum over positions (ascending) of e * v[d]. Writes (m, l) and o[256] per (row, head, chunk).
+// PRO: q (and on a producer, the position's K and V rows) come from the prologue run here.
+template <bool PRO>
 __global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
     const float *q, const float *k_cache, const float *v_cache, int64_t cache_row_stride, int heads,
-    int pos_host, const int32_t *pos_dev, int window, float *part_ml, float *part_o, int max_chunks) {
+    int pos_host, const int32_t *pos_dev, int window, float *part_ml, float *part_o, int max_chunks,
+    AttnPrologue pro) {
     __shared__ __align__(16) float qs[kAttnMaxHeads * kDecThreads];
     __shared__ __align__(16) float es[kAttnMaxHeads * kAttnChunk];
+    __shared__ __align__(16) float kvnew[PRO ? 2 * kDecThreads : 1];
     const int t = threadIdx.x;
     const int c = blockIdx.x;
     const int64_t row = blockIdx.y;
@@ -146,8 +193,8 @@ __global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
     if (c >= chunks) return;  // whole block
     const int start = lo + c * kAttnChunk;
     const int cnt = min(kAttnChunk, pos + 1 - start);
-    const float *kb = k_cache + row * cache_row_stride;
-    const float *vb = v_cache + row * cache_row_stride;
+    float *kb = const_cast<float *>(k_cache) + row * cache_row_stride;
+    float *vb = const_cast<float *>(v_cache) + row * cache_row_stride;
     // the chunk's K segment and V rows are requested before the q staging so the loads overlap it
     const int j = t >> 3, sg = t & 7;
     const float4 *kr = reinterpret_cast<const float4 *>(
@@ -159,9 +206,41 @@ __global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
 #pragma unroll
     for (int u = 0; u < kAttnChunk; ++u)
         vv[u] = vb[(int64_t)(start + min(u, cnt - 1)) * kDecThreads + t];
-    for (int i = t; i < heads * kDecThreads; i += kDecThreads)
-        qs[i] = q[row * heads * kDecThreads + i];
+    // the producer's new K and V rows belong to the chunk that holds the position (its last)
+    const bool store_kv = PRO && pro.k_codes && c == chunks - 1;
+    if (PRO) {
+        const int w = t >> 6;
+        const float *cos_row = pro.cos_tab + (int64_t)pos * (kDecThreads / 2);
+        const float *sin_row = pro.sin_tab + (int64_t)pos * (kDecThreads / 2);
+        for (int h = w; h < heads; h += kDecThreads / 64)
+            wave_norm_rope(pro.q_codes + (row * heads + h) * kDecThreads, pro.q_scale, pro.q_gain,
+                           cos_row, sin_row, true, pro.eps, qs + h * kDecThreads);
+        if (store_kv && w == 2)
+            wave_norm_rope(pro.k_codes + row * kDecThreads, pro.k_scale, pro.k_gain, cos_row,
+                           sin_row, true, pro.eps, kvnew);
+        if (store_kv && w == 3)
+            wave_norm_rope(pro.v_codes + row * kDecThreads, pro.v_scale, nullptr, cos_row, sin_row,
+                           false, pro.eps, kvnew + kDecThreads);
+    } else {
+        for (int i = t; i < heads * kDecThreads; i += kDecThreads)
+            qs[i] = q[row * heads * kDecThreads + i];
+    }
     __syncthreads();
+    if (store_kv) {
+        // the position's row: the cache gets it, and this block's operands take it in place of the
+        // stale row they loaded
+        const int jp = pos - start;
+        kb[(int64_t)pos * kDecThreads + t] = kvnew[t];
+        vb[(int64_t)pos * kDecThreads + t] = kvnew[kDecThreads + t];
+        if (j == jp) {
+#pragma unroll
+            for (int i4 = 0; i4 < 8; ++i4)
+                kq[i4] = *reinterpret_cast<const float4 *>(kvnew + sg * 32 + 4 * i4);
+        }
+#pragma unroll
+        for (int u = 0; u < kAttnChunk; ++u)
+            if (u == jp) vv[u] = kvnew[kDecThreads + t];
+    }
 
     // scores
     float sc[kAttnMaxHeads];
@@ -447,6 +526,36 @@ static int attn_chunks(int pos, int window) {
     return (pos - lo + 1 + kAttnChunk - 1) / kAttnChunk;
 }
 
+namespace g4 {
+
+int attention_decode_fused(const AttnPrologue &pro, float *k_cache, float *v_cache,
+                           int64_t cache_row_stride, int rows, int heads, int pos,
+                           const int32_t *pos_dev, int window, float *workspace,
+                           size_t workspace_bytes, float in_scale, int8_t *codes, void *stream) {
+    if (!pro.q_codes || !pro.q_gain || !pro.cos_tab || !pro.sin_tab || !k_cache || !v_cache ||
+        !workspace || !codes || rows <= 0 || heads <= 0 || heads > kAttnMaxHeads || pos < 0 ||
+        window < 0 || in_scale == 0.0f)
+        return set_error(G4_ERR_INVALID, "attention (fused prologue): bad arguments");
+    if (pro.k_codes && (!pro.v_codes || !pro.k_gain))
+        return set_error(G4_ERR_INVALID, "attention (fused prologue): k without v or k gain");
+    const int chunks = attn_chunks(pos, window);
+    if (workspace_bytes < g4_attention_workspace_bytes(rows, heads, pos, window))
+        return set_error(G4_ERR_INVALID, "attention (fused prologue): workspace too small");
+    float *part_ml = workspace;
+    float *part_o = workspace + (size_t)rows * heads * chunks * 2;
+    hipLaunchKernelGGL(attn_split_kernel<true>, dim3(chunks, rows), dim3(kDecThreads), 0,
+                       as_stream(stream), nullptr, k_cache, v_cache, cache_row_stride, heads, pos,
+                       pos_dev, window, part_ml, part_o, chunks, pro);
+    G4_LAUNCHED("attn_split_kernel");
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(heads, rows), dim3(kDecThreads), 0,
+                       as_stream(stream), part_ml, part_o, heads, pos, pos_dev, window, chunks,
+                       in_scale, codes, nullptr);
+    G4_LAUNCHED("attn_merge_kernel");
+    return G4_OK;
+}
+
+}  // namespace g4
+
 extern "C" {
 
 int g4_rms_join(const void *src, int src_kind, float src_scale, const float *gain,
@@ -533,9 +642,9 @@ int g4_attention_decode(const float *q, const float *k_cache, const float *v_cac
                          workspace_bytes, need);
     float *part_ml = workspace;
     float *part_o = workspace + (size_t)rows * heads * chunks * 2;
-    hipLaunchKernelGGL(attn_split_kernel, dim3(chunks, rows), dim3(kDecThreads), 0,
+    hipLaunchKernelGGL(attn_split_kernel<false>, dim3(chunks, rows), dim3(kDecThreads), 0,
                        as_stream(stream), q, k_cache, v_cache, cache_row_stride, heads, pos,
-                       pos_dev, window, part_ml, part_o, chunks);
+                       pos_dev, window, part_ml, part_o, chunks, AttnPrologue{});
     G4_LAUNCHED("attn_split_kernel");
     hipLaunchKernelGGL(attn_merge_kernel, dim3(heads, rows), dim3(kDecThreads), 0,
                        as_stream(stream), part_ml, part_o, heads, pos, pos_dev, window, chunks,

@@ -7,8 +7,8 @@
 // Per layer (plan.ts:487-665, with the synthetic config's uniform FFN and head_dim):
 //   [layer 0: input_layernorm, from the embedding phase]
 //   q (+ k, v on a producer) GEMV        -> int8 codes on out_scale
-//   q-norm-rope (+ kv-norm-rope-store)   -> q f32; K, V rows at the position
-//   attention decode over the layer's cache (own, or the last producer of its kind) -> o input snap
+//   attention decode over the layer's cache (own, or the last producer of its kind) -> o input
+//   snap, with q-norm-rope (+ kv-norm-rope-store) run inside its split kernel
 //   o GEMV; norm-residual-norm (post_attention_layernorm, residual, pre_feedforward_layernorm)
 //   gate and up GEMV with the gelu-mul pass in their epilogue (batch 1: one paired launch), or the
 //   two GEMVs then the gelu-mul pass; down GEMV
@@ -68,7 +68,7 @@ struct g4_decode {
     int32_t *pos = nullptr;
     float *identity = nullptr, *per_layer = nullptr;
     float *hbuf[2] = {nullptr, nullptr};  // the residual stream's two rows (a join reads one, writes the other)
-    float *q = nullptr, *attn_ws = nullptr, *logits = nullptr;
+    float *attn_ws = nullptr, *logits = nullptr;
     size_t attn_ws_bytes = 0, argmax_ws_bytes = 0;
     void *argmax_ws = nullptr;
     int8_t *embed_codes = nullptr, *ple_codes = nullptr, *xcodes = nullptr, *qc = nullptr,
@@ -287,7 +287,6 @@ int build(g4_decode &d) {
     G4_TRY(f32(&d.per_layer, (size_t)B * PL));
     G4_TRY(f32(&d.hbuf[0], (size_t)B * H));
     G4_TRY(f32(&d.hbuf[1], (size_t)B * H));
-    G4_TRY(f32(&d.q, (size_t)B * QW));
     G4_TRY(f32(&d.logits, (size_t)B * s.vocab));
     d.attn_ws_bytes = g4_attention_workspace_bytes(B, s.q_heads, s.kv_capacity - 1, 0);
     G4_TRY(m.get((void **)&d.attn_ws, d.attn_ws_bytes));
@@ -406,13 +405,21 @@ int run_layer(g4_decode &d, int l, void *st) {
     const int64_t row_stride = (int64_t)2 * s.kv_capacity * s.head_dim;
     const float *cos_tab = glob ? d.w.rope_global_cos : d.w.rope_local_cos;
     const float *sin_tab = glob ? d.w.rope_global_sin : d.w.rope_local_sin;
-    G4_TRY(g4_attn_prologue(d.qc, out, prod ? d.kc : nullptr, out, prod ? d.vc : nullptr, out,
-                            L.q_norm, prod ? L.k_norm : nullptr, cos_tab, sin_tab, B, s.q_heads,
-                            s.head_dim, s.eps, d.q, prod ? kb : nullptr, prod ? vb : nullptr,
-                            row_stride, s.kv_capacity - 1, d.pos, st));
-    G4_TRY(g4_attention_decode(d.q, kb, vb, row_stride, B, s.q_heads, s.head_dim,
-                               s.kv_capacity - 1, d.pos, glob ? 0 : s.sliding_window, d.attn_ws,
-                               d.attn_ws_bytes, in, d.attn_codes, nullptr, st));
+    AttnPrologue pro{};
+    pro.q_codes = d.qc;
+    pro.q_scale = out;
+    pro.k_codes = prod ? d.kc : nullptr;
+    pro.k_scale = out;
+    pro.v_codes = prod ? d.vc : nullptr;
+    pro.v_scale = out;
+    pro.q_gain = L.q_norm;
+    pro.k_gain = prod ? L.k_norm : nullptr;
+    pro.cos_tab = cos_tab;
+    pro.sin_tab = sin_tab;
+    pro.eps = s.eps;
+    G4_TRY(attention_decode_fused(pro, kb, vb, row_stride, B, s.q_heads, s.kv_capacity - 1, d.pos,
+                                  glob ? 0 : s.sliding_window, d.attn_ws, d.attn_ws_bytes, in,
+                                  d.attn_codes, st));
     G4_TRY(run_linear_rows(d, plan(P_O), desc(L.o, L.o_s, d.attn_codes, d.oc, 4, QW, H, G4_KIND_I8, in, out), st));
     G4_TRY(run_join(d, join_index(l, 0), st));
     // MLP block: gate, up and the gelu-mul pass (one paired launch when folded), then down

@@ -102,6 +102,31 @@ struct LinearOut {
 int linear_grouped(int bits, const void *x, int x_kind, int k, int m, float in_scale,
                    float out_scale, int out_kind, const LinearOut *outs, int count, void *stream);
 
+// The attention prologue (q-norm + RoPE; on a producer layer k-norm + RoPE, the weightless
+// v-norm and the KV store at the position) run inside the split attention kernel, the decode
+// runner's form of g4_attn_prologue + g4_attention_decode with no q buffer between them
+// (decode.hip). Every block rebuilds the query heads; the block whose chunk holds the position
+// builds and stores the new K and V rows.
+struct AttnPrologue {
+    const int8_t *q_codes;
+    float q_scale;
+    const int8_t *k_codes;  // null on a consumer layer (no KV store)
+    float k_scale;
+    const int8_t *v_codes;
+    float v_scale;
+    const float *q_gain;
+    const float *k_gain;
+    const float *cos_tab;  // [positions][128]
+    const float *sin_tab;
+    float eps;
+};
+
+// g4_attention_decode with the prologue fused (head_dim 256, int8 codes out on in_scale).
+int attention_decode_fused(const AttnPrologue &pro, float *k_cache, float *v_cache,
+                           int64_t cache_row_stride, int rows, int heads, int pos,
+                           const int32_t *pos_dev, int window, float *workspace,
+                           size_t workspace_bytes, float in_scale, int8_t *codes, void *stream);
+
 // The internal form of a public g4_gelu_act (NULL or a NULL up: no prologue).
 GeluAct gelu_act_of(const g4_gelu_act *a);
 
