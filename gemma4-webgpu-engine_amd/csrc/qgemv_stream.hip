@@ -357,9 +357,13 @@ __device__ __forceinline__ void stream_store_gelu(const StreamJob &J, int row, f
 // (row index clamped, so every load is valid) and the row scale, the dot against the LDS codes,
 // the fixed reduction over the row's LPR lanes (exact int32), and the row's output from one lane.
 // PAIR: the same rows of the paired up projection stream beside the gate's, for the gelu epilogue.
-template <int BITS, int LPR, int CPL, bool PAIR>
-__device__ __forceinline__ void stream_tile(const StreamJob &J, int t, const uint8_t *xs, int sx,
-                                            int wave, int lane) {
+// PRE (a block's first tile in a plan with a prologue join): the tile's weight loads go out first,
+// then the block runs the join into the LDS codes (sx is its code sum), so the join's own memory
+// latency overlaps the weight stream's. Returns sx.
+template <int BITS, int LPR, int CPL, bool PAIR, bool PRE = false>
+__device__ __forceinline__ int stream_tile(const StreamJob &J, int t, uint8_t *xs, int sx, int wave,
+                                           int lane, const JoinTail *pre = nullptr,
+                                           int *s_sum = nullptr) {
     constexpr int RPW = 64 / LPR;
     constexpr int ROW_BYTES = LPR * CPL * 16;
     const int lr = lane & (LPR - 1);
@@ -377,6 +381,7 @@ __device__ __forceinline__ void stream_tile(const StreamJob &J, int t, const uin
     }
     const float scale = gload<float>(J.scales + rc);
     const float scale2 = PAIR ? gload<float>(J.aux_scales + rc) : 0.0f;
+    if (PRE) sx = snap_join_codes(pre, BITS == 4, xs, s_sum, threadIdx.x);
     int acc = 0, acc2 = 0;
 #pragma unroll
     for (int u = 0; u < CPL; ++u) acc = chunk_dot<BITS>(w[u], xs, lr + u * LPR, acc);
@@ -386,7 +391,7 @@ __device__ __forceinline__ void stream_tile(const StreamJob &J, int t, const uin
     }
     acc = row_reduce<LPR>(acc);
     if (PAIR) acc2 = row_reduce<LPR>(acc2);
-    if (lr != 0 || row >= J.rows) return;
+    if (lr != 0 || row >= J.rows) return sx;
     const int a = BITS == 4 ? acc - 8 * sx : acc;
     if (J.epi == 0) {
         stream_store(J, row, a, scale);
@@ -399,10 +404,43 @@ __device__ __forceinline__ void stream_tile(const StreamJob &J, int t, const uin
         stream_store_gelu(J, row, linear_epilogue(J.in_scale, scale, (float)a),
                           gload<float>(reinterpret_cast<const float *>(J.aux) + row));
     }
+    return sx;
+}
+
+// A block's first tile in a plan with a prologue join (stream_tile PRE); returns the code sum.
+template <bool PAIR>
+__device__ __forceinline__ int stream_dispatch_join(const StreamJob &J, int t, uint8_t *xs, int wave,
+                                                    int lane, const JoinTail *pre, int *s_sum) {
+    if (PAIR && J.epi == 1) {
+        switch (J.cls) {
+#define G4_CASE(i)                                                                               \
+    case i:                                                                                      \
+        return stream_tile<kClasses[i].bits, kClasses[i].lpr, kClasses[i].cpl, true, true>(      \
+            J, t, xs, 0, wave, lane, pre, s_sum);
+            G4_CASE(0) G4_CASE(1) G4_CASE(2) G4_CASE(3) G4_CASE(4) G4_CASE(5) G4_CASE(6) G4_CASE(7)
+#undef G4_CASE
+            default:
+                break;
+        }
+    } else {
+        switch (J.cls) {
+#define G4_CASE(i)                                                                               \
+    case i:                                                                                      \
+        return stream_tile<kClasses[i].bits, kClasses[i].lpr, kClasses[i].cpl, false, true>(     \
+            J, t, xs, 0, wave, lane, pre, s_sum);
+            G4_CASE(0) G4_CASE(1) G4_CASE(2) G4_CASE(3) G4_CASE(4) G4_CASE(5) G4_CASE(6) G4_CASE(7)
+            G4_CASE(8) G4_CASE(9) G4_CASE(10) G4_CASE(11) G4_CASE(12) G4_CASE(13) G4_CASE(14)
+            G4_CASE(15) G4_CASE(16)
+#undef G4_CASE
+            default:
+                break;
+        }
+    }
+    return snap_join_codes(pre, J.bits == 4, xs, s_sum, threadIdx.x);  // no class: codes only
 }
 
 template <bool PAIR>
-__device__ __forceinline__ void stream_dispatch(const StreamJob &J, int t, const uint8_t *xs,
+__device__ __forceinline__ void stream_dispatch(const StreamJob &J, int t, uint8_t *xs,
                                                 int sx, int wave, int lane) {
     if (PAIR && J.epi == 1) {
         // paired gate/up rows: the 4-bit classes only (the host refuses others)
@@ -437,8 +475,8 @@ static_assert(kNumClasses == 17, "stream_dispatch lists every class");
 static_assert(kClasses[7].bits == 4 && kClasses[8].bits == 8, "classes 0-7 are the 4-bit ones");
 
 // JOIN (plan launches whose jobs all read a prologue join's codes): the block's codes come from
-// the join, computed before the job is loaded for the tile loop (so the job's fields are not live
-// across the join, whose registers would push them to scratch), and stay for every job.
+// the join, run inside its first tile after that tile's weight loads are out, and stay for every
+// job.
 template <bool TABLE, bool PAIR, bool JOIN>
 __device__ __forceinline__ void stream_body(const StreamArgs &A, uint8_t *xs, int *s_sum) {
     const int tid = threadIdx.x;
@@ -457,15 +495,12 @@ __device__ __forceinline__ void stream_body(const StreamArgs &A, uint8_t *xs, in
             if (i < A.njobs && t0 >= A.job[i].tile_begin) j = i;
     }
     int sx;
-    StreamJob J;
-    if (JOIN) {
-        sx = snap_join_codes(A.pre, A.table[j].bits == 4, xs, s_sum, tid);
-        J = A.table[j];
-    } else {
-        J = TABLE ? A.table[j] : A.job[j];
+    StreamJob J = TABLE ? A.table[j] : A.job[j];
+    if (JOIN)
+        sx = stream_dispatch_join<PAIR>(J, t0, xs, wave, lane, A.pre, s_sum);  // tile t0 done
+    else
         sx = snap_activations(J, xs, s_sum, tid);
-    }
-    for (int t = t0; t < t1; ++t) {
+    for (int t = JOIN ? t0 + 1 : t0; t < t1; ++t) {
         if (t >= J.tile_begin + J.tiles) {
             ++j;
             J = TABLE ? A.table[j] : A.job[j];
@@ -478,8 +513,11 @@ __device__ __forceinline__ void stream_body(const StreamArgs &A, uint8_t *xs, in
     }
 }
 
+// A plan with a prologue join holds its first tile's weights across the join, which needs more
+// than the 64 registers of 8 waves per SIMD; such plans are small (the q/k/v, gate/up and
+// per-layer-input projections of a decode step), so their blocks fit the chip at 4.
 template <bool TABLE, bool JOIN>
-__global__ __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
+__global__ __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(JOIN ? 4 : 8, 8)))
 void qgemv_stream_kernel(StreamArgs A) {
     extern __shared__ __align__(16) uint8_t xs[];
     __shared__ int s_sum;
