@@ -426,13 +426,20 @@ int run_layer(g4_decode &d, int l, void *st) {
     if (plan(P_GATEUP).gelu) {
         G4_TRY(g4_qgemv_plan_launch(plan(P_GATEUP).p, st));
     } else {
-        if (plan(P_GATEUP).p) {
-            G4_TRY(g4_qgemv_plan_launch(plan(P_GATEUP).p, st));
-        } else {  // gate and up over the same codes: one grouped launch
-            const LinearOut gu[2] = {{L.gate, L.gate_s, d.gc, F}, {L.up, L.up_s, d.uc, F}};
-            G4_TRY(linear_grouped(4, d.xcodes, G4_KIND_I8, H, B, in, out, G4_KIND_I8, gu, 2, st));
+        // batch > 1: the small-M kernel with paired gate/up rows and the gelu-mul epilogue
+        bool fused = false;
+        if (!plan(P_GATEUP).p)
+            G4_TRY(linear_gelu(4, d.xcodes, H, B, in, out, L.gate, L.gate_s, L.up, L.up_s, nullptr,
+                               0, F, in, d.act, st, &fused));
+        if (!fused) {
+            if (plan(P_GATEUP).p) {
+                G4_TRY(g4_qgemv_plan_launch(plan(P_GATEUP).p, st));
+            } else {  // gate and up over the same codes: one grouped launch
+                const LinearOut gu[2] = {{L.gate, L.gate_s, d.gc, F}, {L.up, L.up_s, d.uc, F}};
+                G4_TRY(linear_grouped(4, d.xcodes, G4_KIND_I8, H, B, in, out, G4_KIND_I8, gu, 2, st));
+            }
+            G4_TRY(g4_gelu_mul(d.gc, out, d.uc, out, nullptr, 0, B, F, in, d.act, st));
         }
-        G4_TRY(g4_gelu_mul(d.gc, out, d.uc, out, nullptr, 0, B, F, in, d.act, st));
     }
     G4_TRY(run_linear_rows(d, plan(P_DOWN), desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out), st));
     G4_TRY(run_join(d, join_index(l, 1), st));
@@ -441,9 +448,16 @@ int run_layer(g4_decode &d, int l, void *st) {
     if (plan(P_PLE_GATE).gelu) {
         G4_TRY(g4_qgemv_plan_launch(plan(P_PLE_GATE).p, st));
     } else {
-        G4_TRY(run_linear_rows(d, plan(P_PLE_GATE), desc(L.ple_gate, L.ple_gate_s, d.xcodes, d.pgc, 8, H, s.ple_dim, G4_KIND_I8, in, out), st));
-        G4_TRY(g4_gelu_mul(d.pgc, out, nullptr, 0.0f, d.per_layer + (size_t)l * s.ple_dim,
-                           (int64_t)s.layers * s.ple_dim, B, s.ple_dim, in, d.pac, st));
+        bool fused = false;
+        if (!plan(P_PLE_GATE).p)
+            G4_TRY(linear_gelu(8, d.xcodes, H, B, in, out, L.ple_gate, L.ple_gate_s, nullptr, nullptr,
+                               d.per_layer + (size_t)l * s.ple_dim, (int64_t)s.layers * s.ple_dim,
+                               s.ple_dim, in, d.pac, st, &fused));
+        if (!fused) {
+            G4_TRY(run_linear_rows(d, plan(P_PLE_GATE), desc(L.ple_gate, L.ple_gate_s, d.xcodes, d.pgc, 8, H, s.ple_dim, G4_KIND_I8, in, out), st));
+            G4_TRY(g4_gelu_mul(d.pgc, out, nullptr, 0.0f, d.per_layer + (size_t)l * s.ple_dim,
+                               (int64_t)s.layers * s.ple_dim, B, s.ple_dim, in, d.pac, st));
+        }
     }
     G4_TRY(run_linear_rows(d, plan(P_PLE_PROJ), desc(L.ple_proj, L.ple_proj_s, d.pac, d.ppc, 8, s.ple_dim, H, G4_KIND_I8, in, out), st));
     // the tail join: residual, layer scalar, then the next input norm (or the final norm)

@@ -102,6 +102,15 @@ struct LinearOut {
 int linear_grouped(int bits, const void *x, int x_kind, int k, int m, float in_scale,
                    float out_scale, int out_kind, const LinearOut *outs, int count, void *stream);
 
+// The gate linear of m int8-coded rows with the gelu-mul pass in its epilogue (qgemm.hip): act =
+// srq(gelu(gate code * out_scale) * u, act_scale), u the same row of a paired 4-bit up projection
+// (w_up, s_up; its code times out_scale) or up_vec[row * up_stride + i] (f32). Runs when the shape
+// takes the small-M kernel (m 3..32); otherwise enqueues nothing and sets *launched = false.
+int linear_gelu(int bits, const void *x, int k, int m, float in_scale, float out_scale,
+                const void *w_gate, const float *s_gate, const void *w_up, const float *s_up,
+                const float *up_vec, int64_t up_stride, int n, float act_scale, int8_t *act,
+                void *stream, bool *launched);
+
 // The attention prologue (q-norm + RoPE; on a producer layer k-norm + RoPE, the weightless
 // v-norm and the KV store at the position) run inside the split attention kernel, the decode
 // runner's form of g4_attn_prologue + g4_attention_decode with no q buffer between them

@@ -139,6 +139,11 @@ __device__ __forceinline__ void store_tile_out(void *dst, int m, int n, int N, i
 //
 // Grouped launches: up to kSmallMaxJobs projections of the same x, K and scales (q, k, v; gate and
 // up) share one grid; block b belongs to the first job whose block_end exceeds it.
+//
+// EPI (one job, its rows the gate): the gelu-mul pass in the epilogue, as the batch-1 plans fold
+// it: the gate's output code back on out_scale, times the up value (EPI 1: the same row of the
+// paired up projection w_up / s_up, streamed beside the gate's and snapped on out_scale; EPI 2:
+// aux[m * aux_stride + n], f32), and dst receives srq(gelu(g) * u, act_scale).
 constexpr int kSmallMaxJobs = 4;
 struct SmallJobs {
     const uint8_t *w[kSmallMaxJobs];
@@ -147,11 +152,16 @@ struct SmallJobs {
     int n[kSmallMaxJobs];
     int block_end[kSmallMaxJobs];  // cumulative 16-row blocks
     int count;
+    const uint8_t *w_up;
+    const float *s_up;
+    const float *aux;
+    int64_t aux_stride;
+    float act_scale;
 };
 
 template <int MT, int WAVES> constexpr int small_kc() { return (WAVES >= 16 ? 65536 : 32768) / MT; }
 
-template <int BITS, int MT, int WAVES>
+template <int BITS, int MT, int WAVES, int EPI>
 __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
     const void *__restrict__ x, int x_kind, SmallJobs jobs, int M, int K, float in_scale,
     float out_scale, int out_kind) {
@@ -160,9 +170,13 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
     constexpr int KC = small_kc<MT, WAVES>();  // codes of a row per LDS chunk
     constexpr int XSTR = KC + 16;              // LDS bytes per token row
     constexpr int BATCH = WAVES >= 16 ? 1 : 4;
-    constexpr int NACC = BITS == 4 ? 2 * TM : TM;  // products, then (4-bit) the row sums
-    __shared__ __align__(16) int8_t xs[MT * XSTR];
-    __shared__ v4i red[WAVES - 1][NACC][64];
+    constexpr int NP = EPI == 1 ? 2 : 1;             // product sets: the gate's (and the up's)
+    constexpr int NACC = BITS == 4 ? (NP + 1) * TM : NP * TM;  // products, then the row sums
+    // the codes during the K loop, then every wave's partial tiles for the fold (the same bytes)
+    constexpr int XS_BYTES = MT * XSTR, RED_BYTES = WAVES * NACC * 64 * 16;
+    __shared__ __align__(16) int8_t smem[XS_BYTES > RED_BYTES ? XS_BYTES : RED_BYTES];
+    int8_t *xs = smem;
+    v4i(*red)[NACC][64] = reinterpret_cast<v4i(*)[NACC][64]>(smem);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -188,6 +202,7 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
     const int n = min(n0 + j, N - 1);
     const int row_bytes = BITS == 4 ? (K >> 1) : K;
     const uint8_t *wrow = W + (int64_t)n * row_bytes;
+    const uint8_t *wrow2 = EPI == 1 ? jobs.w_up + (int64_t)n * row_bytes : wrow;
     bool r_ok;
     const float rcp = srq_recip(in_scale, r_ok);
     v4i acc[NACC];
@@ -271,16 +286,20 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
         const int ksteps = kcn / kTileBK;
         const int kbase = kc0 / kTileBK;
         for (int kb0 = wave; kb0 < ksteps; kb0 += WAVES * BATCH) {
-            u32x4 bw[BATCH][BITS == 4 ? 1 : 2];
+            u32x4 bw[NP][BATCH][BITS == 4 ? 1 : 2];
 #pragma unroll
-            for (int u = 0; u < BATCH; ++u) {
-                const int kb = min(kb0 + WAVES * u, ksteps - 1);  // clamped: every load is valid
-                if (BITS == 4) {
-                    bw[u][0] = *reinterpret_cast<const u32x4 *>(wrow + (kbase + kb) * 64 + g * 16);
-                } else {
-                    bw[u][0] = *reinterpret_cast<const u32x4 *>(wrow + (kbase + kb) * 128 + g * 32);
-                    bw[u][BITS == 4 ? 0 : 1] =
-                        *reinterpret_cast<const u32x4 *>(wrow + (kbase + kb) * 128 + g * 32 + 16);
+            for (int p = 0; p < NP; ++p) {
+                const uint8_t *wr = p == 0 ? wrow : wrow2;
+#pragma unroll
+                for (int u = 0; u < BATCH; ++u) {
+                    const int kb = min(kb0 + WAVES * u, ksteps - 1);  // clamped: every load is valid
+                    if (BITS == 4) {
+                        bw[p][u][0] = *reinterpret_cast<const u32x4 *>(wr + (kbase + kb) * 64 + g * 16);
+                    } else {
+                        bw[p][u][0] = *reinterpret_cast<const u32x4 *>(wr + (kbase + kb) * 128 + g * 32);
+                        bw[p][u][BITS == 4 ? 0 : 1] =
+                            *reinterpret_cast<const u32x4 *>(wr + (kbase + kb) * 128 + g * 32 + 16);
+                    }
                 }
             }
 #pragma unroll
@@ -289,67 +308,79 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
                 if (kb < ksteps) {
 #pragma unroll
                     for (int s = 0; s < 2; ++s) {
-                        v4i b;
-                        if (BITS == 4)
-                            b = b_operand<4>(bw[u][0].x, bw[u][0].y, bw[u][0].z, bw[u][0].w, s);
-                        else
-                            b = __builtin_bit_cast(v4i, bw[u][BITS == 4 ? 0 : s]);
+                        v4i b[NP];
+#pragma unroll
+                        for (int p = 0; p < NP; ++p) {
+                            if (BITS == 4)
+                                b[p] = b_operand<4>(bw[p][u][0].x, bw[p][u][0].y, bw[p][u][0].z,
+                                                    bw[p][u][0].w, s);
+                            else
+                                b[p] = __builtin_bit_cast(v4i, bw[p][u][BITS == 4 ? 0 : s]);
+                        }
 #pragma unroll
                         for (int t = 0; t < TM; ++t) {
                             const v4i a = *reinterpret_cast<const v4i *>(
                                 &xs[(t * 16 + j) * XSTR + kb * kTileBK + g * 32 + s * 16]);
-                            acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[t], 0, 0, 0);
+#pragma unroll
+                            for (int p = 0; p < NP; ++p)
+                                acc[p * TM + t] =
+                                    __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[p], acc[p * TM + t], 0, 0, 0);
                             if (BITS == 4)  // each code counted once: both halves
-                                acc[TM + t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, ones, acc[TM + t], 0, 0, 0);
+                                acc[NP * TM + t] =
+                                    __builtin_amdgcn_mfma_i32_16x16x64_i8(a, ones, acc[NP * TM + t], 0, 0, 0);
                         }
                     }
                 }
             }
         }
     }
-    // Fold the waves' partial tiles through LDS, then wave 0 writes.
-    if (wave > 0) {
-#pragma unroll
-        for (int t = 0; t < NACC; ++t) red[wave - 1][t][lane] = acc[t];
-    }
+    // Fold: every wave leaves its partial tiles in LDS (over the codes, once all waves are done
+    // with them); then the block's threads take the outputs, each summing the waves' partials of
+    // one (row, column) in wave order, so the epilogue (a gelu for EPI) is spread over all waves.
     __syncthreads();
-    if (wave == 0) {
-        bool o_ok;
-        const float orcp = srq_recip(out_scale, o_ok);
-        const int nn = n0 + j;
-        if (nn < N) {
-            const float rs = __fmul_rn(in_scale, scales[nn]);
 #pragma unroll
-            for (int t = 0; t < TM; ++t) {
-                v4i a = acc[t];
-                v4i rsum = BITS == 4 ? acc[TM + t] : v4i{0, 0, 0, 0};
+    for (int t = 0; t < NACC; ++t) red[wave][t][lane] = acc[t];
+    __syncthreads();
+    bool o_ok;
+    const float orcp = srq_recip(out_scale, o_ok);
+    for (int q = tid; q < TM * 256; q += THREADS) {
+        // D layout: lane l, register r -> row 4 (l / 16) + r of A, column l % 16 of B.
+        const int t = q >> 8, ln = (q >> 2) & 63, r = q & 3;
+        const int lr = t * 16 + 4 * (ln >> 4) + r;
+        const int m = m0 + lr, nn = n0 + (ln & 15);
+        if (m >= M || nn >= N) continue;
+        int v = 0, v2 = 0, rsum = 0;
 #pragma unroll
-                for (int w = 0; w < WAVES - 1; ++w) {
-                    a += red[w][t][lane];
-                    if (BITS == 4) rsum += red[w][TM + t][lane];
-                }
-                // D layout: lane l, register r -> row 4 (l / 16) + r of A, column l % 16 of B.
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int lr = t * 16 + 4 * g + r;
-                    const int m = m0 + lr;
-                    if (m < M) {
-                        int v = a[r];
-                        if (BITS == 4) v -= 8 * rsum[r];  // the ones product: sum(xq) of row lr
-                        const float yv = __fmul_rn(rs, (float)v);
-                        const int64_t o = (int64_t)m * N + nn;
-                        if (out_kind == G4_KIND_I8) {
-                            reinterpret_cast<int8_t *>(dst)[o] = (int8_t)srq_code_fast(yv, out_scale, orcp, o_ok);
-                        } else if (out_kind == G4_KIND_I32) {
-                            reinterpret_cast<int32_t *>(dst)[o] = v;
-                        } else {
-                            float f = yv;
-                            if (out_scale != 0.0f) f = __fmul_rn(srq_code_fast(yv, out_scale, orcp, o_ok), out_scale);
-                            reinterpret_cast<float *>(dst)[o] = f;
-                        }
-                    }
-                }
+        for (int w = 0; w < WAVES; ++w) {
+            v += reinterpret_cast<const int *>(&red[w][t][ln])[r];
+            if (EPI == 1) v2 += reinterpret_cast<const int *>(&red[w][TM + t][ln])[r];
+            if (BITS == 4) rsum += reinterpret_cast<const int *>(&red[w][NP * TM + t][ln])[r];
+        }
+        if (BITS == 4) {  // the ones product: sum(xq) of row lr
+            v -= 8 * rsum;
+            v2 -= 8 * rsum;
+        }
+        const float yv = __fmul_rn(__fmul_rn(in_scale, scales[nn]), (float)v);
+        const int64_t o = (int64_t)m * N + nn;
+        if (EPI != 0) {  // gelu(gate) * up, snapped for the consumer
+            const float gq = __fmul_rn(srq_code_fast(yv, out_scale, orcp, o_ok), out_scale);
+            float uq;
+            if (EPI == 1) {
+                const float yu = __fmul_rn(__fmul_rn(in_scale, jobs.s_up[nn]), (float)v2);
+                uq = __fmul_rn(srq_code_fast(yu, out_scale, orcp, o_ok), out_scale);
+            } else {
+                uq = jobs.aux[(int64_t)m * jobs.aux_stride + nn];
             }
+            reinterpret_cast<int8_t *>(dst)[o] =
+                (int8_t)srq_code_i(__fmul_rn(d_gelu(gq), uq), jobs.act_scale);
+        } else if (out_kind == G4_KIND_I8) {
+            reinterpret_cast<int8_t *>(dst)[o] = (int8_t)srq_code_fast(yv, out_scale, orcp, o_ok);
+        } else if (out_kind == G4_KIND_I32) {
+            reinterpret_cast<int32_t *>(dst)[o] = v;
+        } else {
+            float f = yv;
+            if (out_scale != 0.0f) f = __fmul_rn(srq_code_fast(yv, out_scale, orcp, o_ok), out_scale);
+            reinterpret_cast<float *>(dst)[o] = f;
         }
     }
 }
@@ -724,28 +755,34 @@ static const char *choice_name(KernelChoice c, int bits) {
 // The small-M kernel over `jobs` (16-row blocks laid end to end): 16 waves per block when the
 // grid has no more blocks than the device has CUs (each block then walks its K four times
 // faster), else 4.
-template <int BITS, int MT>
+template <int BITS, int MT, int EPI>
 static void launch_small_t(const void *x, int x_kind, const SmallJobs &jobs, int m, int k,
                            float in_scale, float out_scale, int out_kind, hipStream_t stream) {
     const dim3 grid(jobs.block_end[jobs.count - 1], (m + MT - 1) / MT);
     if ((int64_t)grid.x * grid.y <= device_cu_count())
-        hipLaunchKernelGGL((qgemm_small_kernel<BITS, MT, 16>), grid, dim3(1024), 0, stream, x,
+        hipLaunchKernelGGL((qgemm_small_kernel<BITS, MT, 16, EPI>), grid, dim3(1024), 0, stream, x,
                            x_kind, jobs, m, k, in_scale, out_scale, out_kind);
     else
-        hipLaunchKernelGGL((qgemm_small_kernel<BITS, MT, 4>), grid, dim3(256), 0, stream, x,
+        hipLaunchKernelGGL((qgemm_small_kernel<BITS, MT, 4, EPI>), grid, dim3(256), 0, stream, x,
                            x_kind, jobs, m, k, in_scale, out_scale, out_kind);
 }
 
-static int launch_small(int bits, int mt, const void *x, int x_kind, const SmallJobs &jobs, int m,
-                        int k, float in_scale, float out_scale, int out_kind, hipStream_t stream) {
-    if (bits == 4 && mt == 16)
-        launch_small_t<4, 16>(x, x_kind, jobs, m, k, in_scale, out_scale, out_kind, stream);
-    else if (bits == 4)
-        launch_small_t<4, 32>(x, x_kind, jobs, m, k, in_scale, out_scale, out_kind, stream);
-    else if (mt == 16)
-        launch_small_t<8, 16>(x, x_kind, jobs, m, k, in_scale, out_scale, out_kind, stream);
-    else
-        launch_small_t<8, 32>(x, x_kind, jobs, m, k, in_scale, out_scale, out_kind, stream);
+// epi: 0 plain (any job count), 1 the paired gate/up gelu epilogue (4-bit), 2 the f32-vector one.
+static int launch_small(int bits, int mt, int epi, const void *x, int x_kind, const SmallJobs &jobs,
+                        int m, int k, float in_scale, float out_scale, int out_kind,
+                        hipStream_t stream) {
+#define G4_SMALL(B, T, E) launch_small_t<B, T, E>(x, x_kind, jobs, m, k, in_scale, out_scale, out_kind, stream)
+    if (epi == 1 && mt == 16) G4_SMALL(4, 16, 1);
+    else if (epi == 1) G4_SMALL(4, 32, 1);
+    else if (epi == 2 && bits == 4 && mt == 16) G4_SMALL(4, 16, 2);
+    else if (epi == 2 && bits == 4) G4_SMALL(4, 32, 2);
+    else if (epi == 2 && mt == 16) G4_SMALL(8, 16, 2);
+    else if (epi == 2) G4_SMALL(8, 32, 2);
+    else if (bits == 4 && mt == 16) G4_SMALL(4, 16, 0);
+    else if (bits == 4) G4_SMALL(4, 32, 0);
+    else if (mt == 16) G4_SMALL(8, 16, 0);
+    else G4_SMALL(8, 32, 0);
+#undef G4_SMALL
     G4_LAUNCHED("qgemm_small_kernel");
     return G4_OK;
 }
@@ -811,7 +848,7 @@ static int run_linear(int bits, const void *wq, const float *scales, const void 
         jobs.n[0] = n;
         jobs.block_end[0] = (n + 15) / 16;
         jobs.count = 1;
-        return launch_small(bits, c == K_SKINNY16 ? 16 : 32, x, x_kind, jobs, m, k, in_scale,
+        return launch_small(bits, c == K_SKINNY16 ? 16 : 32, 0, x, x_kind, jobs, m, k, in_scale,
                             out_scale, out_kind, stream);
     }
     const int kp = k;  // k % 128 == 0 on the MFMA kernels
@@ -864,8 +901,40 @@ int linear_grouped(int bits, const void *x, int x_kind, int k, int m, float in_s
         jobs.block_end[i] = blocks;
     }
     jobs.count = count;
-    return launch_small(bits, m <= 16 ? 16 : 32, x, x_kind, jobs, m, k, in_scale, out_scale,
+    return launch_small(bits, m <= 16 ? 16 : 32, 0, x, x_kind, jobs, m, k, in_scale, out_scale,
                         out_kind, as_stream(stream));
+}
+
+int linear_gelu(int bits, const void *x, int k, int m, float in_scale, float out_scale,
+                const void *w_gate, const float *s_gate, const void *w_up, const float *s_up,
+                const float *up_vec, int64_t up_stride, int n, float act_scale, int8_t *act,
+                void *stream, bool *launched) {
+    *launched = false;
+    const char *who = "gelu linear";
+    int rc = check_linear(bits, w_gate, s_gate, x, G4_KIND_I8, act, G4_KIND_I8, k, n, m, in_scale,
+                          out_scale, who);
+    if (rc) return rc;
+    const KernelChoice c = pick_kernel(bits, m, n, k, in_scale);
+    if ((c != K_SKINNY16 && c != K_SKINNY32) || k > 16384 || act_scale == 0.0f) return G4_OK;
+    if (w_up ? (bits != 4 || !s_up || (reinterpret_cast<uintptr_t>(w_up) & 15)) : (!up_vec || up_stride < n))
+        return set_error(G4_ERR_INVALID, "gelu linear: the up operand (4-bit paired rows with scales, "
+                                         "or an f32 vector with stride >= n)");
+    SmallJobs jobs{};
+    jobs.w[0] = reinterpret_cast<const uint8_t *>(w_gate);
+    jobs.scales[0] = s_gate;
+    jobs.dst[0] = act;
+    jobs.n[0] = n;
+    jobs.block_end[0] = (n + 15) / 16;
+    jobs.count = 1;
+    jobs.w_up = reinterpret_cast<const uint8_t *>(w_up);
+    jobs.s_up = s_up;
+    jobs.aux = up_vec;
+    jobs.aux_stride = up_stride;
+    jobs.act_scale = act_scale;
+    rc = launch_small(bits, c == K_SKINNY16 ? 16 : 32, w_up ? 1 : 2, x, G4_KIND_I8, jobs, m, k,
+                      in_scale, out_scale, G4_KIND_I8, as_stream(stream));
+    if (rc == G4_OK) *launched = true;
+    return rc;
 }
 
 }  // namespace g4
