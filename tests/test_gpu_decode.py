@@ -304,11 +304,16 @@ def check_step(got, want, dev_kv, ref_kv):
             assert same(a, b), f"kv layer {p}"
 
 
-@pytest.mark.parametrize("batch", [1, 3])
-def test_decode_step_tiny(gpu, batch):
-    print(f"decode tiny batch={batch}", flush=True)
-    shape = tiny_shape(batch)
-    toks = [[5, 2999, 1234][:batch], [7, 0, 1][:batch]]
+# batch 1: the streaming plans with carried joins; 3: the small-M kernel on 16-row tiles; 20 and
+# 32: on 32-row tiles, with the gelu-mul epilogues on 16-wave (FFN 1024: 64 blocks) and 4-wave
+# (FFN 6144: 384 blocks) grids
+@pytest.mark.parametrize("batch,ffn", [(1, 1024), (3, 1024), (20, 1024), (32, 6144)])
+def test_decode_step_tiny(gpu, batch, ffn):
+    print(f"decode tiny batch={batch} ffn={ffn}", flush=True)
+    shape = tiny_shape(batch, ffn=ffn)
+    rng = np.random.default_rng(batch)
+    extra = [int(t) for t in rng.integers(0, 3000, max(0, batch - 3))]
+    toks = [([5, 2999, 1234] + extra)[:batch], ([7, 0, 1] + extra[::-1])[:batch]]
     for got, want, dkv, rkv in run_steps(gpu, shape, toks, pos0=700):
         check_step(got, want, dkv, rkv)
         if "next" in got:
