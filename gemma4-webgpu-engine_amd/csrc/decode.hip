@@ -28,24 +28,12 @@ namespace g4 {
 constexpr int kDecThreads = 256;
 constexpr int kAttnChunk = 32;
 constexpr int kAttnMaxHeads = 8;
+static_assert(kAttnMaxHeads <= 2 * (kDecThreads / 64), "the split kernel's waves take two heads each");
 
 // d_expf, d_tanhf and d_gelu (the deterministic exp / tanh / gelu) live in g4_internal.h, shared
 // with the GEMV gelu prologues; block_tree_sum, inv_rms and the RMS join row in g4_rowops.h, shared
 // with the GEMV whose last block runs a join.
 static_assert(kDecThreads == kRowThreads, "the glue kernels run the shared 256-lane row operations");
-
-__device__ float block_max(float v, float *lds) {
-    const int t = threadIdx.x;
-    lds[t] = v;
-    __syncthreads();
-    for (int stride = kDecThreads / 2; stride >= 1; stride >>= 1) {
-        if (t < stride) lds[t] = fmaxf(lds[t], lds[t + stride]);
-        __syncthreads();
-    }
-    const float m = lds[0];
-    __syncthreads();
-    return m;
-}
 
 // ---- rms-norm / norm-residual / norm-residual-norm --------------------------------------------------
 
@@ -127,22 +115,35 @@ __global__ __launch_bounds__(kDecThreads) void attn_prologue_kernel(
 // attn_prologue_kernel's arithmetic for one 256-wide head vector on one wave: lane l holds
 // elements l, l + 64, l + 128 and l + 192, so the block tree's levels 128 and 64 are in-lane adds
 // in the same order (x[l]^2 + x[l+128]^2, then + (x[l+64]^2 + x[l+192]^2)) and the rest is the same
-// shuffle tree; the RoPE pairs (i, i + 128) are in-lane too. Writes the four results to out.
-__device__ __forceinline__ void wave_norm_rope(const int8_t *src, float scale, const float *gain,
-                                               const float *cos_row, const float *sin_row,
-                                               bool rotate, float eps, float *out) {
-    const int l = threadIdx.x & 63;
+// shuffle tree; the RoPE pairs (i, i + 128) are in-lane too. The operands are loaded first
+// (NormRopeIn), so a caller can put them ahead of a longer stream of loads.
+struct NormRopeIn {
     float x[4], gt[4], c[2], sn[2];
+};
+
+__device__ __forceinline__ NormRopeIn wave_norm_rope_load(const int8_t *src, float scale,
+                                                          const float *gain, const float *cos_row,
+                                                          const float *sin_row, bool rotate) {
+    const int l = threadIdx.x & 63;
+    NormRopeIn in;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        x[k] = __fmul_rn((float)src[l + 64 * k], scale);
-        gt[k] = gain ? gain[l + 64 * k] : 1.0f;
+        in.x[k] = __fmul_rn((float)src[l + 64 * k], scale);
+        in.gt[k] = gain ? gain[l + 64 * k] : 1.0f;
     }
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-        c[k] = rotate ? cos_row[l + 64 * k] : 0.0f;
-        sn[k] = rotate ? sin_row[l + 64 * k] : 0.0f;
+        in.c[k] = rotate ? cos_row[l + 64 * k] : 0.0f;
+        in.sn[k] = rotate ? sin_row[l + 64 * k] : 0.0f;
     }
+    return in;
+}
+
+// Writes the four results of the lane to out[l + 64 k].
+__device__ __forceinline__ void wave_norm_rope(const NormRopeIn &in, bool gain, bool rotate,
+                                               float eps, float *out) {
+    const int l = threadIdx.x & 63;
+    const float *x = in.x;
     float part = __fadd_rn(__fadd_rn(__fmul_rn(x[0], x[0]), __fmul_rn(x[2], x[2])),
                            __fadd_rn(__fmul_rn(x[1], x[1]), __fmul_rn(x[3], x[3])));
 #pragma unroll
@@ -152,7 +153,7 @@ __device__ __forceinline__ void wave_norm_rope(const int8_t *src, float scale, c
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         y[k] = __fmul_rn(x[k], inv);
-        if (gain) y[k] = __fmul_rn(y[k], gt[k]);
+        if (gain) y[k] = __fmul_rn(y[k], in.gt[k]);
     }
     if (!rotate) {
 #pragma unroll
@@ -162,8 +163,8 @@ __device__ __forceinline__ void wave_norm_rope(const int8_t *src, float scale, c
 #pragma unroll
     for (int k = 0; k < 2; ++k) {  // pair (l + 64 k, l + 64 k + 128)
         const float lo = y[k], hi = y[k + 2];
-        out[l + 64 * k] = __fsub_rn(__fmul_rn(lo, c[k]), __fmul_rn(hi, sn[k]));
-        out[l + 64 * k + 128] = __fadd_rn(__fmul_rn(hi, c[k]), __fmul_rn(lo, sn[k]));
+        out[l + 64 * k] = __fsub_rn(__fmul_rn(lo, in.c[k]), __fmul_rn(hi, in.sn[k]));
+        out[l + 64 * k + 128] = __fadd_rn(__fmul_rn(hi, in.c[k]), __fmul_rn(lo, in.sn[k]));
     }
 }
 
@@ -195,7 +196,30 @@ __global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
     const int cnt = min(kAttnChunk, pos + 1 - start);
     float *kb = const_cast<float *>(k_cache) + row * cache_row_stride;
     float *vb = const_cast<float *>(v_cache) + row * cache_row_stride;
-    // the chunk's K segment and V rows are requested before the q staging so the loads overlap it
+    // the producer's new K and V rows belong to the chunk that holds the position (its last)
+    const bool store_kv = PRO && pro.k_codes && c == chunks - 1;
+    // the prologue's few operands go out first (each wave: its query heads, and in the position's
+    // block the K or V row), then the chunk's K segment and V rows, so the prologue's arithmetic
+    // waits for its own loads only and overlaps the chunk's
+    const int w = t >> 6;
+    NormRopeIn qin[kAttnMaxHeads / 4], kvin;
+    const float *cos_row = PRO ? pro.cos_tab + (int64_t)pos * (kDecThreads / 2) : nullptr;
+    const float *sin_row = PRO ? pro.sin_tab + (int64_t)pos * (kDecThreads / 2) : nullptr;
+    if (PRO) {
+#pragma unroll
+        for (int i = 0; i < kAttnMaxHeads / 4; ++i) {
+            const int h = w + 4 * i;
+            if (h < heads)
+                qin[i] = wave_norm_rope_load(pro.q_codes + (row * heads + h) * kDecThreads,
+                                             pro.q_scale, pro.q_gain, cos_row, sin_row, true);
+        }
+        if (store_kv && w == 2)
+            kvin = wave_norm_rope_load(pro.k_codes + row * kDecThreads, pro.k_scale, pro.k_gain,
+                                       cos_row, sin_row, true);
+        if (store_kv && w == 3)
+            kvin = wave_norm_rope_load(pro.v_codes + row * kDecThreads, pro.v_scale, nullptr,
+                                       cos_row, sin_row, false);
+    }
     const int j = t >> 3, sg = t & 7;
     const float4 *kr = reinterpret_cast<const float4 *>(
         kb + (int64_t)(start + min(j, cnt - 1)) * kDecThreads + sg * 32);
@@ -206,21 +230,14 @@ __global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
 #pragma unroll
     for (int u = 0; u < kAttnChunk; ++u)
         vv[u] = vb[(int64_t)(start + min(u, cnt - 1)) * kDecThreads + t];
-    // the producer's new K and V rows belong to the chunk that holds the position (its last)
-    const bool store_kv = PRO && pro.k_codes && c == chunks - 1;
     if (PRO) {
-        const int w = t >> 6;
-        const float *cos_row = pro.cos_tab + (int64_t)pos * (kDecThreads / 2);
-        const float *sin_row = pro.sin_tab + (int64_t)pos * (kDecThreads / 2);
-        for (int h = w; h < heads; h += kDecThreads / 64)
-            wave_norm_rope(pro.q_codes + (row * heads + h) * kDecThreads, pro.q_scale, pro.q_gain,
-                           cos_row, sin_row, true, pro.eps, qs + h * kDecThreads);
-        if (store_kv && w == 2)
-            wave_norm_rope(pro.k_codes + row * kDecThreads, pro.k_scale, pro.k_gain, cos_row,
-                           sin_row, true, pro.eps, kvnew);
-        if (store_kv && w == 3)
-            wave_norm_rope(pro.v_codes + row * kDecThreads, pro.v_scale, nullptr, cos_row, sin_row,
-                           false, pro.eps, kvnew + kDecThreads);
+#pragma unroll
+        for (int i = 0; i < kAttnMaxHeads / 4; ++i) {
+            const int h = w + 4 * i;
+            if (h < heads) wave_norm_rope(qin[i], true, true, pro.eps, qs + h * kDecThreads);
+        }
+        if (store_kv && w == 2) wave_norm_rope(kvin, true, true, pro.eps, kvnew);
+        if (store_kv && w == 3) wave_norm_rope(kvin, false, false, pro.eps, kvnew + kDecThreads);
     } else {
         for (int i = t; i < heads * kDecThreads; i += kDecThreads)
             qs[i] = q[row * heads * kDecThreads + i];
@@ -305,11 +322,14 @@ __global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
 
 // Grid (heads, rows); thread d merges dim d over the chunks in ascending order: M = max m_c,
 // w_c = exp(m_c - M) (once per chunk, staged in LDS), L = sum l_c w_c, O = sum o_c w_c,
-// out = O / L, then the o_proj input snap.
+// out = O / L, then the o_proj input snap. Every load that does not depend on M goes out first
+// (the chunk's (m, l) pairs and the first kB partials of the thread's dim); M is a shuffle max in
+// each wave and a max over the four waves (max is exact in any order).
 __global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(
     const float *part_ml, const float *part_o, int heads, int pos_host, const int32_t *pos_dev,
     int window, int max_chunks, float in_scale, int8_t *codes, float *out_f32) {
-    __shared__ float red[kDecThreads];
+    constexpr int kB = 16;  // partials loaded together (indices clamped, so all valid)
+    __shared__ float red[kDecThreads / 64];
     __shared__ float ws[kDecThreads];
     __shared__ float ls[kDecThreads];
     const int t = threadIdx.x, h = blockIdx.x;
@@ -318,23 +338,31 @@ __global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(
     const int lo = window > 0 ? max(0, pos - window + 1) : 0;
     const int chunks = (pos - lo + 1 + kAttnChunk - 1) / kAttnChunk;
     const int64_t slot0 = (row * heads + h) * max_chunks;
-    float m = -__int_as_float(0x7f800000);
+    float oo[kB];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) oo[u] = part_o[(slot0 + min(u, chunks - 1)) * kDecThreads + t];
+    float m = -__int_as_float(0x7f800000), lt = 0.0f;
     for (int c = t; c < chunks; c += kDecThreads) m = fmaxf(m, part_ml[(slot0 + c) * 2]);
-    const float M = block_max(m, red);
+    if (t < chunks) lt = part_ml[(slot0 + t) * 2 + 1];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((t & 63) == 0) red[t >> 6] = m;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float L = 0.0f, O = 0.0f;
     for (int c0 = 0; c0 < chunks; c0 += kDecThreads) {
         const int n = min(kDecThreads, chunks - c0);
         if (t < n) {
             ws[t] = d_expf(__fsub_rn(part_ml[(slot0 + c0 + t) * 2], M));
-            ls[t] = part_ml[(slot0 + c0 + t) * 2 + 1];
+            ls[t] = c0 == 0 ? lt : part_ml[(slot0 + c0 + t) * 2 + 1];
         }
         __syncthreads();
-        constexpr int kB = 16;  // partials loaded together (indices clamped, so all valid)
         for (int u0 = 0; u0 < n; u0 += kB) {
-            float oo[kB];
+            if (c0 + u0 > 0) {
 #pragma unroll
-            for (int u = 0; u < kB; ++u)
-                oo[u] = part_o[(slot0 + c0 + min(u0 + u, n - 1)) * kDecThreads + t];
+                for (int u = 0; u < kB; ++u)
+                    oo[u] = part_o[(slot0 + c0 + min(u0 + u, n - 1)) * kDecThreads + t];
+            }
 #pragma unroll
             for (int u = 0; u < kB; ++u) {
                 if (u0 + u < n) {
