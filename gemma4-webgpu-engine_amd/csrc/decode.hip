@@ -39,7 +39,7 @@ static_assert(kDecThreads == kRowThreads, "the glue kernels run the shared 256-l
 
 // One block per row (rms_join_row).
 __global__ __launch_bounds__(kDecThreads) void join_kernel(JoinTail J) {
-    __shared__ float lds[kDecThreads];
+    __shared__ float lds[2 * kDecThreads];
     rms_join_row(J, blockIdx.x, lds);
 }
 
@@ -313,8 +313,13 @@ __global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
         if (h < heads) {
             float o = 0.0f;
 #pragma unroll
-            for (int u = 0; u < kAttnChunk; ++u)
-                if (u < cnt) o = __fadd_rn(o, __fmul_rn(es[h * kAttnChunk + u], vv[u]));
+            for (int u4 = 0; u4 < kAttnChunk; u4 += 4) {  // four weights per LDS read
+                const float4 e4 = *reinterpret_cast<const float4 *>(es + h * kAttnChunk + u4);
+                const float e[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (u4 + i < cnt) o = __fadd_rn(o, __fmul_rn(e[i], vv[u4 + i]));
+            }
             part_o[((row * heads + h) * max_chunks + c) * kDecThreads + t] = o;
         }
     }

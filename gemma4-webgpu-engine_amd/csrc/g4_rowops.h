@@ -16,26 +16,21 @@ constexpr int kRowThreads = 256;
 constexpr int kJoinMaxPer = 8;  // an RMS join serves widths up to 8 * 256
 
 // The pairwise tree over 256 lanes: level s adds lane l + s into lane l for l < s, s = 128 .. 1
-// (every thread of the block calls it; returns the total). The two cross-wave levels go through
-// LDS, the six in-wave levels through lane shuffles, so the same tree costs three barriers.
-// lds: at least 193 floats.
+// (every thread of the block calls it; returns the total). The 256 partials go through LDS once;
+// then every wave evaluates the whole tree itself: lane l takes levels 128 and 64 in-lane
+// ((p[l] + p[l+128]) + (p[l+64] + p[l+192])) and the six in-wave levels by shuffles. One barrier.
+// lds: 256 floats that the block does not write again before another barrier (two trees in a row
+// take two regions).
 __device__ __forceinline__ float block_tree_sum(float part, float *lds) {
-    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-    if (w >= 2) lds[t - 128] = part;
+    const int t = threadIdx.x, lane = t & 63;
+    lds[t] = part;
     __syncthreads();
-    if (w < 2) part = __fadd_rn(part, lds[t]);           // s = 128
-    if (w == 1) lds[128 + lane] = part;
-    __syncthreads();
-    if (w == 0) {
-        part = __fadd_rn(part, lds[128 + lane]);         // s = 64
+    const float a = __fadd_rn(lds[lane], lds[lane + 128]);       // s = 128, lanes l < 64
+    const float b = __fadd_rn(lds[lane + 64], lds[lane + 192]);  // s = 128, lanes 64 .. 127
+    float v = __fadd_rn(a, b);                                   // s = 64
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, __shfl_down(part, off));
-        if (lane == 0) lds[192] = part;
-    }
-    __syncthreads();
-    const float total = lds[192];
-    __syncthreads();  // the caller may reuse lds at once
-    return total;
+    for (int off = 32; off >= 1; off >>= 1) v = __fadd_rn(v, __shfl_down(v, off));
+    return __shfl(v, 0);
 }
 
 // sqrtf, not __fsqrt_rn: on this toolchain __fsqrt_rn is the native (approximate) v_sqrt_f32
@@ -57,7 +52,7 @@ __device__ __forceinline__ int8_t snap_code(float v, float s) { return (int8_t)s
 // with a residual, hidden = resid + y, times alpha when alpha != 1. Outputs: hidden (f32, when
 // J.hidden is set), and emit(i, code) for every element i < width with the code of either the
 // second norm of hidden (gain2 given) or of hidden itself, snapped on in_scale (when J.codes is
-// set). lds: at least 193 floats.
+// set). lds: 512 floats (the two reductions take one half each).
 template <typename Emit>
 __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row, float *lds,
                                                   Emit emit) {
@@ -98,7 +93,7 @@ __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row
     }
     if (!J.codes) return;
     if (J.gain2) {
-        const float inv2 = inv_rms(block_tree_sum(part2, lds), width, J.eps);
+        const float inv2 = inv_rms(block_tree_sum(part2, lds + kRowThreads), width, J.eps);
 #pragma unroll
         for (int e = 0; e < kJoinMaxPer; ++e) {
             const int i = t + e * kRowThreads;
@@ -113,7 +108,7 @@ __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row
     }
 }
 
-// The join kernel's form: codes to J.codes[row][i].
+// The join kernel's form: codes to J.codes[row][i]. lds: 512 floats.
 __device__ __forceinline__ void rms_join_row(const JoinTail &J, int64_t row, float *lds) {
     int8_t *codes = J.codes;
     const int64_t base = row * J.width;

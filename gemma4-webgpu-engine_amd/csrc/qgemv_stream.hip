@@ -765,8 +765,8 @@ int g4_qgemv_plan_launch(const g4_gemv_plan *p, void *stream) {
     A.njobs = p->njobs;
     A.total_tiles = p->total_tiles;
     A.pre = p->pre;
-    // with a prologue join, the join's reduction tree follows the codes
-    const size_t lds = (size_t)((p->max_k + 15) & ~15) + (p->pre ? kRowThreads * sizeof(float) : 0);
+    // with a prologue join, the join's two reduction buffers follow the codes
+    const size_t lds = (size_t)((p->max_k + 15) & ~15) + (p->pre ? 2 * kRowThreads * sizeof(float) : 0);
     const dim3 grid(p->grid), block(kStreamThreads);
     const hipStream_t st = as_stream(stream);
     if (p->paired && p->pre)
