@@ -367,6 +367,12 @@ int build(g4_decode &d) {
     g4_gemv_desc hd = desc(d.w.embed, d.w.embed_s, d.head_codes, d.logits, 4, H, (int)s.vocab,
                            G4_KIND_F32, in, 0.0f);
     G4_TRY(try_plan(&hd, 1, d.head_plan));
+    // the plans without a join snap inside their first tile
+    for (int l = 0; l < s.layers; ++l) {
+        const Plan *P = &d.plans[(size_t)l * P_PER_LAYER];
+        for (int i : {P_O, P_DOWN, P_PLE_PROJ})
+            if (P[i].p) G4_TRY(gemv_plan_set_first_tile_snap(P[i].p));
+    }
     // each join rides in the plan that reads its codes
     G4_TRY(carry_join(d, 0, d.plans[P_QKV]));
     for (int l = 0; l < s.layers; ++l) {

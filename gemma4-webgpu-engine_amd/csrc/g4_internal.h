@@ -136,6 +136,10 @@ int attention_decode_fused(const AttnPrologue &pro, float *k_cache, float *v_cac
                            const int32_t *pos_dev, int window, float *workspace,
                            size_t workspace_bytes, float in_scale, int8_t *codes, void *stream);
 
+// Makes a plan snap each block's first activation vector inside its first tile, after that tile's
+// weight loads are out (the decode runner's small plans: the snap's latency overlaps the weights').
+int gemv_plan_set_first_tile_snap(g4_gemv_plan *p);
+
 // The internal form of a public g4_gelu_act (NULL or a NULL up: no prologue).
 GeluAct gelu_act_of(const g4_gelu_act *a);
 

@@ -357,10 +357,10 @@ __device__ __forceinline__ void stream_store_gelu(const StreamJob &J, int row, f
 // (row index clamped, so every load is valid) and the row scale, the dot against the LDS codes,
 // the fixed reduction over the row's LPR lanes (exact int32), and the row's output from one lane.
 // PAIR: the same rows of the paired up projection stream beside the gate's, for the gelu epilogue.
-// PRE (a block's first tile in a plan with a prologue join): the tile's weight loads go out first,
-// then the block runs the join into the LDS codes (sx is its code sum), so the join's own memory
-// latency overlaps the weight stream's. Returns sx.
-template <int BITS, int LPR, int CPL, bool PAIR, bool PRE = false>
+// PRE (a block's first tile): the tile's weight loads go out first, then the block fills the LDS
+// codes (sx is their sum): 1, the plan's prologue join; 2, the job's own snap. The codes' memory
+// latency then overlaps the weight stream's. Returns sx.
+template <int BITS, int LPR, int CPL, bool PAIR, int PRE = 0>
 __device__ __forceinline__ int stream_tile(const StreamJob &J, int t, uint8_t *xs, int sx, int wave,
                                            int lane, const JoinTail *pre = nullptr,
                                            int *s_sum = nullptr) {
@@ -381,7 +381,8 @@ __device__ __forceinline__ int stream_tile(const StreamJob &J, int t, uint8_t *x
     }
     const float scale = gload<float>(J.scales + rc);
     const float scale2 = PAIR ? gload<float>(J.aux_scales + rc) : 0.0f;
-    if (PRE) sx = snap_join_codes(pre, BITS == 4, xs, s_sum, threadIdx.x);
+    if (PRE == 1) sx = snap_join_codes(pre, BITS == 4, xs, s_sum, threadIdx.x);
+    if (PRE == 2) sx = snap_activations(J, xs, s_sum, threadIdx.x);
     int acc = 0, acc2 = 0;
 #pragma unroll
     for (int u = 0; u < CPL; ++u) acc = chunk_dot<BITS>(w[u], xs, lr + u * LPR, acc);
@@ -407,15 +408,15 @@ __device__ __forceinline__ int stream_tile(const StreamJob &J, int t, uint8_t *x
     return sx;
 }
 
-// A block's first tile in a plan with a prologue join (stream_tile PRE); returns the code sum.
-template <bool PAIR>
-__device__ __forceinline__ int stream_dispatch_join(const StreamJob &J, int t, uint8_t *xs, int wave,
-                                                    int lane, const JoinTail *pre, int *s_sum) {
+// A block's first tile with its codes filled inside it (stream_tile PRE); returns the code sum.
+template <bool PAIR, int PRE>
+__device__ __forceinline__ int stream_dispatch_first(const StreamJob &J, int t, uint8_t *xs, int wave,
+                                                     int lane, const JoinTail *pre, int *s_sum) {
     if (PAIR && J.epi == 1) {
         switch (J.cls) {
 #define G4_CASE(i)                                                                               \
     case i:                                                                                      \
-        return stream_tile<kClasses[i].bits, kClasses[i].lpr, kClasses[i].cpl, true, true>(      \
+        return stream_tile<kClasses[i].bits, kClasses[i].lpr, kClasses[i].cpl, true, PRE>(       \
             J, t, xs, 0, wave, lane, pre, s_sum);
             G4_CASE(0) G4_CASE(1) G4_CASE(2) G4_CASE(3) G4_CASE(4) G4_CASE(5) G4_CASE(6) G4_CASE(7)
 #undef G4_CASE
@@ -426,7 +427,7 @@ __device__ __forceinline__ int stream_dispatch_join(const StreamJob &J, int t, u
         switch (J.cls) {
 #define G4_CASE(i)                                                                               \
     case i:                                                                                      \
-        return stream_tile<kClasses[i].bits, kClasses[i].lpr, kClasses[i].cpl, false, true>(     \
+        return stream_tile<kClasses[i].bits, kClasses[i].lpr, kClasses[i].cpl, false, PRE>(      \
             J, t, xs, 0, wave, lane, pre, s_sum);
             G4_CASE(0) G4_CASE(1) G4_CASE(2) G4_CASE(3) G4_CASE(4) G4_CASE(5) G4_CASE(6) G4_CASE(7)
             G4_CASE(8) G4_CASE(9) G4_CASE(10) G4_CASE(11) G4_CASE(12) G4_CASE(13) G4_CASE(14)
@@ -436,7 +437,9 @@ __device__ __forceinline__ int stream_dispatch_join(const StreamJob &J, int t, u
                 break;
         }
     }
-    return snap_join_codes(pre, J.bits == 4, xs, s_sum, threadIdx.x);  // no class: codes only
+    // no class: codes only
+    if (PRE == 1) return snap_join_codes(pre, J.bits == 4, xs, s_sum, threadIdx.x);
+    return snap_activations(J, xs, s_sum, threadIdx.x);
 }
 
 template <bool PAIR>
@@ -474,10 +477,11 @@ __device__ __forceinline__ void stream_dispatch(const StreamJob &J, int t, uint8
 static_assert(kNumClasses == 17, "stream_dispatch lists every class");
 static_assert(kClasses[7].bits == 4 && kClasses[8].bits == 8, "classes 0-7 are the 4-bit ones");
 
-// JOIN (plan launches whose jobs all read a prologue join's codes): the block's codes come from
+// MODE 1 (plan launches whose jobs all read a prologue join's codes): the block's codes come from
 // the join, run inside its first tile after that tile's weight loads are out, and stay for every
-// job.
-template <bool TABLE, bool PAIR, bool JOIN>
+// job. MODE 2: the first job's snap runs inside the first tile the same way; later jobs snap as
+// usual. MODE 0: every snap before its tiles.
+template <bool TABLE, bool PAIR, int MODE>
 __device__ __forceinline__ void stream_body(const StreamArgs &A, uint8_t *xs, int *s_sum) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -496,15 +500,15 @@ __device__ __forceinline__ void stream_body(const StreamArgs &A, uint8_t *xs, in
     }
     int sx;
     StreamJob J = TABLE ? A.table[j] : A.job[j];
-    if (JOIN)
-        sx = stream_dispatch_join<PAIR>(J, t0, xs, wave, lane, A.pre, s_sum);  // tile t0 done
+    if (MODE != 0)
+        sx = stream_dispatch_first<PAIR, MODE>(J, t0, xs, wave, lane, A.pre, s_sum);  // tile t0 done
     else
         sx = snap_activations(J, xs, s_sum, tid);
-    for (int t = JOIN ? t0 + 1 : t0; t < t1; ++t) {
+    for (int t = MODE != 0 ? t0 + 1 : t0; t < t1; ++t) {
         if (t >= J.tile_begin + J.tiles) {
             ++j;
             J = TABLE ? A.table[j] : A.job[j];
-            if (!JOIN) {
+            if (MODE != 1) {
                 __syncthreads();  // every wave is done with the previous job's codes
                 sx = snap_activations(J, xs, s_sum, tid);
             }
@@ -513,24 +517,24 @@ __device__ __forceinline__ void stream_body(const StreamArgs &A, uint8_t *xs, in
     }
 }
 
-// A plan with a prologue join holds its first tile's weights across the join, which needs more
-// than the 64 registers of 8 waves per SIMD; such plans are small (the q/k/v, gate/up and
-// per-layer-input projections of a decode step), so their blocks fit the chip at 4.
-template <bool TABLE, bool JOIN>
-__global__ __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(JOIN ? 4 : 8, 8)))
+// A plan that fills its codes inside the first tile (MODE 1 or 2) holds that tile's weights across
+// the join or snap, which needs more than the 64 registers of 8 waves per SIMD; such plans are
+// small (the projections of a decode step), so their blocks fit the chip at 4.
+template <bool TABLE, int MODE>
+__global__ __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(MODE ? 4 : 8, 8)))
 void qgemv_stream_kernel(StreamArgs A) {
     extern __shared__ __align__(16) uint8_t xs[];
     __shared__ int s_sum;
-    stream_body<TABLE, false, JOIN>(A, xs, &s_sum);
+    stream_body<TABLE, false, MODE>(A, xs, &s_sum);
 }
 
 // The same with paired gate/up jobs: twice the weight registers, so half the waves per SIMD.
-template <bool TABLE, bool JOIN>
+template <bool TABLE, int MODE>
 __global__ __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(4, 8)))
 void qgemv_stream_pair_kernel(StreamArgs A) {
     extern __shared__ __align__(16) uint8_t xs[];
     __shared__ int s_sum;
-    stream_body<TABLE, true, JOIN>(A, xs, &s_sum);
+    stream_body<TABLE, true, MODE>(A, xs, &s_sum);
 }
 
 // Fills a StreamJob from a validated descriptor and prologue; returns false when no class fits.
@@ -585,7 +589,7 @@ int launch_stream_karg(StreamJob *jobs, int count, hipStream_t stream) {
     A.njobs = count;
     for (int i = 0; i < count; ++i) A.job[i] = jobs[i];
     const int grid = grid_for(A.total_tiles);
-    hipLaunchKernelGGL((qgemv_stream_kernel<false, false>), dim3(grid), dim3(kStreamThreads),
+    hipLaunchKernelGGL((qgemv_stream_kernel<false, 0>), dim3(grid), dim3(kStreamThreads),
                        (size_t)((max_k + 15) & ~15), stream, A);
     G4_LAUNCHED("qgemv_stream_kernel");
     return G4_OK;
@@ -621,6 +625,7 @@ struct g4_gemv_plan {
     int device = 0;
     bool paired = false;  // launches qgemv_stream_pair_kernel
     JoinTail *pre = nullptr;  // device copy of the prologue join, or null
+    bool first_tile_snap = false;  // MODE 2: the snap inside each block's first tile
 };
 
 namespace g4 {
@@ -693,6 +698,12 @@ int gemv_plan_create_epilogue(const g4_gemv_desc *descs, const GeluEpilogue *epi
         }
     }
     return plan_from_jobs(jobs, out);
+}
+
+int gemv_plan_set_first_tile_snap(g4_gemv_plan *p) {
+    if (!p) return set_error(G4_ERR_INVALID, "GEMV plan: plan is NULL");
+    p->first_tile_snap = true;
+    return G4_OK;
 }
 
 int gemv_plan_set_prologue_join(g4_gemv_plan *p, const JoinTail &j) {
@@ -769,14 +780,19 @@ int g4_qgemv_plan_launch(const g4_gemv_plan *p, void *stream) {
     const size_t lds = (size_t)((p->max_k + 15) & ~15) + (p->pre ? 2 * kRowThreads * sizeof(float) : 0);
     const dim3 grid(p->grid), block(kStreamThreads);
     const hipStream_t st = as_stream(stream);
-    if (p->paired && p->pre)
-        hipLaunchKernelGGL((qgemv_stream_pair_kernel<true, true>), grid, block, lds, st, A);
+    const int mode = p->pre ? 1 : p->first_tile_snap ? 2 : 0;
+    if (p->paired && mode == 1)
+        hipLaunchKernelGGL((qgemv_stream_pair_kernel<true, 1>), grid, block, lds, st, A);
+    else if (p->paired && mode == 2)
+        hipLaunchKernelGGL((qgemv_stream_pair_kernel<true, 2>), grid, block, lds, st, A);
     else if (p->paired)
-        hipLaunchKernelGGL((qgemv_stream_pair_kernel<true, false>), grid, block, lds, st, A);
-    else if (p->pre)
-        hipLaunchKernelGGL((qgemv_stream_kernel<true, true>), grid, block, lds, st, A);
+        hipLaunchKernelGGL((qgemv_stream_pair_kernel<true, 0>), grid, block, lds, st, A);
+    else if (mode == 1)
+        hipLaunchKernelGGL((qgemv_stream_kernel<true, 1>), grid, block, lds, st, A);
+    else if (mode == 2)
+        hipLaunchKernelGGL((qgemv_stream_kernel<true, 2>), grid, block, lds, st, A);
     else
-        hipLaunchKernelGGL((qgemv_stream_kernel<true, false>), grid, block, lds, st, A);
+        hipLaunchKernelGGL((qgemv_stream_kernel<true, 0>), grid, block, lds, st, A);
     G4_LAUNCHED("qgemv_stream_kernel");
     return G4_OK;
 }
