@@ -28,7 +28,6 @@ namespace g4 {
 constexpr int kDecThreads = 256;
 constexpr int kAttnChunk = 32;
 constexpr int kAttnMaxHeads = 8;
-static_assert(kAttnMaxHeads <= 2 * (kDecThreads / 64), "the split kernel's waves take two heads each");
 
 // d_expf, d_tanhf and d_gelu (the deterministic exp / tanh / gelu) live in g4_internal.h, shared
 // with the GEMV gelu prologues; block_tree_sum, inv_rms and the RMS join row in g4_rowops.h, shared
@@ -115,20 +114,21 @@ __global__ __launch_bounds__(kDecThreads) void attn_prologue_kernel(
 // attn_prologue_kernel's arithmetic for one 256-wide head vector on one wave: lane l holds
 // elements l, l + 64, l + 128 and l + 192, so the block tree's levels 128 and 64 are in-lane adds
 // in the same order (x[l]^2 + x[l+128]^2, then + (x[l+64]^2 + x[l+192]^2)) and the rest is the same
-// shuffle tree; the RoPE pairs (i, i + 128) are in-lane too. The operands are loaded first
-// (NormRopeIn), so a caller can put them ahead of a longer stream of loads.
+// shuffle tree; the RoPE pairs (i, i + 128) are in-lane too. The operands are loaded first and kept
+// raw (NormRopeIn), so a caller can put them ahead of a longer stream of loads without waiting.
 struct NormRopeIn {
-    float x[4], gt[4], c[2], sn[2];
+    int code[4];
+    float gt[4], c[2], sn[2];
 };
 
-__device__ __forceinline__ NormRopeIn wave_norm_rope_load(const int8_t *src, float scale,
-                                                          const float *gain, const float *cos_row,
-                                                          const float *sin_row, bool rotate) {
+__device__ __forceinline__ NormRopeIn wave_norm_rope_load(const int8_t *src, const float *gain,
+                                                          const float *cos_row, const float *sin_row,
+                                                          bool rotate) {
     const int l = threadIdx.x & 63;
     NormRopeIn in;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        in.x[k] = __fmul_rn((float)src[l + 64 * k], scale);
+        in.code[k] = src[l + 64 * k];
         in.gt[k] = gain ? gain[l + 64 * k] : 1.0f;
     }
 #pragma unroll
@@ -140,10 +140,12 @@ __device__ __forceinline__ NormRopeIn wave_norm_rope_load(const int8_t *src, flo
 }
 
 // Writes the four results of the lane to out[l + 64 k].
-__device__ __forceinline__ void wave_norm_rope(const NormRopeIn &in, bool gain, bool rotate,
-                                               float eps, float *out) {
+__device__ __forceinline__ void wave_norm_rope(const NormRopeIn &in, float scale, bool gain,
+                                               bool rotate, float eps, float *out) {
     const int l = threadIdx.x & 63;
-    const float *x = in.x;
+    float x[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[k] = __fmul_rn((float)in.code[k], scale);
     float part = __fadd_rn(__fadd_rn(__fmul_rn(x[0], x[0]), __fmul_rn(x[2], x[2])),
                            __fadd_rn(__fmul_rn(x[1], x[1]), __fmul_rn(x[3], x[3])));
 #pragma unroll
@@ -168,24 +170,34 @@ __device__ __forceinline__ void wave_norm_rope(const NormRopeIn &in, bool gain, 
     }
 }
 
-// Grid (max chunks, rows), 256 threads. Chunk c covers positions lo + 32 c .. min(+32, pos + 1), for
-// every query head of the row at once (heads <= 8 share the one KV head), so each K and V row of
-// the chunk is read once. Scores: thread t takes eighth t & 7 (32 dims, sequential) of position
-// t >> 3 against every head, and the position's eight lanes combine by the pairwise tree
+// Grid (max chunks, rows), HALVES x 256 threads (t = the thread's index in its half of 256).
+// Chunk c covers positions lo + 32 c .. min(+32, pos + 1), for every query head of the row at once
+// (heads <= 8 share the one KV head), so each K and V row of the chunk is fetched once per block.
+// HALVES 2 (a grid no wider than the CU count: batch 1): half 0 takes heads 0..3, half 1 heads
+// 4..7, two waves per SIMD with half the dependent chains each; HALVES 1 (wide grids, where the
+// chip is full anyway): every thread takes all heads. Scores: thread t takes eighth t & 7 (32 dims, sequential) of position t >> 3 against its
+// half's heads, and the position's eight lanes combine by the pairwise tree
 // ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)) (an xor butterfly: IEEE addition commutes, so
-// every lane ends with the tree's value). Per head (one 32-lane half-wave each): m = max,
-// e = exp(s - m), l = the 32-lane pairwise tree of e. Then thread d accumulates, for every head,
-// sum over positions (ascending) of e * v[d]. Writes (m, l) and o[256] per (row, head, chunk).
-// PRO: q (and on a producer, the position's K and V rows) come from the prologue run here.
-template <bool PRO>
-__global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
+// every lane ends with the tree's value). Per head (one 32-lane group of half 0 each): m = max,
+// e = exp(s - m), l = the 32-lane pairwise tree of e. Then thread t accumulates, for its half's
+// heads, sum over positions (ascending) of e * v[t]. Writes (m, l) and o[256] per (row, head,
+// chunk). PRO: q (and on a producer, the position's K and V rows) come from the prologue run here:
+// wave w rebuilds query heads w, w + waves, ...; in the block whose chunk holds the position, waves
+// 0 and 1 also build the new K and V rows, which the block stores and uses in place of the stale
+// rows it loaded.
+template <bool PRO, int HALVES>
+__global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
     const float *q, const float *k_cache, const float *v_cache, int64_t cache_row_stride, int heads,
     int pos_host, const int32_t *pos_dev, int window, float *part_ml, float *part_o, int max_chunks,
     AttnPrologue pro) {
     __shared__ __align__(16) float qs[kAttnMaxHeads * kDecThreads];
     __shared__ __align__(16) float es[kAttnMaxHeads * kAttnChunk];
     __shared__ __align__(16) float kvnew[PRO ? 2 * kDecThreads : 1];
-    const int t = threadIdx.x;
+    constexpr int THREADS = HALVES * kDecThreads, WAVES = THREADS / 64;
+    constexpr int HH = kAttnMaxHeads / HALVES;        // heads per thread in scores and PV
+    constexpr int QPW = (kAttnMaxHeads + WAVES - 1) / WAVES;  // query heads per wave (prologue)
+    const int tid = threadIdx.x;
+    const int half = tid >> 8, t = tid & (kDecThreads - 1), w = tid >> 6;
     const int c = blockIdx.x;
     const int64_t row = blockIdx.y;
     const int pos = step_pos(pos_host, pos_dev);
@@ -198,27 +210,25 @@ __global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
     float *vb = const_cast<float *>(v_cache) + row * cache_row_stride;
     // the producer's new K and V rows belong to the chunk that holds the position (its last)
     const bool store_kv = PRO && pro.k_codes && c == chunks - 1;
-    // the prologue's few operands go out first (each wave: its query heads, and in the position's
-    // block the K or V row), then the chunk's K segment and V rows, so the prologue's arithmetic
-    // waits for its own loads only and overlaps the chunk's
-    const int w = t >> 6;
-    NormRopeIn qin[kAttnMaxHeads / 4], kvin;
+    // the prologue's few operands go out first, then the chunk's K segment and V rows, so the
+    // prologue's arithmetic waits for its own loads only and overlaps the chunk's
+    NormRopeIn qin[QPW], kvin;
     const float *cos_row = PRO ? pro.cos_tab + (int64_t)pos * (kDecThreads / 2) : nullptr;
     const float *sin_row = PRO ? pro.sin_tab + (int64_t)pos * (kDecThreads / 2) : nullptr;
     if (PRO) {
 #pragma unroll
-        for (int i = 0; i < kAttnMaxHeads / 4; ++i) {
-            const int h = w + 4 * i;
+        for (int i = 0; i < QPW; ++i) {
+            const int h = w + WAVES * i;
             if (h < heads)
                 qin[i] = wave_norm_rope_load(pro.q_codes + (row * heads + h) * kDecThreads,
-                                             pro.q_scale, pro.q_gain, cos_row, sin_row, true);
+                                             pro.q_gain, cos_row, sin_row, true);
         }
-        if (store_kv && w == 2)
-            kvin = wave_norm_rope_load(pro.k_codes + row * kDecThreads, pro.k_scale, pro.k_gain,
-                                       cos_row, sin_row, true);
-        if (store_kv && w == 3)
-            kvin = wave_norm_rope_load(pro.v_codes + row * kDecThreads, pro.v_scale, nullptr,
-                                       cos_row, sin_row, false);
+        if (store_kv && w == 0)
+            kvin = wave_norm_rope_load(pro.k_codes + row * kDecThreads, pro.k_gain, cos_row, sin_row,
+                                       true);
+        if (store_kv && w == 1)
+            kvin = wave_norm_rope_load(pro.v_codes + row * kDecThreads, nullptr, cos_row, sin_row,
+                                       false);
     }
     const int j = t >> 3, sg = t & 7;
     const float4 *kr = reinterpret_cast<const float4 *>(
@@ -232,14 +242,15 @@ __global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
         vv[u] = vb[(int64_t)(start + min(u, cnt - 1)) * kDecThreads + t];
     if (PRO) {
 #pragma unroll
-        for (int i = 0; i < kAttnMaxHeads / 4; ++i) {
-            const int h = w + 4 * i;
-            if (h < heads) wave_norm_rope(qin[i], true, true, pro.eps, qs + h * kDecThreads);
+        for (int i = 0; i < QPW; ++i) {
+            const int h = w + WAVES * i;
+            if (h < heads) wave_norm_rope(qin[i], pro.q_scale, true, true, pro.eps, qs + h * kDecThreads);
         }
-        if (store_kv && w == 2) wave_norm_rope(kvin, true, true, pro.eps, kvnew);
-        if (store_kv && w == 3) wave_norm_rope(kvin, false, false, pro.eps, kvnew + kDecThreads);
+        if (store_kv && w == 0) wave_norm_rope(kvin, pro.k_scale, true, true, pro.eps, kvnew);
+        if (store_kv && w == 1)
+            wave_norm_rope(kvin, pro.v_scale, false, false, pro.eps, kvnew + kDecThreads);
     } else {
-        for (int i = t; i < heads * kDecThreads; i += kDecThreads)
+        for (int i = tid; i < heads * kDecThreads; i += THREADS)
             qs[i] = q[row * heads * kDecThreads + i];
     }
     __syncthreads();
@@ -247,8 +258,10 @@ __global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
         // the position's row: the cache gets it, and this block's operands take it in place of the
         // stale row they loaded
         const int jp = pos - start;
-        kb[(int64_t)pos * kDecThreads + t] = kvnew[t];
-        vb[(int64_t)pos * kDecThreads + t] = kvnew[kDecThreads + t];
+        if (half == 0) {
+            kb[(int64_t)pos * kDecThreads + t] = kvnew[t];
+            vb[(int64_t)pos * kDecThreads + t] = kvnew[kDecThreads + t];
+        }
         if (j == jp) {
 #pragma unroll
             for (int i4 = 0; i4 < 8; ++i4)
@@ -259,10 +272,11 @@ __global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
             if (u == jp) vv[u] = kvnew[kDecThreads + t];
     }
 
-    // scores
-    float sc[kAttnMaxHeads];
+    // scores of this half's heads
+    float sc[HH];
 #pragma unroll
-    for (int h = 0; h < kAttnMaxHeads; ++h) {
+    for (int hh = 0; hh < HH; ++hh) {
+        const int h = half * HH + hh;
         float a = 0.0f;
         if (h < heads) {
             const float *qh = qs + h * kDecThreads + sg * 32;
@@ -278,18 +292,20 @@ __global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
         }
         a = __fadd_rn(a, __shfl_xor(a, 1));
         a = __fadd_rn(a, __shfl_xor(a, 2));
-        sc[h] = __fadd_rn(a, __shfl_xor(a, 4));
+        sc[hh] = __fadd_rn(a, __shfl_xor(a, 4));
     }
     if (sg == 0) {
 #pragma unroll
-        for (int h = 0; h < kAttnMaxHeads; ++h)
-            if (h < heads) es[h * kAttnChunk + j] = j < cnt ? sc[h] : -__int_as_float(0x7f800000);
+        for (int hh = 0; hh < HH; ++hh) {
+            const int h = half * HH + hh;
+            if (h < heads) es[h * kAttnChunk + j] = j < cnt ? sc[hh] : -__int_as_float(0x7f800000);
+        }
     }
     __syncthreads();
 
-    // per head, uniform within its 32-lane half-wave: max, exp, the pairwise sum
+    // per head, uniform within its 32-lane group of half 0: max, exp, the pairwise sum
     const int hh = t >> 5, p = t & 31;
-    if (hh < heads) {
+    if (half == 0 && hh < heads) {
         const float x = es[hh * kAttnChunk + p];
         float m = x;
 #pragma unroll
@@ -307,9 +323,10 @@ __global__ __launch_bounds__(kDecThreads) void attn_split_kernel(
     }
     __syncthreads();
 
-    // o[h][d] = sum over positions (ascending) of e[h][j] * v[j][d]
+    // o[h][d] = sum over positions (ascending) of e[h][j] * v[j][d], for this half's heads
 #pragma unroll
-    for (int h = 0; h < kAttnMaxHeads; ++h) {
+    for (int g = 0; g < HH; ++g) {
+        const int h = half * HH + g;
         if (h < heads) {
             float o = 0.0f;
 #pragma unroll
@@ -576,9 +593,14 @@ int attention_decode_fused(const AttnPrologue &pro, float *k_cache, float *v_cac
         return set_error(G4_ERR_INVALID, "attention (fused prologue): workspace too small");
     float *part_ml = workspace;
     float *part_o = workspace + (size_t)rows * heads * chunks * 2;
-    hipLaunchKernelGGL(attn_split_kernel<true>, dim3(chunks, rows), dim3(kDecThreads), 0,
-                       as_stream(stream), nullptr, k_cache, v_cache, cache_row_stride, heads, pos,
-                       pos_dev, window, part_ml, part_o, chunks, pro);
+    if ((int64_t)chunks * rows <= device_cu_count())
+        hipLaunchKernelGGL((attn_split_kernel<true, 2>), dim3(chunks, rows), dim3(2 * kDecThreads), 0,
+                           as_stream(stream), nullptr, k_cache, v_cache, cache_row_stride, heads,
+                           pos, pos_dev, window, part_ml, part_o, chunks, pro);
+    else
+        hipLaunchKernelGGL((attn_split_kernel<true, 1>), dim3(chunks, rows), dim3(kDecThreads), 0,
+                           as_stream(stream), nullptr, k_cache, v_cache, cache_row_stride, heads,
+                           pos, pos_dev, window, part_ml, part_o, chunks, pro);
     G4_LAUNCHED("attn_split_kernel");
     hipLaunchKernelGGL(attn_merge_kernel, dim3(heads, rows), dim3(kDecThreads), 0,
                        as_stream(stream), part_ml, part_o, heads, pos, pos_dev, window, chunks,
@@ -675,9 +697,14 @@ int g4_attention_decode(const float *q, const float *k_cache, const float *v_cac
                          workspace_bytes, need);
     float *part_ml = workspace;
     float *part_o = workspace + (size_t)rows * heads * chunks * 2;
-    hipLaunchKernelGGL(attn_split_kernel<false>, dim3(chunks, rows), dim3(kDecThreads), 0,
-                       as_stream(stream), q, k_cache, v_cache, cache_row_stride, heads, pos,
-                       pos_dev, window, part_ml, part_o, chunks, AttnPrologue{});
+    if ((int64_t)chunks * rows <= device_cu_count())
+        hipLaunchKernelGGL((attn_split_kernel<false, 2>), dim3(chunks, rows), dim3(2 * kDecThreads),
+                           0, as_stream(stream), q, k_cache, v_cache, cache_row_stride, heads, pos,
+                           pos_dev, window, part_ml, part_o, chunks, AttnPrologue{});
+    else
+        hipLaunchKernelGGL((attn_split_kernel<false, 1>), dim3(chunks, rows), dim3(kDecThreads), 0,
+                           as_stream(stream), q, k_cache, v_cache, cache_row_stride, heads, pos,
+                           pos_dev, window, part_ml, part_o, chunks, AttnPrologue{});
     G4_LAUNCHED("attn_split_kernel");
     hipLaunchKernelGGL(attn_merge_kernel, dim3(heads, rows), dim3(kDecThreads), 0,
                        as_stream(stream), part_ml, part_o, heads, pos, pos_dev, window, chunks,
