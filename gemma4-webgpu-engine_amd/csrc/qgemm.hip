@@ -159,7 +159,7 @@ struct SmallJobs {
     float act_scale;
 };
 
-template <int MT, int WAVES> constexpr int small_kc() { return (WAVES >= 16 ? 65536 : 32768) / MT; }
+template <int MT, int WAVES> constexpr int small_kc() { return (WAVES >= 16 ? 98304 : 32768) / MT; }
 
 template <int BITS, int MT, int WAVES, int EPI>
 __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
