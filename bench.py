@@ -14,7 +14,8 @@ Reported beside it (under "extra", not the headline):
     launch granularity costs;
   - config 0 (one 1536 x 1536 GEMV) as a single launch;
   - config 2's gate GEMM at M = 512 in int8 TOPS (MFMA), with and without the activation snap;
-  - config 3's split PLE gather (5 slices, 2048 Zipf tokens, f16 out) in GB/s.
+  - config 3's split PLE gather (5 slices, 2048 Zipf tokens, f16 out) in GB/s;
+  - a measured HBM reference (a 1 GiB device-to-device copy) beside the 8 TB/s spec peak.
 
 cpu_baseline: the oracle's C restatement (OpenMP over the host cores) on a bounded sample of the
 same layer set, in the same unit. It is a baseline, not a target.
@@ -265,6 +266,24 @@ def traffic_probe(plan, h):
     log(f"traffic probe done: copy {n} B x3, plan x5")
 
 
+def hbm_copy_rate(h, nbytes=1 << 30, reps=20):
+    """A measured reference for the HBM peak: a device-to-device copy of 1 GiB (the runtime's copy,
+    reading and writing every byte once, far past the 256 MB Infinity Cache); the rate counts
+    both directions."""
+    a = g4.DeviceBuffer(nbytes)
+    b = g4.DeviceBuffer(nbytes)
+    a.fill(1)
+    g4.synchronize()
+    ms = timed(h, lambda: g4._check(g4.lib().g4_memcpy_d2d(g4._ptr(b), g4._ptr(a), nbytes, h)),
+               reps, 3)
+    gbs = 2 * nbytes / (ms * 1e-3) / 1e9
+    a.close()
+    b.close()
+    return {"bytes_moved": 2 * nbytes, "ms": round(ms, 4), "gbs": round(gbs, 1),
+            "frac_of_spec": round(gbs / HBM_PEAK_GBS, 4),
+            "note": "hipMemcpyAsync device to device, 1 GiB read + 1 GiB written"}
+
+
 def decode_step_bytes(shape, pos):
     """Algorithmic HBM bytes of one E2B-shape decode step at `pos` for `batch` rows: every weight
     byte and row scale the step reads once (35 layers of q/k/v/o/gate/up/down int4 and the int8
@@ -484,6 +503,8 @@ def main():
         log("config 2 sweep over M, config 1 int8 down")
         sweep = bench_gemm_sweep(h)
         down8 = bench_int8_down(h)
+        log("measured HBM copy rate")
+        hbm = hbm_copy_rate(h)
         log("config 4 decode step, batch 1 and 32")
         dec1 = bench_decode(h, 1, cpu=not args.no_cpu_baseline)
         dec32 = bench_decode(h, 32)
@@ -500,6 +521,7 @@ def main():
             "gemm_sweep_config2": sweep,
             "config1_int8_down": down8,
             "ple_gather": ga,
+            "hbm_measured": hbm,
         }
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle on host cores)")
