@@ -2,10 +2,11 @@
 // qmatmul-8bit (src/kernels/pleMatmul.ts), plus the shape routing of src/execute.ts:372-430.
 //
 // Pipeline of one call (calibrated path):
-//  1. The activation snap (the SRQ input prologue) runs once per row: quantize_rows_kernel writes
-//     int8 codes to a per-stream workspace, each 8-code group interleaved [x0 x2 x4 x6 x1 x3 x5 x7]
-//     for 4-bit weights so a weight word's even and odd nibble lanes line up with the codes.
-//     (M <= 32 fuses the snap into its kernel instead.)
+//  1. The activation snap (the SRQ input prologue): M <= 32 fuses it into the small kernel (codes
+//     in LDS, each 8-code group interleaved [x0 x2 x4 x6 x1 x3 x5 x7] for 4-bit weights so a weight
+//     word's even and odd nibble lanes line up with the codes); the tile kernel reads natural-order
+//     codes, taken as given from an int8 caller, or snapped once per row by quantize_rows_kernel
+//     into a per-stream workspace.
 //  2. An MFMA kernel contracts codes x weights with v_mfma_i32_16x16x64_i8 in exact int32. The
 //     int32 sums are exact, so the k order the MFMA uses internally is irrelevant; only the A and
 //     B operands have to agree on it, and they do by construction.
@@ -42,8 +43,8 @@ __device__ __forceinline__ uint32_t pack4b(int a, int b, int c, int d) {
            ((uint32_t)(d & 0xff) << 24);
 }
 
-// One block per token row: snap K activations into codes (interleaved per 8-code group when PERM)
-// and zero the pad up to kp.
+// One block per token row: snap K activations into codes (interleaved per 8-code group when PERM;
+// the tile kernel takes them natural) and zero the pad up to kp.
 template <bool PERM>
 __global__ __launch_bounds__(kQuantThreads) void quantize_rows_kernel(
     const void *x, int x_kind, int k, int kp, float scale, int8_t *codes) {
@@ -401,7 +402,7 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
 // Operand layouts (the k assignment inside an MFMA is free as long as A and B agree, because the
 // int32 sums are exact):
 //   lane (j = lane % 16, g = lane / 16), half-step s takes codes 32 g + 16 s .. +16 of the stage.
-//   A is the per-8 interleaved code row [x0 x2 x4 x6 x1 x3 x5 x7] (4-bit) or natural (8-bit).
+//   A is the natural code row; the 4-bit B is put in the same order by nib_natural16.
 //   4-bit B: a lane's 16 bytes of column j are codes 32 g .. 32 g + 31; with w' = w ^ 0x88888888,
 //   (w' << 4) & 0xF0F0F0F0 holds 16 * (even codes) and w' & 0xF0F0F0F0 16 * (odd codes) as signed
 //   bytes, so the accumulator is 16 * sum(code * x), exact (|sum| <= 2^31 / 16 for K <= 16384),
@@ -446,6 +447,14 @@ template <int DPS> __device__ __forceinline__ void tile_wait_stages(int later) {
 
 __device__ __forceinline__ uint32_t nib_even16(uint32_t w) { return ((w ^ 0x88888888u) << 4) & 0xF0F0F0F0u; }
 __device__ __forceinline__ uint32_t nib_odd16(uint32_t w) { return (w ^ 0x88888888u) & 0xF0F0F0F0u; }
+// Eight packed codes c0..c7 (one weight word) as 16 x code signed bytes in natural order: the even
+// and odd nibble bytes [c0 c2 c4 c6] and [c1 c3 c5 c7] interleaved by two byte permutes into
+// [c0 c1 c2 c3] and [c4 c5 c6 c7], so the activation codes need no interleave.
+__device__ __forceinline__ void nib_natural16(uint32_t w, int &lo, int &hi) {
+    const uint32_t e = nib_even16(w), o = nib_odd16(w);
+    lo = (int)__builtin_amdgcn_perm(o, e, 0x05010400u);  // bytes e0 o0 e1 o1
+    hi = (int)__builtin_amdgcn_perm(o, e, 0x07030602u);  // bytes e2 o2 e3 o3
+}
 
 template <int BITS, int NS>
 __global__ __launch_bounds__(256) void qgemm_tile_kernel(
@@ -555,8 +564,13 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(
         for (int u = 0; u < TN; ++u) {
             if (BITS == 4) {
                 const u32x4 w = bw[u][0];
-                bo[0][u] = v4i{(int)nib_even16(w.x), (int)nib_odd16(w.x), (int)nib_even16(w.y), (int)nib_odd16(w.y)};
-                bo[1][u] = v4i{(int)nib_even16(w.z), (int)nib_odd16(w.z), (int)nib_even16(w.w), (int)nib_odd16(w.w)};
+                int a0, a1, b0, b1, c0, c1, d0, d1;
+                nib_natural16(w.x, a0, a1);
+                nib_natural16(w.y, b0, b1);
+                nib_natural16(w.z, c0, c1);
+                nib_natural16(w.w, d0, d1);
+                bo[0][u] = v4i{a0, a1, b0, b1};
+                bo[1][u] = v4i{c0, c1, d0, d1};
             } else {
                 bo[0][u] = __builtin_bit_cast(v4i, bw[u][0]);
                 bo[1][u] = __builtin_bit_cast(v4i, bw[u][BR - 1]);
@@ -851,18 +865,19 @@ static int run_linear(int bits, const void *wq, const float *scales, const void 
         return launch_small(bits, c == K_SKINNY16 ? 16 : 32, 0, x, x_kind, jobs, m, k, in_scale,
                             out_scale, out_kind, stream);
     }
-    const int kp = k;  // k % 128 == 0 on the MFMA kernels
-    void *ws = nullptr;
-    int rc = workspace(stream, (size_t)m * kp, &ws);
-    if (rc) return rc;
-    int8_t *codes = reinterpret_cast<int8_t *>(ws);
-    if (bits == 4)
-        hipLaunchKernelGGL(quantize_rows_kernel<true>, dim3(m), dim3(kQuantThreads), 0, stream, x,
-                           x_kind, k, kp, in_scale, codes);
-    else
+    // The tile kernel reads natural-order codes: int8 input goes to it as given (one launch);
+    // f16 / f32 input is snapped once into a per-stream workspace first.
+    const int8_t *codes = reinterpret_cast<const int8_t *>(x);
+    if (x_kind != G4_KIND_I8) {
+        const int kp = k;  // k % 128 == 0 on the MFMA kernels
+        void *ws = nullptr;
+        int rc = workspace(stream, (size_t)m * kp, &ws);
+        if (rc) return rc;
         hipLaunchKernelGGL(quantize_rows_kernel<false>, dim3(m), dim3(kQuantThreads), 0, stream, x,
-                           x_kind, k, kp, in_scale, codes);
-    G4_LAUNCHED("quantize_rows_kernel");
+                           x_kind, k, kp, in_scale, reinterpret_cast<int8_t *>(ws));
+        G4_LAUNCHED("quantize_rows_kernel");
+        codes = reinterpret_cast<const int8_t *>(ws);
+    }
     const uint8_t *w = reinterpret_cast<const uint8_t *>(wq);
     if (bits == 4)
         return launch_tile<4>(codes, w, scales, dst, m, n, k, in_scale, out_scale, out_kind, stream);
