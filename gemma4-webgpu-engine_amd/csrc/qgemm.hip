@@ -4,9 +4,9 @@
 // Pipeline of one call (calibrated path):
 //  1. The activation snap (the SRQ input prologue): M <= 32 fuses it into the small kernel (codes
 //     in LDS, each 8-code group interleaved [x0 x2 x4 x6 x1 x3 x5 x7] for 4-bit weights so a weight
-//     word's even and odd nibble lanes line up with the codes); the tile kernel reads natural-order
-//     codes, taken as given from an int8 caller, or snapped once per row by quantize_rows_kernel
-//     into a per-stream workspace.
+//     word's even and odd nibble lanes line up with the codes). The tile kernel takes an int8
+//     caller's natural-order codes as given (and permutes the 4-bit B to match); f16 / f32 input is
+//     snapped once per row by quantize_rows_kernel into a per-stream workspace, interleaved.
 //  2. An MFMA kernel contracts codes x weights with v_mfma_i32_16x16x64_i8 in exact int32. The
 //     int32 sums are exact, so the k order the MFMA uses internally is irrelevant; only the A and
 //     B operands have to agree on it, and they do by construction.
@@ -43,8 +43,8 @@ __device__ __forceinline__ uint32_t pack4b(int a, int b, int c, int d) {
            ((uint32_t)(d & 0xff) << 24);
 }
 
-// One block per token row: snap K activations into codes (interleaved per 8-code group when PERM;
-// the tile kernel takes them natural) and zero the pad up to kp.
+// One block per token row: snap K activations into codes (interleaved per 8-code group when PERM)
+// and zero the pad up to kp.
 template <bool PERM>
 __global__ __launch_bounds__(kQuantThreads) void quantize_rows_kernel(
     const void *x, int x_kind, int k, int kp, float scale, int8_t *codes) {
@@ -402,7 +402,8 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
 // Operand layouts (the k assignment inside an MFMA is free as long as A and B agree, because the
 // int32 sums are exact):
 //   lane (j = lane % 16, g = lane / 16), half-step s takes codes 32 g + 16 s .. +16 of the stage.
-//   A is the natural code row; the 4-bit B is put in the same order by nib_natural16.
+//   A is the per-8 interleaved code row [x0 x2 x4 x6 x1 x3 x5 x7] (4-bit) or natural (8-bit, and
+//   4-bit NAT, where nib_natural16 puts B in natural order instead).
 //   4-bit B: a lane's 16 bytes of column j are codes 32 g .. 32 g + 31; with w' = w ^ 0x88888888,
 //   (w' << 4) & 0xF0F0F0F0 holds 16 * (even codes) and w' & 0xF0F0F0F0 16 * (odd codes) as signed
 //   bytes, so the accumulator is 16 * sum(code * x), exact (|sum| <= 2^31 / 16 for K <= 16384),
@@ -456,7 +457,9 @@ __device__ __forceinline__ void nib_natural16(uint32_t w, int &lo, int &hi) {
     hi = (int)__builtin_amdgcn_perm(o, e, 0x07030602u);  // bytes e2 o2 e3 o3
 }
 
-template <int BITS, int NS>
+// NAT (4-bit): A holds natural-order codes and B is permuted to match in registers; otherwise A is
+// the per-8 interleaved row the nibble lanes read directly (no permutes).
+template <int BITS, int NS, bool NAT>
 __global__ __launch_bounds__(256) void qgemm_tile_kernel(
     const int8_t *__restrict__ A, const uint8_t *__restrict__ W, const float *__restrict__ scales,
     void *dst, int M, int N, int K, float in_scale, float out_scale, int out_kind, int tiles_m,
@@ -564,13 +567,18 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(
         for (int u = 0; u < TN; ++u) {
             if (BITS == 4) {
                 const u32x4 w = bw[u][0];
-                int a0, a1, b0, b1, c0, c1, d0, d1;
-                nib_natural16(w.x, a0, a1);
-                nib_natural16(w.y, b0, b1);
-                nib_natural16(w.z, c0, c1);
-                nib_natural16(w.w, d0, d1);
-                bo[0][u] = v4i{a0, a1, b0, b1};
-                bo[1][u] = v4i{c0, c1, d0, d1};
+                if (NAT) {
+                    int a0, a1, b0, b1, c0, c1, d0, d1;
+                    nib_natural16(w.x, a0, a1);
+                    nib_natural16(w.y, b0, b1);
+                    nib_natural16(w.z, c0, c1);
+                    nib_natural16(w.w, d0, d1);
+                    bo[0][u] = v4i{a0, a1, b0, b1};
+                    bo[1][u] = v4i{c0, c1, d0, d1};
+                } else {
+                    bo[0][u] = v4i{(int)nib_even16(w.x), (int)nib_odd16(w.x), (int)nib_even16(w.y), (int)nib_odd16(w.y)};
+                    bo[1][u] = v4i{(int)nib_even16(w.z), (int)nib_odd16(w.z), (int)nib_even16(w.w), (int)nib_odd16(w.w)};
+                }
             } else {
                 bo[0][u] = __builtin_bit_cast(v4i, bw[u][0]);
                 bo[1][u] = __builtin_bit_cast(v4i, bw[u][BR - 1]);
@@ -802,19 +810,23 @@ static int launch_small(int bits, int mt, int epi, const void *x, int x_kind, co
 }
 
 template <int BITS>
-static int launch_tile(const int8_t *codes, const uint8_t *w, const float *scales, void *dst, int m,
-                       int n, int k, float in_scale, float out_scale, int out_kind,
-                       hipStream_t stream) {
+static int launch_tile(const int8_t *codes, bool natural, const uint8_t *w, const float *scales,
+                       void *dst, int m, int n, int k, float in_scale, float out_scale,
+                       int out_kind, hipStream_t stream) {
     const int tiles_m = (m + kTileBM - 1) / kTileBM;
     const int tiles_n = (n + kTileBN - 1) / kTileBN;
     const int blocks = tiles_m * ((tiles_n + 7) / 8) * 8;  // XCD-aware order: whole groups of 8
     const int nk = k / kTileBK;  // >= 2 (k % 128 == 0 and k >= 256 here)
-    if (nk >= 3)
-        hipLaunchKernelGGL((qgemm_tile_kernel<BITS, 4>), dim3(blocks), dim3(256), 0, stream, codes,
-                           w, scales, dst, m, n, k, in_scale, out_scale, out_kind, tiles_m, tiles_n);
-    else
-        hipLaunchKernelGGL((qgemm_tile_kernel<BITS, 3>), dim3(blocks), dim3(256), 0, stream, codes,
-                           w, scales, dst, m, n, k, in_scale, out_scale, out_kind, tiles_m, tiles_n);
+    // 8-bit weights are natural-order bytes already: their A is natural either way
+    const bool nat = BITS == 4 && natural;
+#define G4_TILE(NS_, NAT_)                                                                        \
+    hipLaunchKernelGGL((qgemm_tile_kernel<BITS, NS_, NAT_>), dim3(blocks), dim3(256), 0, stream,   \
+                       codes, w, scales, dst, m, n, k, in_scale, out_scale, out_kind, tiles_m, tiles_n)
+    if (nk >= 3 && nat) G4_TILE(4, true);
+    else if (nk >= 3) G4_TILE(4, false);
+    else if (nat) G4_TILE(3, true);
+    else G4_TILE(3, false);
+#undef G4_TILE
     G4_LAUNCHED("qgemm_tile_kernel");
     return G4_OK;
 }
@@ -865,23 +877,31 @@ static int run_linear(int bits, const void *wq, const float *scales, const void 
         return launch_small(bits, c == K_SKINNY16 ? 16 : 32, 0, x, x_kind, jobs, m, k, in_scale,
                             out_scale, out_kind, stream);
     }
-    // The tile kernel reads natural-order codes: int8 input goes to it as given (one launch);
-    // f16 / f32 input is snapped once into a per-stream workspace first.
+    // An int8 caller's natural-order codes go to the tile kernel as given (one launch; the 4-bit
+    // B operand is permuted to match). f16 / f32 input is snapped once into a per-stream
+    // workspace, interleaved for 4-bit weights so the tile kernel needs no permutes.
     const int8_t *codes = reinterpret_cast<const int8_t *>(x);
-    if (x_kind != G4_KIND_I8) {
+    const bool natural = x_kind == G4_KIND_I8;
+    if (!natural) {
         const int kp = k;  // k % 128 == 0 on the MFMA kernels
         void *ws = nullptr;
         int rc = workspace(stream, (size_t)m * kp, &ws);
         if (rc) return rc;
-        hipLaunchKernelGGL(quantize_rows_kernel<false>, dim3(m), dim3(kQuantThreads), 0, stream, x,
-                           x_kind, k, kp, in_scale, reinterpret_cast<int8_t *>(ws));
+        if (bits == 4)
+            hipLaunchKernelGGL(quantize_rows_kernel<true>, dim3(m), dim3(kQuantThreads), 0, stream,
+                               x, x_kind, k, kp, in_scale, reinterpret_cast<int8_t *>(ws));
+        else
+            hipLaunchKernelGGL(quantize_rows_kernel<false>, dim3(m), dim3(kQuantThreads), 0, stream,
+                               x, x_kind, k, kp, in_scale, reinterpret_cast<int8_t *>(ws));
         G4_LAUNCHED("quantize_rows_kernel");
         codes = reinterpret_cast<const int8_t *>(ws);
     }
     const uint8_t *w = reinterpret_cast<const uint8_t *>(wq);
     if (bits == 4)
-        return launch_tile<4>(codes, w, scales, dst, m, n, k, in_scale, out_scale, out_kind, stream);
-    return launch_tile<8>(codes, w, scales, dst, m, n, k, in_scale, out_scale, out_kind, stream);
+        return launch_tile<4>(codes, natural, w, scales, dst, m, n, k, in_scale, out_scale, out_kind,
+                              stream);
+    return launch_tile<8>(codes, natural, w, scales, dst, m, n, k, in_scale, out_scale, out_kind,
+                          stream);
 }
 
 int linear_grouped(int bits, const void *x, int x_kind, int k, int m, float in_scale,
