@@ -389,18 +389,22 @@ def bench_decode(h, batch, steps=20, warmup=3, probe=False, cpu=False):
 
 
 def gemm_probe(h):
-    """Launches for rocprofv3 --kernel-trace --stats: the config-2 gate GEMM with f16 activations
-    (activation snap + tile kernel) 50 times at M=512 and 20 times at M=2048."""
+    """Launches for rocprofv3 --kernel-trace --stats: the config-2 gate GEMM 50 times at M=512
+    and 20 times at M=2048, first with f16 activations (activation snap + tile kernel), then with
+    int8 codes already snapped (the tile kernel alone)."""
     n, k = syn.FFN, syn.HIDDEN
     w = g4.DeviceBuffer.from_array(syn.int4_weights("c2", "gate", n, k))
     s = g4.DeviceBuffer.from_array(syn.row_scales("c2", "gate", n))
     for m, reps in ((512, 50), (2048, 20)):
         x = g4.DeviceBuffer.from_array(syn.activations("c2", f"x{m}", m, k, outlier_frac=0.01))
+        codes = g4.DeviceBuffer.empty((m, k), np.int8)
+        g4.srq_quantize(x, codes, m * k, syn.IN_SCALE, stream=h)
         d = g4.DeviceBuffer.empty((m, n), np.int8)
-        for _ in range(reps):
-            g4.qgemm(4, w, s, x, d, k, n, m, syn.IN_SCALE, syn.OUT_SCALE, stream=h)
-        g4.synchronize()
-        log(f"gemm probe M={m}: {reps} launches")
+        for src, name in ((x, "f16"), (codes, "int8")):
+            for _ in range(reps):
+                g4.qgemm(4, w, s, src, d, k, n, m, syn.IN_SCALE, syn.OUT_SCALE, stream=h)
+            g4.synchronize()
+            log(f"gemm probe M={m} {name} in: {reps} launches")
 
 
 def main():
@@ -412,7 +416,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true")
     ap.add_argument("--gemm-probe", action="store_true",
-                    help="only the config-2 GEMM launches (M=512 and M=2048, f16 in), for rocprofv3")
+                    help="only the config-2 GEMM launches (M=512 and M=2048, f16 then int8 in), for rocprofv3")
     ap.add_argument("--decode-probe", type=int, default=0, metavar="BATCH",
                     help="only config-4 decode steps at this batch (graph replays), for rocprofv3")
     args = ap.parse_args()
