@@ -185,7 +185,16 @@ __device__ __forceinline__ void wave_norm_rope(const NormRopeIn &in, float scale
 // wave w rebuilds query heads w, w + waves, ...; in the block whose chunk holds the position, waves
 // 0 and 1 also build the new K and V rows, which the block stores and uses in place of the stale
 // rows it loaded.
-template <bool PRO, int HALVES>
+// Float4 slot of the chunk's K group (row r, float4 column c4) in the split kernel's LDS copy.
+// Within each 8-slot segment (one lane's 32 dims), slot m moves to (m + seg/2 + 4*(r&1)) mod 8:
+// the 16 lanes of one ds_read_b128 phase (two rows x eight segments, same m) then hit 16
+// distinct 4-bank groups, and 16 consecutive columns of one row (a write phase) stay distinct.
+__device__ __forceinline__ int k_slot(int r, int c4) {
+    const int seg = c4 >> 3;
+    return r * (kDecThreads / 4) + seg * 8 + (((c4 & 7) + (seg >> 1) + 4 * (r & 1)) & 7);
+}
+
+template <bool PRO, int HALVES, bool KST>
 __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
     const float *q, const float *k_cache, const float *v_cache, int64_t cache_row_stride, int heads,
     int pos_host, const int32_t *pos_dev, int window, float *part_ml, float *part_o, int max_chunks,
@@ -193,6 +202,7 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
     __shared__ __align__(16) float qs[kAttnMaxHeads * kDecThreads];
     __shared__ __align__(16) float es[kAttnMaxHeads * kAttnChunk];
     __shared__ __align__(16) float kvnew[PRO ? 2 * kDecThreads : 1];
+    __shared__ __align__(16) float4 ks[KST ? kAttnChunk * kDecThreads / 4 : 1];
     constexpr int THREADS = HALVES * kDecThreads, WAVES = THREADS / 64;
     constexpr int HH = kAttnMaxHeads / HALVES;        // heads per thread in scores and PV
     constexpr int QPW = (kAttnMaxHeads + WAVES - 1) / WAVES;  // query heads per wave (prologue)
@@ -231,11 +241,25 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
                                        false);
     }
     const int j = t >> 3, sg = t & 7;
-    const float4 *kr = reinterpret_cast<const float4 *>(
-        kb + (int64_t)(start + min(j, cnt - 1)) * kDecThreads + sg * 32);
     float4 kq[8];
+    // KST: the chunk's K rows come in as whole-row float4 runs (one load instruction covers
+    // consecutive 16-byte columns) and reach the lanes' 32-dim segments through LDS; otherwise
+    // each lane reads its own segment (eight loads, each spread over 64 lines)
+    constexpr int KPT = KST ? kAttnChunk * kDecThreads / 4 / THREADS : 1;
+    float4 kl[KPT];
+    if (KST) {
 #pragma unroll
-    for (int i4 = 0; i4 < 8; ++i4) kq[i4] = kr[i4];
+        for (int i = 0; i < KPT; ++i) {
+            const int f = tid + i * THREADS, r = f / (kDecThreads / 4), c4 = f % (kDecThreads / 4);
+            kl[i] = reinterpret_cast<const float4 *>(
+                kb + (int64_t)(start + min(r, cnt - 1)) * kDecThreads)[c4];
+        }
+    } else {
+        const float4 *kr = reinterpret_cast<const float4 *>(
+            kb + (int64_t)(start + min(j, cnt - 1)) * kDecThreads + sg * 32);
+#pragma unroll
+        for (int i4 = 0; i4 < 8; ++i4) kq[i4] = kr[i4];
+    }
     float vv[kAttnChunk];
 #pragma unroll
     for (int u = 0; u < kAttnChunk; ++u)
@@ -253,7 +277,18 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
         for (int i = tid; i < heads * kDecThreads; i += THREADS)
             qs[i] = q[row * heads * kDecThreads + i];
     }
+    if (KST) {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int f = tid + i * THREADS;
+            ks[k_slot(f / (kDecThreads / 4), f % (kDecThreads / 4))] = kl[i];
+        }
+    }
     __syncthreads();
+    if (KST) {
+#pragma unroll
+        for (int i4 = 0; i4 < 8; ++i4) kq[i4] = ks[k_slot(j, sg * 8 + i4)];
+    }
     if (store_kv) {
         // the position's row: the cache gets it, and this block's operands take it in place of the
         // stale row they loaded
@@ -340,6 +375,32 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
             part_o[((row * heads + h) * max_chunks + c) * kDecThreads + t] = o;
         }
     }
+}
+
+// The split launch: two halves of four heads while the grid fits the CUs once; the chunk's K
+// staged through LDS while the grid stays resident at that kernel's occupancy (its 44 KB of LDS
+// allows three blocks per CU), else each lane loads its own K segment (11 KB, eight blocks per
+// CU), which measured faster for grids of several rounds (E2B global layers at batch 32: 78.9
+// against 85.3 us).
+template <bool PRO>
+static void launch_split(int chunks, int rows, hipStream_t st, const float *q, const float *k_cache,
+                         const float *v_cache, int64_t cache_row_stride, int heads, int pos,
+                         const int32_t *pos_dev, int window, float *part_ml, float *part_o,
+                         const AttnPrologue &pro) {
+    const int64_t blocks = (int64_t)chunks * rows, cus = device_cu_count();
+    const dim3 grid(chunks, rows);
+    if (blocks <= cus)
+        hipLaunchKernelGGL((attn_split_kernel<PRO, 2, true>), grid, dim3(2 * kDecThreads), 0, st,
+                           q, k_cache, v_cache, cache_row_stride, heads, pos, pos_dev, window,
+                           part_ml, part_o, chunks, pro);
+    else if (blocks <= 3 * cus)
+        hipLaunchKernelGGL((attn_split_kernel<PRO, 1, true>), grid, dim3(kDecThreads), 0, st, q,
+                           k_cache, v_cache, cache_row_stride, heads, pos, pos_dev, window, part_ml,
+                           part_o, chunks, pro);
+    else
+        hipLaunchKernelGGL((attn_split_kernel<PRO, 1, false>), grid, dim3(kDecThreads), 0, st, q,
+                           k_cache, v_cache, cache_row_stride, heads, pos, pos_dev, window, part_ml,
+                           part_o, chunks, pro);
 }
 
 // Grid (heads, rows); thread d merges dim d over the chunks in ascending order: M = max m_c,
@@ -593,14 +654,8 @@ int attention_decode_fused(const AttnPrologue &pro, float *k_cache, float *v_cac
         return set_error(G4_ERR_INVALID, "attention (fused prologue): workspace too small");
     float *part_ml = workspace;
     float *part_o = workspace + (size_t)rows * heads * chunks * 2;
-    if ((int64_t)chunks * rows <= device_cu_count())
-        hipLaunchKernelGGL((attn_split_kernel<true, 2>), dim3(chunks, rows), dim3(2 * kDecThreads), 0,
-                           as_stream(stream), nullptr, k_cache, v_cache, cache_row_stride, heads,
-                           pos, pos_dev, window, part_ml, part_o, chunks, pro);
-    else
-        hipLaunchKernelGGL((attn_split_kernel<true, 1>), dim3(chunks, rows), dim3(kDecThreads), 0,
-                           as_stream(stream), nullptr, k_cache, v_cache, cache_row_stride, heads,
-                           pos, pos_dev, window, part_ml, part_o, chunks, pro);
+    launch_split<true>(chunks, rows, as_stream(stream), nullptr, k_cache, v_cache,
+                                cache_row_stride, heads, pos, pos_dev, window, part_ml, part_o, pro);
     G4_LAUNCHED("attn_split_kernel");
     hipLaunchKernelGGL(attn_merge_kernel, dim3(heads, rows), dim3(kDecThreads), 0,
                        as_stream(stream), part_ml, part_o, heads, pos, pos_dev, window, chunks,
@@ -697,14 +752,8 @@ int g4_attention_decode(const float *q, const float *k_cache, const float *v_cac
                          workspace_bytes, need);
     float *part_ml = workspace;
     float *part_o = workspace + (size_t)rows * heads * chunks * 2;
-    if ((int64_t)chunks * rows <= device_cu_count())
-        hipLaunchKernelGGL((attn_split_kernel<false, 2>), dim3(chunks, rows), dim3(2 * kDecThreads),
-                           0, as_stream(stream), q, k_cache, v_cache, cache_row_stride, heads, pos,
-                           pos_dev, window, part_ml, part_o, chunks, AttnPrologue{});
-    else
-        hipLaunchKernelGGL((attn_split_kernel<false, 1>), dim3(chunks, rows), dim3(kDecThreads), 0,
-                           as_stream(stream), q, k_cache, v_cache, cache_row_stride, heads, pos,
-                           pos_dev, window, part_ml, part_o, chunks, AttnPrologue{});
+    launch_split<false>(chunks, rows, as_stream(stream), q, k_cache, v_cache,
+                                cache_row_stride, heads, pos, pos_dev, window, part_ml, part_o, AttnPrologue{});
     G4_LAUNCHED("attn_split_kernel");
     hipLaunchKernelGGL(attn_merge_kernel, dim3(heads, rows), dim3(kDecThreads), 0,
                        as_stream(stream), part_ml, part_o, heads, pos, pos_dev, window, chunks,

@@ -129,13 +129,18 @@ def test_attn_prologue(gpu, producer, use_dev_pos):
     assert np.all(got_cache[:, :, mask] == 5.0)
 
 
-@pytest.mark.parametrize("pos,window", [(0, 0), (1, 0), (255, 0), (256, 0), (700, 0), (4095, 0),
-                                        (4095, 512), (511, 512), (512, 512), (1000, 512)])
-def test_attention_decode(gpu, pos, window):
-    print(f"attention pos={pos} window={window}", flush=True)
+# rows 2: two halves of four heads with K staged in LDS (grids up to 256 blocks); at position
+# 4095 (128 chunks) rows 5 stage K with one half (640 blocks) and rows 7 load per-lane K segments
+# (896 blocks)
+@pytest.mark.parametrize("pos,window,rows", [(0, 0, 2), (1, 0, 2), (255, 0, 2), (256, 0, 2),
+                                             (700, 0, 2), (4095, 0, 2), (4095, 512, 2),
+                                             (511, 512, 2), (512, 512, 2), (1000, 512, 2),
+                                             (4095, 0, 5), (4095, 0, 7)])
+def test_attention_decode(gpu, pos, window, rows):
+    print(f"attention pos={pos} window={window} rows={rows}", flush=True)
     L = gpu.lib()
-    rng = np.random.default_rng(pos * 3 + window)
-    rows, heads, hd = 2, 8, 256
+    rng = np.random.default_rng(pos * 3 + window + 1000 * (rows - 2))
+    heads, hd = 8, 256
     cap = max(pos + 1, 300)
     q = (rng.standard_normal((rows, heads, hd)) * 0.25).astype(np.float32)
     kv = rng.uniform(-1.7, 1.7, (rows, 2, cap, hd)).astype(np.float32)
@@ -306,15 +311,18 @@ def check_step(got, want, dev_kv, ref_kv):
 
 # batch 1: the streaming plans with carried joins; 3: the small-M kernel on 16-row tiles; 20 and
 # 32: on 32-row tiles, with the gelu-mul epilogues on 16-wave (FFN 1024: 64 blocks) and 4-wave
-# (FFN 6144: 384 blocks) grids
-@pytest.mark.parametrize("batch,ffn", [(1, 1024), (3, 1024), (20, 1024), (32, 6144)])
-def test_decode_step_tiny(gpu, batch, ffn):
-    print(f"decode tiny batch={batch} ffn={ffn}", flush=True)
+# (FFN 6144: 384 blocks) grids. Attention grids (chunks x batch): two halves with K staged in LDS
+# up to 256 blocks, K staged up to 768 (batch 20 and 32 at position 700: 22 x 32 = 704), and the
+# per-lane K segments beyond (batch 32 at position 1000: 32 x 32 = 1024).
+@pytest.mark.parametrize("batch,ffn,pos0", [(1, 1024, 700), (3, 1024, 700), (20, 1024, 700),
+                                            (32, 6144, 700), (32, 1024, 1000)])
+def test_decode_step_tiny(gpu, batch, ffn, pos0):
+    print(f"decode tiny batch={batch} ffn={ffn} pos0={pos0}", flush=True)
     shape = tiny_shape(batch, ffn=ffn)
     rng = np.random.default_rng(batch)
     extra = [int(t) for t in rng.integers(0, 3000, max(0, batch - 3))]
     toks = [([5, 2999, 1234] + extra)[:batch], ([7, 0, 1] + extra[::-1])[:batch]]
-    for got, want, dkv, rkv in run_steps(gpu, shape, toks, pos0=700):
+    for got, want, dkv, rkv in run_steps(gpu, shape, toks, pos0=pos0):
         check_step(got, want, dkv, rkv)
         if "next" in got:
             print("next tokens", got["next"], flush=True)

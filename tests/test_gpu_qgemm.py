@@ -177,3 +177,8 @@ def test_short_k_and_odd_n(gpu, oracle, bits, m, n, k):
     o32 = out_buf(gpu, (m, n), np.int32)
     gpu.qgemm(bits, dev(gpu, w), dev(gpu, s), dev(gpu, x), o32, k, n, m, 0.05, 0.1)
     assert np.array_equal(o32.download(), acc)
+    # the same rows as int8 codes: the tile path reads them in natural order, with no snap pass
+    xq = np.clip(np.rint(x.astype(np.float32) / np.float32(0.05)), -128, 127).astype(np.int8)
+    o32.fill(0x7B)
+    gpu.qgemm(bits, dev(gpu, w), dev(gpu, s), dev(gpu, xq), o32, k, n, m, 0.05, 0.1)
+    assert np.array_equal(o32.download(), acc)
