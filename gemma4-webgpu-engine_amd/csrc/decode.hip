@@ -36,10 +36,22 @@ static_assert(kDecThreads == kRowThreads, "the glue kernels run the shared 256-l
 
 // ---- rms-norm / norm-residual / norm-residual-norm --------------------------------------------------
 
-// One block per row (rms_join_row).
+// One block per row (rms_join_row). ACC: the source is split accumulators (load_acc).
+template <bool ACC>
 __global__ __launch_bounds__(kDecThreads) void join_kernel(JoinTail J) {
     __shared__ float lds[2 * kDecThreads];
-    rms_join_row(J, blockIdx.x, lds);
+    rms_join_row<ACC>(J, blockIdx.x, lds);
+}
+
+int join_acc(const JoinTail &J, int rows, hipStream_t stream) {
+    if (J.src_kind != G4_KIND_I32 || !J.src || !J.acc_scales || J.acc_splits < 1 ||
+        J.acc_splits > kSplitAccMax || rows <= 0 || J.width <= 0 ||
+        J.width > kJoinMaxPer * kDecThreads || J.src_scale == 0.0f || !J.codes ||
+        J.in_scale == 0.0f)
+        return set_error(G4_ERR_INVALID, "join over split accumulators: bad arguments");
+    hipLaunchKernelGGL((join_kernel<true>), dim3(rows), dim3(kDecThreads), 0, stream, J);
+    G4_LAUNCHED("join_kernel");
+    return G4_OK;
 }
 
 // ---- q-norm-rope and kv-norm-rope-store ----------------------------------------------------------
@@ -695,7 +707,7 @@ int g4_rms_join(const void *src, int src_kind, float src_scale, const float *gai
     J.in_scale = in_scale;
     J.hidden = hidden;
     J.codes = codes;
-    hipLaunchKernelGGL(join_kernel, dim3(rows), dim3(kDecThreads), 0, as_stream(stream), J);
+    hipLaunchKernelGGL((join_kernel<false>), dim3(rows), dim3(kDecThreads), 0, as_stream(stream), J);
     G4_LAUNCHED("join_kernel");
     return G4_OK;
 }

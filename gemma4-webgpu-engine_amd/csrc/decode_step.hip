@@ -75,6 +75,9 @@ struct g4_decode {
            *kc = nullptr, *vc = nullptr, *attn_codes = nullptr, *oc = nullptr, *gc = nullptr,
            *uc = nullptr, *act = nullptr, *dc = nullptr, *pgc = nullptr, *pac = nullptr,
            *ppc = nullptr, *head_codes = nullptr;
+    // batch 3..32: down_proj runs as kAccSplits K ranges of int32 accumulators, summed by the
+    // post-FFN join (null when down is one launch)
+    int32_t *acc = nullptr;
     std::vector<float *> kv;  // per producer: [batch][2][capacity][head_dim]
     int stop = -1;
     // M = 1 GEMV plans per layer: qkv (or q), o, gate+up, down, ple gate, ple projection.
@@ -238,6 +241,29 @@ JoinTail make_join(g4_decode &d, int k, const void *src, int src_kind, float src
     return j;
 }
 
+// down_proj over two K ranges, each range's blocks a grid of their own: at batch 32 the E2B
+// shape's 96 column blocks each walked K = 6144 as two LDS chunks one after the other (18 us);
+// split, 192 blocks take one chunk each and the join adds the two exact int32 partials (step
+// 4.25 -> 4.08 ms). o_proj (K = 2048, one chunk) split the same way measured no faster at batch
+// 32 and slower at batch 3.
+constexpr int kAccSplits = 2;
+static_assert(kAccSplits <= kSplitAccMax, "the join sums at most kSplitAccMax partials");
+
+bool acc_split(const g4_decode_shape &s) {
+    return s.batch >= 3 && s.batch <= 32 && s.ffn % (kAccSplits * 128) == 0 &&
+           kAccSplits * ((s.hidden + 15) / 16) <= device_cu_count();
+}
+
+// Join j reads the split accumulators of the linear (scales, in_scale) in place of its codes.
+void join_from_acc(const g4_decode &d, JoinTail &j, const float *scales) {
+    j.src = d.acc;
+    j.src_kind = G4_KIND_I32;
+    j.acc_scales = scales;
+    j.acc_in_scale = d.s.in_scale;
+    j.acc_splits = kAccSplits;
+    j.acc_split_stride = (int64_t)d.s.batch * d.s.hidden;
+}
+
 void build_joins(g4_decode &d) {
     const g4_decode_shape &s = d.s;
     const float out = s.out_scale;
@@ -251,6 +277,7 @@ void build_joins(g4_decode &d) {
                                     1.0f, L.pre_ffn_norm, d.xcodes));
         d.joins.push_back(make_join(d, join_index(l, 1), d.dc, G4_KIND_I8, out, L.post_ffn_norm,
                                     1.0f, nullptr, d.xcodes));
+        if (d.acc) join_from_acc(d, d.joins.back(), L.down_s);
         d.joins.push_back(make_join(d, join_index(l, 2), d.ppc, G4_KIND_I8, out, L.post_ple_norm,
                                     L.layer_scalar, last ? d.w.final_norm : d.layers[l + 1].input_norm,
                                     last ? d.head_codes : d.xcodes));
@@ -270,6 +297,7 @@ int carry_join(g4_decode &d, int k, const Plan &plan) {
 int run_join(g4_decode &d, int k, void *st) {
     if (d.carried[k]) return G4_OK;
     const JoinTail &j = d.joins[k];
+    if (j.src_kind == G4_KIND_I32) return join_acc(j, d.s.batch, as_stream(st));
     return g4_rms_join(j.src, j.src_kind, j.src_scale, j.gain, j.resid, j.alpha, j.gain2, d.s.batch,
                        j.width, j.eps, j.in_scale, j.hidden, j.codes, st);
 }
@@ -308,6 +336,8 @@ int build(g4_decode &d) {
     G4_TRY(i8(&d.pac, (size_t)B * s.ple_dim));
     G4_TRY(i8(&d.ppc, (size_t)B * H));
     G4_TRY(i8(&d.head_codes, (size_t)B * H));
+    if (acc_split(s))
+        G4_TRY(m.get((void **)&d.acc, (size_t)kAccSplits * B * H * sizeof(int32_t)));
     const size_t cache = (size_t)B * 2 * s.kv_capacity * s.head_dim;
     d.kv.assign(s.kv_producers, nullptr);
     for (int p = 0; p < s.kv_producers; ++p) {
@@ -447,7 +477,11 @@ int run_layer(g4_decode &d, int l, void *st) {
             G4_TRY(g4_gelu_mul(d.gc, out, d.uc, out, nullptr, 0, B, F, in, d.act, st));
         }
     }
-    G4_TRY(run_linear_rows(d, plan(P_DOWN), desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out), st));
+    if (d.acc)
+        G4_TRY(linear_split_acc(4, static_cast<const uint8_t *>(L.down), L.down_s, d.act, F, H, B,
+                                kAccSplits, d.acc, as_stream(st)));
+    else
+        G4_TRY(run_linear_rows(d, plan(P_DOWN), desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out), st));
     G4_TRY(run_join(d, join_index(l, 1), st));
     // per-layer-input block: the gate (with gelu times the layer's row folded when planned), then
     // per_layer_projection

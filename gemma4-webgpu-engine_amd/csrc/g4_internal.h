@@ -80,7 +80,26 @@ struct JoinTail {
     float in_scale = 0.0f;
     float *hidden = nullptr;
     int8_t *codes = nullptr;
+    // src_kind G4_KIND_I32 (join_acc): src holds acc_splits int32 partial accumulators of the
+    // producing linear, split s at src + s * acc_split_stride, each laid out [row][width]; their
+    // sum is the linear's exact accumulator, and element i is the linear's int8 output code
+    // snap(f32(acc_in_scale * acc_scales[i]) * f32(sum)) on src_scale, times src_scale
+    const float *acc_scales = nullptr;
+    float acc_in_scale = 0.0f;
+    int acc_splits = 0;
+    int64_t acc_split_stride = 0;
 };
+
+constexpr int kSplitAccMax = 4;
+
+// The small-M MFMA kernel over K split in `splits` equal ranges (k a multiple of splits * 128,
+// 3 <= m <= 32, int8 codes in): part[s][m][n] = the int32 accumulator of range s (zero point
+// included), for a consumer that sums them (join_acc).
+int linear_split_acc(int bits, const uint8_t *wq, const float *scales, const int8_t *x, int k,
+                     int n, int m, int splits, int32_t *part, hipStream_t stream);
+
+// The RMS join of `rows` rows over a JoinTail whose src holds split accumulators (src_kind int32).
+int join_acc(const JoinTail &J, int rows, hipStream_t stream);
 
 // Makes the RMS join `j` the prologue of a plan (the decode runner's launch fold, no reference
 // counterpart): every projection of the plan reads j.codes (at one bit width), and takes them

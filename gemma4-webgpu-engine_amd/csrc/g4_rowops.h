@@ -53,7 +53,19 @@ __device__ __forceinline__ int8_t snap_code(float v, float s) { return (int8_t)s
 // J.hidden is set), and emit(i, code) for every element i < width with the code of either the
 // second norm of hidden (gain2 given) or of hidden itself, snapped on in_scale (when J.codes is
 // set). lds: 512 floats (the two reductions take one half each).
-template <typename Emit>
+// The value of element i (flat index idx) of a join over split accumulators: the producing
+// linear's epilogue f32(in_scale * scale) * f32(acc), its int8 snap, dequantized by the join.
+__device__ __forceinline__ float load_acc(const JoinTail &J, int64_t idx, int i) {
+    const int32_t *p = reinterpret_cast<const int32_t *>(J.src) + idx;
+    int acc = 0;
+#pragma unroll
+    for (int s = 0; s < kSplitAccMax; ++s)
+        if (s < J.acc_splits) acc += p[s * J.acc_split_stride];
+    const float y = __fmul_rn(__fmul_rn(J.acc_in_scale, J.acc_scales[i]), (float)acc);
+    return __fmul_rn((float)snap_code(y, J.src_scale), J.src_scale);
+}
+
+template <bool ACC = false, typename Emit>
 __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row, float *lds,
                                                   Emit emit) {
     const int t = threadIdx.x;
@@ -66,7 +78,10 @@ __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row
     for (int e = 0; e < kJoinMaxPer; ++e) {
         const int i = t + e * kRowThreads;
         const bool in = i < width;
-        v[e] = in ? load_val(J.src, J.src_kind, J.src_scale, base + i) : 0.0f;
+        if (ACC)
+            v[e] = in ? load_acc(J, base + i, i) : 0.0f;
+        else
+            v[e] = in ? load_val(J.src, J.src_kind, J.src_scale, base + i) : 0.0f;
         ga[e] = in && J.gain ? J.gain[i] : 1.0f;
         re[e] = in && J.resid ? J.resid[base + i] : 0.0f;
         g2[e] = in && J.gain2 ? J.gain2[i] : 0.0f;
@@ -109,10 +124,11 @@ __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row
 }
 
 // The join kernel's form: codes to J.codes[row][i]. lds: 512 floats.
+template <bool ACC = false>
 __device__ __forceinline__ void rms_join_row(const JoinTail &J, int64_t row, float *lds) {
     int8_t *codes = J.codes;
     const int64_t base = row * J.width;
-    rms_join_row_emit(J, row, lds, [=](int i, int8_t c) { codes[base + i] = c; });
+    rms_join_row_emit<ACC>(J, row, lds, [=](int i, int8_t c) { codes[base + i] = c; });
 }
 
 }  // namespace g4

@@ -165,7 +165,7 @@ template <int MT, int WAVES> constexpr int small_kc() { return (WAVES >= 16 ? 98
 template <int BITS, int MT, int WAVES, int EPI>
 __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
     const void *__restrict__ x, int x_kind, SmallJobs jobs, int M, int K, float in_scale,
-    float out_scale, int out_kind) {
+    float out_scale, int out_kind, int ksplit) {
     constexpr int THREADS = WAVES * 64;
     constexpr int TM = MT / 16;
     constexpr int KC = small_kc<MT, WAVES>();  // codes of a row per LDS chunk
@@ -211,8 +211,12 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
     for (int t = 0; t < NACC; ++t) acc[t] = v4i{0, 0, 0, 0};
     const v4i ones = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};
 
-    for (int kc0 = 0; kc0 < K; kc0 += KC) {
-        const int kcn = min(KC, K - kc0);
+    // ksplit > 0: block z takes codes [z ksplit, (z + 1) ksplit) of K and stores its int32 partial
+    // accumulator (out_kind int32) to dst[z][M][N]; the splits' sum is the exact accumulator
+    const int kbeg = ksplit > 0 ? (int)blockIdx.z * ksplit : 0;
+    const int kend = ksplit > 0 ? min(K, kbeg + ksplit) : K;
+    for (int kc0 = kbeg; kc0 < kend; kc0 += KC) {
+        const int kcn = min(KC, kend - kc0);
         const int gpr = kcn >> 3;  // 8-code groups per row in this chunk
         lds_barrier();  // the previous chunk's codes are no longer read
         // the snap: each thread issues the loads of SB groups (indices clamped, so every load is
@@ -377,7 +381,7 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
         } else if (out_kind == G4_KIND_I8) {
             reinterpret_cast<int8_t *>(dst)[o] = (int8_t)srq_code_fast(yv, out_scale, orcp, o_ok);
         } else if (out_kind == G4_KIND_I32) {
-            reinterpret_cast<int32_t *>(dst)[o] = v;
+            reinterpret_cast<int32_t *>(dst)[o + (int64_t)blockIdx.z * M * N] = v;
         } else {
             float f = yv;
             if (out_scale != 0.0f) f = __fmul_rn(srq_code_fast(yv, out_scale, orcp, o_ok), out_scale);
@@ -779,14 +783,16 @@ static const char *choice_name(KernelChoice c, int bits) {
 // faster), else 4.
 template <int BITS, int MT, int EPI>
 static void launch_small_t(const void *x, int x_kind, const SmallJobs &jobs, int m, int k,
-                           float in_scale, float out_scale, int out_kind, hipStream_t stream) {
-    const dim3 grid(jobs.block_end[jobs.count - 1], (m + MT - 1) / MT);
-    if ((int64_t)grid.x * grid.y <= device_cu_count())
+                           float in_scale, float out_scale, int out_kind, hipStream_t stream,
+                           int splits = 1) {
+    const int ksplit = splits > 1 ? k / splits : 0;
+    const dim3 grid(jobs.block_end[jobs.count - 1], (m + MT - 1) / MT, splits);
+    if ((int64_t)grid.x * grid.y * grid.z <= device_cu_count())
         hipLaunchKernelGGL((qgemm_small_kernel<BITS, MT, 16, EPI>), grid, dim3(1024), 0, stream, x,
-                           x_kind, jobs, m, k, in_scale, out_scale, out_kind);
+                           x_kind, jobs, m, k, in_scale, out_scale, out_kind, ksplit);
     else
         hipLaunchKernelGGL((qgemm_small_kernel<BITS, MT, 4, EPI>), grid, dim3(256), 0, stream, x,
-                           x_kind, jobs, m, k, in_scale, out_scale, out_kind);
+                           x_kind, jobs, m, k, in_scale, out_scale, out_kind, ksplit);
 }
 
 // epi: 0 plain (any job count), 1 the paired gate/up gelu epilogue (4-bit), 2 the f32-vector one.
@@ -805,6 +811,31 @@ static int launch_small(int bits, int mt, int epi, const void *x, int x_kind, co
     else if (mt == 16) G4_SMALL(8, 16, 0);
     else G4_SMALL(8, 32, 0);
 #undef G4_SMALL
+    G4_LAUNCHED("qgemm_small_kernel");
+    return G4_OK;
+}
+
+int linear_split_acc(int bits, const uint8_t *wq, const float *scales, const int8_t *x, int k,
+                     int n, int m, int splits, int32_t *part, hipStream_t stream) {
+    if (!wq || !scales || !x || !part || m < 3 || m > 32 || n <= 0 || splits < 2 ||
+        splits > kSplitAccMax || k % (splits * kTileBK))
+        return set_error(G4_ERR_INVALID, "split accumulators: bad arguments (m %d, k %d, splits %d)",
+                         m, k, splits);
+    SmallJobs jobs{};
+    jobs.w[0] = wq;
+    jobs.scales[0] = scales;
+    jobs.dst[0] = part;
+    jobs.n[0] = n;
+    jobs.block_end[0] = (n + 15) / 16;
+    jobs.count = 1;
+    if (bits == 4 && m <= 16)
+        launch_small_t<4, 16, 0>(x, G4_KIND_I8, jobs, m, k, 1.0f, 0.0f, G4_KIND_I32, stream, splits);
+    else if (bits == 4)
+        launch_small_t<4, 32, 0>(x, G4_KIND_I8, jobs, m, k, 1.0f, 0.0f, G4_KIND_I32, stream, splits);
+    else if (m <= 16)
+        launch_small_t<8, 16, 0>(x, G4_KIND_I8, jobs, m, k, 1.0f, 0.0f, G4_KIND_I32, stream, splits);
+    else
+        launch_small_t<8, 32, 0>(x, G4_KIND_I8, jobs, m, k, 1.0f, 0.0f, G4_KIND_I32, stream, splits);
     G4_LAUNCHED("qgemm_small_kernel");
     return G4_OK;
 }
