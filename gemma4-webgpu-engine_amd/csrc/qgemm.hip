@@ -160,7 +160,10 @@ struct SmallJobs {
     float act_scale;
 };
 
-template <int MT, int WAVES> constexpr int small_kc() { return (WAVES >= 16 ? 98304 : 32768) / MT; }
+// Codes of a row per LDS chunk: 3072 (16-wave blocks) or 1536 (4-wave) at MT = 32, so the E2B
+// shape's K = 1536 projections take one chunk (the gate / up pair at batch 32: two 1024-code
+// chunks measured a 4.09 ms step, one chunk 4.01 ms).
+template <int MT, int WAVES> constexpr int small_kc() { return (WAVES >= 16 ? 98304 : 49152) / MT; }
 
 template <int BITS, int MT, int WAVES, int EPI>
 __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
