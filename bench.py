@@ -473,7 +473,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "qgemv_stream_kernel<true, false> (plan launch, 245 projections)",
+            "kernel": "qgemv_stream_kernel<true, 0> (plan launch, 245 projections)",
             "achieved": round(value, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -175,6 +175,16 @@ int stream_try_launch(const g4_gemv_desc *descs, const GeluAct *acts, int count,
 // The streaming shape class of a row of K codes at `bits`, or -1 (qgemv_stream.hip).
 int stream_class_for(int bits, int k);
 
+// Releases the GEMM workspace of a stream about to be destroyed (qgemm.hip, g4_workspace.h).
+int workspace_forget_stream(void *stream);
+
+// g4_qgemm with the caller's buffer for the snapped activation codes in place of the stream's
+// workspace (codes_bytes bytes; refused when the call's path needs more). Allocates nothing.
+int qgemm_given_codes(int bits, const void *wq, const float *scales, const void *x, int x_kind,
+                      void *dst, int out_kind, int k, int num_rows, int m_cols, float in_scale,
+                      float out_scale, void *stream, int8_t *codes, size_t codes_bytes,
+                      const char *who);
+
 // ---- device: the static range quantization arithmetic (src/quant.ts:248-357) -----------------
 
 // srqCodes at 8 bits: clamp(RNE(f32(v / s)), -128, 127). __fdiv_rn is the IEEE binary32 divide;

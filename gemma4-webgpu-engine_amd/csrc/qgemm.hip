@@ -22,11 +22,10 @@
 //                  qgemm_tile_kernel: 64 x 96 output tiles, activation codes and weights streamed
 //                  global -> LDS by direct loads through a 3-4 stage ring, XCD-aware tile order.
 #include "g4_internal.h"
+#include "g4_workspace.h"
 
 #include <algorithm>
-#include <map>
-#include <mutex>
-#include <utility>
+#include <string>
 
 namespace g4 {
 
@@ -91,6 +90,49 @@ __global__ void srq_quantize_kernel(const void *x, int x_kind, int8_t *codes, in
     const float r = srq_recip(s, r_ok);
     for (int64_t e = i; e < n; e += stride)
         codes[e] = (int8_t)srq_code_fast(load_act(x, x_kind, e), s, r, r_ok);
+}
+
+// qmatmul-8bit on its uncalibrated path (inScale 0; pleMatmul.ts:139-147, oracle :212-222): one
+// thread per (row, token column), a serial loop over the row's 4-code words. Each word's four
+// products are summed in order starting from 0, then added to the accumulator, every step one f32
+// rounding; the closing multiply is f32(f32(1 * scale) * acc). The order is the reference's
+// definition, so nothing here may be reassociated: no FMA, no split of K across lanes. Each thread
+// reads 16 codes (one 16-byte load) per iteration; K % 16 == 0 is checked by the caller.
+template <bool F16>
+__global__ __launch_bounds__(256) void qmatmul8_serial_kernel(
+    const int8_t *wq, const float *scales, const void *x, void *dst, int out_kind, int k, int n,
+    float out_scale) {
+    const int row = blockIdx.x * 256 + threadIdx.x;
+    const int col = blockIdx.y;
+    if (row >= n) return;
+    const uint4 *w = reinterpret_cast<const uint4 *>(wq + (int64_t)row * k);
+    float acc = 0.0f;
+    for (int i = 0; i < k / 16; ++i) {
+        const uint4 ww = w[i];
+        const uint32_t words[4] = {ww.x, ww.y, ww.z, ww.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t e = (int64_t)col * k + 16 * i + 4 * j;
+            float xs[4];
+            if (F16) {  // f16 activations widen exactly to the reference's f32
+                const __half2 *h = reinterpret_cast<const __half2 *>(reinterpret_cast<const __half *>(x) + e);
+                const float2 a = __half22float2(h[0]), b = __half22float2(h[1]);
+                xs[0] = a.x, xs[1] = a.y, xs[2] = b.x, xs[3] = b.y;
+            } else {
+                const float4 xv = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(x) + e);
+                xs[0] = xv.x, xs[1] = xv.y, xs[2] = xv.z, xs[3] = xv.w;
+            }
+            float d = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                d = __fadd_rn(d, __fmul_rn((float)(int8_t)((words[j] >> (8 * e)) & 0xff), xs[e]));
+            acc = __fadd_rn(acc, d);
+        }
+    }
+    const float sr = scales[row];
+    const float scale = isfinite(sr) ? sr : 0.0f;
+    const float y = __fmul_rn(__fmul_rn(1.0f, scale), acc);
+    store_linear_out(dst, (int64_t)col * n + row, out_kind, y, 0, out_scale);
 }
 
 // The B operand of one 16x16x64 step from 8 bytes (16 codes) of weights at `p`.
@@ -724,40 +766,55 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(
 
 // ---- per-stream workspace for the snapped activation codes ------------------------------------
 
-struct Workspace {
-    void *ptr = nullptr;
-    size_t bytes = 0;
-};
+namespace {
 
-static std::mutex g_ws_mu;
-static std::map<std::pair<int, void *>, Workspace> g_ws;
+int ws_alloc(void **p, size_t bytes) { return hipMalloc(p, bytes) != hipSuccess; }
+int ws_release(void *p) { return hipFree(p) != hipSuccess; }
+int ws_drain(void *s) { return hipStreamSynchronize(as_stream(s)) != hipSuccess; }
+int ws_capturing(void *s, bool *yes) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(as_stream(s), &st) != hipSuccess) return 1;
+    *yes = st != hipStreamCaptureStatusNone;
+    return 0;
+}
 
-// Returns a device buffer of at least `bytes` owned by (device, stream). Calls on one stream are
-// ordered, so they may share it; calls on different streams get different buffers.
+WorkspaceCache &ws_cache() {
+    static WorkspaceCache cache(WorkspaceOps{ws_alloc, ws_release, ws_drain, ws_capturing});
+    return cache;
+}
+
+}  // namespace
+
+// A device buffer of at least `bytes` owned by (device, stream), under the rules of
+// g4_workspace.h: never grown inside a capture, never freed while a captured graph may hold it.
 static int workspace(void *stream, size_t bytes, void **out) {
     int dev = 0;
     G4_HIP(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    Workspace &ws = g_ws[{dev, stream}];
-    if (ws.bytes < bytes) {
-        if (ws.ptr) {
-            G4_HIP(hipStreamSynchronize(as_stream(stream)));
-            G4_HIP(hipFree(ws.ptr));
-            ws.ptr = nullptr;
-            ws.bytes = 0;
-        }
-        size_t grow = std::max(bytes, (size_t)4 << 20);
-        G4_HIP(hipMalloc(&ws.ptr, grow));
-        ws.bytes = grow;
+    std::string err;
+    switch (ws_cache().get(dev, stream, bytes, out, &err)) {
+        case WorkspaceCache::kOk: return G4_OK;
+        case WorkspaceCache::kRefused: return set_error(G4_ERR_INVALID, "qgemm: %s", err.c_str());
+        default: return set_error(G4_ERR_HIP, "qgemm: %s", err.c_str());
     }
-    *out = ws.ptr;
+}
+
+int workspace_forget_stream(void *stream) {
+    int dev = 0;
+    G4_HIP(hipGetDevice(&dev));
+    if (ws_cache().forget_stream(dev, stream) != WorkspaceCache::kOk)
+        return set_error(G4_ERR_HIP, "stream destroy: draining the stream's workspace failed");
     return G4_OK;
 }
 
-enum KernelChoice { K_GEMV = 0, K_SKINNY16, K_SKINNY32, K_TILE128, K_GEMV_F32, K_GEMV_COLS };
+enum KernelChoice { K_GEMV = 0, K_SKINNY16, K_SKINNY32, K_TILE128, K_GEMV_F32, K_GEMV_COLS,
+                    K_SERIAL8 };
 
-static KernelChoice pick_kernel(int bits, int m, int n, int k, float in_scale) {
-    if (in_scale == 0.0f) return K_GEMV_F32;
+// gemm_mode: the caller named qgemm-4bit / qmatmul-8bit (execute.ts matmulKernel in gemm mode).
+// Uncalibrated qmatmul-8bit then keeps the reference's serial per-output order at any M; the
+// routed g4_linear is gemm mode only above two tokens (a decode step's 8-bit linear is qgemv-8bit,
+// execute.ts:372-375).
+static KernelChoice pick_kernel(int bits, int m, int n, int k, float in_scale, bool gemm_mode) {
+    if (in_scale == 0.0f) return bits == 8 && gemm_mode ? K_SERIAL8 : K_GEMV_F32;
     if (m <= 2) return K_GEMV;
     if (k % kTileBK != 0) return K_GEMV_COLS;
     // the small kernel snaps all of x in each 16-row block: past 32768 rows (the tied head) the
@@ -777,6 +834,7 @@ static const char *choice_name(KernelChoice c, int bits) {
         case K_SKINNY32: return bits == 4 ? "qgemm-4bit-mfma-small32" : "qmatmul-8bit-mfma-small32";
         case K_TILE128: return bits == 4 ? "qgemm-4bit-mfma-tile" : "qmatmul-8bit-mfma-tile";
         case K_GEMV_F32: return bits == 4 ? "qgemv-4bit-f32" : "qgemv-8bit-f32";
+        case K_SERIAL8: return "qmatmul-8bit-serial";
         default: return bits == 4 ? "qgemv-4bit-columns" : "qgemv-8bit-columns";
     }
 }
@@ -890,10 +948,33 @@ static int check_linear(int bits, const void *wq, const float *scales, const voi
     return G4_OK;
 }
 
+// Whether a call takes the tile kernel with f16 / f32 activations, which are snapped into a
+// buffer of M * K codes first (the only path of this file that needs memory beyond its operands).
+static bool needs_codes_buffer(int bits, int m, int n, int k, float in_scale, int x_kind,
+                               bool gemm_mode) {
+    return pick_kernel(bits, m, n, k, in_scale, gemm_mode) == K_TILE128 && x_kind != G4_KIND_I8;
+}
+
+// given_codes: a caller's buffer for the snapped codes (at least M * K bytes, checked by the
+// caller), or null for the stream's workspace.
 static int run_linear(int bits, const void *wq, const float *scales, const void *x, int x_kind,
                       void *dst, int out_kind, int k, int n, int m, float in_scale,
-                      float out_scale, hipStream_t stream, const char *who) {
-    const KernelChoice c = pick_kernel(bits, m, n, k, in_scale);
+                      float out_scale, hipStream_t stream, const char *who, bool gemm_mode = true,
+                      int8_t *given_codes = nullptr) {
+    const KernelChoice c = pick_kernel(bits, m, n, k, in_scale, gemm_mode);
+    if (c == K_SERIAL8) {
+        const dim3 grid((n + 255) / 256, m);
+        if (x_kind == G4_KIND_F16)
+            hipLaunchKernelGGL(qmatmul8_serial_kernel<true>, grid, dim3(256), 0, stream,
+                               reinterpret_cast<const int8_t *>(wq), scales, x, dst, out_kind, k, n,
+                               out_scale);
+        else
+            hipLaunchKernelGGL(qmatmul8_serial_kernel<false>, grid, dim3(256), 0, stream,
+                               reinterpret_cast<const int8_t *>(wq), scales, x, dst, out_kind, k, n,
+                               out_scale);
+        G4_LAUNCHED("qmatmul8_serial_kernel");
+        return G4_OK;
+    }
     if (c == K_GEMV || c == K_GEMV_F32 || c == K_GEMV_COLS)
         return gemv_columns(bits, wq, scales, x, x_kind, dst, out_kind, k, n, m, in_scale,
                             out_scale, stream, who);
@@ -918,9 +999,11 @@ static int run_linear(int bits, const void *wq, const float *scales, const void 
     const bool natural = x_kind == G4_KIND_I8;
     if (!natural) {
         const int kp = k;  // k % 128 == 0 on the MFMA kernels
-        void *ws = nullptr;
-        int rc = workspace(stream, (size_t)m * kp, &ws);
-        if (rc) return rc;
+        void *ws = given_codes;
+        if (!ws) {
+            int rc = workspace(stream, (size_t)m * kp, &ws);
+            if (rc) return rc;
+        }
         if (bits == 4)
             hipLaunchKernelGGL(quantize_rows_kernel<true>, dim3(m), dim3(kQuantThreads), 0, stream,
                                x, x_kind, k, kp, in_scale, reinterpret_cast<int8_t *>(ws));
@@ -948,7 +1031,7 @@ int linear_grouped(int bits, const void *x, int x_kind, int k, int m, float in_s
         int rc = check_linear(bits, o.wq, o.scales, x, x_kind, o.dst, out_kind, k, o.n, m, in_scale,
                               out_scale, who);
         if (rc) return rc;
-        const KernelChoice c = pick_kernel(bits, m, o.n, k, in_scale);
+        const KernelChoice c = pick_kernel(bits, m, o.n, k, in_scale, false);
         small &= c == K_SKINNY16 || c == K_SKINNY32;
     }
     if (!small) {  // one call each, through the library's routing
@@ -983,7 +1066,7 @@ int linear_gelu(int bits, const void *x, int k, int m, float in_scale, float out
     int rc = check_linear(bits, w_gate, s_gate, x, G4_KIND_I8, act, G4_KIND_I8, k, n, m, in_scale,
                           out_scale, who);
     if (rc) return rc;
-    const KernelChoice c = pick_kernel(bits, m, n, k, in_scale);
+    const KernelChoice c = pick_kernel(bits, m, n, k, in_scale, false);
     if ((c != K_SKINNY16 && c != K_SKINNY32) || k > 16384 || act_scale == 0.0f) return G4_OK;
     if (w_up ? (bits != 4 || !s_up || (reinterpret_cast<uintptr_t>(w_up) & 15)) : (!up_vec || up_stride < n))
         return set_error(G4_ERR_INVALID, "gelu linear: the up operand (4-bit paired rows with scales, "
@@ -1006,16 +1089,10 @@ int linear_gelu(int bits, const void *x, int k, int m, float in_scale, float out
     return rc;
 }
 
-}  // namespace g4
-
-using namespace g4;
-
-extern "C" {
-
-// qgemm-4bit (qgemm.ts:589-639) and qmatmul-8bit (pleMatmul.ts:257-303).
-int g4_qgemm(int bits, const void *wq, const float *scales, const void *x, int x_kind, void *dst,
-             int out_kind, int k, int num_rows, int m_cols, float in_scale, float out_scale,
-             void *stream) {
+// The bind-time refusals of qgemm-4bit (qgemm.ts:589-639) and qmatmul-8bit (pleMatmul.ts:257-303).
+static int check_qgemm(int bits, const void *wq, const float *scales, const void *x, int x_kind,
+                       void *dst, int out_kind, int k, int num_rows, int m_cols, float in_scale,
+                       float out_scale) {
     const char *who = bits == 4 ? "qgemm-4bit" : "qmatmul-8bit";
     if (bits == 4) {
         if (k <= 0 || num_rows <= 0 || m_cols <= 0)
@@ -1038,23 +1115,65 @@ int g4_qgemm(int bits, const void *wq, const float *scales, const void *x, int x
     } else {
         return set_error(G4_ERR_INVALID, "qgemm: bits must be 4 or 8, got %d", bits);
     }
-    int rc = check_linear(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols,
-                          in_scale, out_scale, who);
-    if (rc) return rc;
-    return run_linear(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols, in_scale,
-                      out_scale, as_stream(stream), who);
+    return check_linear(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols, in_scale,
+                        out_scale, who);
 }
 
+// g4_qgemm with the snapped-codes buffer supplied by the caller (codes_bytes bytes at `codes`):
+// nothing is allocated. A call whose path needs more codes than that is refused.
+int qgemm_given_codes(int bits, const void *wq, const float *scales, const void *x, int x_kind,
+                      void *dst, int out_kind, int k, int num_rows, int m_cols, float in_scale,
+                      float out_scale, void *stream, int8_t *codes, size_t codes_bytes,
+                      const char *who) {
+    int rc = check_qgemm(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols, in_scale,
+                         out_scale);
+    if (rc) return rc;
+    if (needs_codes_buffer(bits, m_cols, num_rows, k, in_scale, x_kind, true)) {
+        const size_t need = (size_t)m_cols * (size_t)k;
+        if (!codes || need > codes_bytes)
+            return set_error(G4_ERR_INVALID,
+                             "%s: M * K = %zu activation codes exceed the %zu-byte scratch buffer "
+                             "(pass int8 codes already snapped, or a smaller M)",
+                             who, need, codes_bytes);
+    }
+    return run_linear(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols, in_scale,
+                      out_scale, as_stream(stream), bits == 4 ? "qgemm-4bit" : "qmatmul-8bit", true,
+                      codes);
+}
+
+}  // namespace g4
+
+using namespace g4;
+
+extern "C" {
+
+// qgemm-4bit (qgemm.ts:589-639) and qmatmul-8bit (pleMatmul.ts:257-303).
+int g4_qgemm(int bits, const void *wq, const float *scales, const void *x, int x_kind, void *dst,
+             int out_kind, int k, int num_rows, int m_cols, float in_scale, float out_scale,
+             void *stream) {
+    int rc = check_qgemm(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols, in_scale,
+                         out_scale);
+    if (rc) return rc;
+    return run_linear(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols, in_scale,
+                      out_scale, as_stream(stream), bits == 4 ? "qgemm-4bit" : "qmatmul-8bit", true);
+}
+
+// execute.ts:372-430: a step over more than two tokens is gemm mode (qgemm-4bit / qmatmul-8bit),
+// one or two tokens the decode GEMV family (qgemv-4/8bit, -m2).
 int g4_linear(int bits, const void *wq, const float *scales, const void *x, int x_kind, void *dst,
               int out_kind, int k, int num_rows, int m_cols, float in_scale, float out_scale,
               void *stream) {
-    return g4_qgemm(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols, in_scale,
-                    out_scale, stream);
+    int rc = check_qgemm(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols, in_scale,
+                         out_scale);
+    if (rc) return rc;
+    return run_linear(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols, in_scale,
+                      out_scale, as_stream(stream), bits == 4 ? "qgemm-4bit" : "qmatmul-8bit",
+                      m_cols > 2);
 }
 
 int g4_kernel_for_shape(int bits, int m_cols, int num_rows, int k, char *buf, size_t buf_len) {
     if (!buf || buf_len == 0) return set_error(G4_ERR_INVALID, "g4_kernel_for_shape: no buffer");
-    const KernelChoice c = pick_kernel(bits, m_cols, num_rows, k, 1.0f);
+    const KernelChoice c = pick_kernel(bits, m_cols, num_rows, k, 1.0f, true);
     const char *name = choice_name(c, bits);
     if (c == K_GEMV && m_cols == 1 && stream_class_for(bits, k) >= 0)
         name = bits == 4 ? "qgemv-4bit-stream" : "qgemv-8bit-stream";

@@ -140,8 +140,12 @@ int g4_stream_create(void **stream) {
 }
 
 int g4_stream_destroy(void *stream) {
-    if (stream) G4_HIP(hipStreamDestroy(as_stream(stream)));
-    return G4_OK;
+    if (!stream) return G4_OK;
+    // the stream's GEMM workspace goes with it (freed, or kept when a captured graph holds it), so
+    // a later stream that reuses the handle does not inherit it
+    int rc = workspace_forget_stream(stream);
+    G4_HIP(hipStreamDestroy(as_stream(stream)));
+    return rc;
 }
 
 int g4_stream_synchronize(void *stream) {
@@ -209,7 +213,10 @@ int g4_graph_launch(void *graph_exec, void *stream) {
 }
 
 int g4_graph_destroy(void *graph_exec) {
-    if (graph_exec) G4_HIP(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph_exec)));
+    if (!graph_exec) return G4_OK;
+    // the exec may still be running from its last launch (on any stream): finish it first
+    G4_HIP(hipDeviceSynchronize());
+    G4_HIP(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph_exec)));
     return G4_OK;
 }
 

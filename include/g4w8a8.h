@@ -79,8 +79,12 @@ int g4_event_elapsed_ms(float *ms, void *start, void *end);
 /* HIP graphs: capture a sequence of enqueues on `stream` once, replay it with one launch. The
  * decode loop is launch-bound (a launch costs microseconds of host time, more than a small GEMV
  * runs); the reference caches its per-token encode the same way (runtime.ts:702-767). Kernels of
- * this library never allocate or memset inside a capture; g4_qgemm/g4_linear with M > 2 need their
- * workspace to exist first (run the same shape once on the stream before capturing). */
+ * this library never allocate or memset inside a capture. g4_qgemm / g4_linear with f16 or f32
+ * activations at M > 32 snap them into a per-stream workspace: it must already be large enough when
+ * the capture starts (run the same shape once on the stream first); a call that would grow it
+ * inside a capture is refused with G4_ERR_INVALID. A workspace whose address a capture took is never
+ * freed (a graph may be replayed later, on any stream); g4_stream_destroy frees the stream's
+ * workspace otherwise. g4_graph_destroy waits for the device before it destroys the graph. */
 int g4_graph_begin_capture(void *stream);
 int g4_graph_end_capture(void *stream, void **graph_exec);
 int g4_graph_launch(void *graph_exec, void *stream);
@@ -104,6 +108,10 @@ int g4_qgemv(int bits, const void *wq, const float *scales, const void *x, int x
  * Replaces bindGemm (src/kernels/qgemm.ts:589-639; entries :641, :717, :725) and bindQmatmul8
  * (src/kernels/pleMatmul.ts:257-303; entry :323). bits 4 needs K % 256 == 0 (qgemm.ts:598-600);
  * bits 8 needs K % 4 == 0 (pleMatmul.ts:266-271). The calibrated path runs on int8 MFMA.
+ * Uncalibrated qmatmul-8bit (bits 8, inScale 0) keeps the reference's serial per-output f32 order at
+ * every M (pleMatmul.ts:139-147, oracle :212-222): one thread per output, each 4-code word summed
+ * in order from 0, then added to the accumulator. Uncalibrated bits 4 is the f32 code dot of
+ * qgemv-4bit per column.
  */
 int g4_qgemm(int bits, const void *wq, const float *scales, const void *x, int x_kind, void *dst,
              int out_kind, int k, int num_rows, int m_cols, float in_scale, float out_scale,
@@ -112,7 +120,8 @@ int g4_qgemm(int bits, const void *wq, const float *scales, const void *x, int x
 /*
  * The execute.ts routing (src/execute.ts:372-430 matmulKernel/gemvWide/pleKernel) folded into one
  * call: picks the kernel for (bits, M, N, K) on this GPU. M <= 2 -> the GEMV family, larger M ->
- * the MFMA GEMM. Same arguments as g4_qgemm.
+ * the MFMA GEMM. Same arguments as g4_qgemm. M <= 2 is the decode GEMV's mode: an uncalibrated
+ * 8-bit call there is qgemv-8bit's f32 path (execute.ts:372-375), above two tokens qmatmul-8bit's.
  */
 int g4_linear(int bits, const void *wq, const float *scales, const void *x, int x_kind, void *dst,
               int out_kind, int k, int num_rows, int m_cols, float in_scale, float out_scale,

@@ -397,7 +397,7 @@ def test_decode_graph_replay(gpu):
         assert same(le, lg)
 
 
-@pytest.mark.parametrize("batch", [1, 3])
+@pytest.mark.parametrize("batch", [1, 3, 32])
 def test_decode_step_e2b_full(gpu, batch):
     """BASELINE config 4 at its real shape: 35 layers (15 KV producers), hidden 1536, FFN 6144,
     8 query heads over one KV head of 256, tied int4 head over 262144 rows, a 4096-position seeded
@@ -417,7 +417,10 @@ def test_decode_step_e2b_full(gpu, batch):
     for p in range(shape.kv_producers):
         k, v = dec.download_kv(p)
         kv[p] = (k.copy(), v.copy())
-    toks = [1234, 262143, 7][:batch]
+    # batch 32 adds seeded ids over the whole vocabulary (the rows run different kernels than at
+    # batch 1 and 3: 16-wave small-M grids, split down_proj accumulators, the 64-row tile head)
+    toks = ([1234, 262143, 7] + [int(t) for t in np.random.default_rng(32).integers(
+        0, 262144, 29)])[:batch]
     nxt = gpu.DeviceBuffer.empty((batch,), np.int32)
     dec.set_position(pos)
     dec.step(dev(gpu, np.array(toks, np.int32)), nxt)
