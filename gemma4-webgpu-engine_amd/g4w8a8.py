@@ -138,6 +138,9 @@ SIGNATURES = {
                           _c_float, _c_float, _vp]),
     "g4_linear": (_c_int, [_c_int, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
                            _c_float, _c_float, _vp]),
+    "g4_qgemm_noalloc": (_c_int, [_c_int, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int,
+                                  _c_int, _c_float, _c_float, _vp]),
+    "g4_qgemm_noalloc_max_codes": (ctypes.c_size_t, []),
     "g4_kernel_for_shape": (_c_int, [_c_int, _c_int, _c_int, _c_int, ctypes.c_char_p,
                                      ctypes.c_size_t]),
     "g4_projection_batch": (_c_int, [_c_int, _c_int, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _vp,
@@ -398,6 +401,15 @@ def qgemm(bits, wq, scales, x, dst, k, num_rows, m_cols, in_scale=0.0, out_scale
                           x.kind if x_kind is None else x_kind, _ptr(dst),
                           dst.kind if out_kind is None else out_kind, k, num_rows, m_cols,
                           float(in_scale), float(out_scale), stream))
+
+
+def qgemm_noalloc(bits, wq, scales, x, dst, k, num_rows, m_cols, in_scale=0.0, out_scale=0.0,
+                  x_kind=None, out_kind=None, stream=None):
+    """g4_qgemm without any device allocation (a static scratch array; see include/g4w8a8.h)."""
+    _check(lib().g4_qgemm_noalloc(bits, _ptr(wq), _ptr(scales), _ptr(x),
+                                  x.kind if x_kind is None else x_kind, _ptr(dst),
+                                  dst.kind if out_kind is None else out_kind, k, num_rows, m_cols,
+                                  float(in_scale), float(out_scale), stream))
 
 
 def linear(bits, wq, scales, x, dst, k, num_rows, m_cols, in_scale=0.0, out_scale=0.0,

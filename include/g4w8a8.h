@@ -127,6 +127,21 @@ int g4_linear(int bits, const void *wq, const float *scales, const void *x, int 
               int out_kind, int k, int num_rows, int m_cols, float in_scale, float out_scale,
               void *stream);
 
+/*
+ * g4_qgemm for callers that cannot allocate device memory: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc. No counterpart in the reference. Same arguments,
+ * routing and results as g4_qgemm. The one buffer g4_qgemm needs beyond its operands (the snapped
+ * activation codes of the tile path: f16 / f32 x at M > 32, M * K bytes) is a static device array of
+ * g4_qgemm_noalloc_max_codes() bytes (8 MiB) that each GPU holds until the process ends; a call
+ * whose path needs more is refused with G4_ERR_INVALID before anything is enqueued. It calls no
+ * hipMalloc / hipFree. Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other host threads) race and must be ordered by the caller.
+ */
+int g4_qgemm_noalloc(int bits, const void *wq, const float *scales, const void *x, int x_kind,
+                     void *dst, int out_kind, int k, int num_rows, int m_cols, float in_scale,
+                     float out_scale, void *stream);
+size_t g4_qgemm_noalloc_max_codes(void);
+
 /* Name of the kernel g4_linear picks for a shape, written into buf (NUL terminated). */
 int g4_kernel_for_shape(int bits, int m_cols, int num_rows, int k, char *buf, size_t buf_len);
 
