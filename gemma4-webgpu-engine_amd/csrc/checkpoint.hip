@@ -718,6 +718,99 @@ int g4_st_upload(const g4_st *st, const char *name, void *device_dst, size_t dst
     return rc;
 }
 
+int g4_st_upload_split(const g4_st *st, const char *name, const g4_table_slice *slices,
+                       int num_slices, void *const *slice_dst, void *stream) {
+    if (!st || !name) return g4::set_error(G4_ERR_INVALID, "g4_st_upload_split: null argument");
+    if (num_slices < 1 || !slices || !slice_dst)
+        return g4::set_error(G4_ERR_INVALID, "BufferManager.declareSplit: %s needs at least one range",
+                             name);
+    const Entry *e = find_entry(st, name);
+    if (!e) return st_error("bad-entry", "tensor %s is not in this checkpoint", name);
+    // declareSplit (buffers.ts:291-327): the ranges partition the tensor in offset order
+    int64_t expect = 0;
+    for (int i = 0; i < num_slices; ++i) {
+        const g4_table_slice &r = slices[i];
+        if (r.byte_offset != expect)
+            return g4::set_error(G4_ERR_INVALID,
+                                 "BufferManager.declareSplit: %s slice %lld starts at %lld, not at "
+                                 "%lld; the ranges have to partition the tensor in offset order",
+                                 name, (long long)r.index, (long long)r.byte_offset,
+                                 (long long)expect);
+        if (r.byte_offset % 4 != 0)
+            return g4::set_error(G4_ERR_INVALID,
+                                 "BufferManager.declareSplit: %s slice %lld starts at %lld, which is "
+                                 "not four byte aligned", name, (long long)r.index,
+                                 (long long)r.byte_offset);
+        if (r.byte_length <= 0 || !slice_dst[i])
+            return g4::set_error(G4_ERR_INVALID, "g4_st_upload_split: %s slice %lld has no bytes or no buffer",
+                                 name, (long long)r.index);
+        expect += r.byte_length;
+    }
+    if (expect != e->byte_length)
+        return g4::set_error(G4_ERR_INVALID,
+                             "BufferManager.uploadWeight: %s is %lld bytes and the declared slices "
+                             "cover %lld, so a piece would fall outside every declared slice",
+                             name, (long long)e->byte_length, (long long)expect);
+    constexpr size_t kChunk = 64u << 20;
+    const int64_t total = e->byte_length;
+    void *pinned = nullptr;
+    const size_t cap = (size_t)std::min<int64_t>((int64_t)kChunk, total);
+    hipError_t err = hipHostMalloc(&pinned, cap, hipHostMallocDefault);
+    if (err != hipSuccess) return g4::hip_status(err, "g4_st_upload_split: hipHostMalloc");
+    int rc = G4_OK;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    for (int64_t piece = 0; piece < total && rc == G4_OK; piece += (int64_t)cap) {
+        const int64_t n = std::min<int64_t>((int64_t)cap, total - piece);
+        rc = g4_st_read(st, name, piece, pinned, (size_t)n);
+        if (rc) break;
+        // uploadSplitWeight (buffers.ts:384-423): the piece's intersection with each slice, rebased
+        for (int i = 0; i < num_slices && err == hipSuccess; ++i) {
+            const int64_t from = std::max(piece, slices[i].byte_offset);
+            const int64_t to = std::min(piece + n, slices[i].byte_offset + slices[i].byte_length);
+            if (to <= from) continue;
+            err = hipMemcpyAsync(reinterpret_cast<uint8_t *>(slice_dst[i]) + (from - slices[i].byte_offset),
+                                 reinterpret_cast<uint8_t *>(pinned) + (from - piece),
+                                 (size_t)(to - from), hipMemcpyHostToDevice, s);
+        }
+        if (err == hipSuccess) err = hipStreamSynchronize(s);  // the bounce buffer is reused
+        if (err != hipSuccess) rc = g4::hip_status(err, "g4_st_upload_split: copy");
+    }
+    (void)hipHostFree(pinned);
+    return rc;
+}
+
+int g4_st_plan_ple_split(const g4_st *st, const char *codes_name, int64_t groups_per_row,
+                         const g4_gather_limits *limits, g4_gather_split_plans *plans,
+                         g4_table_slice *slices, int64_t max_slices) {
+    if (!st || !codes_name || !limits || !plans)
+        return g4::set_error(G4_ERR_INVALID, "g4_st_plan_ple_split: null argument");
+    const Entry *e = find_entry(st, codes_name);
+    if (!e) return st_error("bad-entry", "tensor %s is not in this checkpoint", codes_name);
+    const int64_t rows = e->shape.empty() ? 0 : e->shape[0];
+    if (rows <= 0 || e->byte_length % rows != 0)
+        return g4::set_error(G4_ERR_INVALID,
+                             "gemma4 engine: %s has shape %s and %lld bytes, which is not a whole "
+                             "number of bytes per vocabulary row, so its split cannot be planned. A "
+                             "table that cannot be split cannot be loaded on an adapter that needs one.",
+                             codes_name, shape_text(e->shape).c_str(), (long long)e->byte_length);
+    int rc = g4_plan_gather_split(rows, e->byte_length / rows, groups_per_row, limits, plans, slices,
+                                  slices ? max_slices : 0, nullptr, 0);
+    if (rc) return rc;
+    if (plans->codes.single) return G4_OK;
+    if (!plans->codes.feasible)
+        return g4::set_error(G4_ERR_UNSUPPORTED,
+                             "gemma4 engine: %s codes need %lld slices of 4 storage bindings against "
+                             "a budget of %lld", codes_name, (long long)plans->codes.num_slices,
+                             (long long)plans->codes.binding_budget);
+    if (!plans->scales_single)
+        return g4::set_error(G4_ERR_UNSUPPORTED,
+                             "gemma4 engine: %s scales do NOT fit in one binding on this adapter, and "
+                             "the sliced gather addresses scales by the absolute vocabulary row, so "
+                             "this configuration needs a second slice index before it is correct",
+                             codes_name);
+    return G4_OK;
+}
+
 int g4_st_upload_f32(const g4_st *st, const char *name, float *device_dst, int64_t count,
                      void *stream) {
     if (!st || !name || !device_dst) return g4::set_error(G4_ERR_INVALID, "g4_st_upload_f32: null argument");

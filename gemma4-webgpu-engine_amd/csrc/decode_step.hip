@@ -38,6 +38,10 @@ namespace {
 
 using namespace g4;
 
+// Writes one int32 from a kernel argument: the position word, set in stream order (and inside a
+// graph capture) without a host copy.
+__global__ void set_word_kernel(int32_t *word, int32_t value) { *word = value; }
+
 struct Plan {
     g4_gemv_plan *p = nullptr;
     bool gelu = false;  // the gelu-mul pass is folded into this plan's epilogue
@@ -64,6 +68,8 @@ struct g4_decode {
     g4_decode_shape s{};
     g4_decode_weights w{};
     std::vector<g4_decode_layer> layers;
+    std::vector<const void *> ple_split_codes;  // the split PLE table's slices (empty: one table)
+    std::vector<int64_t> ple_split_start, ple_split_rows;
     DeviceAlloc mem;
     int32_t *pos = nullptr;
     float *identity = nullptr, *per_layer = nullptr;
@@ -170,7 +176,24 @@ int check_shape(const g4_decode_shape &s) {
 }
 
 int check_weights(const g4_decode_shape &s, const g4_decode_weights &w) {
-    if (!w.embed || !w.embed_s || !w.ple_table || !w.ple_table_s || !w.ple_model_proj ||
+    if (w.ple_num_slices < 0 || w.ple_num_slices > 16)
+        return set_error(G4_ERR_INVALID, "decode: %d PLE slices (0..16)", w.ple_num_slices);
+    if (w.ple_num_slices > 0) {
+        if (!w.ple_slice_codes || !w.ple_slice_start || !w.ple_slice_rows)
+            return set_error(G4_ERR_INVALID, "decode: PLE slices need codes, starts and row counts");
+        int64_t expect = 0;
+        for (int i = 0; i < w.ple_num_slices; ++i) {
+            if (!w.ple_slice_codes[i] || w.ple_slice_start[i] != expect || w.ple_slice_rows[i] <= 0)
+                return set_error(G4_ERR_INVALID,
+                                 "decode: PLE slice %d must start at row %lld with rows and a buffer",
+                                 i, (long long)expect);
+            expect += w.ple_slice_rows[i];
+        }
+        if (expect != s.vocab)
+            return set_error(G4_ERR_INVALID, "decode: the PLE slices cover %lld rows, not the vocabulary's %lld",
+                             (long long)expect, (long long)s.vocab);
+    }
+    if (!w.embed || !w.embed_s || (!w.ple_table && w.ple_num_slices == 0) || !w.ple_table_s || !w.ple_model_proj ||
         !w.ple_model_proj_s || !w.ple_proj_norm || !w.final_norm || !w.rope_local_cos ||
         !w.rope_local_sin || !w.rope_global_cos || !w.rope_global_sin || !w.layer)
         return set_error(G4_ERR_INVALID, "decode: a model-level weight is missing");
@@ -535,6 +558,14 @@ int g4_decode_create(const g4_decode_shape *shape, const g4_decode_weights *weig
     d->w = *weights;
     d->layers.assign(weights->layer, weights->layer + shape->layers);
     d->w.layer = d->layers.data();
+    if (weights->ple_num_slices > 0) {
+        const int n = weights->ple_num_slices;
+        d->ple_split_codes.assign(weights->ple_slice_codes, weights->ple_slice_codes + n);
+        d->ple_split_start.assign(weights->ple_slice_start, weights->ple_slice_start + n);
+        d->ple_split_rows.assign(weights->ple_slice_rows, weights->ple_slice_rows + n);
+    }
+    d->w.ple_slice_codes = nullptr;  // the copies above are the runner's
+    d->w.ple_slice_start = d->w.ple_slice_rows = nullptr;
     int rc = build(*d);
     if (rc != G4_OK) {
         delete d;
@@ -564,6 +595,16 @@ int g4_decode_kv(g4_decode *d, int layer, float **k, float **v, int64_t *row_str
 int g4_decode_position(g4_decode *d, int32_t **pos) {
     if (!d || !pos) return set_error(G4_ERR_INVALID, "decode: null argument");
     *pos = d->pos;
+    return G4_OK;
+}
+
+int g4_decode_set_position(g4_decode *d, int pos, void *stream) {
+    if (!d) return set_error(G4_ERR_INVALID, "decode: null argument");
+    if (pos < 0 || pos >= d->s.kv_capacity)
+        return set_error(G4_ERR_INVALID, "decode: position %d outside the KV capacity %d", pos,
+                         d->s.kv_capacity);
+    hipLaunchKernelGGL(set_word_kernel, dim3(1), dim3(1), 0, as_stream(stream), d->pos, pos);
+    G4_LAUNCHED("set_word_kernel");
     return G4_OK;
 }
 
@@ -607,9 +648,15 @@ int g4_decode_step(g4_decode *d, const int32_t *tokens, int32_t *next_tokens, vo
     const float embed_scale = (float)std::sqrt((double)H);
     G4_TRY(g4_embed_tokens(d->w.embed, d->w.embed_s, tokens, B, s.vocab, H, embed_scale, in,
                            d->hbuf[0], d->embed_codes, stream));
-    // the unsliced gather over all `vocab` rows: an id outside them gives a zero row
-    G4_TRY(g4_ple_gather(d->w.ple_table, d->w.ple_table_s, 0, tokens, d->identity, G4_KIND_F32,
-                         B, PL, s.ple_dim, s.layers, 0, 0, s.vocab, stream));
+    // the unsliced gather over all `vocab` rows, or every slice of a split table in one launch;
+    // either way an id outside the vocabulary gives a zero row
+    if (d->ple_split_codes.empty())
+        G4_TRY(g4_ple_gather(d->w.ple_table, d->w.ple_table_s, 0, tokens, d->identity, G4_KIND_F32,
+                             B, PL, s.ple_dim, s.layers, 0, 0, s.vocab, stream));
+    else
+        G4_TRY(g4_ple_gather_split(d->ple_split_codes.data(), d->ple_split_start.data(),
+                                   d->ple_split_rows.data(), (int)d->ple_split_codes.size(), d->w.ple_table_s, G4_KIND_F32, tokens,
+                                   d->identity, G4_KIND_F32, B, PL, s.ple_dim, s.layers, stream));
     G4_TRY(run_linear_rows(*d, d->ple_model_plan,
                            desc(d->w.ple_model_proj, d->w.ple_model_proj_s, d->embed_codes,
                                 d->ple_codes, 4, H, PL, G4_KIND_I8, in, out),

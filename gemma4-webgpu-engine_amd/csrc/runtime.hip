@@ -100,6 +100,7 @@ int g4_free(void *ptr) {
 
 int g4_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream) {
     if (bytes == 0) return G4_OK;
+    if (!dst || !src) return set_error(G4_ERR_INVALID, "g4_memcpy_h2d: a NULL address");
     G4_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream)));
     G4_HIP(hipStreamSynchronize(as_stream(stream)));
     return G4_OK;
@@ -107,6 +108,7 @@ int g4_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream) {
 
 int g4_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream) {
     if (bytes == 0) return G4_OK;
+    if (!dst || !src) return set_error(G4_ERR_INVALID, "g4_memcpy_d2h: a NULL address");
     G4_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream)));
     G4_HIP(hipStreamSynchronize(as_stream(stream)));
     return G4_OK;
@@ -114,6 +116,7 @@ int g4_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream) {
 
 int g4_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream) {
     if (bytes == 0) return G4_OK;
+    if (!dst || !src) return set_error(G4_ERR_INVALID, "g4_memcpy_d2d: a NULL address");
     G4_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)));
     return G4_OK;
 }
@@ -275,6 +278,29 @@ int g4_plan_table_split(const g4_table_split_input *in, g4_table_split_plan *pla
     plan->single = n == 1;
     plan->dispatches_per_gather = n;
     plan->feasible = kGatherBindings <= plan->binding_budget;
+    return G4_OK;
+}
+
+// tableSplit.ts:257-287 planGatherSplit: the codes and the f32 scales planned separately under
+// the same limits (they reach the cap at very different sizes), scalesSingle from the scale plan.
+int g4_plan_gather_split(int64_t rows, int64_t code_row_bytes, int64_t scales_per_row,
+                         const g4_gather_limits *limits, g4_gather_split_plans *plans,
+                         g4_table_slice *code_slices, int64_t max_code_slices,
+                         g4_table_slice *scale_slices, int64_t max_scale_slices) {
+    if (!limits || !plans) return set_error(G4_ERR_INVALID, "g4_plan_gather_split: NULL argument");
+    g4_table_split_input in{};
+    in.rows = rows;
+    in.max_storage_buffer_binding_size = limits->max_storage_buffer_binding_size;
+    in.max_buffer_size = limits->max_buffer_size;
+    in.max_storage_buffers_per_shader_stage = limits->max_storage_buffers_per_shader_stage;
+    in.max_slice_bytes = 0;
+    in.row_bytes = code_row_bytes;
+    int rc = g4_plan_table_split(&in, &plans->codes, code_slices, code_slices ? max_code_slices : 0);
+    if (rc) return rc;
+    in.row_bytes = scales_per_row * 4;
+    rc = g4_plan_table_split(&in, &plans->scales, scale_slices, scale_slices ? max_scale_slices : 0);
+    if (rc) return rc;
+    plans->scales_single = plans->scales.single;
     return G4_OK;
 }
 

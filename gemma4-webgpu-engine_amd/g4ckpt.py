@@ -136,6 +136,30 @@ class Directory:
         g4._check(g4.lib().g4_st_upload(self.handle, name.encode(), g4._ptr(dst), dst.nbytes, stream))
         return dst
 
+    def plan_ple_split(self, codes_name: str, groups_per_row: int, max_binding: int,
+                       max_buffer: int, max_buffers_per_stage: int = 10):
+        """declarePleSplit's planning (engine.ts:308-345): (GatherSplitPlans, code slices). The
+        slices are empty when the table fits one buffer (plans.codes.single)."""
+        lim = g4.GatherLimits(max_binding, max_buffer, max_buffers_per_stage)
+        plans = g4.GatherSplitPlans()
+        cap = 4096
+        sl = (g4.TableSlice * cap)()
+        g4._check(g4.lib().g4_st_plan_ple_split(self.handle, codes_name.encode(), groups_per_row,
+                                                ctypes.byref(lim), ctypes.byref(plans), sl, cap))
+        n = 0 if plans.codes.single else min(plans.codes.num_slices, cap)
+        return plans, [sl[i] for i in range(n)]
+
+    def upload_split(self, name: str, slices, dsts=None, stream=None) -> list:
+        """declareSplit + uploadWeight (buffers.ts:291-423): the tensor's bytes routed into one
+        device buffer per slice (new buffers unless dsts is given)."""
+        if dsts is None:
+            dsts = [g4.DeviceBuffer(sl.byte_length) for sl in slices]
+        arr = (g4.TableSlice * max(1, len(slices)))(*slices)
+        ptrs = (_vp * max(1, len(dsts)))(*[g4._ptr(b) for b in dsts])
+        g4._check(g4.lib().g4_st_upload_split(self.handle, name.encode(), arr, len(slices), ptrs,
+                                              stream))
+        return dsts
+
     def upload_f32(self, name: str, stream=None) -> "g4.DeviceBuffer":
         """A BF16 / F16 / F32 tensor widened exactly to f32 in device memory."""
         t = self.find(name)

@@ -227,6 +227,23 @@ class SyntheticModel:
             self.buffers[name] = g4.DeviceBuffer.from_array(a)
         self.layer_scalar = layer_scalars(s, seed)
         self._keep = None
+        self.ple_split = None  # [(device buffer, start row, rows)] when the PLE table is split
+
+    def split_ple(self, slices, drop_whole: bool = False):
+        """Carry the PLE table as one device buffer per slice (g4_table_slice rows), copied from the
+        whole table, the way a split checkpoint upload leaves it (buffers.ts sliceName)."""
+        whole = self.buffers["ple_table"]
+        row_bytes = whole.shape[1]
+        parts = []
+        for sl in slices:
+            b = g4.DeviceBuffer(sl.row_count * row_bytes)
+            g4._check(g4.lib().g4_memcpy_d2d(b.ptr, whole.ptr + sl.start_row * row_bytes,
+                                              sl.row_count * row_bytes, None))
+            parts.append((b, sl.start_row, sl.row_count))
+        g4.synchronize()
+        self.ple_split = parts
+        if drop_whole:
+            self.buffers.pop("ple_table").close()
 
     def ptr(self, name):
         b = self.buffers.get(name)
@@ -236,7 +253,17 @@ class SyntheticModel:
         return self.buffers[name].download()
 
     def host_rows(self, name, rows) -> np.ndarray:
-        """Selected rows of a 2-D device tensor (the PLE table is 1.2 GB; tests read a few rows)."""
+        """Selected rows of a 2-D device tensor (the PLE table is 1.2 GB; tests read a few rows).
+        A split PLE table is read from the slice that carries each row."""
+        split = getattr(self, "ple_split", None)
+        if name == "ple_table" and split and "ple_table" not in self.buffers:
+            width = self.shape.layers * self.shape.ple_dim // 2
+            out = np.empty((len(rows), width), dtype=np.uint8)
+            for i, r in enumerate(rows):
+                b, start, n = next(p for p in split if p[1] <= int(r) < p[1] + p[2])
+                g4._check(g4.lib().g4_memcpy_d2h(out[i].ctypes.data, b.ptr + (int(r) - start) * width,
+                                                  width, None))
+            return out
         b = self.buffers[name]
         width = b.shape[1]
         out = np.empty((len(rows), width), dtype=b.dtype)
@@ -255,7 +282,19 @@ class SyntheticModel:
             L.layer_scalar = float(self.layer_scalar[l])
         w = g4.DecodeWeights(**{f: self.ptr(f) for f in g4.DECODE_MODEL_FIELDS})
         w.layer = ctypes.cast(layers, ctypes.POINTER(g4.DecodeLayer))
-        self._keep = layers
+        keep = [layers]
+        split = getattr(self, "ple_split", None)
+        if split:
+            n = len(split)
+            codes = (ctypes.c_void_p * n)(*[b.ptr for b, _, _ in split])
+            starts = (ctypes.c_int64 * n)(*[st for _, st, _ in split])
+            rows = (ctypes.c_int64 * n)(*[r for _, _, r in split])
+            w.ple_num_slices = n
+            w.ple_slice_codes = ctypes.cast(codes, ctypes.POINTER(ctypes.c_void_p))
+            w.ple_slice_start = ctypes.cast(starts, ctypes.POINTER(ctypes.c_int64))
+            w.ple_slice_rows = ctypes.cast(rows, ctypes.POINTER(ctypes.c_int64))
+            keep += [codes, starts, rows]
+        self._keep = keep
         return w
 
     def nbytes(self) -> int:
@@ -296,7 +335,9 @@ class CheckpointModel:
     and int8 I8 [N, K] are served; the 2-bit families and the bf16 dense per-layer projection are
     not, and neither are activation scales that differ from the shape's one static pair."""
 
-    def __init__(self, shape: Shape, path: str, stream=None):
+    def __init__(self, shape: Shape, path: str, stream=None, limits=None):
+        """limits: (maxStorageBufferBindingSize, maxBufferSize) of the device profile; when the
+        PLE table does not fit them it is planned and uploaded split (engine.ts:308-345)."""
         import g4ckpt as ck
         self.shape = s = shape
         self.buffers: dict[str, g4.DeviceBuffer] = {}
@@ -335,8 +376,16 @@ class CheckpointModel:
                                      f"{which} scale, {want}")
             return bits
 
+        self.ple_split = None
+        if limits is not None:
+            plans, slices = d.plan_ple_split(CKPT_MODEL["ple_table"], s.layers, *limits)
+            if slices:
+                parts = d.upload_split(CKPT_MODEL["ple_table"], slices, stream=stream)
+                self.ple_split = [(b, sl.start_row, sl.row_count) for b, sl in zip(parts, slices)]
         for key, name in CKPT_MODEL.items():
             if key.endswith("_s") or key in ("ple_model_proj",):
+                continue
+            if key == "ple_table" and self.ple_split:
                 continue
             if key.endswith("norm"):
                 self.buffers[key] = d.upload_f32(name, stream=stream)
@@ -404,6 +453,10 @@ class Decoder:
         if stream is None:
             g4.synchronize()
         self._last_pos = a  # keep the host word alive until the copy has run
+
+    def set_position_async(self, pos: int, stream=None):
+        """The position word written in stream order (g4_decode_set_position): no host wait."""
+        g4._check(g4.lib().g4_decode_set_position(self.handle, pos, stream))
 
     def step(self, tokens, next_tokens, stream=None):
         g4._check(g4.lib().g4_decode_step(self.handle, g4._ptr(tokens), g4._ptr(next_tokens), stream))

@@ -63,6 +63,18 @@ class TableSplitPlan(ctypes.Structure):
                 ("binding_budget", _i64), ("dispatches_per_gather", _i64)]
 
 
+class GatherLimits(ctypes.Structure):
+    """include/g4w8a8.h g4_gather_limits (tableSplit.ts GatherLimits)."""
+    _fields_ = [("max_storage_buffer_binding_size", _i64), ("max_buffer_size", _i64),
+                ("max_storage_buffers_per_shader_stage", _i64)]
+
+
+class GatherSplitPlans(ctypes.Structure):
+    """include/g4w8a8.h g4_gather_split_plans (tableSplit.ts GatherSplitPlans, no note)."""
+    _fields_ = [("codes", TableSplitPlan), ("scales", TableSplitPlan),
+                ("scales_single", ctypes.c_int32)]
+
+
 class DecodeShape(ctypes.Structure):
     """include/g4decode.h g4_decode_shape."""
     _fields_ = [(n, _c_int) for n in ("layers", "kv_producers", "hidden", "ffn", "q_heads",
@@ -90,7 +102,10 @@ DECODE_MODEL_FIELDS = ("embed", "embed_s", "ple_table", "ple_table_s", "ple_mode
 
 class DecodeWeights(ctypes.Structure):
     """include/g4decode.h g4_decode_weights."""
-    _fields_ = [(n, _vp) for n in DECODE_MODEL_FIELDS] + [("layer", ctypes.POINTER(DecodeLayer))]
+    _fields_ = [(n, _vp) for n in DECODE_MODEL_FIELDS] + [
+        ("layer", ctypes.POINTER(DecodeLayer)), ("ple_num_slices", _c_int),
+        ("ple_slice_codes", ctypes.POINTER(_vp)), ("ple_slice_start", ctypes.POINTER(_i64)),
+        ("ple_slice_rows", ctypes.POINTER(_i64))]
 
 
 class StTensor(ctypes.Structure):
@@ -173,6 +188,9 @@ SIGNATURES = {
                                      ctypes.POINTER(TableSplitPlan), ctypes.POINTER(TableSlice),
                                      _i64]),
     "g4_slice_for_row": (_i64, [ctypes.POINTER(TableSlice), _i64, _i64]),
+    "g4_plan_gather_split": (_c_int, [_i64, _i64, _i64, ctypes.POINTER(GatherLimits),
+                                      ctypes.POINTER(GatherSplitPlans), ctypes.POINTER(TableSlice),
+                                      _i64, ctypes.POINTER(TableSlice), _i64]),
     # include/g4decode.h
     "g4_rms_join": (_c_int, [_vp, _c_int, _c_float, _vp, _vp, _c_float, _vp, _c_int, _c_int,
                              _c_float, _c_float, _vp, _vp, _vp]),
@@ -199,6 +217,7 @@ SIGNATURES = {
                               ctypes.POINTER(_i64)]),
     "g4_decode_position": (_c_int, [_vp, ctypes.POINTER(_vp)]),
     "g4_decode_step": (_c_int, [_vp, _vp, _vp, _vp]),
+    "g4_decode_set_position": (_c_int, [_vp, _c_int, _vp]),
     "g4_decode_buffer": (_c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp),
                                   ctypes.POINTER(_sz)]),
     "g4_decode_set_stop": (_c_int, [_vp, _c_int]),
@@ -220,6 +239,11 @@ SIGNATURES = {
     "g4_st_read": (_c_int, [_vp, ctypes.c_char_p, _i64, _vp, _sz]),
     "g4_st_upload": (_c_int, [_vp, ctypes.c_char_p, _vp, _sz, _vp]),
     "g4_st_upload_f32": (_c_int, [_vp, ctypes.c_char_p, _vp, _i64, _vp]),
+    "g4_st_upload_split": (_c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(TableSlice), _c_int,
+                                    ctypes.POINTER(_vp), _vp]),
+    "g4_st_plan_ple_split": (_c_int, [_vp, ctypes.c_char_p, _i64, ctypes.POINTER(GatherLimits),
+                                      ctypes.POINTER(GatherSplitPlans), ctypes.POINTER(TableSlice),
+                                      _i64]),
     "g4_tie_guard": (_c_int, [_vp, _sz, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _sz]),
     "g4_sha256_hex": (None, [_vp, _sz, ctypes.c_char_p]),
     "g4_quant_bits": (_c_int, [ctypes.c_char_p]),
@@ -574,6 +598,19 @@ def plan_table_split(rows, row_bytes, max_binding, max_buffer, max_buffers_per_s
     slices = (TableSlice * cap)()
     _check(lib().g4_plan_table_split(ctypes.byref(inp), ctypes.byref(plan), slices, cap))
     return plan, [slices[i] for i in range(min(plan.num_slices, cap))]
+
+
+def plan_gather_split(rows, code_row_bytes, scales_per_row, max_binding, max_buffer,
+                      max_buffers_per_stage=10):
+    """planGatherSplit (tableSplit.ts:257-287): (plans, code slices, scale slices)."""
+    lim = GatherLimits(max_binding, max_buffer, max_buffers_per_stage)
+    plans = GatherSplitPlans()
+    cap = 4096
+    cs, ss = (TableSlice * cap)(), (TableSlice * cap)()
+    _check(lib().g4_plan_gather_split(rows, code_row_bytes, scales_per_row, ctypes.byref(lim),
+                                      ctypes.byref(plans), cs, cap, ss, cap))
+    return (plans, [cs[i] for i in range(min(plans.codes.num_slices, cap))],
+            [ss[i] for i in range(min(plans.scales.num_slices, cap))])
 
 
 def slice_for_row(slices, row) -> int:

@@ -10,6 +10,7 @@
 #include <string>
 #include <vector>
 
+#include "../../include/g4decode.h"
 #include "../../include/g4w8a8.h"
 
 namespace {
@@ -160,30 +161,30 @@ napi_value Free(napi_env env, napi_callback_info info) {
 }
 
 napi_value Upload(napi_env env, napi_callback_info info) {
-    Args a(env, info, 2);
+    Args a(env, info, 3);
     void *data;
     size_t len;
     if (a.size() < 2 || !host_bytes(env, a.v[1], &data, &len)) {
-        throw_type(env, "upload(ptr, TypedArray|ArrayBuffer|Buffer)");
+        throw_type(env, "upload(ptr, TypedArray|ArrayBuffer|Buffer[, stream])");
         return nullptr;
     }
-    if (throw_status(env, g4_memcpy_h2d(a.ptr(0), data, len, nullptr))) return nullptr;
+    if (throw_status(env, g4_memcpy_h2d(a.ptr(0), data, len, a.ptr(2)))) return nullptr;
     return undefined(env);
 }
 
 napi_value Download(napi_env env, napi_callback_info info) {
-    Args a(env, info, 2);
+    Args a(env, info, 3);
     size_t len = (size_t)a.num(1);
     void *data = nullptr;
     napi_value ab;
     napi_create_arraybuffer(env, len, &data, &ab);
-    if (throw_status(env, g4_memcpy_d2h(data, a.ptr(0), len, nullptr))) return nullptr;
+    if (throw_status(env, g4_memcpy_d2h(data, a.ptr(0), len, a.ptr(2)))) return nullptr;
     return ab;
 }
 
 napi_value Fill(napi_env env, napi_callback_info info) {
-    Args a(env, info, 3);
-    if (throw_status(env, g4_fill_u8(a.ptr(0), (uint8_t)a.i32(1), (size_t)a.num(2), nullptr)))
+    Args a(env, info, 4);
+    if (throw_status(env, g4_fill_u8(a.ptr(0), (uint8_t)a.i32(1), (size_t)a.num(2), a.ptr(3))))
         return nullptr;
     return undefined(env);
 }
@@ -200,31 +201,32 @@ napi_value LastError(napi_env env, napi_callback_info) {
     return s;
 }
 
-// ---- the entry points (argument order = the C ABI's, stream omitted = default stream) ----
+// ---- the entry points (argument order = the C ABI's; the stream is the optional last
+// argument, a handle from streamCreate, omitted or 0 = the default stream) ----
 
 napi_value Qgemv(napi_env env, napi_callback_info info) {
-    Args a(env, info, 12);
+    Args a(env, info, 13);
     int st = g4_qgemv(a.i32(0), a.ptr(1), (const float *)a.ptr(2), a.ptr(3), a.i32(4), a.ptr(5),
                       a.i32(6), a.i32(7), a.i32(8), a.i32(9, 1), (float)a.num(10), (float)a.num(11),
-                      nullptr);
+                      a.ptr(12));
     if (throw_status(env, st)) return nullptr;
     return undefined(env);
 }
 
 napi_value Qgemm(napi_env env, napi_callback_info info) {
-    Args a(env, info, 12);
+    Args a(env, info, 13);
     int st = g4_qgemm(a.i32(0), a.ptr(1), (const float *)a.ptr(2), a.ptr(3), a.i32(4), a.ptr(5),
                       a.i32(6), a.i32(7), a.i32(8), a.i32(9, 1), (float)a.num(10), (float)a.num(11),
-                      nullptr);
+                      a.ptr(12));
     if (throw_status(env, st)) return nullptr;
     return undefined(env);
 }
 
 napi_value Linear(napi_env env, napi_callback_info info) {
-    Args a(env, info, 12);
+    Args a(env, info, 13);
     int st = g4_linear(a.i32(0), a.ptr(1), (const float *)a.ptr(2), a.ptr(3), a.i32(4), a.ptr(5),
                        a.i32(6), a.i32(7), a.i32(8), a.i32(9, 1), (float)a.num(10),
-                       (float)a.num(11), nullptr);
+                       (float)a.num(11), a.ptr(12));
     if (throw_status(env, st)) return nullptr;
     return undefined(env);
 }
@@ -241,7 +243,7 @@ napi_value KernelForShape(napi_env env, napi_callback_info info) {
 
 // projectionBatch(bits, [w], [s], x, xKind, [out], outKind, [rows], [inScales], [outScales], k)
 napi_value ProjectionBatch(napi_env env, napi_callback_info info) {
-    Args a(env, info, 11);
+    Args a(env, info, 12);
     if (a.size() < 11) {
         throw_type(env, "projectionBatch needs 11 arguments");
         return nullptr;
@@ -268,14 +270,14 @@ napi_value ProjectionBatch(napi_env env, napi_callback_info info) {
     }
     int st = g4_projection_batch(a.i32(0), (int)n, wp.data(), sp.data(), a.ptr(3), a.i32(4),
                                  op.data(), a.i32(6), rp.data(), ip.data(), up.data(), a.i32(10),
-                                 nullptr);
+                                 a.ptr(11));
     if (throw_status(env, st)) return nullptr;
     return undefined(env);
 }
 
 // qgemvGrouped([{wq, scales, x, dst, bits, xKind, outKind, k, numRows, inScale, outScale}])
 napi_value QgemvGrouped(napi_env env, napi_callback_info info) {
-    Args a(env, info, 1);
+    Args a(env, info, 2);
     bool is_arr = false;
     if (a.size() < 1 || (napi_is_array(env, a.v[0], &is_arr), !is_arr)) {
         throw_type(env, "qgemvGrouped(descs: object[])");
@@ -299,7 +301,7 @@ napi_value QgemvGrouped(napi_env env, napi_callback_info info) {
         d[i].in_scale = (float)prop(env, o, "inScale");
         d[i].out_scale = (float)prop(env, o, "outScale");
     }
-    if (throw_status(env, g4_qgemv_grouped(d.data(), (int)n, nullptr))) return nullptr;
+    if (throw_status(env, g4_qgemv_grouped(d.data(), (int)n, a.ptr(1)))) return nullptr;
     return undefined(env);
 }
 
@@ -342,9 +344,9 @@ napi_value QgemvPlanCreate(napi_env env, napi_callback_info info) {
 }
 
 napi_value QgemvPlanLaunch(napi_env env, napi_callback_info info) {
-    Args a(env, info, 1);
+    Args a(env, info, 2);
     if (throw_status(env, g4_qgemv_plan_launch(reinterpret_cast<const g4_gemv_plan *>(a.ptr(0)),
-                                               nullptr)))
+                                               a.ptr(1))))
         return nullptr;
     return undefined(env);
 }
@@ -357,10 +359,10 @@ napi_value QgemvPlanDestroy(napi_env env, napi_callback_info info) {
 }
 
 napi_value QgemvSplit(napi_env env, napi_callback_info info) {
-    Args a(env, info, 11);
+    Args a(env, info, 12);
     int st = g4_qgemv_split(a.i32(0), a.ptr(1), (const float *)a.ptr(2), a.ptr(3), a.i32(4),
                             (float *)a.ptr(5), a.i32(6), a.i32(7), a.i32(8), a.i32(9),
-                            (float)a.num(10), nullptr);
+                            (float)a.num(10), a.ptr(11));
     if (throw_status(env, st)) return nullptr;
     return undefined(env);
 }
@@ -368,11 +370,11 @@ napi_value QgemvSplit(napi_env env, napi_callback_info info) {
 // qgemv-4bit-gelu / qgemv-8bit-gelu: (bits, wq, scales, gate, gateKind, up, upKind, upOffset,
 // dst, outKind, k, numRows, inScale, outScale[, gateScale, upScale])
 napi_value QgemvGelu(napi_env env, napi_callback_info info) {
-    Args a(env, info, 16);
+    Args a(env, info, 17);
     g4_gelu_act act{a.ptr(5), a.i32(6), (float)a.num(14), (float)a.num(15), (int64_t)a.num(7)};
     int st = g4_qgemv_gelu(a.i32(0), a.ptr(1), (const float *)a.ptr(2), a.ptr(3), a.i32(4), &act,
                            a.ptr(8), a.i32(9), a.i32(10), a.i32(11), (float)a.num(12),
-                           (float)a.num(13), nullptr);
+                           (float)a.num(13), a.ptr(16));
     if (throw_status(env, st)) return nullptr;
     return undefined(env);
 }
@@ -380,36 +382,36 @@ napi_value QgemvGelu(napi_env env, napi_callback_info info) {
 // qgemv-4bit-gelu-exact-split: (bits, wq, scales, gate, gateKind, up, upKind, upOffset, partials,
 // k, numRows, kSplits, exact, inScale[, gateScale, upScale])
 napi_value QgemvGeluSplit(napi_env env, napi_callback_info info) {
-    Args a(env, info, 16);
+    Args a(env, info, 17);
     g4_gelu_act act{a.ptr(5), a.i32(6), (float)a.num(14), (float)a.num(15), (int64_t)a.num(7)};
     int st = g4_qgemv_gelu_split(a.i32(0), a.ptr(1), (const float *)a.ptr(2), a.ptr(3), a.i32(4),
                                  &act, (float *)a.ptr(8), a.i32(9), a.i32(10), a.i32(11),
-                                 a.i32(12), (float)a.num(13), nullptr);
+                                 a.i32(12), (float)a.num(13), a.ptr(16));
     if (throw_status(env, st)) return nullptr;
     return undefined(env);
 }
 
 napi_value QgemvMerge(napi_env env, napi_callback_info info) {
-    Args a(env, info, 6);
+    Args a(env, info, 7);
     int st = g4_qgemv_merge((const float *)a.ptr(0), a.ptr(1), a.i32(2), a.i32(3), a.i32(4),
-                            (float)a.num(5), nullptr);
+                            (float)a.num(5), a.ptr(6));
     if (throw_status(env, st)) return nullptr;
     return undefined(env);
 }
 
 napi_value QgemvExactMerge(napi_env env, napi_callback_info info) {
-    Args a(env, info, 8);
+    Args a(env, info, 9);
     int st = g4_qgemv_exact_merge((const float *)a.ptr(0), (const float *)a.ptr(1), a.ptr(2),
                                   a.i32(3), a.i32(4), a.i32(5), (float)a.num(6), (float)a.num(7),
-                                  nullptr);
+                                  a.ptr(8));
     if (throw_status(env, st)) return nullptr;
     return undefined(env);
 }
 
 napi_value SrqQuantize(napi_env env, napi_callback_info info) {
-    Args a(env, info, 5);
+    Args a(env, info, 6);
     int st = g4_srq_quantize(a.ptr(0), a.i32(1), (int8_t *)a.ptr(2), (int64_t)a.num(3),
-                             (float)a.num(4), nullptr);
+                             (float)a.num(4), a.ptr(5));
     if (throw_status(env, st)) return nullptr;
     return undefined(env);
 }
@@ -417,10 +419,10 @@ napi_value SrqQuantize(napi_env env, napi_callback_info info) {
 // pleGather(codes, scales, scaleKind, ids, dst, outKind, slots, cols, groupSize, groupsPerRow,
 //           sliced, sliceStartRow, sliceRowCount)
 napi_value PleGather(napi_env env, napi_callback_info info) {
-    Args a(env, info, 13);
+    Args a(env, info, 14);
     int st = g4_ple_gather(a.ptr(0), a.ptr(1), a.i32(2), (const int32_t *)a.ptr(3), a.ptr(4),
                            a.i32(5), a.i32(6), a.i32(7), a.i32(8), a.i32(9), a.i32(10),
-                           (int64_t)a.num(11), (int64_t)a.num(12), nullptr);
+                           (int64_t)a.num(11), (int64_t)a.num(12), a.ptr(13));
     if (throw_status(env, st)) return nullptr;
     return undefined(env);
 }
@@ -428,7 +430,7 @@ napi_value PleGather(napi_env env, napi_callback_info info) {
 // pleGatherSplit([codes], [starts], [counts], scales, scaleKind, ids, dst, outKind, slots, cols,
 //                groupSize, groupsPerRow)
 napi_value PleGatherSplit(napi_env env, napi_callback_info info) {
-    Args a(env, info, 12);
+    Args a(env, info, 13);
     if (a.size() < 12) {
         throw_type(env, "pleGatherSplit needs 12 arguments");
         return nullptr;
@@ -447,32 +449,14 @@ napi_value PleGatherSplit(napi_env env, napi_callback_info info) {
     }
     int st = g4_ple_gather_split(cp.data(), sp.data(), np.data(), (int)c.size(), a.ptr(3),
                                  a.i32(4), (const int32_t *)a.ptr(5), a.ptr(6), a.i32(7), a.i32(8),
-                                 a.i32(9), a.i32(10), a.i32(11), nullptr);
+                                 a.i32(9), a.i32(10), a.i32(11), a.ptr(12));
     if (throw_status(env, st)) return nullptr;
     return undefined(env);
 }
 
-// planTableSplit({rows, rowBytes, maxStorageBufferBindingSize, maxBufferSize,
-//                 maxStorageBuffersPerShaderStage, maxSliceBytes?}) -> plan with slices
-napi_value PlanTableSplit(napi_env env, napi_callback_info info) {
-    Args a(env, info, 1);
-    if (a.size() < 1) {
-        throw_type(env, "planTableSplit(input)");
-        return nullptr;
-    }
-    napi_value in = a.v[0];
-    g4_table_split_input inp{};
-    inp.rows = (int64_t)prop(env, in, "rows");
-    inp.row_bytes = (int64_t)prop(env, in, "rowBytes");
-    inp.max_storage_buffer_binding_size = (int64_t)prop(env, in, "maxStorageBufferBindingSize");
-    inp.max_buffer_size = (int64_t)prop(env, in, "maxBufferSize");
-    inp.max_storage_buffers_per_shader_stage =
-        (int64_t)prop(env, in, "maxStorageBuffersPerShaderStage");
-    inp.max_slice_bytes = (int64_t)prop(env, in, "maxSliceBytes", 0);
-    g4_table_split_plan plan{};
-    std::vector<g4_table_slice> slices(1 << 16);
-    if (throw_status(env, g4_plan_table_split(&inp, &plan, slices.data(), (int64_t)slices.size())))
-        return nullptr;
+// A TableSplitPlan (tableSplit.ts:90-118) as a JS object with its slices.
+napi_value plan_object(napi_env env, const g4_table_split_plan &plan,
+                       const std::vector<g4_table_slice> &slices) {
     napi_value out, arr;
     napi_create_object(env, &out);
     set_num(env, out, "rows", (double)plan.rows);
@@ -504,6 +488,423 @@ napi_value PlanTableSplit(napi_env env, napi_callback_info info) {
     return out;
 }
 
+// planTableSplit({rows, rowBytes, maxStorageBufferBindingSize, maxBufferSize,
+//                 maxStorageBuffersPerShaderStage, maxSliceBytes?}) -> plan with slices
+napi_value PlanTableSplit(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    if (a.size() < 1) {
+        throw_type(env, "planTableSplit(input)");
+        return nullptr;
+    }
+    napi_value in = a.v[0];
+    g4_table_split_input inp{};
+    inp.rows = (int64_t)prop(env, in, "rows");
+    inp.row_bytes = (int64_t)prop(env, in, "rowBytes");
+    inp.max_storage_buffer_binding_size = (int64_t)prop(env, in, "maxStorageBufferBindingSize");
+    inp.max_buffer_size = (int64_t)prop(env, in, "maxBufferSize");
+    inp.max_storage_buffers_per_shader_stage =
+        (int64_t)prop(env, in, "maxStorageBuffersPerShaderStage");
+    inp.max_slice_bytes = (int64_t)prop(env, in, "maxSliceBytes", 0);
+    g4_table_split_plan plan{};
+    std::vector<g4_table_slice> slices(1 << 16);
+    if (throw_status(env, g4_plan_table_split(&inp, &plan, slices.data(), (int64_t)slices.size())))
+        return nullptr;
+    return plan_object(env, plan, slices);
+}
+
+// planGatherSplit(rows, codeRowBytes, scalesPerRow, {maxStorageBufferBindingSize, maxBufferSize,
+// maxStorageBuffersPerShaderStage}) -> {codes, scales, scalesSingle} (tableSplit.ts:257-287).
+napi_value PlanGatherSplit(napi_env env, napi_callback_info info) {
+    Args a(env, info, 4);
+    if (a.size() < 4) {
+        throw_type(env, "planGatherSplit(rows, codeRowBytes, scalesPerRow, limits)");
+        return nullptr;
+    }
+    g4_gather_limits lim{};
+    lim.max_storage_buffer_binding_size = (int64_t)prop(env, a.v[3], "maxStorageBufferBindingSize");
+    lim.max_buffer_size = (int64_t)prop(env, a.v[3], "maxBufferSize");
+    lim.max_storage_buffers_per_shader_stage =
+        (int64_t)prop(env, a.v[3], "maxStorageBuffersPerShaderStage");
+    g4_gather_split_plans plans{};
+    std::vector<g4_table_slice> cs(1 << 16), ss(1 << 16);
+    if (throw_status(env, g4_plan_gather_split((int64_t)a.num(0), (int64_t)a.num(1),
+                                               (int64_t)a.num(2), &lim, &plans, cs.data(),
+                                               (int64_t)cs.size(), ss.data(), (int64_t)ss.size())))
+        return nullptr;
+    napi_value out, b;
+    napi_create_object(env, &out);
+    napi_set_named_property(env, out, "codes", plan_object(env, plans.codes, cs));
+    napi_set_named_property(env, out, "scales", plan_object(env, plans.scales, ss));
+    napi_get_boolean(env, plans.scales_single != 0, &b);
+    napi_set_named_property(env, out, "scalesSingle", b);
+    return out;
+}
+
+
+// ---- streams, events and graphs (runtime.ts's queue and its cached per-token encode) ----
+
+napi_value StreamCreate(napi_env env, napi_callback_info) {
+    void *st = nullptr;
+    if (throw_status(env, g4_stream_create(&st))) return nullptr;
+    return make_num(env, (double)(uintptr_t)st);
+}
+
+napi_value StreamDestroy(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    if (throw_status(env, g4_stream_destroy(a.ptr(0)))) return nullptr;
+    return undefined(env);
+}
+
+napi_value StreamSynchronize(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    if (throw_status(env, g4_stream_synchronize(a.ptr(0)))) return nullptr;
+    return undefined(env);
+}
+
+napi_value EventCreate(napi_env env, napi_callback_info) {
+    void *e = nullptr;
+    if (throw_status(env, g4_event_create(&e))) return nullptr;
+    return make_num(env, (double)(uintptr_t)e);
+}
+
+napi_value EventRecord(napi_env env, napi_callback_info info) {
+    Args a(env, info, 2);
+    if (throw_status(env, g4_event_record(a.ptr(0), a.ptr(1)))) return nullptr;
+    return undefined(env);
+}
+
+napi_value EventElapsedMs(napi_env env, napi_callback_info info) {
+    Args a(env, info, 2);
+    float ms = 0;
+    if (throw_status(env, g4_event_elapsed_ms(&ms, a.ptr(0), a.ptr(1)))) return nullptr;
+    return make_num(env, ms);
+}
+
+napi_value EventDestroy(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    if (throw_status(env, g4_event_destroy(a.ptr(0)))) return nullptr;
+    return undefined(env);
+}
+
+napi_value GraphBeginCapture(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    if (throw_status(env, g4_graph_begin_capture(a.ptr(0)))) return nullptr;
+    return undefined(env);
+}
+
+napi_value GraphEndCapture(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    void *g = nullptr;
+    if (throw_status(env, g4_graph_end_capture(a.ptr(0), &g))) return nullptr;
+    return make_num(env, (double)(uintptr_t)g);
+}
+
+napi_value GraphLaunch(napi_env env, napi_callback_info info) {
+    Args a(env, info, 2);
+    if (throw_status(env, g4_graph_launch(a.ptr(0), a.ptr(1)))) return nullptr;
+    return undefined(env);
+}
+
+napi_value GraphDestroy(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    if (throw_status(env, g4_graph_destroy(a.ptr(0)))) return nullptr;
+    return undefined(env);
+}
+
+// ---- asynchronous waits (the reference's mapAsync readback, runtime.ts:866-878) ----
+//
+// The wait runs on a libuv worker thread and settles a Promise on the JS thread, so the event loop
+// keeps running (the host can encode the next step) while the device works. g4_last_error is per
+// thread: the worker copies its message for the settle.
+
+struct AsyncWait {
+    napi_async_work work = nullptr;
+    napi_deferred deferred = nullptr;
+    napi_ref buffer = nullptr;  // the ArrayBuffer a download fills (null: a plain synchronize)
+    void *host = nullptr;
+    const void *device = nullptr;
+    size_t bytes = 0;
+    void *stream = nullptr;
+    int status = G4_OK;
+    std::string message;
+};
+
+void async_execute(napi_env, void *data) {
+    AsyncWait *w = static_cast<AsyncWait *>(data);
+    w->status = w->buffer ? g4_memcpy_d2h(w->host, w->device, w->bytes, w->stream)
+                          : g4_stream_synchronize(w->stream);
+    if (w->status != G4_OK) w->message = g4_last_error();
+}
+
+void async_complete(napi_env env, napi_status, void *data) {
+    AsyncWait *w = static_cast<AsyncWait *>(data);
+    if (w->status == G4_OK) {
+        napi_value v;
+        if (w->buffer) napi_get_reference_value(env, w->buffer, &v);
+        else napi_get_undefined(env, &v);
+        napi_resolve_deferred(env, w->deferred, v);
+    } else {
+        std::string msg = w->message.empty() ? "g4w8a8 async wait failed" : w->message;
+        napi_value err, m, code;
+        napi_create_string_utf8(env, msg.c_str(), msg.size(), &m);
+        napi_create_error(env, nullptr, m, &err);
+        napi_create_int32(env, w->status, &code);
+        napi_set_named_property(env, err, "status", code);
+        napi_reject_deferred(env, w->deferred, err);
+    }
+    if (w->buffer) napi_delete_reference(env, w->buffer);
+    napi_delete_async_work(env, w->work);
+    delete w;
+}
+
+napi_value queue_wait(napi_env env, AsyncWait *w) {
+    napi_value promise, name;
+    napi_create_promise(env, &w->deferred, &promise);
+    napi_create_string_utf8(env, "g4w8a8.wait", NAPI_AUTO_LENGTH, &name);
+    napi_create_async_work(env, nullptr, name, async_execute, async_complete, w, &w->work);
+    napi_queue_async_work(env, w->work);
+    return promise;
+}
+
+// synchronizeAsync(stream?) -> Promise<void>: resolves once the stream's work has finished.
+napi_value SynchronizeAsync(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    AsyncWait *w = new AsyncWait();
+    w->stream = a.ptr(0);
+    return queue_wait(env, w);
+}
+
+// downloadAsync(ptr, bytes, stream?) -> Promise<ArrayBuffer>: the copy is ordered after the work
+// already enqueued on the stream.
+napi_value DownloadAsync(napi_env env, napi_callback_info info) {
+    Args a(env, info, 3);
+    AsyncWait *w = new AsyncWait();
+    w->device = a.ptr(0);
+    w->bytes = (size_t)a.num(1);
+    w->stream = a.ptr(2);
+    napi_value ab;
+    napi_create_arraybuffer(env, w->bytes, &w->host, &ab);
+    napi_create_reference(env, ab, 1, &w->buffer);
+    return queue_wait(env, w);
+}
+
+// ---- the decode runner (include/g4decode.h) ----
+
+uint64_t u64_arg(napi_env env, napi_value v) {
+    napi_valuetype t;
+    napi_typeof(env, v, &t);
+    if (t == napi_string) {
+        char buf[32] = {0};
+        size_t n = 0;
+        napi_get_value_string_utf8(env, v, buf, sizeof buf, &n);
+        return strtoull(buf, nullptr, 10);
+    }
+    if (t == napi_bigint) {
+        uint64_t r = 0;
+        bool lossless = false;
+        napi_get_value_bigint_uint64(env, v, &r, &lossless);
+        return r;
+    }
+    double d = 0;
+    napi_get_value_double(env, v, &d);
+    return (uint64_t)d;
+}
+
+// fillHashF32(ptr, n, seed, lo, hi, stream?) / fillHashU8(ptr, n, seed, stream?); seed: decimal
+// string, BigInt or number.
+napi_value FillHashF32(napi_env env, napi_callback_info info) {
+    Args a(env, info, 6);
+    if (a.size() < 5) {
+        throw_type(env, "fillHashF32(ptr, n, seed, lo, hi[, stream])");
+        return nullptr;
+    }
+    int st = g4_fill_hash_f32((float *)a.ptr(0), (int64_t)a.num(1), u64_arg(env, a.v[2]),
+                              (float)a.num(3), (float)a.num(4), a.ptr(5));
+    if (throw_status(env, st)) return nullptr;
+    return undefined(env);
+}
+
+napi_value FillHashU8(napi_env env, napi_callback_info info) {
+    Args a(env, info, 4);
+    if (a.size() < 3) {
+        throw_type(env, "fillHashU8(ptr, n, seed[, stream])");
+        return nullptr;
+    }
+    if (throw_status(env, g4_fill_hash_u8(a.ptr(0), (int64_t)a.num(1), u64_arg(env, a.v[2]), a.ptr(3))))
+        return nullptr;
+    return undefined(env);
+}
+
+const void *addr_prop(napi_env env, napi_value o, const char *name) {
+    return reinterpret_cast<const void *>((uintptr_t)prop(env, o, name));
+}
+
+// decodeCreate(shape, weights) -> handle. shape: the g4_decode_shape fields by their C names;
+// weights: the model fields by their C names (device addresses), `layer`: an array of per-layer
+// objects, and optionally `ple_slices`: [{codes, start_row, row_count}] (a split PLE table).
+napi_value DecodeCreate(napi_env env, napi_callback_info info) {
+    Args a(env, info, 2);
+    if (a.size() < 2) {
+        throw_type(env, "decodeCreate(shape, weights)");
+        return nullptr;
+    }
+    napi_value so = a.v[0], wo = a.v[1];
+    g4_decode_shape sh{};
+    sh.layers = (int)prop(env, so, "layers");
+    sh.kv_producers = (int)prop(env, so, "kv_producers");
+    sh.hidden = (int)prop(env, so, "hidden");
+    sh.ffn = (int)prop(env, so, "ffn");
+    sh.q_heads = (int)prop(env, so, "q_heads");
+    sh.head_dim = (int)prop(env, so, "head_dim");
+    sh.ple_dim = (int)prop(env, so, "ple_dim");
+    sh.global_period = (int)prop(env, so, "global_period");
+    sh.sliding_window = (int)prop(env, so, "sliding_window");
+    sh.kv_capacity = (int)prop(env, so, "kv_capacity");
+    sh.batch = (int)prop(env, so, "batch");
+    sh.vocab = (int64_t)prop(env, so, "vocab");
+    sh.eps = (float)prop(env, so, "eps");
+    sh.final_softcap = (float)prop(env, so, "final_softcap");
+    sh.in_scale = (float)prop(env, so, "in_scale");
+    sh.out_scale = (float)prop(env, so, "out_scale");
+    g4_decode_weights w{};
+    w.embed = addr_prop(env, wo, "embed");
+    w.embed_s = (const float *)addr_prop(env, wo, "embed_s");
+    w.ple_table = addr_prop(env, wo, "ple_table");
+    w.ple_table_s = (const float *)addr_prop(env, wo, "ple_table_s");
+    w.ple_model_proj = addr_prop(env, wo, "ple_model_proj");
+    w.ple_model_proj_s = (const float *)addr_prop(env, wo, "ple_model_proj_s");
+    w.ple_proj_norm = (const float *)addr_prop(env, wo, "ple_proj_norm");
+    w.final_norm = (const float *)addr_prop(env, wo, "final_norm");
+    w.rope_local_cos = (const float *)addr_prop(env, wo, "rope_local_cos");
+    w.rope_local_sin = (const float *)addr_prop(env, wo, "rope_local_sin");
+    w.rope_global_cos = (const float *)addr_prop(env, wo, "rope_global_cos");
+    w.rope_global_sin = (const float *)addr_prop(env, wo, "rope_global_sin");
+    napi_value layers;
+    bool is_arr = false;
+    napi_get_named_property(env, wo, "layer", &layers);
+    napi_is_array(env, layers, &is_arr);
+    uint32_t nl = 0;
+    if (is_arr) napi_get_array_length(env, layers, &nl);
+    if (!is_arr || (int)nl != sh.layers) {
+        throw_type(env, "decodeCreate: weights.layer must hold one object per layer");
+        return nullptr;
+    }
+    std::vector<g4_decode_layer> L(nl);
+    for (uint32_t l = 0; l < nl; ++l) {
+        napi_value o;
+        napi_get_element(env, layers, l, &o);
+        g4_decode_layer &x = L[l];
+        const void **vp[] = {&x.q, &x.k, &x.v, &x.o, &x.gate, &x.up, &x.down, &x.ple_gate, &x.ple_proj};
+        const char *vn[] = {"q", "k", "v", "o", "gate", "up", "down", "ple_gate", "ple_proj"};
+        for (int i = 0; i < 9; ++i) *vp[i] = addr_prop(env, o, vn[i]);
+        const float **fp[] = {&x.q_s, &x.k_s, &x.v_s, &x.o_s, &x.gate_s, &x.up_s, &x.down_s,
+                              &x.ple_gate_s, &x.ple_proj_s, &x.input_norm, &x.post_attn_norm,
+                              &x.pre_ffn_norm, &x.post_ffn_norm, &x.post_ple_norm, &x.q_norm,
+                              &x.k_norm};
+        const char *fn[] = {"q_s", "k_s", "v_s", "o_s", "gate_s", "up_s", "down_s", "ple_gate_s",
+                            "ple_proj_s", "input_norm", "post_attn_norm", "pre_ffn_norm",
+                            "post_ffn_norm", "post_ple_norm", "q_norm", "k_norm"};
+        for (int i = 0; i < 16; ++i) *fp[i] = (const float *)addr_prop(env, o, fn[i]);
+        x.layer_scalar = (float)prop(env, o, "layer_scalar", 1.0);
+    }
+    w.layer = L.data();
+    std::vector<const void *> sc;
+    std::vector<int64_t> ss, sn;
+    bool has = false;
+    napi_has_named_property(env, wo, "ple_slices", &has);
+    if (has) {
+        napi_value arr;
+        napi_get_named_property(env, wo, "ple_slices", &arr);
+        napi_is_array(env, arr, &is_arr);
+        uint32_t n = 0;
+        if (is_arr) napi_get_array_length(env, arr, &n);
+        for (uint32_t i = 0; i < n; ++i) {
+            napi_value o;
+            napi_get_element(env, arr, i, &o);
+            sc.push_back(addr_prop(env, o, "codes"));
+            ss.push_back((int64_t)prop(env, o, "start_row"));
+            sn.push_back((int64_t)prop(env, o, "row_count"));
+        }
+        w.ple_num_slices = (int)n;
+        w.ple_slice_codes = sc.data();
+        w.ple_slice_start = ss.data();
+        w.ple_slice_rows = sn.data();
+    }
+    g4_decode *d = nullptr;
+    if (throw_status(env, g4_decode_create(&sh, &w, &d))) return nullptr;
+    return make_num(env, (double)(uintptr_t)d);
+}
+
+napi_value DecodeDestroy(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    if (throw_status(env, g4_decode_destroy((g4_decode *)a.ptr(0)))) return nullptr;
+    return undefined(env);
+}
+
+// decodeStep(handle, tokens, nextTokens, stream?): launches only.
+napi_value DecodeStep(napi_env env, napi_callback_info info) {
+    Args a(env, info, 4);
+    int st = g4_decode_step((g4_decode *)a.ptr(0), (const int32_t *)a.ptr(1), (int32_t *)a.ptr(2),
+                            a.ptr(3));
+    if (throw_status(env, st)) return nullptr;
+    return undefined(env);
+}
+
+// decodeSetPosition(handle, pos, stream?): the position word written in stream order.
+napi_value DecodeSetPosition(napi_env env, napi_callback_info info) {
+    Args a(env, info, 3);
+    if (throw_status(env, g4_decode_set_position((g4_decode *)a.ptr(0), a.i32(1), a.ptr(2))))
+        return nullptr;
+    return undefined(env);
+}
+
+napi_value DecodeKv(napi_env env, napi_callback_info info) {
+    Args a(env, info, 2);
+    float *k = nullptr, *v = nullptr;
+    int64_t stride = 0;
+    if (throw_status(env, g4_decode_kv((g4_decode *)a.ptr(0), a.i32(1), &k, &v, &stride)))
+        return nullptr;
+    napi_value o;
+    napi_create_object(env, &o);
+    set_num(env, o, "k", (double)(uintptr_t)k);
+    set_num(env, o, "v", (double)(uintptr_t)v);
+    set_num(env, o, "rowStride", (double)stride);
+    return o;
+}
+
+napi_value DecodeBuffer(napi_env env, napi_callback_info info) {
+    Args a(env, info, 2);
+    char name[64] = {0};
+    size_t n = 0;
+    if (a.size() < 2 || napi_get_value_string_utf8(env, a.v[1], name, sizeof name, &n) != napi_ok) {
+        throw_type(env, "decodeBuffer(handle, name)");
+        return nullptr;
+    }
+    void *p = nullptr;
+    size_t bytes = 0;
+    if (throw_status(env, g4_decode_buffer((g4_decode *)a.ptr(0), name, &p, &bytes))) return nullptr;
+    napi_value o;
+    napi_create_object(env, &o);
+    set_num(env, o, "addr", (double)(uintptr_t)p);
+    set_num(env, o, "bytes", (double)bytes);
+    return o;
+}
+
+napi_value DecodeSetStop(napi_env env, napi_callback_info info) {
+    Args a(env, info, 2);
+    if (throw_status(env, g4_decode_set_stop((g4_decode *)a.ptr(0), a.i32(1, -1)))) return nullptr;
+    return undefined(env);
+}
+
+napi_value QgemmNoalloc(napi_env env, napi_callback_info info) {
+    Args a(env, info, 13);
+    int st = g4_qgemm_noalloc(a.i32(0), a.ptr(1), (const float *)a.ptr(2), a.ptr(3), a.i32(4),
+                              a.ptr(5), a.i32(6), a.i32(7), a.i32(8), a.i32(9, 1), (float)a.num(10),
+                              (float)a.num(11), a.ptr(12));
+    if (throw_status(env, st)) return nullptr;
+    return undefined(env);
+}
+
 napi_value Init(napi_env env, napi_value exports) {
     struct Fn {
         const char *name;
@@ -520,6 +921,17 @@ napi_value Init(napi_env env, napi_value exports) {
         {"pleGather", PleGather}, {"pleGatherSplit", PleGatherSplit},
         {"planTableSplit", PlanTableSplit}, {"qgemvPlanCreate", QgemvPlanCreate},
         {"qgemvPlanLaunch", QgemvPlanLaunch}, {"qgemvPlanDestroy", QgemvPlanDestroy},
+        {"planGatherSplit", PlanGatherSplit}, {"qgemmNoalloc", QgemmNoalloc},
+        {"streamCreate", StreamCreate}, {"streamDestroy", StreamDestroy},
+        {"streamSynchronize", StreamSynchronize}, {"eventCreate", EventCreate},
+        {"eventRecord", EventRecord}, {"eventElapsedMs", EventElapsedMs},
+        {"eventDestroy", EventDestroy}, {"graphBeginCapture", GraphBeginCapture},
+        {"graphEndCapture", GraphEndCapture}, {"graphLaunch", GraphLaunch},
+        {"graphDestroy", GraphDestroy}, {"synchronizeAsync", SynchronizeAsync},
+        {"downloadAsync", DownloadAsync}, {"fillHashF32", FillHashF32}, {"fillHashU8", FillHashU8},
+        {"decodeCreate", DecodeCreate}, {"decodeDestroy", DecodeDestroy},
+        {"decodeStep", DecodeStep}, {"decodeSetPosition", DecodeSetPosition},
+        {"decodeKv", DecodeKv}, {"decodeBuffer", DecodeBuffer}, {"decodeSetStop", DecodeSetStop},
     };
     for (const Fn &f : fns) {
         napi_value v;

@@ -50,12 +50,57 @@ class DeviceBuffer {
     return b;
   }
 
-  upload(array) { g4().upload(this.addr, array); }
-  download() { return g4().download(this.addr, this.bytes); }
-  fill(byte) { g4().fill(this.addr, byte, this.bytes); }
+  upload(array, stream) { g4().upload(this.addr, array, streamHandle(stream)); }
+  download(stream) { return g4().download(this.addr, this.bytes, streamHandle(stream)); }
+  /** Promise<ArrayBuffer>: the copy waits on a worker thread, after the stream's queued work. */
+  downloadAsync(stream) { return g4().downloadAsync(this.addr, this.bytes, streamHandle(stream)); }
+  fill(byte, stream) { g4().fill(this.addr, byte, this.bytes, streamHandle(stream)); }
   free() {
     if (this.addr) g4().free(this.addr);
     this.addr = 0;
+  }
+}
+
+/** A stream argument as the addon takes it: a Stream, a raw handle, or undefined (default). */
+function streamHandle(stream) {
+  if (stream === undefined || stream === null) return 0;
+  return typeof stream === 'number' ? stream : stream.handle;
+}
+
+/**
+ * A HIP stream (runtime.ts's queue). Work enqueued on one stream runs in order; synchronize()
+ * blocks, synchronizeAsync() returns a Promise and leaves the event loop free.
+ */
+class Stream {
+  constructor() { this.handle = g4().streamCreate(); }
+  synchronize() { g4().streamSynchronize(this.handle); }
+  synchronizeAsync() { return g4().synchronizeAsync(this.handle); }
+  destroy() {
+    if (this.handle) g4().streamDestroy(this.handle);
+    this.handle = 0;
+  }
+}
+
+/** A captured sequence of enqueues on a stream, replayed with one launch (the cached encode). */
+class Graph {
+  constructor(stream, record) {
+    this.stream = stream;
+    g4().graphBeginCapture(stream.handle);
+    let ok = false;
+    try {
+      record();
+      ok = true;
+    } finally {
+      const h = g4().graphEndCapture(stream.handle);
+      this.handle = ok ? h : 0;
+      if (!ok && h) g4().graphDestroy(h);
+    }
+  }
+
+  launch(stream) { g4().graphLaunch(this.handle, streamHandle(stream || this.stream)); }
+  destroy() {
+    if (this.handle) g4().graphDestroy(this.handle);
+    this.handle = 0;
   }
 }
 
@@ -72,27 +117,27 @@ function num(params, key, dflt) {
 // ---- the registry seam ------------------------------------------------------------------------
 
 function gemvKernel(bits, wide) {
-  return ({ inputs, output, params }) => {
+  return ({ inputs, output, params, stream }) => {
     need(inputs, ['wq', 'scales', 'x'], `qgemv-${bits}bit`);
     g4().qgemv(bits, inputs.wq.addr, inputs.scales.addr, inputs.x.addr, inputs.x.kind, output.addr,
       output.kind, num(params, 'k', 0), num(params, 'numRows', 0), wide ? num(params, 'cols', 1) : 1,
-      num(params, 'inScale', 0), num(params, 'outScale', 0));
+      num(params, 'inScale', 0), num(params, 'outScale', 0), streamHandle(stream));
   };
 }
 
 function gemmKernel(bits) {
-  return ({ inputs, output, params }) => {
+  return ({ inputs, output, params, stream }) => {
     need(inputs, ['wq', 'scales', 'x'], bits === 4 ? 'qgemm-4bit' : 'qmatmul-8bit');
     g4().qgemm(bits, inputs.wq.addr, inputs.scales.addr, inputs.x.addr, inputs.x.kind, output.addr,
       output.kind, num(params, 'k', 0), num(params, 'numRows', 0), num(params, 'mCols', 1),
-      num(params, 'inScale', 0), num(params, 'outScale', 0));
+      num(params, 'inScale', 0), num(params, 'outScale', 0), streamHandle(stream));
   };
 }
 
 // qkv-batch-4bit / gate-up-batch-4bit (projectionBatch.ts:85-128): the bound output is projection
 // `outputIndex`; the others arrive as inputs out0.. .
 function batchKernel(count) {
-  return ({ inputs, output, params }) => {
+  return ({ inputs, output, params, stream }) => {
     const outIndex = num(params, 'outputIndex', count - 1);
     if (outIndex < 0 || outIndex >= count) throw new Error('invalid batch output index');
     const idx = Array.from({ length: count }, (_, i) => i);
@@ -102,19 +147,19 @@ function batchKernel(count) {
     if (!inputs.x || ws.concat(ss, outs).some(b => !b)) {
       throw new Error('batched projection is missing an input buffer');
     }
-    g4().projectionBatch(4, count, ws.map(b => b.addr), ss.map(b => b.addr), inputs.x.addr,
+    g4().projectionBatch(4, ws.map(b => b.addr), ss.map(b => b.addr), inputs.x.addr,
       inputs.x.kind, outs.map(b => b.addr), output.kind, idx.map(i => num(params, `rows${i}`, 0)),
       idx.map(i => num(params, `inScale${i}`, 0)), idx.map(i => num(params, `outScale${i}`, 0)),
-      num(params, 'k', 0));
+      num(params, 'k', 0), streamHandle(stream));
   };
 }
 
 function splitKernel(bits) {
-  return ({ inputs, output, params }) => {
+  return ({ inputs, output, params, stream }) => {
     need(inputs, ['wq', 'scales', 'x'], `qgemv-${bits}bit-split`);
     g4().qgemvSplit(bits, inputs.wq.addr, inputs.scales.addr, inputs.x.addr, inputs.x.kind,
       output.addr, num(params, 'k', 0), num(params, 'numRows', 0), num(params, 'kSplits', 1),
-      num(params, 'exact', 0) ? 1 : 0, num(params, 'inScale', 0));
+      num(params, 'exact', 0) ? 1 : 0, num(params, 'inScale', 0), streamHandle(stream));
   };
 }
 
@@ -122,17 +167,17 @@ function splitKernel(bits) {
 // 19-31): gate and up bound in place of x, upOffset selecting the per-layer row.
 function geluKernel(bits, split) {
   const who = split ? `qgemv-${bits}bit-gelu-exact-split` : `qgemv-${bits}bit-gelu`;
-  return ({ inputs, output, params }) => {
+  return ({ inputs, output, params, stream }) => {
     need(inputs, ['wq', 'scales', 'gate', 'up'], who);
     const head = [bits, inputs.wq.addr, inputs.scales.addr, inputs.gate.addr, inputs.gate.kind,
       inputs.up.addr, inputs.up.kind, num(params, 'upOffset', 0), output.addr];
     const scales = [num(params, 'gateScale', 0), num(params, 'upScale', 0)];
     if (split) {
       g4().qgemvGeluSplit(...head, num(params, 'k', 0), num(params, 'numRows', 0),
-        num(params, 'kSplits', 1), 1, num(params, 'inScale', 0), ...scales);
+        num(params, 'kSplits', 1), 1, num(params, 'inScale', 0), ...scales, streamHandle(stream));
     } else {
       g4().qgemvGelu(...head, output.kind, num(params, 'k', 0), num(params, 'numRows', 0),
-        num(params, 'inScale', 0), num(params, 'outScale', 0), ...scales);
+        num(params, 'inScale', 0), num(params, 'outScale', 0), ...scales, streamHandle(stream));
     }
   };
 }
@@ -142,7 +187,7 @@ const PLE_GROUP_SIZE = 256;
 
 function gatherKernel(sliced) {
   const who = sliced ? 'ple-gather-4bit-sliced' : 'ple-gather-4bit';
-  return ({ inputs, output, params }) => {
+  return ({ inputs, output, params, stream }) => {
     need(inputs, ['codes', 'scales', 'ids'], who);
     const cols = num(params, 'cols', PLE_COLS);
     const group = num(params, 'groupSize', PLE_GROUP_SIZE);
@@ -157,11 +202,12 @@ function gatherKernel(sliced) {
       }
     }
     g4().pleGather(inputs.codes.addr, inputs.scales.addr, inputs.scales.kind, inputs.ids.addr,
-      output.addr, output.kind, slots, cols, group, cols / group, sliced ? 1 : 0, start, count);
+      output.addr, output.kind, slots, cols, group, cols / group, sliced ? 1 : 0, start, count,
+      streamHandle(stream));
   };
 }
 
-const KERNELS = {
+const BINDS = {
   'qgemv-4bit': gemvKernel(4, false),
   'qgemv-8bit': gemvKernel(8, false),
   'qgemv-4bit-m2': gemvKernel(4, true),
@@ -177,27 +223,328 @@ const KERNELS = {
   'qgemv-4bit-gelu-exact-split': geluKernel(4, true),
   'qgemv-4bit-split': splitKernel(4),
   'qgemv-8bit-split': splitKernel(8),
-  'qgemv-merge': ({ inputs, output, params }) => {
+  'qgemv-merge': ({ inputs, output, params, stream }) => {
     if (!inputs.part) throw new Error('qgemv-merge needs an input named part');
     g4().qgemvMerge(inputs.part.addr, output.addr, output.kind, num(params, 'numRows', 0),
-      num(params, 'kSplits', 0), num(params, 'outScale', 0));
+      num(params, 'kSplits', 0), num(params, 'outScale', 0), streamHandle(stream));
   },
-  'qgemv-exact-merge': ({ inputs, output, params }) => {
+  'qgemv-exact-merge': ({ inputs, output, params, stream }) => {
     need(inputs, ['part', 'scales'], 'qgemv-exact-merge');
     g4().qgemvExactMerge(inputs.part.addr, inputs.scales.addr, output.addr, output.kind,
       num(params, 'numRows', 0), num(params, 'kSplits', 0), num(params, 'inScale', 0),
-      num(params, 'outScale', 0));
+      num(params, 'outScale', 0), streamHandle(stream));
   },
   'ple-gather-4bit': gatherKernel(false),
   'ple-gather-4bit-sliced': gatherKernel(true),
 };
 
-/** Run registry kernel `name` with the reference's bind input ({inputs, output, params}). */
+// ---- known-answer cases (registry.ts:72-119: a kernel without cases is not registered) --------
+//
+// The reference's cases name manifest entries its excluded scripts generated; none ship. These are
+// built from the reference's own fixture recipes instead (qgemv.ts:1365-1388: activations on the
+// 1/8 grid, the scales 0.1875 / 0.015625 / 0.0625, ten rows against a workgroup of four, eleven
+// columns against a tile of eight), so every product, sum and scale is a short dyadic rational
+// that f32 holds exactly: the expected outputs below are computed in JS doubles with no rounding
+// to argue about, and every case gates at zero (tolAbs 0, the registry's default).
+
+function rng(seed) {  // mulberry32: deterministic case inputs
+  let t = seed >>> 0;
+  return () => {
+    t = (t + 0x6D2B79F5) >>> 0;
+    let r = Math.imul(t ^ (t >>> 15), 1 | t);
+    r = (r + Math.imul(r ^ (r >>> 7), 61 | r)) ^ r;
+    return ((r ^ (r >>> 14)) >>> 0) / 4294967296;
+  };
+}
+function randInt(next, lo, hi) { return lo + Math.floor(next() * (hi - lo + 1)); }
+const f32 = Math.fround;
+/** srqCodes (quant.ts:309-334) on exact quotients: round half to even, clamp to int8. */
+function snap(v, s) {
+  const q = v / s;
+  let r = Math.round(q);
+  if (Math.abs(q % 1) === 0.5 && r % 2 !== 0) r -= 1;
+  return Math.max(-128, Math.min(127, r));
+}
+const GRID_SCALES = [0.1875, 0.015625, 0.0625];
+
+/** Weights (packed bytes and codes), scales and x [cols][k] on the grid. */
+function gridOperands(seed, bits, rows, k, cols) {
+  const next = rng(seed);
+  const codes = new Int8Array(rows * k);
+  for (let i = 0; i < codes.length; ++i) codes[i] = bits === 4 ? randInt(next, -8, 7) : randInt(next, -127, 127);
+  let wq;
+  if (bits === 4) {
+    wq = new Uint8Array(rows * k / 2);
+    for (let i = 0; i < wq.length; ++i) wq[i] = ((codes[2 * i] + 8) & 15) | (((codes[2 * i + 1] + 8) & 15) << 4);
+  } else {
+    wq = new Uint8Array(codes.buffer.slice(0));
+  }
+  const scales = new Float32Array(rows);
+  for (let r = 0; r < rows; ++r) scales[r] = GRID_SCALES[r % 3];
+  const x = new Float32Array(cols * k);
+  for (let i = 0; i < x.length; ++i) x[i] = randInt(next, -16, 16) / 8;
+  return { codes, wq, scales, x };
+}
+
+/** qgemvOracle (qgemv.ts:1131-1176) on the grid: dst[col * rows + row], f32 (q * out) or int8 q. */
+function gridExpected(op, rows, k, cols, inScale, outScale, kind) {
+  const out = kind === KIND.i8 ? new Int8Array(cols * rows) : new Float32Array(cols * rows);
+  for (let c = 0; c < cols; ++c) {
+    for (let r = 0; r < rows; ++r) {
+      let sum = 0;
+      for (let i = 0; i < k; ++i) {
+        const x = op.x[c * k + i];
+        sum += op.codes[r * k + i] * (inScale !== 0 ? snap(x, inScale) : x);
+      }
+      const y = f32(f32((inScale !== 0 ? inScale : 1) * op.scales[r]) * sum);
+      const q = outScale !== 0 ? snap(y, outScale) : null;
+      out[c * rows + r] = kind === KIND.i8 ? q : (q === null ? y : q * outScale);
+    }
+  }
+  return out;
+}
+
+function linearCase(name, seed, bits, rows, k, cols, inScale, outScale, kind, paramsExtra) {
+  const op = gridOperands(seed, bits, rows, k, cols);
+  const params = Object.assign({ k, numRows: rows, inScale, outScale }, paramsExtra || {});
+  return {
+    name,
+    inputs: { wq: op.wq, scales: op.scales, x: op.x },
+    params,
+    expected: gridExpected(op, rows, k, cols, inScale, outScale, kind),
+    note: 'the qgemv.ts:1365-1388 exact-grid recipe: exact in f32, so it gates at zero',
+  };
+}
+
+function linearCases(bits, colsParam, cols) {
+  const k = bits === 4 ? 256 : 128;
+  const extra = colsParam ? { [colsParam]: cols } : {};
+  return [
+    linearCase('grid-uncalibrated', 11 + bits, bits, 10, k, cols, 0, 0, KIND.f32, extra),
+    linearCase('grid-srq-int8-out', 12 + bits, bits, 10, k, cols, 0.125, 0.0625, KIND.i8, extra),
+    linearCase('grid-srq-f32-out', 13 + bits, bits, 10, k, cols, 0.125, 0.0625, KIND.f32, extra),
+  ];
+}
+
+function batchCases(count) {
+  const rows = 8;
+  const k = 256;
+  const pairs = [[0, 0], [0.125, 0.0625], [0.015625, 0]];
+  const ops = Array.from({ length: count }, (_, i) => gridOperands(40 + i, 4, rows, k, 1));
+  ops.forEach(op => op.x.set(ops[0].x));  // one x for every projection
+  const out = [];
+  for (let oi = 0; oi < count; ++oi) {
+    const inputs = { x: ops[0].x };
+    const params = { k, outputIndex: oi };
+    for (let i = 0; i < count; ++i) {
+      inputs[`w${i}`] = ops[i].wq;
+      inputs[`s${i}`] = ops[i].scales;
+      params[`rows${i}`] = rows;
+      params[`inScale${i}`] = pairs[i][0];
+      params[`outScale${i}`] = pairs[i][1];
+      if (i !== oi) inputs[`out${i}`] = { bytes: rows * 4, kind: KIND.f32 };
+    }
+    out.push({
+      name: `mixed-routing-output-${oi}`, inputs, params,
+      expected: gridExpected(ops[oi], rows, k, 1, pairs[oi][0], pairs[oi][1], KIND.f32),
+      note: 'projectionBatch.ts:130-150: uncalibrated, SRQ and clamped SRQ in one dispatch',
+    });
+  }
+  return out;
+}
+
+/** The split band of qgemv.ts:521-548 (32-word iterations, the tail in the band past kIters). */
+function splitBands(bits, k, splits, exact) {
+  const cpw = bits === 4 ? 8 : 4;
+  const kWords = k / cpw;
+  const kIters = Math.floor(kWords / 32);
+  const slots = kIters + (exact ? (kWords % 32 !== 0 ? 1 : 0) : 1);
+  const per = Math.ceil(slots / splits);
+  const bands = [];
+  for (let s = 0; s < splits; ++s) {
+    const lo = Math.min(s * per, slots);
+    const hi = Math.min(lo + per, slots);
+    let wLo = lo * 32;
+    let wHi = Math.min(hi, kIters) * 32;
+    if (hi > kIters) wHi = kWords;
+    if (wLo > wHi) wLo = wHi;
+    bands.push([wLo * cpw, wHi * cpw]);
+  }
+  return bands;
+}
+
+function splitCase(bits, exact) {
+  const rows = 10;
+  const k = bits === 4 ? 1024 : 512;
+  const splits = 4;  // 1, 2, 4 or 8 (qgemv.ts:253)
+  const op = gridOperands(60 + bits, bits, rows, k, 1);
+  const inScale = 0.125;
+  const bands = splitBands(bits, k, splits, exact);
+  const part = new Float32Array(rows * splits);
+  for (let r = 0; r < rows; ++r) {
+    bands.forEach(([lo, hi], s) => {
+      let sum = 0;
+      for (let i = lo; i < hi; ++i) sum += op.codes[r * k + i] * snap(op.x[i], inScale);
+      part[r * splits + s] = exact ? sum : f32(f32(inScale * op.scales[r]) * sum);
+    });
+  }
+  return {
+    name: exact ? 'grid-exact-partials' : 'grid-scaled-partials',
+    inputs: { wq: op.wq, scales: op.scales, x: op.x },
+    params: { k, numRows: rows, kSplits: splits, exact: exact ? 1 : 0, inScale },
+    expected: part,
+  };
+}
+
+function mergeCases(exact) {
+  const rows = 10;
+  const splits = 4;
+  const next = rng(70);
+  const part = new Float32Array(rows * splits);
+  for (let i = 0; i < part.length; ++i) part[i] = exact ? randInt(next, -500, 500) : randInt(next, -64, 64) / 32;
+  const scales = new Float32Array(rows).map((_, r) => GRID_SCALES[r % 3]);
+  const expected = new Float32Array(rows);
+  for (let r = 0; r < rows; ++r) {
+    let t = 0;
+    for (let s = 0; s < splits; ++s) t += part[r * splits + s];
+    const y = exact ? f32(f32(0.125 * scales[r]) * t) : t;
+    expected[r] = snap(y, 0.0625) * 0.0625;
+  }
+  const inputs = exact ? { part, scales } : { part };
+  const params = exact ? { numRows: rows, kSplits: splits, inScale: 0.125, outScale: 0.0625 }
+    : { numRows: rows, kSplits: splits, outScale: 0.0625 };
+  return [{ name: exact ? 'integer-partials' : 'grid-partials', inputs, params, expected }];
+}
+
+/** gelu(g) is exact at g in {-8, -6, 0, 6, 8}: tanh saturates to +-1 in f32 (geluMul.ts:101-116). */
+function geluCases(bits, split) {
+  const rows = 10;
+  const k = bits === 4 ? 512 : 256;
+  const op = gridOperands(80 + bits, bits, rows, k, 1);
+  const next = rng(81);
+  const gate = new Float32Array(k).map(() => [-8, -6, 0, 6, 8][randInt(next, 0, 4)]);
+  const up = new Float32Array(k).map(() => randInt(next, -8, 8) / 8);
+  const act = new Float32Array(k).map((_, i) => (gate[i] > 0 ? gate[i] : 0) * up[i]);
+  const inScale = 0.125;
+  if (split) {
+    const bands = splitBands(bits, k, 2, true);
+    const part = new Float32Array(rows * 2);
+    for (let r = 0; r < rows; ++r) {
+      bands.forEach(([lo, hi], s) => {
+        let sum = 0;
+        for (let i = lo; i < hi; ++i) sum += op.codes[r * k + i] * snap(act[i], inScale);
+        part[r * 2 + s] = sum;
+      });
+    }
+    return [{ name: 'saturated-gelu-exact-partials', inputs: { wq: op.wq, scales: op.scales, gate, up },
+      params: { k, numRows: rows, kSplits: 2, inScale }, expected: part }];
+  }
+  const geluOp = { codes: op.codes, scales: op.scales, x: act };
+  return [{ name: 'saturated-gelu', inputs: { wq: op.wq, scales: op.scales, gate, up },
+    params: { k, numRows: rows, inScale, outScale: 0.0625 },
+    expected: gridExpected(geluOp, rows, k, 1, inScale, 0.0625, KIND.i8) }];
+}
+
+function gatherCase(sliced) {
+  const rows = 48;
+  const cols = 512;
+  const group = 256;
+  const next = rng(90);
+  const codes = new Uint8Array(rows * cols / 2).map(() => randInt(next, 0, 255));
+  const scales = new Float32Array(rows * 2).map(() => [0.0078125, 0.015625, 0.005859375][randInt(next, 0, 2)]);
+  const ids = new Int32Array([3, 40, 17, 47, 0, 3]);
+  const start = 16;
+  const count = 24;
+  const expected = new Float32Array(ids.length * cols);
+  ids.forEach((id, slot) => {
+    if (sliced && !(id >= start && id < start + count)) return;  // not this slice's: untouched
+    for (let c = 0; c < cols; ++c) {
+      const b = codes[id * cols / 2 + (c >> 1)];
+      const code = ((c & 1) ? b >> 4 : b & 15) - 8;
+      expected[slot * cols + c] = code * f32(16 * scales[id * 2 + Math.floor(c / group)]);
+    }
+  });
+  const table = sliced ? codes.slice(start * cols / 2, (start + count) * cols / 2) : codes;
+  const params = { slots: ids.length, cols, groupSize: group };
+  if (sliced) Object.assign(params, { sliceStartRow: start, sliceRowCount: count });
+  return [{ name: sliced ? 'one-slice-owner-writes' : 'whole-table', inputs: { codes: table, scales, ids },
+    params, expected, outputInit: sliced ? 'zero' : 'sentinel',
+    note: 'embedGather.ts:149-152, 188-196: (code - 8) * f32(16 * scale), a non-owner writes nothing' }];
+}
+
+function registered(name, bind, cases, note) { return { name, bind, cases, note }; }
+
+const KERNELS = {
+  'qgemv-4bit': registered('qgemv-4bit', BINDS['qgemv-4bit'], linearCases(4, null, 1)),
+  'qgemv-8bit': registered('qgemv-8bit', BINDS['qgemv-8bit'], linearCases(8, null, 1)),
+  'qgemv-4bit-m2': registered('qgemv-4bit-m2', BINDS['qgemv-4bit-m2'], linearCases(4, 'cols', 2)),
+  'qgemv-8bit-m2': registered('qgemv-8bit-m2', BINDS['qgemv-8bit-m2'], linearCases(8, 'cols', 2)),
+  'qgemm-4bit': registered('qgemm-4bit', BINDS['qgemm-4bit'], linearCases(4, 'mCols', 11)),
+  'qgemm-4bit-single': registered('qgemm-4bit-single', BINDS['qgemm-4bit-single'], linearCases(4, 'mCols', 1)),
+  'qgemm-4bit-prefill4': registered('qgemm-4bit-prefill4', BINDS['qgemm-4bit-prefill4'], linearCases(4, 'mCols', 40)),
+  'qmatmul-8bit': registered('qmatmul-8bit', BINDS['qmatmul-8bit'], linearCases(8, 'mCols', 3)),
+  'qkv-batch-4bit': registered('qkv-batch-4bit', BINDS['qkv-batch-4bit'], batchCases(3)),
+  'gate-up-batch-4bit': registered('gate-up-batch-4bit', BINDS['gate-up-batch-4bit'], batchCases(2)),
+  'qgemv-4bit-gelu': registered('qgemv-4bit-gelu', BINDS['qgemv-4bit-gelu'], geluCases(4, false)),
+  'qgemv-8bit-gelu': registered('qgemv-8bit-gelu', BINDS['qgemv-8bit-gelu'], geluCases(8, false)),
+  'qgemv-4bit-gelu-exact-split': registered('qgemv-4bit-gelu-exact-split',
+    BINDS['qgemv-4bit-gelu-exact-split'], geluCases(4, true)),
+  'qgemv-4bit-split': registered('qgemv-4bit-split', BINDS['qgemv-4bit-split'], [splitCase(4, false), splitCase(4, true)]),
+  'qgemv-8bit-split': registered('qgemv-8bit-split', BINDS['qgemv-8bit-split'], [splitCase(8, false), splitCase(8, true)]),
+  'qgemv-merge': registered('qgemv-merge', BINDS['qgemv-merge'], mergeCases(false)),
+  'qgemv-exact-merge': registered('qgemv-exact-merge', BINDS['qgemv-exact-merge'], mergeCases(true)),
+  'ple-gather-4bit': registered('ple-gather-4bit', BINDS['ple-gather-4bit'], gatherCase(false)),
+  'ple-gather-4bit-sliced': registered('ple-gather-4bit-sliced', BINDS['ple-gather-4bit-sliced'], gatherCase(true)),
+};
+
+/**
+ * Run registry kernel `name` with the reference's bind input ({inputs, output, params}, plus an
+ * optional `stream`: a Stream or handle; the call only enqueues).
+ */
 function bind(name, input) {
-  const run = KERNELS[name];
-  if (!run) throw Object.assign(new Error(`gemma4 engine: no registered kernel named ${name}`), { status: 2 });
-  run(input);
+  const k = KERNELS[name];
+  if (!k) throw Object.assign(new Error(`gemma4 engine: no registered kernel named ${name}`), { status: 2 });
+  k.bind(input);
   return { kernel: name };
+}
+
+function kindOfArray(a) {
+  if (a instanceof Float32Array) return KIND.f32;
+  if (a instanceof Int32Array) return KIND.i32;
+  return KIND.i8;
+}
+
+/**
+ * Runs every case of `name` (or of every kernel) on the device and compares the output bytes with
+ * the expected ones (the registry's zero tolerance): [{kernel, case, ok, mismatches}].
+ */
+function runCases(name, stream) {
+  const names = name ? [name] : Object.keys(KERNELS);
+  const results = [];
+  for (const n of names) {
+    for (const c of KERNELS[n].cases) {
+      const bufs = [];
+      const inputs = {};
+      for (const key of Object.keys(c.inputs)) {
+        const v = c.inputs[key];
+        const b = ArrayBuffer.isView(v) ? DeviceBuffer.from(v, kindOfArray(v))
+          : new DeviceBuffer(v.bytes, v.kind);
+        inputs[key] = b;
+        bufs.push(b);
+      }
+      const output = new DeviceBuffer(c.expected.byteLength, kindOfArray(c.expected));
+      bufs.push(output);
+      output.fill(c.outputInit === 'zero' ? 0 : 0x7b, stream);
+      bind(n, { inputs, output, params: c.params, stream });
+      const got = new Uint8Array(output.download(stream));
+      const want = new Uint8Array(c.expected.buffer, c.expected.byteOffset, c.expected.byteLength);
+      let mismatches = 0;
+      for (let i = 0; i < want.length; ++i) if (got[i] !== want[i]) mismatches += 1;
+      results.push({ kernel: n, case: c.name, ok: mismatches === 0, mismatches });
+      bufs.forEach(b => b.free());
+    }
+  }
+  return results;
 }
 
 // ---- pure host mirrors (execute.ts:349-430) ------------------------------------------------------
@@ -253,6 +600,20 @@ function matmulKernel(geometry, stepKernel) {
 /** planTableSplit (tableSplit.ts:125-215), computed by the library (pure host code). */
 function planTableSplit(input) { return g4().planTableSplit(input); }
 
+/**
+ * planGatherSplit (tableSplit.ts:257-287): the packed codes and the f32 scales planned separately
+ * under one device's limits; scalesSingle is what the sliced gather assumes.
+ */
+function planGatherSplit(name, rows, codeRowBytes, scalesPerRow, limits) {
+  const plans = g4().planGatherSplit(rows, codeRowBytes, scalesPerRow, limits);
+  plans.name = name;
+  plans.note = plans.scalesSingle
+    ? `${name} codes: ${plans.codes.slices.length} slice(s); ${name} scales: one buffer, which is what the gather kernel assumes.`
+    : `${name} scales do NOT fit in one binding on this adapter, and the sliced gather addresses `
+      + 'scales by the absolute vocabulary row, so this configuration is not served.';
+  return plans;
+}
+
 /** sliceForRow (tableSplit.ts:218-223): the slice index carrying `row`, or -1. */
 function sliceForRow(slices, row) {
   for (const s of slices) if (row >= s.startRow && row < s.startRow + s.rowCount) return s.index;
@@ -287,12 +648,46 @@ class GemvPlan {
   }
 }
 
+/**
+ * The native decode-step runner (include/g4decode.h) over a model already in device memory:
+ * shape and weights use the C structs' field names (weights: device addresses, `layer` one object
+ * per layer, optional `ple_slices` [{codes, start_row, row_count}] for a split PLE table).
+ * step() and setPosition() only enqueue on the given stream, so several tokens' steps can be in
+ * flight at once (the reference's lookahead, plan.ts:942-973): step t+1 reads the next-token
+ * buffer step t writes, and the host awaits only its downloads.
+ */
+class Decoder {
+  constructor(shape, weights) {
+    this.shape = shape;
+    this.handle = g4().decodeCreate(shape, weights);
+  }
+
+  setPosition(pos, stream) { g4().decodeSetPosition(this.handle, pos, streamHandle(stream)); }
+  step(tokens, nextTokens, stream) {
+    g4().decodeStep(this.handle, tokens.addr, nextTokens.addr, streamHandle(stream));
+  }
+
+  /** A named work buffer of the last step: {addr, bytes} ("logits", "hidden", "per_layer", ...). */
+  buffer(name) { return g4().decodeBuffer(this.handle, name); }
+  kv(layer) { return g4().decodeKv(this.handle, layer); }
+  setStop(lastLayer) { g4().decodeSetStop(this.handle, lastLayer); }
+  destroy() {
+    if (this.handle) g4().decodeDestroy(this.handle);
+    this.handle = 0;
+  }
+}
+
 module.exports = {
   KIND,
   DeviceBuffer,
   KERNELS,
   kernelNames: () => Object.keys(KERNELS),
   bind,
+  runCases,
+  Stream,
+  Graph,
+  Decoder,
+  planGatherSplit,
   linearParams,
   gemvWide,
   pleKernel,
@@ -305,6 +700,8 @@ module.exports = {
   deviceCount: () => g4().deviceCount(),
   setDevice: d => g4().setDevice(d),
   synchronize: () => g4().synchronize(),
+  synchronizeAsync: stream => g4().synchronizeAsync(streamHandle(stream)),
+  qgemmNoalloc: (...args) => g4().qgemmNoalloc(...args),
   pleGatherSplit: (...args) => g4().pleGatherSplit(...args),
   addon: g4,
 };

@@ -80,6 +80,30 @@ int g4_st_read(const g4_st *st, const char *name, int64_t offset, void *host_dst
 /* The whole tensor into device memory (a pinned bounce buffer, copies on `stream`, synchronous). */
 int g4_st_upload(const g4_st *st, const char *name, void *device_dst, size_t dst_bytes,
                  void *stream);
+/*
+ * A tensor too large for one buffer, carried as one device buffer per slice (buffers.ts:291-327
+ * declareSplit, :369-423 uploadWeight -> uploadSplitWeight). slices[i] gives the byte range
+ * {byte_offset, byte_length} of slice i (a g4_table_slice from g4_plan_table_split); the ranges
+ * must partition the tensor in offset order with four-byte-aligned starts, and slice_dst[i] holds
+ * at least slices[i].byte_length bytes. The payload is read in pieces of up to 64 MiB; each
+ * piece's intersection with each slice is written at its offset inside that slice (a piece that
+ * straddles a boundary is two writes). Synchronous, like g4_st_upload.
+ */
+int g4_st_upload_split(const g4_st *st, const char *name, const g4_table_slice *slices,
+                       int num_slices, void *const *slice_dst, void *stream);
+
+/*
+ * The PLE table's split for a device (engine.ts:308-345 declarePleSplit): rows from the tensor's
+ * first dimension, row bytes = bytes / rows (refused when that is not whole), then
+ * g4_plan_gather_split with `groups_per_row` f32 scales per row. Refuses an infeasible code plan
+ * and a plan whose scale table does not fit one buffer (the sliced gather addresses scales by the
+ * absolute row). plans->codes.single means no split is needed (upload the table whole); otherwise
+ * up to max_slices code slices are written for g4_st_upload_split.
+ */
+int g4_st_plan_ple_split(const g4_st *st, const char *codes_name, int64_t groups_per_row,
+                         const g4_gather_limits *limits, g4_gather_split_plans *plans,
+                         g4_table_slice *slices, int64_t max_slices);
+
 /* A BF16, F16 or F32 tensor widened exactly to f32 in device memory (the norm weights, the layer
  * scalar; quant.ts:400-411 bf16ToF32). */
 int g4_st_upload_f32(const g4_st *st, const char *name, float *device_dst, int64_t count,

@@ -172,6 +172,16 @@ typedef struct g4_decode_weights {
     const float *rope_local_cos, *rope_local_sin;   /* [kv_capacity][head_dim/2] */
     const float *rope_global_cos, *rope_global_sin; /* [kv_capacity][head_dim/2] */
     const g4_decode_layer *layer; /* host array of `layers` entries (copied by create) */
+    /* Optional split storage of ple_table (buffers.ts sliceName(PLE_CODES, i); plan.ts:709-725 one
+     * gather step per slice, run here as one fused launch): with ple_num_slices >= 1, slice i is a
+     * device buffer of vocabulary rows [ple_slice_start[i], ple_slice_start[i] + ple_slice_rows[i])
+     * and ple_table may be NULL. The slices must partition [0, vocab) in order (at most 16). The
+     * scales stay whole (ple_table_s), addressed by the absolute row. Host arrays, copied by
+     * create. ple_num_slices 0: the single ple_table. */
+    int ple_num_slices;
+    const void *const *ple_slice_codes;
+    const int64_t *ple_slice_start;
+    const int64_t *ple_slice_rows;
 } g4_decode_weights;
 
 typedef struct g4_decode g4_decode;
@@ -187,6 +197,12 @@ int g4_decode_kv(g4_decode *d, int layer, float **k, float **v, int64_t *row_str
 
 /* The device int32 the step reads its position from (set it with a copy before each step). */
 int g4_decode_position(g4_decode *d, int32_t **pos);
+
+/* Sets that word in stream order (a one-thread kernel: no host copy, graph-capturable), so the
+ * steps of several tokens can be enqueued back to back, each reading the tokens the previous one
+ * wrote, with the host waiting only on what it reads back (the reference's lookahead keeps steps
+ * in flight the same way, plan.ts:942-973). */
+int g4_decode_set_position(g4_decode *d, int pos, void *stream);
 
 /*
  * One decode step for every row: token ids [batch] (device int32) at the position held by the

@@ -323,6 +323,31 @@ int g4_plan_table_split(const g4_table_split_input *input, g4_table_split_plan *
 /* tableSplit.ts:218-223 sliceForRow: the slice index carrying `row`, or -1. */
 int64_t g4_slice_for_row(const g4_table_slice *slices, int64_t num_slices, int64_t row);
 
+/* tableSplit.ts:226-230 GatherLimits: the limits half of a device profile. */
+typedef struct g4_gather_limits {
+    int64_t max_storage_buffer_binding_size;
+    int64_t max_buffer_size;
+    int64_t max_storage_buffers_per_shader_stage;
+} g4_gather_limits;
+
+/* tableSplit.ts:232-245 GatherSplitPlans (without the note string): both tables of one gather.
+ * scales_single: the scale table is one buffer, which the sliced gather assumes (it addresses
+ * scales by the absolute vocabulary row, embedGather.ts:248). */
+typedef struct g4_gather_split_plans {
+    g4_table_split_plan codes;
+    g4_table_split_plan scales;
+    int32_t scales_single;
+} g4_gather_split_plans;
+
+/* tableSplit.ts:257-287 planGatherSplit: plans the packed codes ([rows][code_row_bytes]) and the
+ * f32 scales ([rows][scales_per_row]) with planTableSplit under the same limits and the default
+ * slice cap. Up to max_code_slices / max_scale_slices slices are written (either array may be NULL
+ * with a 0 count). Pure host code. */
+int g4_plan_gather_split(int64_t rows, int64_t code_row_bytes, int64_t scales_per_row,
+                         const g4_gather_limits *limits, g4_gather_split_plans *plans,
+                         g4_table_slice *code_slices, int64_t max_code_slices,
+                         g4_table_slice *scale_slices, int64_t max_scale_slices);
+
 #ifdef __cplusplus
 }
 #endif

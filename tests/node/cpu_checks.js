@@ -60,4 +60,30 @@ assert.strictEqual(h.sliceForRow(five.slices, 262144), -1);
 const disp = h.slicedGatherDispatches(five, 64);
 assert.strictEqual(disp.length, 5);
 assert.deepStrictEqual(disp[4].params, { slots: 64, sliceStartRow: 4 * 59904, sliceRowCount: 22528 });
+// planGatherSplit (tableSplit.ts:257-287): nine code slices and one scale buffer at the floor
+const ple = h.planGatherSplit('ple', 262144, 4480, 35, { maxStorageBufferBindingSize: 128 * 2 ** 20,
+  maxBufferSize: 128 * 2 ** 20, maxStorageBuffersPerShaderStage: 10 });
+assert.strictEqual(ple.codes.slices.length, 9);
+assert.strictEqual(ple.scales.totalBytes, 36700160);
+assert.strictEqual(ple.scalesSingle, true);
+const tinyLim = h.planGatherSplit('ple', 262144, 4480, 35, { maxStorageBufferBindingSize: 16 * 2 ** 20,
+  maxBufferSize: 16 * 2 ** 20, maxStorageBuffersPerShaderStage: 10 });
+assert.strictEqual(tinyLim.scalesSingle, false);
+assert.ok(tinyLim.note.includes('NOT fit in one binding'));
+
+// every registry entry carries known-answer cases (registry.ts:106: at least one, or it is not
+// registered), each with inputs, params and an expected output
+for (const name of h.kernelNames()) {
+  const k = h.KERNELS[name];
+  assert.ok(Array.isArray(k.cases) && k.cases.length >= 1, name);
+  for (const c of k.cases) {
+    assert.ok(c.name && c.inputs && c.params && ArrayBuffer.isView(c.expected), `${name}/${c.name}`);
+    assert.ok(c.expected.length > 0, `${name}/${c.name}`);
+  }
+}
+// the gelu cases saturate tanh, so their expected codes are not all zero
+assert.ok(h.KERNELS['qgemv-4bit-gelu'].cases[0].expected.some(v => v !== 0));
+assert.ok(h.KERNELS['ple-gather-4bit-sliced'].cases[0].expected.some(v => v !== 0));
+assert.strictEqual(typeof h.Stream, 'function');
+assert.strictEqual(typeof h.Decoder, 'function');
 console.log('node host cpu checks ok');

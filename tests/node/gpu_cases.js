@@ -1,0 +1,51 @@
+'use strict';
+// Every registry kernel's known-answer cases on the GPU through the Node host (runCases, on a
+// stream of its own), then the asynchronous boundary: a bind enqueued on a stream and read back by
+// downloadAsync, with the event loop shown to run while the device works. Prints one JSON line.
+const path = require('path');
+const h = require(path.join(__dirname, '..', '..', 'gemma4-webgpu-engine_amd', 'host', 'index.js'));
+
+async function main() {
+  h.setDevice(0);
+  const stream = new h.Stream();
+  const results = h.runCases(null, stream);
+  const failed = results.filter(r => !r.ok);
+  console.log(`registry cases: ${results.length} run, ${failed.length} failed`);
+  // async: the config-0 shape on the stream, awaited without blocking the loop
+  const c = h.KERNELS['qgemv-4bit'].cases[1];
+  const inputs = {};
+  for (const k of Object.keys(c.inputs)) inputs[k] = h.DeviceBuffer.from(c.inputs[k]);
+  const out = new h.DeviceBuffer(c.expected.byteLength, h.KIND.i8);
+  out.fill(0x7b, stream);
+  h.bind('qgemv-4bit', { inputs, output: out, params: c.params, stream });
+  let ticks = 0;
+  const timer = setInterval(() => { ticks += 1; }, 0);
+  const pending = out.downloadAsync(stream);
+  const got = new Int8Array(await pending);
+  await stream.synchronizeAsync();
+  clearInterval(timer);
+  let asyncOk = got.every((v, i) => v === c.expected[i]);
+  // the same bind captured into a graph and replayed (the reference's cached per-token encode)
+  const graph = new h.Graph(stream, () => h.bind('qgemv-4bit', { inputs, output: out, params: c.params, stream }));
+  for (let rep = 0; rep < 3; ++rep) {
+    out.fill(0x7b, stream);
+    graph.launch();
+    const again = new Int8Array(await out.downloadAsync(stream));
+    asyncOk = asyncOk && again.every((v, i) => v === c.expected[i]);
+  }
+  graph.destroy();
+  // an async wait on a refused copy (a NULL address, refused on the host) rejects with the
+  // library's message
+  let rejected = null;
+  try {
+    await h.addon().downloadAsync(0, 64, stream.handle);
+  } catch (e) {
+    rejected = e.message;
+  }
+  Object.values(inputs).forEach(b => b.free());
+  out.free();
+  stream.destroy();
+  console.log(JSON.stringify({ cases: results.length, failed, asyncOk, rejected: rejected !== null }));
+  if (failed.length || !asyncOk || rejected === null) process.exit(1);
+}
+main().catch(e => { console.error(e); process.exit(1); });

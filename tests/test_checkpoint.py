@@ -218,3 +218,40 @@ def test_text_allow_list_counts():
     assert "model.language_model.layers.14.self_attn.k_proj.weight" in names
     assert "model.language_model.layers.15.self_attn.k_proj.weight" not in names
     assert "lm_head.weight" not in names and "lm_head.input_activation_scale" in names
+
+
+def test_split_upload_and_plan_refusals(g4, tmp_path):
+    """declareSplit's refusals (buffers.ts:291-327) and declarePleSplit's (engine.ts:308-345),
+    checked before any device work, so they run without a GPU."""
+    import g4ckpt as ck
+    from safetensors.numpy import save_file
+    name = "model.language_model.embed_tokens_per_layer.embedding_quantized"
+    codes = np.zeros((4096, 4480), np.uint8)
+    save_file({name: codes, name.replace("quantized", "scale"): np.zeros((4096, 35), np.float32)},
+              str(tmp_path / "p.safetensors"))
+    with ck.Directory.open(str(tmp_path / "p.safetensors")) as d:
+        # a 4 GiB device: one buffer, no slices
+        plans, slices = d.plan_ple_split(name, 35, 4_294_967_292, 4_294_967_292)
+        assert plans.codes.single and slices == []
+        # 4 MiB bindings: 5 code slices of 928 rows (16-row aligned), scales 573,440 B whole
+        plans, slices = d.plan_ple_split(name, 35, 4 << 20, 4 << 20)
+        assert plans.scales_single and [s.row_count for s in slices] == [928] * 4 + [384]
+        # 256 KiB bindings: the scales split too, which the sliced gather cannot address
+        with pytest.raises(g4.G4Error, match="scales do NOT fit in one binding"):
+            d.plan_ple_split(name, 35, 256 << 10, 256 << 10)
+        with pytest.raises(g4.G4Error, match="storage bindings against a budget of 3"):
+            d.plan_ple_split(name, 35, 4 << 20, 4 << 20, 3)
+
+        def sl(i, off, n):
+            return g4.TableSlice(i, 0, 0, off, n)
+        total = codes.nbytes
+        fake = [16, 16]
+        with pytest.raises(g4.G4Error, match="needs at least one range"):
+            d.upload_split(name, [], [])
+        with pytest.raises(g4.G4Error, match="slice 1 starts at 100, not at 64; the ranges have to "
+                                             "partition the tensor in offset order"):
+            d.upload_split(name, [sl(0, 0, 64), sl(1, 100, total - 100)], fake)
+        with pytest.raises(g4.G4Error, match="slice 1 starts at 66, which is not four byte aligned"):
+            d.upload_split(name, [sl(0, 0, 66), sl(1, 66, total - 66)], fake)
+        with pytest.raises(g4.G4Error, match="outside every declared slice"):
+            d.upload_split(name, [sl(0, 0, 64), sl(1, 64, 64)], fake)

@@ -141,3 +141,62 @@ def test_checkpoint_refusals(gpu, tmp_path):
             retype(p, p, name, "BF16")  # the checkpoint stores it as bf16
         with pytest.raises(ValueError, match=fragment):
             gd.CheckpointModel(shape, str(p))
+
+
+def test_ple_table_split_upload_and_gather(gpu, oracle, tmp_path):
+    """BASELINE config 3 through the loader: the 1,174,405,120-byte PLE tensor of a safetensors
+    file, planned for a device with 1 GiB bindings (engine.ts:308-345 declarePleSplit:
+    planGatherSplit under the default 256 MiB slice cap gives 5 slices, scales whole), uploaded
+    piece by piece into one device buffer per slice (buffers.ts:291-423), then gathered over the
+    split plan for 2048 Zipf ids, bit for bit against the oracle on the host table."""
+    import g4ckpt as ck
+    import g4synth as syn
+    rows, cols, groups = syn.PLE_ROWS, syn.PLE_COLS, syn.PLE_LAYERS
+    print("writing the 1.17 GB PLE tensor", flush=True)
+    table = syn.ple_codes("ckpt-split", rows, cols)
+    scales = syn.ple_scales("ckpt-split", rows, groups).astype(np.float32)
+    name = "model.language_model.embed_tokens_per_layer.embedding_quantized"
+    save(tmp_path / "ple.safetensors", {name: table, name.replace("quantized", "scale"): scales})
+    with ck.Directory.open(str(tmp_path / "ple.safetensors")) as d:
+        plans, slices = d.plan_ple_split(name, groups, 1 << 30, 1 << 30)
+        assert plans.scales_single == 1 and len(slices) == 5
+        assert [(s.start_row, s.row_count) for s in slices] == [
+            (0, 59904), (59904, 59904), (119808, 59904), (179712, 59904), (239616, 22528)]
+        print("uploading into 5 slices", flush=True)
+        parts = d.upload_split(name, slices)
+        s_dev = d.upload(name.replace("quantized", "scale"))
+    ids = syn.zipf_ids("ckpt-split", 2048, rows)
+    ids[:3] = [0, 59904 - 1, rows - 1]  # first row, a slice's last row, the table's last row
+    # every slice holds exactly its rows of the file
+    for p, sl in zip(parts, slices):
+        head = np.empty(4480 * 2, np.uint8)
+        gpu._check(gpu.lib().g4_memcpy_d2h(head.ctypes.data, p.ptr, head.size, None))
+        assert np.array_equal(head.reshape(2, -1), table[sl.start_row:sl.start_row + 2])
+    dids = gpu.DeviceBuffer.from_array(ids)
+    for kind, dt in (("f32", np.float32), ("f16", np.float16)):
+        dst = gpu.DeviceBuffer.empty((ids.size, cols), dt)
+        dst.fill(0x7B)
+        gpu.ple_gather_split(parts, [s.start_row for s in slices], [s.row_count for s in slices],
+                             s_dev, dids, dst, ids.size, cols, syn.PLE_GROUP)
+        want = oracle.embed_gather(table[ids], scales[ids], np.arange(ids.size, dtype=np.int32),
+                                   cols, syn.PLE_GROUP, out_kind=kind)
+        got = dst.download()
+        assert np.array_equal(got.view(np.uint32 if kind == "f32" else np.uint16),
+                              want.view(np.uint32 if kind == "f32" else np.uint16)), kind
+
+
+def test_decode_from_a_split_checkpoint(gpu, tmp_path):
+    """A checkpoint loaded for a device whose bindings cannot hold the PLE table: the table goes
+    into slices and the step's gather runs over them; every output equals the unsplit model's."""
+    import g4decode as gd
+    shape = tiny()
+    write_checkpoint(tmp_path / "m.safetensors", shape, gd.HostReplica(shape, seed=4))
+    row_bytes = shape.layers * shape.ple_dim // 2
+    lim = 600 * row_bytes  # 2000 rows -> slices of 592 rows (16-row aligned): 4 slices
+    split = gd.CheckpointModel(shape, str(tmp_path / "m.safetensors"), limits=(lim, lim))
+    assert split.ple_split and len(split.ple_split) == 4 and "ple_table" not in split.buffers
+    a = run(gpu, shape, split)
+    b = run(gpu, shape, gd.SyntheticModel(shape, seed=4))
+    assert np.array_equal(a[0], b[0])
+    assert np.array_equal(a[1].view(np.uint32), b[1].view(np.uint32))
+    assert np.array_equal(a[2].view(np.uint32), b[2].view(np.uint32))

@@ -438,3 +438,32 @@ def test_decode_step_e2b_full(gpu, batch):
         assert same(got[key], want[key]), key
     for p in kv:
         assert same(dkv[p][0][:, pos], kv[p][0][:, pos]) and same(dkv[p][1][:, pos], kv[p][1][:, pos]), p
+
+
+def test_decode_step_e2b_split_ple_table(gpu):
+    """The E2B-shape step with the 1.17 GB PLE table carried as the 5 slices of the default-cap
+    plan at 1 GiB bindings (tableSplit.ts planTableSplit; plan.ts:709-725 one gather step per
+    slice, one fused launch here): the same next tokens, logits, residual and per-layer inputs as
+    the same model with the table whole."""
+    import g4decode as gd
+    shape = gd.Shape(batch=3, kv_capacity=4096)
+    model = gd.SyntheticModel(shape, seed=4)
+    plan, slices = gpu.plan_table_split(shape.vocab, shape.layers * shape.ple_dim // 2, 1 << 30,
+                                        1 << 30, 10, 0)
+    assert plan.num_slices == 5
+    toks = dev(gpu, np.array([59903, 59904, 262143], np.int32))  # both sides of a slice boundary
+    outs = []
+    for split in (False, True):
+        if split:
+            model.split_ple(slices, drop_whole=True)
+        dec = gd.Decoder(shape, model)
+        dec.fill_kv_history()
+        dec.set_position(4095)
+        nxt = gpu.DeviceBuffer.empty((shape.batch,), np.int32)
+        dec.step(toks, nxt)
+        gpu.synchronize()
+        outs.append([nxt.download(), dec.download("logits", np.float32),
+                     dec.download("hidden", np.float32), dec.download("per_layer", np.float32)])
+        dec.close()
+    for a, b in zip(*outs):
+        assert same(a, b)

@@ -109,3 +109,144 @@ def test_node_host_gpu_parity(tmp_path, oracle):
     assert np.array_equal(np.fromfile(tmp_path / "gelu.out", np.int8), want["gelu"])
     got_ple = np.fromfile(tmp_path / "ple.out", np.float32)
     assert np.array_equal(got_ple.view(np.uint32), want["ple"].view(np.uint32))
+
+
+_NP = {"Float32Array": np.float32, "Int8Array": np.int8, "Uint8Array": np.uint8,
+       "Int32Array": np.int32}
+
+
+def _load(tmp_path, spec):
+    return np.fromfile(tmp_path / spec["file"], _NP[spec["type"]])
+
+
+@needs_node
+def test_node_registry_cases_match_the_oracle(tmp_path, oracle):
+    """The known answers the Node registry carries (registry.ts:72-119 `cases`), computed in JS on
+    the reference's exact-grid recipe, against the C oracle's restatement of each kernel."""
+    import decode_oracle as d
+    r = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "dump_cases.js"), str(tmp_path)],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    cases = json.loads((tmp_path / "cases.json").read_text())
+    seen = set()
+    for c in cases:
+        name, p = c["kernel"], c["params"]
+        I = {k: _load(tmp_path, v) for k, v in c["inputs"].items()}
+        want = _load(tmp_path, c["expected"])
+        bits = 8 if "8bit" in name else 4
+        if name.startswith(("qgemv-4bit", "qgemv-8bit", "qgemm", "qmatmul")) and "gelu" not in name \
+                and "split" not in name:
+            m = p.get("cols", p.get("mCols", 1))
+            k, n = p["k"], p["numRows"]
+            x = I["x"].reshape(m, k)
+            if name == "qmatmul-8bit":
+                got = oracle.qmatmul8(I["wq"], I["scales"], x, n, k, m, p["inScale"], p["outScale"])
+                got = got.reshape(-1)
+                if want.dtype == np.int8:
+                    got = oracle.qgemm(8, I["wq"], I["scales"], x, n, k, m, p["inScale"],
+                                       p["outScale"])[2].reshape(-1)
+            else:
+                y, _, q = oracle.qgemm(bits, I["wq"], I["scales"], x, n, k, m, p["inScale"],
+                                       p["outScale"])
+                got = (q if want.dtype == np.int8 else y).reshape(-1)
+        elif name in ("qkv-batch-4bit", "gate-up-batch-4bit"):
+            i = p["outputIndex"]
+            got = oracle.qgemv(4, I[f"w{i}"], I[f"s{i}"], I["x"], p[f"rows{i}"], p["k"],
+                               p[f"inScale{i}"], p[f"outScale{i}"])[0]
+        elif name.endswith("-split") and "gelu" not in name:
+            got = oracle.qgemv_split(bits, I["wq"], I["scales"], I["x"], p["numRows"], p["k"],
+                                     p["kSplits"], p["exact"], p["inScale"]).reshape(-1)
+        elif name == "qgemv-merge":
+            got = oracle.qgemv_merge(I["part"].reshape(p["numRows"], -1), p["outScale"])
+        elif name == "qgemv-exact-merge":
+            got = oracle.qgemv_exact_merge(I["part"].reshape(p["numRows"], -1), I["scales"],
+                                           p["inScale"], p["outScale"])
+        elif "gelu" in name:
+            act = d.gelu_mul_f32_codes(I["gate"], I["up"], p["inScale"])
+            x = act.astype(np.float32) * np.float32(p["inScale"])
+            if name.endswith("exact-split"):
+                got = oracle.qgemv_split(bits, I["wq"], I["scales"], x, p["numRows"], p["k"],
+                                         p["kSplits"], True, p["inScale"]).reshape(-1)
+            else:
+                got = oracle.qgemv(bits, I["wq"], I["scales"], x, p["numRows"], p["k"],
+                                   p["inScale"], p["outScale"])[2]
+        elif name.startswith("ple-gather"):
+            sliced = name.endswith("sliced")
+            out = np.zeros((p["slots"], p["cols"]), np.float32)
+            oracle.embed_gather(I["codes"], I["scales"], I["ids"], p["cols"], p["groupSize"],
+                                out_kind="f32", sliced=sliced,
+                                slice_start=p.get("sliceStartRow", 0),
+                                slice_count=p.get("sliceRowCount", 0), out=out)
+            got = out.reshape(-1)
+        else:
+            raise AssertionError(f"no oracle for {name}")
+        assert got.dtype == want.dtype or want.dtype == np.float32, (name, c["case"])
+        assert np.array_equal(np.asarray(got, want.dtype).view(np.uint8), want.view(np.uint8)), \
+            (name, c["case"])
+        seen.add(name)
+    assert len(seen) == 19
+
+
+@needs_node
+@pytest.mark.gpu
+def test_node_registry_cases_on_gpu_and_async_readback():
+    """Every registry entry's known-answer cases through the Node host on the device, and the
+    asynchronous boundary: downloadAsync / synchronizeAsync settle Promises from a worker thread
+    (the reference's mapAsync readback, runtime.ts:866-878) and a failing copy rejects."""
+    print("node registry cases", flush=True)
+    r = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "gpu_cases.js")],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    assert res["cases"] >= 40 and res["failed"] == [] and res["asyncOk"] and res["rejected"]
+
+
+@needs_node
+@pytest.mark.gpu
+def test_node_two_decode_steps_in_flight(gpu, tmp_path):
+    """Two decode steps enqueued back to back from Node (the reference keeps steps in flight,
+    plan.ts:942-973): the second step reads the first's next tokens on the device, positions are
+    set in stream order, and the host waits only on async downloads. Both steps are checked
+    against the CPU composition of the oracle on the same seeded model and KV history."""
+    import decode_ref as ref
+    import g4decode as gd
+    shape = gd.Shape(layers=5, kv_producers=3, hidden=512, ffn=1024, q_heads=8, global_period=3,
+                     sliding_window=512, kv_capacity=640, batch=3, vocab=3000)
+    seed, pos, toks = 4, 600, [11, 2999, 1234]
+    spec = {"shape": {f: getattr(shape, f) for f in shape.__dataclass_fields__},
+            "model_fields": list(gpu.DECODE_MODEL_FIELDS),
+            "layer_fields": [f for f in gpu.DECODE_LAYER_FIELDS],
+            "layer_scalar": [float(v) for v in gd.layer_scalars(shape, seed)],
+            "tokens": toks, "pos": pos, "tensors": [],
+            "kv_elems": shape.batch * 2 * shape.kv_capacity * shape.head_dim,
+            "kv_seeds": [str(gd.tensor_seed(gd.KV_SEED, f"kv{p}")) for p in range(shape.kv_producers)],
+            "kv_amplitude": gd.KV_AMPLITUDE}
+    for name, kind, shp, lo, hi in gd.model_spec(shape):
+        spec["tensors"].append({"name": name, "kind": kind, "shape": list(shp),
+                                "seed": str(gd.tensor_seed(seed, name)), "lo": lo, "hi": hi})
+    for name, a in gd._rope_all(shape).items():
+        np.ascontiguousarray(a, np.float32).tofile(tmp_path / f"{name}.bin")
+        spec["tensors"].append({"name": name, "kind": "host", "file": f"{name}.bin",
+                                "shape": list(a.shape)})
+    (tmp_path / "spec.json").write_text(json.dumps(spec))
+    print("node decode in flight", flush=True)
+    r = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "decode_inflight.js"),
+                        str(tmp_path)], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    next0 = np.fromfile(tmp_path / "next0.out", np.int32)
+    next1 = np.fromfile(tmp_path / "next1.out", np.int32)
+    # the same model and history on the Python side, composed on the CPU
+    model = gd.SyntheticModel(shape, seed=seed)
+    dec = gd.Decoder(shape, model)
+    dec.fill_kv_history()
+    gpu.synchronize()
+    kv = {p: tuple(a.copy() for a in dec.download_kv(p)) for p in range(shape.kv_producers)}
+    dec.close()
+    W = ref.Weights(model)
+    want0 = ref.step(shape, W, kv, toks, pos)
+    want1 = ref.step(shape, W, kv, [int(t) for t in want0["next"]], pos + 1)
+    assert np.array_equal(next0, want0["next"]) and np.array_equal(next1, want1["next"])
+    logits = np.fromfile(tmp_path / "logits1.out", np.float32).reshape(shape.batch, -1)
+    hidden = np.fromfile(tmp_path / "hidden1.out", np.float32).reshape(shape.batch, -1)
+    assert np.array_equal(logits.view(np.uint32), np.asarray(want1["logits"], np.float32).view(np.uint32))
+    assert np.array_equal(hidden.view(np.uint32), np.asarray(want1["hidden"], np.float32).view(np.uint32))

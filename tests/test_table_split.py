@@ -68,3 +68,38 @@ def test_oracle_and_abi_agree_on_sweep(oracle, g4, limit, cap):
     assert [(s.start_row, s.row_count) for s in slices] == o["slices"]
     total = sum(c for _, c in o["slices"])
     assert total == ROWS  # the slices partition the vocabulary
+
+
+def test_plan_gather_split_ple_at_spec_floor(oracle, g4):
+    """planGatherSplit (tableSplit.ts:257-287): at the 128 MiB floor the PLE codes take nine slices
+    and the scales, 262144 x 35 f32 = 36,700,160 bytes (the figure tableSplit.ts:249-255 states),
+    stay one buffer, which is what the sliced gather assumes."""
+    floor = 134_217_728
+    plans, cs, ss = g4.plan_gather_split(ROWS, ROW_BYTES, 35, floor, floor)
+    assert plans.codes.num_slices == 9 and not plans.codes.single
+    assert plans.scales.total_bytes == 36_700_160
+    assert plans.scales.single and plans.scales_single == 1 and len(ss) == 1
+    assert [(s.start_row, s.row_count) for s in cs] == oracle.plan_table_split(
+        ROWS, ROW_BYTES, floor, floor)["slices"]
+
+
+def test_plan_gather_split_scales_not_single(oracle, g4):
+    """Below 36.7 MB per binding the scale table itself splits: scalesSingle is false, the plan the
+    gather kernel does not implement (tableSplit.ts:276-283)."""
+    lim = 16 << 20
+    plans, cs, ss = g4.plan_gather_split(ROWS, ROW_BYTES, 35, lim, lim)
+    assert plans.scales_single == 0 and plans.scales.num_slices == len(ss) == 3
+    assert [(s.start_row, s.row_count) for s in ss] == oracle.plan_table_split(
+        ROWS, 35 * 4, lim, lim)["slices"]
+    assert [(s.start_row, s.row_count) for s in cs] == oracle.plan_table_split(
+        ROWS, ROW_BYTES, lim, lim)["slices"]
+
+
+@pytest.mark.parametrize("limit", [8 << 20, 100_000_000, 1 << 30, 4_294_967_292])
+def test_plan_gather_split_is_two_table_plans(oracle, g4, limit):
+    plans, cs, ss = g4.plan_gather_split(ROWS, ROW_BYTES, 35, limit, limit, 10)
+    for plan, slices, row_bytes in ((plans.codes, cs, ROW_BYTES), (plans.scales, ss, 140)):
+        o = oracle.plan_table_split(ROWS, row_bytes, limit, limit)
+        assert [(s.start_row, s.row_count) for s in slices] == o["slices"]
+        assert plan.feasible == 1
+    assert plans.scales_single == plans.scales.single
