@@ -90,30 +90,38 @@ __device__ __forceinline__ void gather_chunk(uint32_t w, float s0, float s1, voi
 // so every load instruction reads one contiguous run of codes and every store instruction writes
 // one contiguous run of the output row; outputs are written non-temporally (they are not re-read
 // by this launch).
-constexpr int kRunsPerThread = 4;
+// RPT runs per thread. A large gather takes 8: a 8960-column row is then 192 threads, three waves,
+// so a 2048-token gather's blocks are all resident at once (32 waves per CU), where 4 runs per
+// thread needed a second round (11.9 -> 9.7 us). A small one (a decode step's few tokens) takes 4,
+// which halves each thread's serial work.
+constexpr int kSmallGatherSlots = 256;
 
+template <int RPT>
 __device__ __forceinline__ void gather_row(const uint8_t *row_codes, const void *scales,
                                            int scale_kind, int64_t row, void *dst, int out_kind,
                                            int64_t slot, int cols, int group_size,
                                            int groups_per_row) {
     const int runs = cols >> 3;
     const int T = blockDim.x;
-    for (int base = threadIdx.x; base < runs; base += kRunsPerThread * T) {
+    // a run of 8 codes lies in one group when the group size is a multiple of 8: one scale load
+    const bool one_scale = (group_size & 7) == 0;
+    for (int base = threadIdx.x; base < runs; base += RPT * T) {
         // All of this thread's code words and scales are requested before any is converted.
-        uint32_t w[kRunsPerThread];
-        float s0[kRunsPerThread], s1[kRunsPerThread];
+        uint32_t w[RPT];
+        float s0[RPT], s1[RPT];
 #pragma unroll
-        for (int u = 0; u < kRunsPerThread; ++u) {
+        for (int u = 0; u < RPT; ++u) {
             const int ch = base + u * T;
             const bool live = row_codes && ch < runs;
             w[u] = live ? *reinterpret_cast<const uint32_t *>(row_codes + (int64_t)ch * 4)
                         : 0x88888888u;
             s0[u] = live ? vec4_scale(scales, scale_kind, row, ch * 8, group_size, groups_per_row) : 0.0f;
-            s1[u] = live ? vec4_scale(scales, scale_kind, row, ch * 8 + 4, group_size, groups_per_row)
-                         : 0.0f;
+            s1[u] = !live ? 0.0f
+                    : one_scale ? s0[u]
+                                : vec4_scale(scales, scale_kind, row, ch * 8 + 4, group_size, groups_per_row);
         }
 #pragma unroll
-        for (int u = 0; u < kRunsPerThread; ++u) {
+        for (int u = 0; u < RPT; ++u) {
             const int ch = base + u * T;
             if (ch < runs) gather_chunk(w[u], s0[u], s1[u], dst, out_kind, slot, ch, cols);
         }
@@ -122,6 +130,7 @@ __device__ __forceinline__ void gather_row(const uint8_t *row_codes, const void 
 
 // One slice (or the whole table with start 0 and count = rows): ids outside the slice are left
 // untouched when `sliced`, and written as zeros when not (an id the table does not hold).
+template <int RPT>
 __global__ __launch_bounds__(1024) void ple_gather_kernel(
     const uint8_t *codes, const void *scales, int scale_kind, const int32_t *ids, void *dst,
     int out_kind, int slots, int cols, int group_size, int groups_per_row, int sliced,
@@ -130,11 +139,12 @@ __global__ __launch_bounds__(1024) void ple_gather_kernel(
     const int64_t row = (int64_t)(uint32_t)ids[slot];
     const bool inside = row >= start && row - start < count;
     if (!inside && sliced) return;  // uniform
-    gather_row(inside ? codes + (row - start) * (int64_t)(cols >> 1) : nullptr, scales, scale_kind,
+    gather_row<RPT>(inside ? codes + (row - start) * (int64_t)(cols >> 1) : nullptr, scales, scale_kind,
                row, dst, out_kind, slot, cols, group_size, groups_per_row);
 }
 
 // Every slice of a split table in one launch: each slot finds the slice that carries its id.
+template <int RPT>
 __global__ __launch_bounds__(1024) void ple_gather_split_kernel(
     SliceTable tab, const void *scales, int scale_kind, const int32_t *ids, void *dst, int out_kind,
     int slots, int cols, int group_size, int groups_per_row) {
@@ -144,13 +154,13 @@ __global__ __launch_bounds__(1024) void ple_gather_split_kernel(
     for (int s = 0; s < tab.n; ++s)
         if (row >= tab.start[s] && row - tab.start[s] < tab.count[s])
             src = tab.codes[s] + (row - tab.start[s]) * (int64_t)(cols >> 1);
-    gather_row(src, scales, scale_kind, row, dst, out_kind, slot, cols, group_size, groups_per_row);
+    gather_row<RPT>(src, scales, scale_kind, row, dst, out_kind, slot, cols, group_size, groups_per_row);
 }
 
-// Threads per block: enough for kRunsPerThread 8-code runs each, whole waves, at most 1024.
-static int gather_threads(int cols) {
+// Threads per block: enough for rpt 8-code runs each, whole waves, at most 1024.
+static int gather_threads(int cols, int rpt) {
     const int runs = cols >> 3;
-    int t = (runs + kRunsPerThread - 1) / kRunsPerThread;
+    int t = (runs + rpt - 1) / rpt;
     t = ((t + 63) / 64) * 64;
     return t < 64 ? 64 : (t > 1024 ? 1024 : t);
 }
@@ -203,10 +213,17 @@ int g4_ple_gather(const void *codes, const void *scales, int scale_kind, const i
         return set_error(G4_ERR_INVALID, "ple-gather-4bit: an unsliced table starts at row 0");
     if (reinterpret_cast<uintptr_t>(codes) & 3)
         return set_error(G4_ERR_INVALID, "%s: codes must be 4-byte aligned", who);
-    hipLaunchKernelGGL(ple_gather_kernel, dim3((unsigned)slots), dim3(gather_threads(cols)), 0,
-                       as_stream(stream), reinterpret_cast<const uint8_t *>(codes), scales,
-                       scale_kind, ids, dst, out_kind, slots, cols, group_size, groups_per_row,
-                       sliced ? 1 : 0, slice_start_row, slice_row_count);
+    const int rpt = slots < kSmallGatherSlots ? 4 : 8;
+    if (rpt == 4)
+        hipLaunchKernelGGL(ple_gather_kernel<4>, dim3((unsigned)slots), dim3(gather_threads(cols, 4)),
+                           0, as_stream(stream), reinterpret_cast<const uint8_t *>(codes), scales,
+                           scale_kind, ids, dst, out_kind, slots, cols, group_size, groups_per_row,
+                           sliced ? 1 : 0, slice_start_row, slice_row_count);
+    else
+        hipLaunchKernelGGL(ple_gather_kernel<8>, dim3((unsigned)slots), dim3(gather_threads(cols, 8)),
+                           0, as_stream(stream), reinterpret_cast<const uint8_t *>(codes), scales,
+                           scale_kind, ids, dst, out_kind, slots, cols, group_size, groups_per_row,
+                           sliced ? 1 : 0, slice_start_row, slice_row_count);
     G4_LAUNCHED("ple_gather_kernel");
     return G4_OK;
 }
@@ -234,9 +251,14 @@ int g4_ple_gather_split(const void *const *slice_codes, const int64_t *slice_sta
         tab.start[s] = slice_starts[s];
         tab.count[s] = slice_counts[s];
     }
-    hipLaunchKernelGGL(ple_gather_split_kernel, dim3((unsigned)slots), dim3(gather_threads(cols)), 0,
-                       as_stream(stream), tab, scales, scale_kind, ids, dst, out_kind, slots, cols,
-                       group_size, groups_per_row);
+    if (slots < kSmallGatherSlots)
+        hipLaunchKernelGGL(ple_gather_split_kernel<4>, dim3((unsigned)slots),
+                           dim3(gather_threads(cols, 4)), 0, as_stream(stream), tab, scales,
+                           scale_kind, ids, dst, out_kind, slots, cols, group_size, groups_per_row);
+    else
+        hipLaunchKernelGGL(ple_gather_split_kernel<8>, dim3((unsigned)slots),
+                           dim3(gather_threads(cols, 8)), 0, as_stream(stream), tab, scales,
+                           scale_kind, ids, dst, out_kind, slots, cols, group_size, groups_per_row);
     G4_LAUNCHED("ple_gather_split_kernel");
     return G4_OK;
 }
