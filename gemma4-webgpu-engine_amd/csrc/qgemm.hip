@@ -26,6 +26,7 @@
 
 #include <algorithm>
 #include <string>
+#include <type_traits>
 
 namespace g4 {
 
@@ -764,6 +765,279 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(
     }
 }
 
+// ---- the wide tile: 4-bit weights, 64 x 192 outputs per block of 8 waves -----------------------
+//
+// For grids that fill the device (M >= 256 and at least one block per CU). Against the 64 x 96
+// tile above it halves the unpack work and the LDS operand reads per MFMA:
+//   - each wave owns 64 x 48 outputs (4 x 3 MFMA tiles) over one K half of every 128-code stage:
+//     wave = 4 kh + wn, kh the K half (codes 16 (2 g + kh) .. +15 of the stage for lane group g),
+//     wn the 48-column quarter. One unpacked weight operand feeds four MFMAs, where the 2 x 2
+//     layout of the narrow tile fed two;
+//   - waves 0-3 load the stage's activation rows (2 direct loads each), waves 4-7 its weight
+//     columns (3 each); both stream global -> LDS through a 4-stage ring (80 KB, two blocks per CU
+//     at large M);
+//   - the stage barrier does not drain the LDS reads: the reads of stage st+1 are issued between
+//     stage st's MFMAs and only the ring slot of stage st-1 (read a full stage earlier) is
+//     refilled after the barrier;
+//   - the MFMA takes the weights as its A operand, so the accumulator is the transposed tile: lane
+//     (j, g) holds output row j, columns 4 g .. 4 g + 3 of each 16 x 16 tile, and the epilogue
+//     stores 4 consecutive outputs per lane;
+//   - the two K halves meet through LDS (each wave keeps two of its four row tiles), then every
+//     wave snaps 2 x 3 groups of 4 outputs. A group falls back to the IEEE divide only when some
+//     lane's quotient lies within 2^-13 of a half integer (one branch per group, not per output).
+// The LDS layouts, swizzles and the stage's A and B loads are the narrow tile's (a stage buffer is
+// 64 activation rows then 192 weight columns).
+constexpr int kWideBM = 64;
+constexpr int kWideBN = 192;
+constexpr int kWideNS = 4;
+constexpr int kWideA = kWideBM * 128;              // activation bytes per stage
+constexpr int kWideSB = kWideA + kWideBN * 64;     // stage buffer: activations + packed weights
+
+template <int N, bool LGKM> __device__ __forceinline__ void wide_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+    if (LGKM) __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+template <int DPS, bool LGKM> __device__ __forceinline__ void wide_wait_stages(int later) {
+    switch (later) {
+        case 0: wide_wait<0, LGKM>(); break;
+        case 1: wide_wait<1 * DPS, LGKM>(); break;
+        case 2: wide_wait<2 * DPS, LGKM>(); break;
+        default: wide_wait<0, LGKM>(); break;
+    }
+}
+
+struct WideOps {
+    v4i a[4];
+    uint2 b[3];
+};
+
+// The K loop of one wave. NL direct loads per stage (src[i] advancing STEP bytes a stage into ring
+// offset dst[i]); nk >= kWideNS - 1 stages.
+template <int NL, int STEP, bool NAT>
+__device__ __forceinline__ void wide_k_loop(const uint8_t *const (&src)[NL], const uint32_t (&dst)[NL],
+                                            uint32_t sbase, const uint8_t *smem, uint32_t aoff,
+                                            uint32_t boff, int nk, v4i (&acc)[4][3]) {
+    constexpr int NS = kWideNS;
+    auto issue = [&](int st, int buf) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) lds_dma16(src[i] + st * STEP, sbase + buf * kWideSB + dst[i]);
+    };
+    auto read_ops = [&](int buf, WideOps &o) {
+        const uint8_t *p = smem + buf * kWideSB;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o.a[t] = *reinterpret_cast<const v4i *>(p + aoff + t * 2048);
+#pragma unroll
+        for (int u = 0; u < 3; ++u) o.b[u] = *reinterpret_cast<const uint2 *>(p + boff + u * 1024);
+    };
+    auto mfma_cols = [&](const WideOps &o, int ulo, int uhi) {
+#pragma unroll
+        for (int u = 0; u < 3; ++u) {
+            if (u < ulo || u >= uhi) continue;
+            v4i bo;
+            if (NAT) {
+                int l0, h0, l1, h1;
+                nib_natural16(o.b[u].x, l0, h0);
+                nib_natural16(o.b[u].y, l1, h1);
+                bo = v4i{l0, h0, l1, h1};
+            } else {
+                bo = v4i{(int)nib_even16(o.b[u].x), (int)nib_odd16(o.b[u].x), (int)nib_even16(o.b[u].y),
+                         (int)nib_odd16(o.b[u].y)};
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                acc[t][u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bo, o.a[t], acc[t][u], 0, 0, 0);
+        }
+    };
+    WideOps r[2];
+#pragma unroll
+    for (int st = 0; st < NS - 1; ++st) issue(st, st);
+    wide_wait_stages<NL, true>(NS - 2);
+    read_ops(0, r[0]);
+    int s0 = 0;
+    // Stage st: the barrier after stage st+1 landed; refill the slot of stage st-1 (its operands
+    // were read during stage st-2 and consumed by stage st-1) with stage st+NS-1; two column tiles
+    // of MFMAs; the operand reads of stage st+1; the last column tile.
+    for (; s0 + NS + 1 <= nk; s0 += 2) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int st = s0 + h;
+            wide_wait_stages<NL, false>(NS - 3);
+            issue(st + NS - 1, (st + NS - 1) % NS);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_cols(r[h], 0, 2);
+            __builtin_amdgcn_sched_barrier(0);
+            read_ops((st + 1) % NS, r[h ^ 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_cols(r[h], 2, 3);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    for (; s0 < nk; s0 += 2) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int st = s0 + h;
+            if (st >= nk) break;
+            if (st + 1 < nk) {
+                const int last = min(nk - 1, st + NS - 2);  // the last stage issued so far
+                wide_wait_stages<NL, false>(last - (st + 1));
+                read_ops((st + 1) % NS, r[h ^ 1]);
+                if (st + NS - 1 < nk) issue(st + NS - 1, (st + NS - 1) % NS);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_cols(r[h], 0, 3);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    wide_wait<0, true>();  // the ring is free for the epilogue
+}
+
+template <bool NAT>
+__global__ __launch_bounds__(512, 4) void qgemm_wide_kernel(
+    const int8_t *__restrict__ A, const uint8_t *__restrict__ W, const float *__restrict__ scales,
+    void *dst, int M, int N, int K, float in_scale, float out_scale, int out_kind, int tiles_m,
+    int tiles_n) {
+    __shared__ __align__(1024) uint8_t smem[kWideNS * kWideSB];
+    static_assert(kWideNS * kWideSB >= 8 * 6 * 1024 + kWideBN * 4, "the K-half exchange and the scales fit the ring");
+    // XCD-aware order as in the narrow tile: one XCD takes every M tile of a run of N tiles.
+    const int b = blockIdx.x;
+    const int xcd = b & 7, idx = b >> 3;
+    const int tm = idx % tiles_m;
+    const int tn = (idx / tiles_m) * 8 + xcd;
+    if (tn >= tiles_n) return;  // whole block, before any barrier
+    const int m0 = tm * kWideBM, n0 = tn * kWideBN;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kh = wave >> 2, wn = wave & 3;
+    const int j = lane & 15, g = lane >> 4;
+    const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+    const int row_bytes = K >> 1;
+    // this lane's operand offsets in a stage buffer (the narrow tile's swizzles)
+    const int sig = (j & 7) ^ ((j >> 3) & 1);
+    const uint32_t aoff = (j >> 3) * 1024 + (j & 7) * 128 + 16 * ((2 * g + kh) ^ sig);
+    const uint32_t boff = kWideA + (wn * 48 + j) * 64 + 16 * (g ^ (((j >> 1) ^ (j >> 3)) & 3)) + 8 * kh;
+    // the tile's column scales (one per thread), loaded now so their latency hides under the K loop
+    const float col_scale = tid < kWideBN ? scales[min(n0 + tid, N - 1)] : 0.0f;
+    v4i acc[4][3];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int u = 0; u < 3; ++u) acc[t][u] = v4i{0, 0, 0, 0};
+    const int nk = K / kTileBK;
+    if (kh == 0) {  // activation rows 8 q .. 8 q + 7, q = wn and wn + 4
+        const uint8_t *src[2];
+        uint32_t dsto[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int q = wn + 4 * i;
+            const int r = 8 * q + (lane >> 3);
+            const int c = (lane & 7) ^ (((lane >> 3) & 7) ^ (q & 1));
+            src[i] = reinterpret_cast<const uint8_t *>(A + (int64_t)min(m0 + r, M - 1) * K + 16 * c);
+            dsto[i] = q * 1024;
+        }
+        wide_k_loop<2, 128, NAT>(src, dsto, sbase, smem, aoff, boff, nk, acc);
+    } else {  // weight columns 16 q .. 16 q + 15, q = wn, wn + 4, wn + 8
+        const uint8_t *src[3];
+        uint32_t dsto[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int q = wn + 4 * i;
+            const int cl = lane >> 2;
+            const int c = (lane & 3) ^ (((cl >> 1) ^ (cl >> 3)) & 3);
+            src[i] = W + (int64_t)min(n0 + 16 * q + cl, N - 1) * row_bytes + 16 * c;
+            dsto[i] = kWideA + q * 1024;
+        }
+        wide_k_loop<3, 64, NAT>(src, dsto, sbase, smem, aoff, boff, nk, acc);
+    }
+
+    // The K halves meet: wave (wn, kh) keeps row tiles 2 kh, 2 kh + 1 and hands the other two to
+    // wave (wn, 1 - kh). Register indices stay compile-time constants.
+    v4i *P = reinterpret_cast<v4i *>(smem);
+    float *S = reinterpret_cast<float *>(smem + 8 * 6 * 1024);  // the column scales, after P
+    v4i sum[2][3];
+    auto meet = [&](auto khc) {
+        constexpr int KH = decltype(khc)::value;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int u = 0; u < 3; ++u) P[(wave * 6 + tt * 3 + u) * 64 + lane] = acc[2 * (1 - KH) + tt][u];
+        if (tid < kWideBN) S[tid] = col_scale;
+        __syncthreads();
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int u = 0; u < 3; ++u)
+                sum[tt][u] = acc[2 * KH + tt][u] + P[((wave ^ 4) * 6 + tt * 3 + u) * 64 + lane];
+    };
+    if (kh == 0) meet(std::integral_constant<int, 0>{});
+    else meet(std::integral_constant<int, 1>{});
+
+    bool r_ok;
+    const float rcp = srq_recip(out_scale, r_ok);
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int m = m0 + (2 * kh + tt) * 16 + j;
+#pragma unroll
+        for (int u = 0; u < 3; ++u) {
+            const int n = n0 + wn * 48 + u * 16 + 4 * g;
+            const int live = min(4, N - n);
+            const bool row_ok = m < M && live > 0;
+            const int64_t o = (int64_t)m * N + n;
+            const int v[4] = {sum[tt][u].x >> 4, sum[tt][u].y >> 4, sum[tt][u].z >> 4, sum[tt][u].w >> 4};
+            if (out_kind == G4_KIND_I32) {
+                if (!row_ok) continue;
+                int32_t *d = reinterpret_cast<int32_t *>(dst) + o;
+                if (live == 4 && (o & 3) == 0) *reinterpret_cast<v4i *>(d) = v4i{v[0], v[1], v[2], v[3]};
+                else for (int e = 0; e < live; ++e) d[e] = v[e];
+                continue;
+            }
+            const float4 s4 = *reinterpret_cast<const float4 *>(S + wn * 48 + u * 16 + 4 * g);
+            const float sc[4] = {s4.x, s4.y, s4.z, s4.w};
+            float y[4], code[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = __fmul_rn(__fmul_rn(in_scale, sc[e]), (float)v[e]);  // the reference's order
+            if (out_scale == 0.0f) {  // f32 output without an output snap (int8 needs a scale)
+                if (!row_ok) continue;
+                float *d = reinterpret_cast<float *>(dst) + o;
+                if (live == 4 && (o & 3) == 0) *reinterpret_cast<float4 *>(d) = make_float4(y[0], y[1], y[2], y[3]);
+                else for (int e = 0; e < live; ++e) d[e] = y[e];
+                continue;
+            }
+            float worst = r_ok ? 0.0f : 1.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float t = __fmul_rn(y[e], rcp);
+                code[e] = rintf(t);
+                worst = fmaxf(worst, fabsf(t - code[e]));
+            }
+            // |fl(y * fl(1/s)) - fl(y / s)| < 2^-13 while |y / s| <= 256 (beyond, both clamp): a
+            // quotient farther than that from a half integer rounds the same either way.
+            if (worst >= 0.5f - 0x1p-13f) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) code[e] = rintf(__fdiv_rn(y[e], out_scale));
+            }
+            if (!row_ok) continue;
+            if (out_kind == G4_KIND_I8) {
+                int c[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) c[e] = (int)fminf(fmaxf(code[e], -128.0f), 127.0f);
+                int8_t *d = reinterpret_cast<int8_t *>(dst) + o;
+                if (live == 4 && (o & 3) == 0) *reinterpret_cast<uint32_t *>(d) = pack4b(c[0], c[1], c[2], c[3]);
+                else for (int e = 0; e < live; ++e) d[e] = (int8_t)c[e];
+            } else {  // f32: q * outScale
+                float f[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) f[e] = __fmul_rn(fminf(fmaxf(code[e], -128.0f), 127.0f), out_scale);
+                float *d = reinterpret_cast<float *>(dst) + o;
+                if (live == 4 && (o & 3) == 0) *reinterpret_cast<float4 *>(d) = make_float4(f[0], f[1], f[2], f[3]);
+                else for (int e = 0; e < live; ++e) d[e] = f[e];
+            }
+        }
+    }
+}
+
 // ---- per-stream workspace for the snapped activation codes ------------------------------------
 
 namespace {
@@ -807,7 +1081,7 @@ int workspace_forget_stream(void *stream) {
 }
 
 enum KernelChoice { K_GEMV = 0, K_SKINNY16, K_SKINNY32, K_TILE128, K_GEMV_F32, K_GEMV_COLS,
-                    K_SERIAL8 };
+                    K_SERIAL8, K_WIDE };
 
 // gemm_mode: the caller named qgemm-4bit / qmatmul-8bit (execute.ts matmulKernel in gemm mode).
 // Uncalibrated qmatmul-8bit then keeps the reference's serial per-output order at any M; the
@@ -823,7 +1097,10 @@ static KernelChoice pick_kernel(int bits, int m, int n, int k, float in_scale, b
     if (m <= 16) return K_SKINNY16;
     if (k < 2 * kTileBK) return K_SKINNY32;  // the tile ring needs two K stages
     if (m <= 32) return K_SKINNY32;
-    (void)bits;
+    // the wide tile once its grid fills the device: 4-bit weights, M >= 256, three K stages
+    const int64_t wide_blocks = (int64_t)((m + kWideBM - 1) / kWideBM) * ((n + kWideBN - 1) / kWideBN);
+    if (bits == 4 && m >= 256 && k >= kWideNS * kTileBK - kTileBK && wide_blocks >= device_cu_count())
+        return K_WIDE;
     return K_TILE128;
 }
 
@@ -833,6 +1110,7 @@ static const char *choice_name(KernelChoice c, int bits) {
         case K_SKINNY16: return bits == 4 ? "qgemm-4bit-mfma-small16" : "qmatmul-8bit-mfma-small16";
         case K_SKINNY32: return bits == 4 ? "qgemm-4bit-mfma-small32" : "qmatmul-8bit-mfma-small32";
         case K_TILE128: return bits == 4 ? "qgemm-4bit-mfma-tile" : "qmatmul-8bit-mfma-tile";
+        case K_WIDE: return "qgemm-4bit-mfma-wide";
         case K_GEMV_F32: return bits == 4 ? "qgemv-4bit-f32" : "qgemv-8bit-f32";
         case K_SERIAL8: return "qmatmul-8bit-serial";
         default: return bits == 4 ? "qgemv-4bit-columns" : "qgemv-8bit-columns";
@@ -952,7 +1230,8 @@ static int check_linear(int bits, const void *wq, const float *scales, const voi
 // buffer of M * K codes first (the only path of this file that needs memory beyond its operands).
 static bool needs_codes_buffer(int bits, int m, int n, int k, float in_scale, int x_kind,
                                bool gemm_mode) {
-    return pick_kernel(bits, m, n, k, in_scale, gemm_mode) == K_TILE128 && x_kind != G4_KIND_I8;
+    const KernelChoice c = pick_kernel(bits, m, n, k, in_scale, gemm_mode);
+    return (c == K_TILE128 || c == K_WIDE) && x_kind != G4_KIND_I8;
 }
 
 // given_codes: a caller's buffer for the snapped codes (at least M * K bytes, checked by the
@@ -1014,6 +1293,19 @@ static int run_linear(int bits, const void *wq, const float *scales, const void 
         codes = reinterpret_cast<const int8_t *>(ws);
     }
     const uint8_t *w = reinterpret_cast<const uint8_t *>(wq);
+    if (c == K_WIDE) {
+        const int tiles_m = (m + kWideBM - 1) / kWideBM;
+        const int tiles_n = (n + kWideBN - 1) / kWideBN;
+        const int blocks = tiles_m * ((tiles_n + 7) / 8) * 8;
+        if (natural)
+            hipLaunchKernelGGL(qgemm_wide_kernel<true>, dim3(blocks), dim3(512), 0, stream, codes, w,
+                               scales, dst, m, n, k, in_scale, out_scale, out_kind, tiles_m, tiles_n);
+        else
+            hipLaunchKernelGGL(qgemm_wide_kernel<false>, dim3(blocks), dim3(512), 0, stream, codes, w,
+                               scales, dst, m, n, k, in_scale, out_scale, out_kind, tiles_m, tiles_n);
+        G4_LAUNCHED("qgemm_wide_kernel");
+        return G4_OK;
+    }
     if (bits == 4)
         return launch_tile<4>(codes, natural, w, scales, dst, m, n, k, in_scale, out_scale, out_kind,
                               stream);

@@ -86,7 +86,9 @@ def test_kernel_choice_per_shape(g4):
     assert g4.kernel_for_shape(4, 1, 16, 1280) == "qgemv-4bit"  # 40 chunks: no streaming class
     assert g4.kernel_for_shape(4, 2, 6144, 1536) == "qgemv-4bit"
     assert g4.kernel_for_shape(4, 8, 6144, 1536) == "qgemm-4bit-mfma-small16"
-    assert g4.kernel_for_shape(4, 512, 6144, 1536) == "qgemm-4bit-mfma-tile"
+    assert g4.kernel_for_shape(4, 512, 6144, 1536) == "qgemm-4bit-mfma-wide"
+    assert g4.kernel_for_shape(4, 128, 6144, 1536) == "qgemm-4bit-mfma-tile"
+    assert g4.kernel_for_shape(8, 512, 6144, 1536) == "qmatmul-8bit-mfma-tile"
     assert g4.kernel_for_shape(8, 4, 1536, 6144) == "qmatmul-8bit-mfma-small16"
     assert g4.kernel_for_shape(4, 32, 1536, 6144) == "qgemm-4bit-mfma-small32"
     # the tied head at a decode batch: the small kernel would re-snap x in each of 16384 blocks

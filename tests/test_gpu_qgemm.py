@@ -182,3 +182,34 @@ def test_short_k_and_odd_n(gpu, oracle, bits, m, n, k):
     o32.fill(0x7B)
     gpu.qgemm(bits, dev(gpu, w), dev(gpu, s), dev(gpu, xq), o32, k, n, m, 0.05, 0.1)
     assert np.array_equal(o32.download(), acc)
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 6144, 1536), (300, 12291, 512)])
+def test_wide_tile_kinds_and_ragged_edges(gpu, oracle, m, n, k):
+    # The 64 x 192 tile (8 waves, K halves met through LDS, transposed accumulators): every output
+    # kind, f16 activations (snapped, interleaved) and int8 codes (natural order), the config-2
+    # gate shape and a ragged one (last M tile 44 rows, last N tile 3 columns, N odd so the packed
+    # 4-output stores fall back to single ones on misaligned rows).
+    assert gpu.kernel_for_shape(4, m, n, k) == "qgemm-4bit-mfma-wide"
+    w = syn.int4_weights("wide", f"{m}x{n}x{k}", n, k)
+    s = syn.row_scales("wide", f"{m}x{n}x{k}", n)
+    x = syn.activations("wide", f"{m}x{n}x{k}", m, k, outlier_frac=0.01)
+    want, acc, codes = oracle.qgemm(4, w, s, x.astype(np.float32), n, k, m, syn.IN_SCALE,
+                                    syn.OUT_SCALE)
+    xq = np.clip(np.rint(x.astype(np.float32) / np.float32(syn.IN_SCALE)), -128, 127).astype(np.int8)
+    wb, sb = dev(gpu, w), dev(gpu, s)
+    for src_name, src in (("f16", dev(gpu, x)), ("i8", dev(gpu, xq))):
+        for name, dt, ref in (("i8", np.int8, codes), ("i32", np.int32, acc), ("f32", np.float32, want)):
+            print(f"wide m={m} n={n} k={k} x={src_name} out={name}", flush=True)
+            o = out_buf(gpu, (m, n), dt)
+            gpu.qgemm(4, wb, sb, src, o, k, n, m, syn.IN_SCALE, syn.OUT_SCALE)
+            got = o.download()
+            if name == "f32":
+                assert f32_equal(got, ref)
+            else:
+                assert np.array_equal(got, ref), f"{int((got != ref).sum())} outputs differ"
+    # f32 output without an output snap (outScale 0): y itself
+    y0, _, _ = oracle.qgemm(4, w, s, x.astype(np.float32), n, k, m, syn.IN_SCALE, 0.0)
+    o = out_buf(gpu, (m, n), np.float32)
+    gpu.qgemm(4, wb, sb, dev(gpu, xq), o, k, n, m, syn.IN_SCALE, 0.0)
+    assert f32_equal(o.download(), y0)

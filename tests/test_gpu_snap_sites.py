@@ -3,8 +3,8 @@ reciprocal fast path alone would round the other way (tests/snapcases.py builds 
 
 Sites: the streaming GEMV's activation snap and output snap (M = 1), the generic GEMV (M = 2),
 the small-M MFMA kernel's fused snap and epilogue (4- and 16-wave grids), quantize_rows and the
-tile kernel's epilogue (M > 32, f32 and int8 codes in), the standalone srq kernel, and the gelu
-prologue. Each site also runs the in-tree known answer srqCodes(-11.435039520263672,
+tile kernel's epilogue (M > 32, f32 and int8 codes in), the wide tile's grouped epilogue
+(M >= 256), the standalone srq kernel, and the gelu prologue. Each site also runs the in-tree known answer srqCodes(-11.435039520263672,
 0.6181102395057678) = -18 (quant.ts:324-329) as an activation and as an output.
 Also here: uncalibrated qmatmul-8bit in the reference's serial vec4 f32 order
 (pleMatmul.ts:212-222) against or_qmatmul8 on off-grid inputs."""
@@ -136,6 +136,23 @@ def test_tile_snap(gpu, oracle, bits, mode):
             print(f"tile bits={bits} mode={mode} x={src_name} out={name}", flush=True)
             dst = out_buf(gpu, (m, n), dt)
             gpu.qgemm(bits, dw, ds, src, dst, k, n, m, sin, sout)
+            check(dst.download(), want, dst.kind, gpu)
+
+
+@pytest.mark.parametrize("mode", ["adv", "ka"])
+def test_wide_tile_snap(gpu, oracle, mode):
+    """M >= 256 over a grid that fills the device: the 64 x 192 tile's grouped epilogue snap
+    (one divide fallback per group of 4 outputs), f32 and int8 codes in."""
+    m, n, k = 512, 6144, 512
+    w, s, x, sin, sout, want = case(oracle, 4, m, n, k, mode, 47)
+    assert gpu.kernel_for_shape(4, m, n, k) == "qgemm-4bit-mfma-wide"
+    dw, ds = dev(gpu, w), dev(gpu, s)
+    codes = oracle.srq_codes(x.reshape(-1), sin).reshape(m, k)
+    for src_name, src in (("f32", dev(gpu, x)), ("i8", dev(gpu, codes))):
+        for name, dt in KINDS:
+            print(f"wide mode={mode} x={src_name} out={name}", flush=True)
+            dst = out_buf(gpu, (m, n), dt)
+            gpu.qgemm(4, dw, ds, src, dst, k, n, m, sin, sout)
             check(dst.download(), want, dst.kind, gpu)
 
 
