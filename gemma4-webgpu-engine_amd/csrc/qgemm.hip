@@ -770,9 +770,11 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(
 // For grids that fill the device (M >= 256 and at least one block per CU). Against the 64 x 96
 // tile above it halves the unpack work and the LDS operand reads per MFMA:
 //   - each wave owns 64 x 48 outputs (4 x 3 MFMA tiles) over one K half of every 128-code stage:
-//     wave = 4 kh + wn, kh the K half (codes 16 (2 g + kh) .. +15 of the stage for lane group g),
+//     wave = 4 kh + wn, kh the K half (codes 64 kh + 16 g .. +15 of the stage for lane group g),
 //     wn the 48-column quarter. One unpacked weight operand feeds four MFMAs, where the 2 x 2
-//     layout of the narrow tile fed two;
+//     layout of the narrow tile fed two. Lane groups g and g + 1 read the two 8-byte halves of
+//     one 16-byte weight chunk, so a 32-lane pass of the 8-byte reads covers 16 columns x 16 bytes
+//     at distinct swizzled chunk positions: no bank conflicts;
 //   - waves 0-3 load the stage's activation rows (2 direct loads each), waves 4-7 its weight
 //     columns (3 each); both stream global -> LDS through a 4-stage ring (80 KB, two blocks per CU
 //     at large M);
@@ -781,7 +783,8 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(
 //     refilled after the barrier;
 //   - the MFMA takes the weights as its A operand, so the accumulator is the transposed tile: lane
 //     (j, g) holds output row j, columns 4 g .. 4 g + 3 of each 16 x 16 tile, and the epilogue
-//     stores 4 consecutive outputs per lane;
+//     stores 4 consecutive outputs per lane (1.7 us faster at M = 512 than storing the 24 outputs
+//     of the untransposed layout one by one);
 //   - the two K halves meet through LDS (each wave keeps two of its four row tiles), then every
 //     wave snaps 2 x 3 groups of 4 outputs. A group falls back to the IEEE divide only when some
 //     lane's quotient lies within 2^-13 of a half integer (one branch per group, not per output).
@@ -816,10 +819,15 @@ struct WideOps {
 
 // The K loop of one wave. NL direct loads per stage (src[i] advancing STEP bytes a stage into ring
 // offset dst[i]); nk >= kWideNS - 1 stages.
-template <int NL, int STEP, bool NAT>
+// NK > 0: the stage count is a compile-time constant and the loop is unrolled whole. Then the
+// compiler's wait for a stage's operands counts only the reads issued after them (lgkmcnt(7)), so
+// stage st+1's reads stay in flight under stage st's MFMAs; across a loop back-edge it waits for
+// every outstanding LDS read instead, which is why the runtime form issues the reads between the
+// MFMAs.
+template <int NL, int STEP, bool NAT, int NK>
 __device__ __forceinline__ void wide_k_loop(const uint8_t *const (&src)[NL], const uint32_t (&dst)[NL],
                                             uint32_t sbase, const uint8_t *smem, uint32_t aoff,
-                                            uint32_t boff, int nk, v4i (&acc)[4][3]) {
+                                            uint32_t boff, int nk_rt, v4i (&acc)[4][3]) {
     constexpr int NS = kWideNS;
     auto issue = [&](int st, int buf) {
 #pragma unroll
@@ -856,6 +864,25 @@ __device__ __forceinline__ void wide_k_loop(const uint8_t *const (&src)[NL], con
     for (int st = 0; st < NS - 1; ++st) issue(st, st);
     wide_wait_stages<NL, true>(NS - 2);
     read_ops(0, r[0]);
+    if constexpr (NK > 0) {
+        // stage st: the barrier after stage st+1 landed, its operand reads, the refill of the slot
+        // of stage st-1 with stage st+NS-1, stage st's MFMAs
+#pragma unroll
+        for (int st = 0; st < NK; ++st) {
+            if (st + 1 < NK) {
+                const int last = min(NK - 1, st + NS - 2);
+                wide_wait_stages<NL, false>(last - (st + 1));
+                read_ops((st + 1) % NS, r[(st + 1) & 1]);
+                if (st + NS - 1 < NK) issue(st + NS - 1, (st + NS - 1) % NS);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_cols(r[st & 1], 0, 3);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        wide_wait<0, true>();
+        return;
+    }
+    const int nk = nk_rt;
     int s0 = 0;
     // Stage st: the barrier after stage st+1 landed; refill the slot of stage st-1 (its operands
     // were read during stage st-2 and consumed by stage st-1) with stage st+NS-1; two column tiles
@@ -916,8 +943,9 @@ __global__ __launch_bounds__(512, 4) void qgemm_wide_kernel(
     const int row_bytes = K >> 1;
     // this lane's operand offsets in a stage buffer (the narrow tile's swizzles)
     const int sig = (j & 7) ^ ((j >> 3) & 1);
-    const uint32_t aoff = (j >> 3) * 1024 + (j & 7) * 128 + 16 * ((2 * g + kh) ^ sig);
-    const uint32_t boff = kWideA + (wn * 48 + j) * 64 + 16 * (g ^ (((j >> 1) ^ (j >> 3)) & 3)) + 8 * kh;
+    const uint32_t aoff = (j >> 3) * 1024 + (j & 7) * 128 + 16 * ((4 * kh + g) ^ sig);
+    const uint32_t boff = kWideA + (wn * 48 + j) * 64 + 16 * ((2 * kh + (g >> 1)) ^ (((j >> 1) ^ (j >> 3)) & 3)) +
+                          8 * (g & 1);
     // the tile's column scales (one per thread), loaded now so their latency hides under the K loop
     const float col_scale = tid < kWideBN ? scales[min(n0 + tid, N - 1)] : 0.0f;
     v4i acc[4][3];
@@ -937,7 +965,9 @@ __global__ __launch_bounds__(512, 4) void qgemm_wide_kernel(
             src[i] = reinterpret_cast<const uint8_t *>(A + (int64_t)min(m0 + r, M - 1) * K + 16 * c);
             dsto[i] = q * 1024;
         }
-        wide_k_loop<2, 128, NAT>(src, dsto, sbase, smem, aoff, boff, nk, acc);
+        if (nk == 12) wide_k_loop<2, 128, NAT, 12>(src, dsto, sbase, smem, aoff, boff, nk, acc);
+        else if (nk == 16) wide_k_loop<2, 128, NAT, 16>(src, dsto, sbase, smem, aoff, boff, nk, acc);
+        else wide_k_loop<2, 128, NAT, 0>(src, dsto, sbase, smem, aoff, boff, nk, acc);
     } else {  // weight columns 16 q .. 16 q + 15, q = wn, wn + 4, wn + 8
         const uint8_t *src[3];
         uint32_t dsto[3];
@@ -949,13 +979,15 @@ __global__ __launch_bounds__(512, 4) void qgemm_wide_kernel(
             src[i] = W + (int64_t)min(n0 + 16 * q + cl, N - 1) * row_bytes + 16 * c;
             dsto[i] = kWideA + q * 1024;
         }
-        wide_k_loop<3, 64, NAT>(src, dsto, sbase, smem, aoff, boff, nk, acc);
+        if (nk == 12) wide_k_loop<3, 64, NAT, 12>(src, dsto, sbase, smem, aoff, boff, nk, acc);
+        else if (nk == 16) wide_k_loop<3, 64, NAT, 16>(src, dsto, sbase, smem, aoff, boff, nk, acc);
+        else wide_k_loop<3, 64, NAT, 0>(src, dsto, sbase, smem, aoff, boff, nk, acc);
     }
 
     // The K halves meet: wave (wn, kh) keeps row tiles 2 kh, 2 kh + 1 and hands the other two to
     // wave (wn, 1 - kh). Register indices stay compile-time constants.
     v4i *P = reinterpret_cast<v4i *>(smem);
-    float *S = reinterpret_cast<float *>(smem + 8 * 6 * 1024);  // the column scales, after P
+    float *S = reinterpret_cast<float *>(smem + 8 * 6 * 1024);  // inScale x the column scales, after P
     v4i sum[2][3];
     auto meet = [&](auto khc) {
         constexpr int KH = decltype(khc)::value;
@@ -963,7 +995,7 @@ __global__ __launch_bounds__(512, 4) void qgemm_wide_kernel(
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int u = 0; u < 3; ++u) P[(wave * 6 + tt * 3 + u) * 64 + lane] = acc[2 * (1 - KH) + tt][u];
-        if (tid < kWideBN) S[tid] = col_scale;
+        if (tid < kWideBN) S[tid] = __fmul_rn(in_scale, col_scale);  // f32(inScale * scale[n])
         __syncthreads();
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
@@ -997,7 +1029,7 @@ __global__ __launch_bounds__(512, 4) void qgemm_wide_kernel(
             const float sc[4] = {s4.x, s4.y, s4.z, s4.w};
             float y[4], code[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = __fmul_rn(__fmul_rn(in_scale, sc[e]), (float)v[e]);  // the reference's order
+            for (int e = 0; e < 4; ++e) y[e] = __fmul_rn(sc[e], (float)v[e]);  // the reference's order
             if (out_scale == 0.0f) {  // f32 output without an output snap (int8 needs a scale)
                 if (!row_ok) continue;
                 float *d = reinterpret_cast<float *>(dst) + o;
@@ -1020,12 +1052,19 @@ __global__ __launch_bounds__(512, 4) void qgemm_wide_kernel(
             }
             if (!row_ok) continue;
             if (out_kind == G4_KIND_I8) {
-                int c[4];
+                // code + 1.5 * 2^23 is exact and its low byte is the code's two's complement byte
+                uint32_t b[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) c[e] = (int)fminf(fmaxf(code[e], -128.0f), 127.0f);
+                for (int e = 0; e < 4; ++e)
+                    b[e] = __float_as_uint(__fadd_rn(fminf(fmaxf(code[e], -128.0f), 127.0f), 12582912.0f));
                 int8_t *d = reinterpret_cast<int8_t *>(dst) + o;
-                if (live == 4 && (o & 3) == 0) *reinterpret_cast<uint32_t *>(d) = pack4b(c[0], c[1], c[2], c[3]);
-                else for (int e = 0; e < live; ++e) d[e] = (int8_t)c[e];
+                if (live == 4 && (o & 3) == 0) {
+                    const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0C0C0400u);  // b0.0 b1.0
+                    const uint32_t hi = __builtin_amdgcn_perm(b[3], b[2], 0x0C0C0400u);  // b2.0 b3.0
+                    *reinterpret_cast<uint32_t *>(d) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+                } else {
+                    for (int e = 0; e < live; ++e) d[e] = (int8_t)(b[e] & 0xffu);
+                }
             } else {  // f32: q * outScale
                 float f[4];
 #pragma unroll

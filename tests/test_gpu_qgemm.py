@@ -184,7 +184,7 @@ def test_short_k_and_odd_n(gpu, oracle, bits, m, n, k):
     assert np.array_equal(o32.download(), acc)
 
 
-@pytest.mark.parametrize("m,n,k", [(512, 6144, 1536), (300, 12291, 512)])
+@pytest.mark.parametrize("m,n,k", [(512, 6144, 1536), (300, 12291, 512), (384, 8192, 2048)])
 def test_wide_tile_kinds_and_ragged_edges(gpu, oracle, m, n, k):
     # The 64 x 192 tile (8 waves, K halves met through LDS, transposed accumulators): every output
     # kind, f16 activations (snapped, interleaved) and int8 codes (natural order), the config-2
