@@ -208,6 +208,27 @@ struct SmallJobs {
 // chunks measured a 4.09 ms step, one chunk 4.01 ms).
 template <int MT, int WAVES> constexpr int small_kc() { return (WAVES >= 16 ? 98304 : 49152) / MT; }
 
+// One batch of a lane's weight loads for K steps kb0, kb0 + WAVES, ... (clamped: every load valid).
+template <int BITS, int NP, int BATCH, int WAVES>
+__device__ __forceinline__ void load_small_weights(u32x4 (&bw)[NP][BATCH][BITS == 4 ? 1 : 2],
+                                                   const uint8_t *wrow, const uint8_t *wrow2, int kb0,
+                                                   int ksteps, int kbase, int g) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const uint8_t *wr = p == 0 ? wrow : wrow2;
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+            const int kb = min(kb0 + WAVES * u, ksteps - 1);
+            if (BITS == 4) {
+                bw[p][u][0] = *reinterpret_cast<const u32x4 *>(wr + (kbase + kb) * 64 + g * 16);
+            } else {
+                bw[p][u][0] = *reinterpret_cast<const u32x4 *>(wr + (kbase + kb) * 128 + g * 32);
+                bw[p][u][BITS == 4 ? 0 : 1] = *reinterpret_cast<const u32x4 *>(wr + (kbase + kb) * 128 + g * 32 + 16);
+            }
+        }
+    }
+}
+
 template <int BITS, int MT, int WAVES, int EPI>
 __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
     const void *__restrict__ x, int x_kind, SmallJobs jobs, int M, int K, float in_scale,
@@ -264,6 +285,12 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
     for (int kc0 = kbeg; kc0 < kend; kc0 += KC) {
         const int kcn = min(KC, kend - kc0);
         const int gpr = kcn >> 3;  // 8-code groups per row in this chunk
+        const int ksteps = kcn / kTileBK;
+        const int kbase = kc0 / kTileBK;
+        // The chunk's first batch of weights is requested before the codes are copied, so the two
+        // memory latencies overlap (the weights do not depend on the codes).
+        u32x4 bw_first[NP][BATCH][BITS == 4 ? 1 : 2];
+        load_small_weights<BITS, NP, BATCH, WAVES>(bw_first, wrow, wrow2, wave, ksteps, kbase, g);
         lds_barrier();  // the previous chunk's codes are no longer read
         // the snap: each thread issues the loads of SB groups (indices clamped, so every load is
         // valid) before converting any, so a chunk costs one memory latency per SB groups. Only
@@ -271,7 +298,35 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
         // products of its own output row, which is never stored.
         constexpr int SB = 4;
         const int total = min(MT, M - m0) * gpr;
-        for (int q0 = tid; q0 < total; q0 += SB * THREADS) {
+        if (x_kind == G4_KIND_I8) {
+            // codes as given: 16-byte loads (two groups), all of a thread's loads in flight at
+            // once, then a byte permute per 8-code group for 4-bit weights
+            constexpr int U16 = (MT * KC / 16 + THREADS - 1) / THREADS;
+            const int upr = kcn >> 4, total16 = min(MT, M - m0) * upr;
+            u32x4 raw[U16];
+            int rr[U16], uu[U16];
+#pragma unroll
+            for (int u = 0; u < U16; ++u) {
+                const int q = min(tid + u * THREADS, total16 - 1);
+                rr[u] = q / upr;
+                uu[u] = q - rr[u] * upr;
+                raw[u] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const int8_t *>(x) +
+                                                          (int64_t)(m0 + rr[u]) * K + kc0 + uu[u] * 16);
+            }
+#pragma unroll
+            for (int u = 0; u < U16; ++u) {
+                if (tid + u * THREADS >= total16) break;
+                u32x4 o = raw[u];
+                if (BITS == 4) {  // [x0 x2 x4 x6 | x1 x3 x5 x7] per 8-code group
+                    o = u32x4{__builtin_amdgcn_perm(raw[u].y, raw[u].x, 0x06040200u),
+                              __builtin_amdgcn_perm(raw[u].y, raw[u].x, 0x07050301u),
+                              __builtin_amdgcn_perm(raw[u].w, raw[u].z, 0x06040200u),
+                              __builtin_amdgcn_perm(raw[u].w, raw[u].z, 0x07050301u)};
+                }
+                *reinterpret_cast<u32x4 *>(&xs[rr[u] * XSTR + uu[u] * 16]) = o;
+            }
+        }
+        for (int q0 = tid; x_kind != G4_KIND_I8 && q0 < total; q0 += SB * THREADS) {
             u32x4 raw_a[SB], raw_b[SB];
             int rr[SB], gg[SB];  // row and group of each load, kept for the stores (one divide)
 #pragma unroll
@@ -334,24 +389,17 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
             }
         }
         lds_barrier();
-        const int ksteps = kcn / kTileBK;
-        const int kbase = kc0 / kTileBK;
         for (int kb0 = wave; kb0 < ksteps; kb0 += WAVES * BATCH) {
             u32x4 bw[NP][BATCH][BITS == 4 ? 1 : 2];
+            if (kb0 == wave) {
 #pragma unroll
-            for (int p = 0; p < NP; ++p) {
-                const uint8_t *wr = p == 0 ? wrow : wrow2;
+                for (int p = 0; p < NP; ++p)
 #pragma unroll
-                for (int u = 0; u < BATCH; ++u) {
-                    const int kb = min(kb0 + WAVES * u, ksteps - 1);  // clamped: every load is valid
-                    if (BITS == 4) {
-                        bw[p][u][0] = *reinterpret_cast<const u32x4 *>(wr + (kbase + kb) * 64 + g * 16);
-                    } else {
-                        bw[p][u][0] = *reinterpret_cast<const u32x4 *>(wr + (kbase + kb) * 128 + g * 32);
-                        bw[p][u][BITS == 4 ? 0 : 1] =
-                            *reinterpret_cast<const u32x4 *>(wr + (kbase + kb) * 128 + g * 32 + 16);
-                    }
-                }
+                    for (int u = 0; u < BATCH; ++u)
+#pragma unroll
+                        for (int h = 0; h < (BITS == 4 ? 1 : 2); ++h) bw[p][u][h] = bw_first[p][u][h];
+            } else {
+                load_small_weights<BITS, NP, BATCH, WAVES>(bw, wrow, wrow2, kb0, ksteps, kbase, g);
             }
 #pragma unroll
             for (int u = 0; u < BATCH; ++u) {
