@@ -319,27 +319,38 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
             if (u == jp) vv[u] = kvnew[kDecThreads + t];
     }
 
-    // scores of this half's heads
+    // scores of this half's heads: eight sequential 32-dim dot products (segment sg) per score,
+    // then the pairwise tree over the segments by DPP within each aligned 8-lane group:
+    // quad_perm(1,0,3,2) and (2,3,0,1) give every lane of a quad ((s0+s1)+(s2+s3)), then
+    // row_half_mirror brings the other quad's sum (a commutative last add). With every head
+    // present the guard-free form lets the eight chains interleave.
     float sc[HH];
+    auto score = [&](int h) {
+        const float *qh = qs + h * kDecThreads + sg * 32;
+        float a = 0.0f;
+#pragma unroll
+        for (int i4 = 0; i4 < 8; ++i4) {
+            const float4 qv = *reinterpret_cast<const float4 *>(qh + 4 * i4);
+            const float4 kv = kq[i4];
+            a = __fadd_rn(a, __fmul_rn(qv.x, kv.x));
+            a = __fadd_rn(a, __fmul_rn(qv.y, kv.y));
+            a = __fadd_rn(a, __fmul_rn(qv.z, kv.z));
+            a = __fadd_rn(a, __fmul_rn(qv.w, kv.w));
+        }
+        return a;
+    };
+    if (heads == kAttnMaxHeads) {
+#pragma unroll
+        for (int hh = 0; hh < HH; ++hh) sc[hh] = score(half * HH + hh);
+    } else {
+#pragma unroll
+        for (int hh = 0; hh < HH; ++hh) sc[hh] = half * HH + hh < heads ? score(half * HH + hh) : 0.0f;
+    }
 #pragma unroll
     for (int hh = 0; hh < HH; ++hh) {
-        const int h = half * HH + hh;
-        float a = 0.0f;
-        if (h < heads) {
-            const float *qh = qs + h * kDecThreads + sg * 32;
-#pragma unroll
-            for (int i4 = 0; i4 < 8; ++i4) {
-                const float4 qv = *reinterpret_cast<const float4 *>(qh + 4 * i4);
-                const float4 kv = kq[i4];
-                a = __fadd_rn(a, __fmul_rn(qv.x, kv.x));
-                a = __fadd_rn(a, __fmul_rn(qv.y, kv.y));
-                a = __fadd_rn(a, __fmul_rn(qv.z, kv.z));
-                a = __fadd_rn(a, __fmul_rn(qv.w, kv.w));
-            }
-        }
-        a = __fadd_rn(a, __shfl_xor(a, 1));
-        a = __fadd_rn(a, __shfl_xor(a, 2));
-        sc[hh] = __fadd_rn(a, __shfl_xor(a, 4));
+        float a = __fadd_rn(sc[hh], dpp_f32_b1(sc[hh]));
+        a = __fadd_rn(a, dpp_f32_4e(a));
+        sc[hh] = __fadd_rn(a, dpp_f32_half_mirror(a));
     }
     if (sg == 0) {
 #pragma unroll
@@ -370,21 +381,32 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
     }
     __syncthreads();
 
-    // o[h][d] = sum over positions (ascending) of e[h][j] * v[j][d], for this half's heads
+    // o[h][d] = sum over positions (ascending) of e[h][j] * v[j][d], for this half's heads; a
+    // whole chunk with every head present takes the guard-free form, whose chains interleave
+    auto pv = [&](int h, bool whole) {
+        float o = 0.0f;
 #pragma unroll
-    for (int g = 0; g < HH; ++g) {
-        const int h = half * HH + g;
-        if (h < heads) {
-            float o = 0.0f;
+        for (int u4 = 0; u4 < kAttnChunk; u4 += 4) {  // four weights per LDS read
+            const float4 e4 = *reinterpret_cast<const float4 *>(es + h * kAttnChunk + u4);
+            const float e[4] = {e4.x, e4.y, e4.z, e4.w};
 #pragma unroll
-            for (int u4 = 0; u4 < kAttnChunk; u4 += 4) {  // four weights per LDS read
-                const float4 e4 = *reinterpret_cast<const float4 *>(es + h * kAttnChunk + u4);
-                const float e[4] = {e4.x, e4.y, e4.z, e4.w};
+            for (int i = 0; i < 4; ++i)
+                if (whole || u4 + i < cnt) o = __fadd_rn(o, __fmul_rn(e[i], vv[u4 + i]));
+        }
+        return o;
+    };
+    if (heads == kAttnMaxHeads && cnt == kAttnChunk) {
+        float o[HH];
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (u4 + i < cnt) o = __fadd_rn(o, __fmul_rn(e[i], vv[u4 + i]));
-            }
-            part_o[((row * heads + h) * max_chunks + c) * kDecThreads + t] = o;
+        for (int g = 0; g < HH; ++g) o[g] = pv(half * HH + g, true);
+#pragma unroll
+        for (int g = 0; g < HH; ++g)
+            part_o[((row * heads + half * HH + g) * max_chunks + c) * kDecThreads + t] = o[g];
+    } else {
+#pragma unroll
+        for (int g = 0; g < HH; ++g) {
+            const int h = half * HH + g;
+            if (h < heads) part_o[((row * heads + h) * max_chunks + c) * kDecThreads + t] = pv(h, false);
         }
     }
 }
