@@ -466,7 +466,31 @@ __global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(
     if ((t & 63) == 0) red[t >> 6] = m;
     __syncthreads();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // The partials of chunk batch u0 + kB are requested while batch u0 is summed (two register
+    // buffers), and a whole batch is summed without per-chunk guards; the order stays ascending.
     float L = 0.0f, O = 0.0f;
+    float ob[kB];
+    auto load = [&](float (&dst)[kB], int c0, int u0, int n) {
+#pragma unroll
+        for (int u = 0; u < kB; ++u) dst[u] = part_o[(slot0 + c0 + min(u0 + u, n - 1)) * kDecThreads + t];
+    };
+    auto accumulate = [&](const float (&src)[kB], int u0, int n) {
+        if (u0 + kB <= n) {
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                L = __fadd_rn(L, __fmul_rn(ls[u0 + u], ws[u0 + u]));
+                O = __fadd_rn(O, __fmul_rn(src[u], ws[u0 + u]));
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                if (u0 + u < n) {
+                    L = __fadd_rn(L, __fmul_rn(ls[u0 + u], ws[u0 + u]));
+                    O = __fadd_rn(O, __fmul_rn(src[u], ws[u0 + u]));
+                }
+            }
+        }
+    };
     for (int c0 = 0; c0 < chunks; c0 += kDecThreads) {
         const int n = min(kDecThreads, chunks - c0);
         if (t < n) {
@@ -474,18 +498,13 @@ __global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(
             ls[t] = c0 == 0 ? lt : part_ml[(slot0 + c0 + t) * 2 + 1];
         }
         __syncthreads();
-        for (int u0 = 0; u0 < n; u0 += kB) {
-            if (c0 + u0 > 0) {
-#pragma unroll
-                for (int u = 0; u < kB; ++u)
-                    oo[u] = part_o[(slot0 + c0 + min(u0 + u, n - 1)) * kDecThreads + t];
-            }
-#pragma unroll
-            for (int u = 0; u < kB; ++u) {
-                if (u0 + u < n) {
-                    L = __fadd_rn(L, __fmul_rn(ls[u0 + u], ws[u0 + u]));
-                    O = __fadd_rn(O, __fmul_rn(oo[u], ws[u0 + u]));
-                }
+        if (c0 > 0) load(oo, c0, 0, n);
+        for (int u0 = 0; u0 < n; u0 += 2 * kB) {
+            if (u0 + kB < n) load(ob, c0, u0 + kB, n);
+            accumulate(oo, u0, n);
+            if (u0 + kB < n) {
+                if (u0 + 2 * kB < n) load(oo, c0, u0 + 2 * kB, n);
+                accumulate(ob, u0 + kB, n);
             }
         }
         __syncthreads();
