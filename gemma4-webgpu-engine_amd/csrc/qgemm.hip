@@ -976,11 +976,14 @@ __global__ __launch_bounds__(512, 4) void qgemm_wide_kernel(
     int tiles_n) {
     __shared__ __align__(1024) uint8_t smem[kWideNS * kWideSB];
     static_assert(kWideNS * kWideSB >= 8 * 6 * 1024 + kWideBN * 4, "the K-half exchange and the scales fit the ring");
-    // XCD-aware order as in the narrow tile: one XCD takes every M tile of a run of N tiles.
+    // XCD-aware order: XCD x takes the N tiles x, x + 8, ... and its consecutive blocks walk those N
+    // tiles fastest, so the blocks resident on one XCD share a run of activation rows (at M = 2048,
+    // two blocks per CU: 16 row tiles x 4 column tiles, 2.1 MB, inside the XCD's 4 MB L2).
     const int b = blockIdx.x;
     const int xcd = b & 7, idx = b >> 3;
-    const int tm = idx % tiles_m;
-    const int tn = (idx / tiles_m) * 8 + xcd;
+    const int tnx = (tiles_n + 7) >> 3;
+    const int tm = idx / tnx;
+    const int tn = (idx % tnx) * 8 + xcd;
     if (tn >= tiles_n) return;  // whole block, before any barrier
     const int m0 = tm * kWideBM, n0 = tn * kWideBN;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1056,6 +1059,42 @@ __global__ __launch_bounds__(512, 4) void qgemm_wide_kernel(
 
     bool r_ok;
     const float rcp = srq_recip(out_scale, r_ok);
+    // A whole tile of int8 outputs (the usual case): the same snap with no row, column or
+    // alignment checks per group of 4 (N % 4 == 0 keeps every 4-byte store aligned).
+    if (out_kind == G4_KIND_I8 && out_scale != 0.0f && m0 + kWideBM <= M && n0 + kWideBN <= N && (N & 3) == 0) {
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            int8_t *drow = reinterpret_cast<int8_t *>(dst) + (int64_t)(m0 + (2 * kh + tt) * 16 + j) * N + n0 +
+                           wn * 48 + 4 * g;
+#pragma unroll
+            for (int u = 0; u < 3; ++u) {
+                const float4 s4 = *reinterpret_cast<const float4 *>(S + wn * 48 + u * 16 + 4 * g);
+                const float sc[4] = {s4.x, s4.y, s4.z, s4.w};
+                const int v[4] = {sum[tt][u].x >> 4, sum[tt][u].y >> 4, sum[tt][u].z >> 4, sum[tt][u].w >> 4};
+                float y[4], code[4];
+                float worst = r_ok ? 0.0f : 1.0f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    y[e] = __fmul_rn(sc[e], (float)v[e]);  // the reference's order
+                    const float t = __fmul_rn(y[e], rcp);
+                    code[e] = rintf(t);
+                    worst = fmaxf(worst, fabsf(t - code[e]));
+                }
+                if (worst >= 0.5f - 0x1p-13f) {  // the quotient bound of the generic path below
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) code[e] = rintf(__fdiv_rn(y[e], out_scale));
+                }
+                uint32_t bb[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    bb[e] = __float_as_uint(__fadd_rn(fminf(fmaxf(code[e], -128.0f), 127.0f), 12582912.0f));
+                const uint32_t lo = __builtin_amdgcn_perm(bb[1], bb[0], 0x0C0C0400u);
+                const uint32_t hi = __builtin_amdgcn_perm(bb[3], bb[2], 0x0C0C0400u);
+                *reinterpret_cast<uint32_t *>(drow + u * 16) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
         const int m = m0 + (2 * kh + tt) * 16 + j;
