@@ -830,9 +830,10 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(
 //     stage st's MFMAs and only the ring slot of stage st-1 (read a full stage earlier) is
 //     refilled after the barrier;
 //   - the MFMA takes the weights as its A operand, so the accumulator is the transposed tile: lane
-//     (j, g) holds output row j, columns 4 g .. 4 g + 3 of each 16 x 16 tile, and the epilogue
-//     stores 4 consecutive outputs per lane (1.7 us faster at M = 512 than storing the 24 outputs
-//     of the untransposed layout one by one);
+//     (j, g) holds output row j, columns 4 g .. 4 g + 3 of each 16 x 16 tile, so the epilogue
+//     packs 4 consecutive int8 outputs per lane into one word; a whole tile's words are gathered
+//     in LDS and written as 16-byte runs of 192-byte tile rows (9.6 -> 9.0 us at M = 512,
+//     28.9 -> 26.0 us at M = 2048, against one 4-byte store per group);
 //   - the two K halves meet through LDS (each wave keeps two of its four row tiles), then every
 //     wave snaps 2 x 3 groups of 4 outputs. A group falls back to the IEEE divide only when some
 //     lane's quotient lies within 2^-13 of a half integer (one branch per group, not per output).
@@ -843,6 +844,11 @@ constexpr int kWideBN = 192;
 constexpr int kWideNS = 4;
 constexpr int kWideA = kWideBM * 128;              // activation bytes per stage
 constexpr int kWideSB = kWideA + kWideBN * 64;     // stage buffer: activations + packed weights
+// The epilogue's int8 code tile, in the ring after the K-half exchange (48 KB) and the scales.
+constexpr int kWideCodeTile = 50 * 1024;
+constexpr int kWideCodeRow = kWideBN + 16;
+static_assert(8 * 6 * 1024 + kWideBN * 4 <= kWideCodeTile && kWideCodeTile + kWideBM * kWideCodeRow <= kWideNS * kWideSB,
+              "the epilogue code tile fits the ring after the exchange and the scales");
 
 template <int N, bool LGKM> __device__ __forceinline__ void wide_wait() {
     static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
@@ -1060,12 +1066,17 @@ __global__ __launch_bounds__(512, 4) void qgemm_wide_kernel(
     bool r_ok;
     const float rcp = srq_recip(out_scale, r_ok);
     // A whole tile of int8 outputs (the usual case): the same snap with no row, column or
-    // alignment checks per group of 4 (N % 4 == 0 keeps every 4-byte store aligned).
-    if (out_kind == G4_KIND_I8 && out_scale != 0.0f && m0 + kWideBM <= M && n0 + kWideBN <= N && (N & 3) == 0) {
+    // alignment checks per group of 4. Each group's 4 codes go to a 64 x 192 code tile in LDS
+    // (rows 208 bytes apart, so the 64 lanes of a group store hit distinct banks); then each
+    // thread stores 16-byte runs of whole tile rows (192 contiguous bytes per row), in place of
+    // 4-byte stores scattered over 16 rows per instruction. N % 16 == 0 and a 16-byte aligned dst
+    // keep every run aligned.
+    if (out_kind == G4_KIND_I8 && out_scale != 0.0f && m0 + kWideBM <= M && n0 + kWideBN <= N && (N & 15) == 0 &&
+        ((uintptr_t)dst & 15) == 0) {
+        uint8_t *T = smem + kWideCodeTile;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
-            int8_t *drow = reinterpret_cast<int8_t *>(dst) + (int64_t)(m0 + (2 * kh + tt) * 16 + j) * N + n0 +
-                           wn * 48 + 4 * g;
+            uint8_t *trow = T + ((2 * kh + tt) * 16 + j) * kWideCodeRow + wn * 48 + 4 * g;
 #pragma unroll
             for (int u = 0; u < 3; ++u) {
                 const float4 s4 = *reinterpret_cast<const float4 *>(S + wn * 48 + u * 16 + 4 * g);
@@ -1090,8 +1101,15 @@ __global__ __launch_bounds__(512, 4) void qgemm_wide_kernel(
                     bb[e] = __float_as_uint(__fadd_rn(fminf(fmaxf(code[e], -128.0f), 127.0f), 12582912.0f));
                 const uint32_t lo = __builtin_amdgcn_perm(bb[1], bb[0], 0x0C0C0400u);
                 const uint32_t hi = __builtin_amdgcn_perm(bb[3], bb[2], 0x0C0C0400u);
-                *reinterpret_cast<uint32_t *>(drow + u * 16) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+                *reinterpret_cast<uint32_t *>(trow + u * 16) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
             }
+        }
+        __syncthreads();
+        for (int c = tid; c < kWideBM * (kWideBN / 16); c += 512) {
+            const int r = c / (kWideBN / 16), cc = c - r * (kWideBN / 16);
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(T + r * kWideCodeRow + cc * 16);
+            __builtin_nontemporal_store(
+                v, reinterpret_cast<u32x4 *>(reinterpret_cast<int8_t *>(dst) + (int64_t)(m0 + r) * N + n0 + cc * 16));
         }
         return;
     }
