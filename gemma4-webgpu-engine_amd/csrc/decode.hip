@@ -36,11 +36,11 @@ static_assert(kDecThreads == kRowThreads, "the glue kernels run the shared 256-l
 
 // ---- rms-norm / norm-residual / norm-residual-norm --------------------------------------------------
 
-// One block per row (rms_join_row). ACC: the source is split accumulators (load_acc).
+// One block per row (rms_join_row). ACC: the source is split accumulators (acc_sum, acc_value).
 template <bool ACC>
 __global__ __launch_bounds__(kDecThreads) void join_kernel(JoinTail J) {
     __shared__ float lds[2 * kDecThreads];
-    rms_join_row<ACC>(J, blockIdx.x, lds);
+    rms_join_row<ACC ? kSplitAccMax : 0>(J, blockIdx.x, lds);
 }
 
 int join_acc(const JoinTail &J, int rows, hipStream_t stream) {
@@ -226,6 +226,9 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
     const int lo = window > 0 ? max(0, pos - window + 1) : 0;
     const int chunks = (pos - lo + 1 + kAttnChunk - 1) / kAttnChunk;
     if (c >= chunks) return;  // whole block
+    // the accumulator the merge adds o_proj's per-head partials into starts at zero
+    if (PRO && pro.zero && c == 0 && row == 0)
+        for (int i = tid; i < pro.zero_n; i += THREADS) pro.zero[i] = 0;
     const int start = lo + c * kAttnChunk;
     const int cnt = min(kAttnChunk, pos + 1 - start);
     float *kb = const_cast<float *>(k_cache) + row * cache_row_stride;
@@ -437,21 +440,16 @@ static void launch_split(int chunks, int rows, hipStream_t st, const float *q, c
                            part_o, chunks, pro);
 }
 
-// Grid (heads, rows); thread d merges dim d over the chunks in ascending order: M = max m_c,
+// Thread d merges dim d of head h, row `row`, over the chunks in ascending order: M = max m_c,
 // w_c = exp(m_c - M) (once per chunk, staged in LDS), L = sum l_c w_c, O = sum o_c w_c,
-// out = O / L, then the o_proj input snap. Every load that does not depend on M goes out first
-// (the chunk's (m, l) pairs and the first kB partials of the thread's dim); M is a shuffle max in
-// each wave and a max over the four waves (max is exact in any order).
-__global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(
-    const float *part_ml, const float *part_o, int heads, int pos_host, const int32_t *pos_dev,
-    int window, int max_chunks, float in_scale, int8_t *codes, float *out_f32) {
+// returns O / L. Every load that does not depend on M goes out first (the chunk's (m, l) pairs
+// and the first kB partials of the thread's dim); M is a shuffle max in each wave and a max over
+// the four waves (max is exact in any order). red: 4 floats, ws / ls: kDecThreads floats of LDS.
+__device__ __forceinline__ float merge_head_dim(const float *part_ml, const float *part_o, int heads,
+                                                int h, int64_t row, int pos, int window,
+                                                int max_chunks, float *red, float *ws, float *ls) {
     constexpr int kB = 16;  // partials loaded together (indices clamped, so all valid)
-    __shared__ float red[kDecThreads / 64];
-    __shared__ float ws[kDecThreads];
-    __shared__ float ls[kDecThreads];
-    const int t = threadIdx.x, h = blockIdx.x;
-    const int64_t row = blockIdx.y;
-    const int pos = step_pos(pos_host, pos_dev);
+    const int t = threadIdx.x;
     const int lo = window > 0 ? max(0, pos - window + 1) : 0;
     const int chunks = (pos - lo + 1 + kAttnChunk - 1) / kAttnChunk;
     const int64_t slot0 = (row * heads + h) * max_chunks;
@@ -509,10 +507,94 @@ __global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(
         }
         __syncthreads();
     }
-    const float y = __fdiv_rn(O, L);
+    return __fdiv_rn(O, L);
+}
+
+// Grid (heads, rows): the merged attention row of head h, then the o_proj input snap.
+__global__ __launch_bounds__(kDecThreads) void attn_merge_kernel(
+    const float *part_ml, const float *part_o, int heads, int pos_host, const int32_t *pos_dev,
+    int window, int max_chunks, float in_scale, int8_t *codes, float *out_f32) {
+    __shared__ float red[kDecThreads / 64];
+    __shared__ float ws[kDecThreads];
+    __shared__ float ls[kDecThreads];
+    const int t = threadIdx.x, h = blockIdx.x;
+    const int64_t row = blockIdx.y;
+    const float y = merge_head_dim(part_ml, part_o, heads, h, row, step_pos(pos_host, pos_dev), window,
+                                   max_chunks, red, ws, ls);
     const int64_t o = (row * heads + h) * kDecThreads + t;
     if (out_f32) out_f32[o] = y;
     if (codes) codes[o] = snap_code(y, in_scale);
+}
+
+// The merge with o_proj folded in (one decode row): grid (heads, n / kMergeRows). Block (h, g)
+// merges head h (the merge kernel's arithmetic, so the same codes), snaps it on o_proj's inScale
+// into LDS, and contracts those 256 codes with the 128-byte slices of o_proj's 4-bit rows
+// g * kMergeRows .. + kMergeRows that head h's columns occupy: the exact int32 accumulator of
+// o_proj row n over K range 256 h .. 256 h + 255 (zero point included), added atomically into
+// acc[n] (zeroed by the split kernel before). Integer addition is exact in any order, so acc[n]
+// is o_proj's accumulator and a consumer that applies o_proj's epilogue to it (acc_value) reads
+// o_proj's codes bit for bit. The weight slices are requested before the merge, so their memory
+// latency overlaps it. Eight lanes share a row: lane t reads the row's 16-byte chunk t % 8, then
+// a three-step xor sum.
+// sum(u * x) over one 16-byte word group of 32 packed 4-bit codes u (unsigned nibbles, low first)
+// and their 32 activation codes x in the snap layout: the low and high nibbles each dot one half.
+__device__ __forceinline__ int chunk_dot4(const u32x4 &w, const uint8_t *x) {
+    const u32x4 xa = *reinterpret_cast<const u32x4 *>(x);
+    const u32x4 xb = *reinterpret_cast<const u32x4 *>(x + 16);
+    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+    const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    int acc = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        acc = __builtin_amdgcn_sdot4((int)(wv[i] & 0x0F0F0F0Fu), (int)xv[2 * i], acc, false);
+        acc = __builtin_amdgcn_sdot4((int)((wv[i] >> 4) & 0x0F0F0F0Fu), (int)xv[2 * i + 1], acc, false);
+    }
+    return acc;
+}
+
+constexpr int kMergeRows = 192;
+__global__ __launch_bounds__(kDecThreads) void attn_merge_o_kernel(
+    const float *part_ml, const float *part_o, int heads, int pos_host, const int32_t *pos_dev,
+    int window, int max_chunks, float in_scale, int8_t *codes, const uint8_t *w, int n_out,
+    int k_total, int32_t *part) {
+    constexpr int kPasses = kMergeRows / (kDecThreads / 8);
+    __shared__ float red[kDecThreads / 64];
+    __shared__ float ws[kDecThreads];
+    __shared__ float ls[kDecThreads];
+    __shared__ __align__(16) uint8_t xs[kDecThreads];
+    __shared__ int csum[kDecThreads / 64];
+    const int t = threadIdx.x, h = blockIdx.x;
+    const int row0 = blockIdx.y * kMergeRows;
+    const int64_t row_bytes = k_total >> 1;
+    u32x4 wv[kPasses];
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        const int r = min(row0 + p * (kDecThreads / 8) + (t >> 3), n_out - 1);
+        wv[p] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4 *>(w + r * row_bytes + h * (kDecThreads / 2) + (t & 7) * 16));
+    }
+    const float y = merge_head_dim(part_ml, part_o, heads, h, 0, step_pos(pos_host, pos_dev), window,
+                                   max_chunks, red, ws, ls);
+    const int c = srq_code_i(y, in_scale);
+    if (blockIdx.y == 0 && codes) codes[h * kDecThreads + t] = (int8_t)c;
+    // codes in the 4-bit snap layout: each 8-code group as [x0 x2 x4 x6 | x1 x3 x5 x7]
+    const int j = t & 7;
+    xs[(t & ~7) + (j & 1 ? 4 : 0) + (j >> 1)] = (uint8_t)c;
+    int s = c;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+    if ((t & 63) == 0) csum[t >> 6] = s;
+    __syncthreads();
+    const int xsum = csum[0] + csum[1] + csum[2] + csum[3];
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        int acc = chunk_dot4(wv[p], xs + (t & 7) * 32);
+        acc += __shfl_xor(acc, 1);
+        acc += __shfl_xor(acc, 2);
+        acc += __shfl_xor(acc, 4);
+        const int r = row0 + p * (kDecThreads / 8) + (t >> 3);
+        if ((t & 7) == 0 && r < n_out) atomicAdd(part + r, acc - 8 * xsum);
+    }
 }
 
 // ---- gelu * up with the consumer's snap ------------------------------------------------------------
@@ -695,7 +777,8 @@ namespace g4 {
 int attention_decode_fused(const AttnPrologue &pro, float *k_cache, float *v_cache,
                            int64_t cache_row_stride, int rows, int heads, int pos,
                            const int32_t *pos_dev, int window, float *workspace,
-                           size_t workspace_bytes, float in_scale, int8_t *codes, void *stream) {
+                           size_t workspace_bytes, float in_scale, int8_t *codes, void *stream,
+                           const MergeLinear *lin) {
     if (!pro.q_codes || !pro.q_gain || !pro.cos_tab || !pro.sin_tab || !k_cache || !v_cache ||
         !workspace || !codes || rows <= 0 || heads <= 0 || heads > kAttnMaxHeads || pos < 0 ||
         window < 0 || in_scale == 0.0f)
@@ -710,11 +793,26 @@ int attention_decode_fused(const AttnPrologue &pro, float *k_cache, float *v_cac
     launch_split<true>(chunks, rows, as_stream(stream), nullptr, k_cache, v_cache,
                                 cache_row_stride, heads, pos, pos_dev, window, part_ml, part_o, pro);
     G4_LAUNCHED("attn_split_kernel");
+    if (lin) {
+        if (!merge_linear_fits(*lin, rows, heads))
+            return set_error(G4_ERR_INVALID, "attention (fused prologue): the folded o_proj does not fit");
+        hipLaunchKernelGGL(attn_merge_o_kernel, dim3(heads, lin->n / kMergeRows), dim3(kDecThreads), 0,
+                           as_stream(stream), part_ml, part_o, heads, pos, pos_dev, window, chunks,
+                           in_scale, codes, reinterpret_cast<const uint8_t *>(lin->w), lin->n, lin->k, lin->part);
+        G4_LAUNCHED("attn_merge_o_kernel");
+        return G4_OK;
+    }
     hipLaunchKernelGGL(attn_merge_kernel, dim3(heads, rows), dim3(kDecThreads), 0,
                        as_stream(stream), part_ml, part_o, heads, pos, pos_dev, window, chunks,
                        in_scale, codes, nullptr);
     G4_LAUNCHED("attn_merge_kernel");
     return G4_OK;
+}
+
+bool merge_linear_fits(const MergeLinear &lin, int rows, int heads) {
+    return lin.w && lin.part && rows == 1 && heads >= 1 && heads <= kAttnMaxHeads && lin.n > 0 &&
+           lin.n % kMergeRows == 0 && lin.k == heads * kDecThreads &&
+           (reinterpret_cast<uintptr_t>(lin.w) & 15) == 0;
 }
 
 }  // namespace g4

@@ -84,6 +84,10 @@ struct g4_decode {
     // batch 3..32: down_proj runs as kAccSplits K ranges of int32 accumulators, summed by the
     // post-FFN join (null when down is one launch)
     int32_t *acc = nullptr;
+    // batch 1: o_proj runs inside the attention merge, each query head's K range added atomically
+    // into this int32 accumulator [hidden] (cleared by the split kernel); the post-attention join
+    // applies o_proj's epilogue to it (null when o_proj is a plan)
+    int32_t *oacc = nullptr;
     std::vector<float *> kv;  // per producer: [batch][2][capacity][head_dim]
     int stop = -1;
     // M = 1 GEMV plans per layer: qkv (or q), o, gate+up, down, ple gate, ple projection.
@@ -369,8 +373,33 @@ int build(g4_decode &d) {
     }
     build_joins(d);
     if (B != 1) return G4_OK;
-    // M = 1: one grouped-GEMV plan per launch group.
     const float in = s.in_scale, out = s.out_scale;
+    // o_proj folded into the attention merge when every layer's weights fit its form: each head's
+    // merge block contracts its 256 codes with that head's K range of o_proj and adds the exact
+    // partial into one int32 accumulator; the post-attention join applies o_proj's epilogue and
+    // snap to it, so it reads o_proj's own codes (one launch fewer per layer)
+    bool fold_o = true;
+    for (int l = 0; l < s.layers; ++l) {
+        MergeLinear lin;
+        lin.w = d.layers[l].o;
+        lin.n = H;
+        lin.k = QW;
+        lin.part = reinterpret_cast<int32_t *>(d.hbuf[0]);  // any non-null pointer: shape check only
+        fold_o = fold_o && merge_linear_fits(lin, B, s.q_heads);
+    }
+    if (fold_o) {
+        G4_TRY(m.get((void **)&d.oacc, (size_t)H * sizeof(int32_t)));
+        for (int l = 0; l < s.layers; ++l) {
+            JoinTail &j = d.joins[join_index(l, 0)];
+            j.src = d.oacc;
+            j.src_kind = G4_KIND_I32;
+            j.acc_scales = d.layers[l].o_s;
+            j.acc_in_scale = in;
+            j.acc_splits = 1;
+            j.acc_split_stride = H;
+        }
+    }
+    // M = 1: one grouped-GEMV plan per launch group.
     d.plans.assign((size_t)s.layers * P_PER_LAYER, Plan{});
     for (int l = 0; l < s.layers; ++l) {
         const g4_decode_layer &L = d.layers[l];
@@ -381,8 +410,10 @@ int build(g4_decode &d) {
             g.push_back(desc(L.v, L.v_s, d.xcodes, d.vc, 4, H, s.head_dim, G4_KIND_I8, in, out));
         }
         G4_TRY(try_plan(g.data(), (int)g.size(), P[P_QKV]));
-        g4_gemv_desc o = desc(L.o, L.o_s, d.attn_codes, d.oc, 4, QW, H, G4_KIND_I8, in, out);
-        G4_TRY(try_plan(&o, 1, P[P_O]));
+        if (!d.oacc) {
+            g4_gemv_desc o = desc(L.o, L.o_s, d.attn_codes, d.oc, 4, QW, H, G4_KIND_I8, in, out);
+            G4_TRY(try_plan(&o, 1, P[P_O]));
+        }
         // gate and up rows stream through one paired tile whose epilogue is the gelu-mul pass:
         // act = srq(gelu(gate code * out) * (up code * out), in), the codes down_proj reads
         GeluEpilogue gue;
@@ -476,10 +507,18 @@ int run_layer(g4_decode &d, int l, void *st) {
     pro.cos_tab = cos_tab;
     pro.sin_tab = sin_tab;
     pro.eps = s.eps;
+    pro.zero = d.oacc;
+    pro.zero_n = d.oacc ? H : 0;
+    MergeLinear lin;
+    lin.w = L.o;
+    lin.n = H;
+    lin.k = QW;
+    lin.part = d.oacc;
     G4_TRY(attention_decode_fused(pro, kb, vb, row_stride, B, s.q_heads, s.kv_capacity - 1, d.pos,
                                   glob ? 0 : s.sliding_window, d.attn_ws, d.attn_ws_bytes, in,
-                                  d.attn_codes, st));
-    G4_TRY(run_linear_rows(d, plan(P_O), desc(L.o, L.o_s, d.attn_codes, d.oc, 4, QW, H, G4_KIND_I8, in, out), st));
+                                  d.attn_codes, st, d.oacc ? &lin : nullptr));
+    if (!d.oacc)
+        G4_TRY(run_linear_rows(d, plan(P_O), desc(L.o, L.o_s, d.attn_codes, d.oc, 4, QW, H, G4_KIND_I8, in, out), st));
     G4_TRY(run_join(d, join_index(l, 0), st));
     // MLP block: gate, up and the gelu-mul pass (one paired launch when folded), then down
     if (plan(P_GATEUP).gelu) {

@@ -147,13 +147,31 @@ struct AttnPrologue {
     const float *cos_tab;  // [positions][128]
     const float *sin_tab;
     float eps;
+    int32_t *zero = nullptr;  // zero_n int32 the split kernel clears (the folded o_proj's accumulator)
+    int zero_n = 0;
 };
 
-// g4_attention_decode with the prologue fused (head_dim 256, int8 codes out on in_scale).
+// o_proj folded into the attention merge (one decode row): w is its 4-bit [n][k] weights with
+// k = heads * 256; part (n int32, zero when the merge starts: AttnPrologue::zero) receives o_proj's
+// exact accumulator, each head's K range added atomically (a JoinTail with src_kind
+// G4_KIND_I32 and one split reads it).
+struct MergeLinear {
+    const void *w = nullptr;
+    int n = 0;
+    int k = 0;
+    int32_t *part = nullptr;
+};
+
+// Whether the merge can fold `lin` in (rows 1, n a multiple of the merge's row block, k = heads * 256).
+bool merge_linear_fits(const MergeLinear &lin, int rows, int heads);
+
+// g4_attention_decode with the prologue fused (head_dim 256, int8 codes out on in_scale). With
+// `lin`, the merge also runs o_proj's per-head partial accumulators (codes stay the merge's).
 int attention_decode_fused(const AttnPrologue &pro, float *k_cache, float *v_cache,
                            int64_t cache_row_stride, int rows, int heads, int pos,
                            const int32_t *pos_dev, int window, float *workspace,
-                           size_t workspace_bytes, float in_scale, int8_t *codes, void *stream);
+                           size_t workspace_bytes, float in_scale, int8_t *codes, void *stream,
+                           const MergeLinear *lin = nullptr);
 
 // Makes a plan snap each block's first activation vector inside its first tile, after that tile's
 // weight loads are out (the decode runner's small plans: the snap's latency overlaps the weights').

@@ -55,17 +55,28 @@ __device__ __forceinline__ int8_t snap_code(float v, float s) { return (int8_t)s
 // set). lds: 512 floats (the two reductions take one half each).
 // The value of element i (flat index idx) of a join over split accumulators: the producing
 // linear's epilogue f32(in_scale * scale) * f32(acc), its int8 snap, dequantized by the join.
-__device__ __forceinline__ float load_acc(const JoinTail &J, int64_t idx, int i) {
+// The int32 sum of element idx's split partials (at most SPLITS of them). Branch free (a split
+// past acc_splits re-reads split 0 and adds nothing), so a caller's loads of several elements all
+// go out before any sum.
+template <int SPLITS>
+__device__ __forceinline__ int acc_sum(const JoinTail &J, int64_t idx) {
     const int32_t *p = reinterpret_cast<const int32_t *>(J.src) + idx;
+    if constexpr (SPLITS == 1) return p[0];
+    int part[SPLITS];
+#pragma unroll
+    for (int s = 0; s < SPLITS; ++s) part[s] = p[(s < J.acc_splits ? s : 0) * J.acc_split_stride];
     int acc = 0;
 #pragma unroll
-    for (int s = 0; s < kSplitAccMax; ++s)
-        if (s < J.acc_splits) acc += p[s * J.acc_split_stride];
-    const float y = __fmul_rn(__fmul_rn(J.acc_in_scale, J.acc_scales[i]), (float)acc);
+    for (int s = 0; s < SPLITS; ++s) acc += s < J.acc_splits ? part[s] : 0;
+    return acc;
+}
+__device__ __forceinline__ float acc_value(const JoinTail &J, int acc, float scale) {
+    const float y = __fmul_rn(__fmul_rn(J.acc_in_scale, scale), (float)acc);
     return __fmul_rn((float)snap_code(y, J.src_scale), J.src_scale);
 }
 
-template <bool ACC = false, typename Emit>
+// ACC > 0: the source is at most ACC split int32 accumulators (src_kind G4_KIND_I32).
+template <int ACC = 0, typename Emit>
 __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row, float *lds,
                                                   Emit emit) {
     const int t = threadIdx.x;
@@ -74,17 +85,27 @@ __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row
     // every operand is loaded before the first barrier (a barrier also fences the compiler's
     // load scheduling, so later loads would each cost a memory latency of their own)
     float v[kJoinMaxPer], ga[kJoinMaxPer], re[kJoinMaxPer], g2[kJoinMaxPer];
+    int ai[ACC ? kJoinMaxPer : 1];
+    float as[ACC ? kJoinMaxPer : 1];
 #pragma unroll
     for (int e = 0; e < kJoinMaxPer; ++e) {
         const int i = t + e * kRowThreads;
         const bool in = i < width;
-        if (ACC)
-            v[e] = in ? load_acc(J, base + i, i) : 0.0f;
-        else
+        if constexpr (ACC > 0) {  // clamped indices, no branch: every element's loads go out before any epilogue
+            const int ic = in ? i : width - 1;
+            ai[e] = acc_sum<ACC>(J, base + ic);
+            as[e] = J.acc_scales[ic];
+        } else {
             v[e] = in ? load_val(J.src, J.src_kind, J.src_scale, base + i) : 0.0f;
+        }
         ga[e] = in && J.gain ? J.gain[i] : 1.0f;
         re[e] = in && J.resid ? J.resid[base + i] : 0.0f;
         g2[e] = in && J.gain2 ? J.gain2[i] : 0.0f;
+    }
+    if constexpr (ACC > 0) {
+#pragma unroll
+        for (int e = 0; e < kJoinMaxPer; ++e)
+            v[e] = t + e * kRowThreads < width ? acc_value(J, ai[e], as[e]) : 0.0f;
     }
     float part = 0.0f;
 #pragma unroll
@@ -124,7 +145,7 @@ __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row
 }
 
 // The join kernel's form: codes to J.codes[row][i]. lds: 512 floats.
-template <bool ACC = false>
+template <int ACC = 0>
 __device__ __forceinline__ void rms_join_row(const JoinTail &J, int64_t row, float *lds) {
     int8_t *codes = J.codes;
     const int64_t base = row * J.width;

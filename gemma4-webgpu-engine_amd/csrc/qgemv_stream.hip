@@ -266,12 +266,16 @@ __device__ __forceinline__ int snap_join(const JoinTail *pre, int four, uint8_t 
     int8_t *codes = blockIdx.x == 0 ? T.codes : nullptr;
     if (blockIdx.x != 0) T.hidden = nullptr;
     int local = 0;
-    rms_join_row_emit(T, 0, red, [&](int i, int8_t c) {
+    auto emit = [&](int i, int8_t c) {
         const int j = i & 7;
         xs[four ? (i & ~7) + (j & 1 ? 4 : 0) + (j >> 1) : i] = (uint8_t)c;
         if (codes) gstore<int8_t>(codes + i, c);
         local += c;
-    });
+    };
+    // an int32 accumulator source (the decode runner's o_proj folded into the attention merge)
+    // runs the producing linear's epilogue and snap first
+    if (T.src_kind == G4_KIND_I32) rms_join_row_emit<1>(T, 0, red, emit);
+    else rms_join_row_emit<0>(T, 0, red, emit);
     return local;
 }
 
@@ -711,8 +715,10 @@ int gemv_plan_set_prologue_join(g4_gemv_plan *p, const JoinTail &j) {
     if (!j.src || j.width <= 0 || j.width > kJoinMaxPer * kRowThreads || (j.width & 7))
         return set_error(G4_ERR_INVALID, "GEMV plan join: width %d (a multiple of 8, at most %d)",
                          j.width, kJoinMaxPer * kRowThreads);
-    if (j.src_kind != G4_KIND_F32 && j.src_kind != G4_KIND_I8)
-        return set_error(G4_ERR_INVALID, "GEMV plan join: src_kind must be f32 or int8 codes");
+    if (j.src_kind != G4_KIND_F32 && j.src_kind != G4_KIND_I8 && j.src_kind != G4_KIND_I32)
+        return set_error(G4_ERR_INVALID, "GEMV plan join: src_kind must be f32, int8 codes or int32 partials");
+    if (j.src_kind == G4_KIND_I32 && (!j.acc_scales || j.acc_splits != 1))
+        return set_error(G4_ERR_INVALID, "GEMV plan join: an int32 accumulator source needs its scales and one split");
     if (!j.codes || j.in_scale == 0.0f)
         return set_error(G4_ERR_INVALID, "GEMV plan join: needs its codes and the consumer's inScale");
     if (j.resid && j.hidden == j.resid)
