@@ -83,29 +83,46 @@ __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row
     const int width = J.width;
     const int64_t base = row * width;
     // every operand is loaded before the first barrier (a barrier also fences the compiler's
-    // load scheduling, so later loads would each cost a memory latency of their own)
+    // load scheduling, so later loads would each cost a memory latency of their own), at indices
+    // clamped into the row and with no branch between them, so no load waits for another; the
+    // conversions and the selects of the out-of-row elements come after all of them
     float v[kJoinMaxPer], ga[kJoinMaxPer], re[kJoinMaxPer], g2[kJoinMaxPer];
-    int ai[ACC ? kJoinMaxPer : 1];
+    int raw[kJoinMaxPer];  // the source element's bits: an int8 code, an f32, or the int32 sum
     float as[ACC ? kJoinMaxPer : 1];
+    int ic[kJoinMaxPer];
 #pragma unroll
-    for (int e = 0; e < kJoinMaxPer; ++e) {
-        const int i = t + e * kRowThreads;
-        const bool in = i < width;
-        if constexpr (ACC > 0) {  // clamped indices, no branch: every element's loads go out before any epilogue
-            const int ic = in ? i : width - 1;
-            ai[e] = acc_sum<ACC>(J, base + ic);
-            as[e] = J.acc_scales[ic];
-        } else {
-            v[e] = in ? load_val(J.src, J.src_kind, J.src_scale, base + i) : 0.0f;
-        }
-        ga[e] = in && J.gain ? J.gain[i] : 1.0f;
-        re[e] = in && J.resid ? J.resid[base + i] : 0.0f;
-        g2[e] = in && J.gain2 ? J.gain2[i] : 0.0f;
-    }
+    for (int e = 0; e < kJoinMaxPer; ++e) ic[e] = min(t + e * kRowThreads, width - 1);
     if constexpr (ACC > 0) {
 #pragma unroll
-        for (int e = 0; e < kJoinMaxPer; ++e)
-            v[e] = t + e * kRowThreads < width ? acc_value(J, ai[e], as[e]) : 0.0f;
+        for (int e = 0; e < kJoinMaxPer; ++e) {
+            raw[e] = acc_sum<ACC>(J, base + ic[e]);
+            as[e] = J.acc_scales[ic[e]];
+        }
+    } else if (J.src_kind == G4_KIND_I8) {
+        const int8_t *src = reinterpret_cast<const int8_t *>(J.src) + base;
+#pragma unroll
+        for (int e = 0; e < kJoinMaxPer; ++e) raw[e] = src[ic[e]];
+    } else {
+        const int *src = reinterpret_cast<const int *>(J.src) + base;
+#pragma unroll
+        for (int e = 0; e < kJoinMaxPer; ++e) raw[e] = src[ic[e]];
+    }
+#pragma unroll
+    for (int e = 0; e < kJoinMaxPer; ++e) {
+        ga[e] = J.gain ? J.gain[ic[e]] : 1.0f;
+        re[e] = J.resid ? J.resid[base + ic[e]] : 0.0f;
+        g2[e] = J.gain2 ? J.gain2[ic[e]] : 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < kJoinMaxPer; ++e) {
+        const bool in = t + e * kRowThreads < width;
+        float x;
+        if constexpr (ACC > 0) x = acc_value(J, raw[e], as[e]);
+        else x = J.src_kind == G4_KIND_I8 ? __fmul_rn((float)raw[e], J.src_scale) : __int_as_float(raw[e]);
+        v[e] = in ? x : 0.0f;
+        ga[e] = in ? ga[e] : 1.0f;
+        re[e] = in ? re[e] : 0.0f;
+        g2[e] = in ? g2[e] : 0.0f;
     }
     float part = 0.0f;
 #pragma unroll
