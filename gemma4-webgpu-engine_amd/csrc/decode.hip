@@ -597,6 +597,98 @@ __global__ __launch_bounds__(kDecThreads) void attn_merge_o_kernel(
     }
 }
 
+// ---- the per-layer-input block at one decode row: join, gate, gelu x row, projection ------------
+
+// per_layer_input_gate and per_layer_projection in one launch (the decode runner at batch 1):
+// block b runs the post-FFN join that produces the gate's input codes (every block, the join
+// kernel's arithmetic; block 0 also stores the join's residual row), the gate rows
+// b * kPleRows .. + kPleRows (8-bit, exact int32 dot, the GEMV epilogue, then the gelu epilogue
+// with the layer's per-layer row: the codes the gate plan would store), and contracts those
+// kPleRows codes with the matching 16 columns of the 8-bit projection: the projection's exact
+// int32 accumulator over that K range, added atomically into acc[n] (zeroed by the split kernel
+// before). The weight loads of both go out before the join, so their memory latency overlaps it.
+constexpr int kPleRows = 16;
+__global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
+    extern __shared__ __align__(16) uint8_t dyn[];
+    constexpr int kGateLanes = kDecThreads / kPleRows;  // 16 lanes per gate row
+    const int t = threadIdx.x;
+    const int r0 = blockIdx.x * kPleRows;
+    const int H = F.join.width;
+    uint8_t *xs = dyn;                                           // H codes, natural order
+    float *red = reinterpret_cast<float *>(dyn + ((H + 15) & ~15));  // 512 floats
+    __shared__ __align__(16) int8_t act[kPleRows];
+    // gate row r0 + t / 16: this lane's 16-byte chunks c = t % 16, c + 16, ... of the row
+    constexpr int kGateChunks = kJoinMaxPer * kDecThreads / 16 / kGateLanes;  // chunks per lane, max
+    const int gchunks = H / 16;                                                  // chunks per row
+    const int grow = r0 + t / kGateLanes, glane = t % kGateLanes;
+    u32x4 gw[kGateChunks];
+#pragma unroll
+    for (int u = 0; u < kGateChunks; ++u)
+        gw[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
+            F.w_gate + (int64_t)grow * H + min(glane + u * kGateLanes, gchunks - 1) * 16));
+    const float gscale = F.s_gate[grow];
+    const float up = F.up_vec[grow];
+    // projection rows n = t + 256 i: the 16 bytes of columns r0 .. r0 + 15
+    u32x4 pw[kJoinMaxPer];
+#pragma unroll
+    for (int i = 0; i < kJoinMaxPer; ++i)
+        pw[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
+            F.w_proj + (int64_t)min(t + i * kDecThreads, H - 1) * F.p + r0));
+    JoinTail J = F.join;  // J.codes stays set: the join emits codes only when it has a destination
+    if (blockIdx.x != 0) J.hidden = nullptr;
+    auto emit = [&](int i, int8_t c) { xs[i] = (uint8_t)c; };  // the codes stay in this block's LDS
+    if (J.src_kind == G4_KIND_I32) rms_join_row_emit<1>(J, 0, red, emit);
+    else rms_join_row_emit<0>(J, 0, red, emit);
+    __syncthreads();
+    int acc = 0;
+#pragma unroll
+    for (int u = 0; u < kGateChunks; ++u) {
+        const int c = glane + u * kGateLanes;
+        if (c < gchunks) {
+            const u32x4 xa = *reinterpret_cast<const u32x4 *>(xs + c * 16);
+            acc = __builtin_amdgcn_sdot4((int)gw[u].x, (int)xa.x, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)gw[u].y, (int)xa.y, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)gw[u].z, (int)xa.z, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)gw[u].w, (int)xa.w, acc, false);
+        }
+    }
+    acc = row16_sum_i32(acc);
+    if (glane == 0) {
+        // the gate plan's epilogue: GEMV output code on out_scale, gelu, times the row, snap
+        const float y = linear_epilogue(F.in_scale, gscale, (float)acc);
+        const float g = __fmul_rn(srq_code_f(y, F.out_scale), F.out_scale);
+        act[t / kGateLanes] = (int8_t)srq_code_i(__fmul_rn(d_gelu(g), up), F.in_scale);
+    }
+    __syncthreads();
+    const u32x4 a = *reinterpret_cast<const u32x4 *>(act);
+#pragma unroll
+    for (int i = 0; i < kJoinMaxPer; ++i) {
+        const int n = t + i * kDecThreads;
+        if (n >= H) break;
+        int pa = __builtin_amdgcn_sdot4((int)pw[i].x, (int)a.x, 0, false);
+        pa = __builtin_amdgcn_sdot4((int)pw[i].y, (int)a.y, pa, false);
+        pa = __builtin_amdgcn_sdot4((int)pw[i].z, (int)a.z, pa, false);
+        pa = __builtin_amdgcn_sdot4((int)pw[i].w, (int)a.w, pa, false);
+        atomicAdd(F.acc + n, pa);
+    }
+}
+
+bool ple_fold_fits(const PleFold &F) {
+    const int H = F.join.width;
+    return F.join.codes && F.w_gate && F.s_gate && F.up_vec && F.w_proj && F.acc && H > 0 && H % (16 * (kDecThreads / kPleRows)) == 0 &&
+           H <= kJoinMaxPer * kDecThreads && F.p > 0 && F.p % kPleRows == 0 &&
+           (reinterpret_cast<uintptr_t>(F.w_gate) & 15) == 0 && (reinterpret_cast<uintptr_t>(F.w_proj) & 15) == 0 &&
+           F.in_scale != 0.0f && F.out_scale != 0.0f;
+}
+
+int ple_block(const PleFold &F, void *stream) {
+    if (!ple_fold_fits(F)) return set_error(G4_ERR_INVALID, "per-layer-input block: shape or operands do not fit");
+    const size_t lds = ((F.join.width + 15) & ~15) + 2 * kRowThreads * sizeof(float);
+    hipLaunchKernelGGL(ple_block_kernel, dim3(F.p / kPleRows), dim3(kDecThreads), lds, as_stream(stream), F);
+    G4_LAUNCHED("ple_block_kernel");
+    return G4_OK;
+}
+
 // ---- gelu * up with the consumer's snap ------------------------------------------------------------
 
 // rows x n: codes = srq(gelu(g * gs) * u, in_scale) with u = up codes * us, or (up_f32 given) the

@@ -88,6 +88,10 @@ struct g4_decode {
     // into this int32 accumulator [hidden] (cleared by the split kernel); the post-attention join
     // applies o_proj's epilogue to it (null when o_proj is a plan)
     int32_t *oacc = nullptr;
+    // batch 1: per_layer_input_gate and per_layer_projection in one launch (ple_block), the
+    // projection's accumulator in oacc + hidden (cleared with it); the tail join reads it
+    bool fold_ple = false;
+    bool fold_o = false;  // o_proj inside the attention merge (its accumulator at oacc)
     std::vector<float *> kv;  // per producer: [batch][2][capacity][head_dim]
     int stop = -1;
     // M = 1 GEMV plans per layer: qkv (or q), o, gate+up, down, ple gate, ple projection.
@@ -320,13 +324,31 @@ int carry_join(g4_decode &d, int k, const Plan &plan) {
     return G4_OK;
 }
 
-// Join k for the step's `batch` rows, unless a plan carries it.
-int run_join(g4_decode &d, int k, void *st) {
-    if (d.carried[k]) return G4_OK;
+// Join k for the step's `batch` rows as a launch of its own (int32 accumulator sources included).
+int launch_join(g4_decode &d, int k, void *st) {
     const JoinTail &j = d.joins[k];
     if (j.src_kind == G4_KIND_I32) return join_acc(j, d.s.batch, as_stream(st));
     return g4_rms_join(j.src, j.src_kind, j.src_scale, j.gain, j.resid, j.alpha, j.gain2, d.s.batch,
                        j.width, j.eps, j.in_scale, j.hidden, j.codes, st);
+}
+
+// Join k for the step's `batch` rows, unless a plan carries it.
+int run_join(g4_decode &d, int k, void *st) { return d.carried[k] ? G4_OK : launch_join(d, k, st); }
+
+// The per-layer-input block of layer l at batch 1 (ple_block), accumulating into acc.
+PleFold ple_fold(const g4_decode &d, int l, void *acc) {
+    const g4_decode_layer &L = d.layers[l];
+    PleFold F;
+    F.join = d.joins[join_index(l, 1)];
+    F.w_gate = static_cast<const int8_t *>(L.ple_gate);
+    F.s_gate = L.ple_gate_s;
+    F.up_vec = d.per_layer + (size_t)l * d.s.ple_dim;
+    F.w_proj = static_cast<const int8_t *>(L.ple_proj);
+    F.p = d.s.ple_dim;
+    F.in_scale = d.s.in_scale;
+    F.out_scale = d.s.out_scale;
+    F.acc = static_cast<int32_t *>(acc);
+    return F;
 }
 
 int build(g4_decode &d) {
@@ -378,7 +400,8 @@ int build(g4_decode &d) {
     // merge block contracts its 256 codes with that head's K range of o_proj and adds the exact
     // partial into one int32 accumulator; the post-attention join applies o_proj's epilogue and
     // snap to it, so it reads o_proj's own codes (one launch fewer per layer)
-    bool fold_o = true;
+    bool &fold_o = d.fold_o;
+    fold_o = true;
     for (int l = 0; l < s.layers; ++l) {
         MergeLinear lin;
         lin.w = d.layers[l].o;
@@ -387,8 +410,25 @@ int build(g4_decode &d) {
         lin.part = reinterpret_cast<int32_t *>(d.hbuf[0]);  // any non-null pointer: shape check only
         fold_o = fold_o && merge_linear_fits(lin, B, s.q_heads);
     }
+    // per_layer_input_gate and per_layer_projection in one launch when every layer fits it: the
+    // post-FFN join, the gate rows with their gelu x per-layer-row epilogue and the projection's
+    // K range of those rows, added atomically into one int32 accumulator that the tail join reads
+    d.fold_ple = true;
+    for (int l = 0; l < s.layers; ++l) d.fold_ple = d.fold_ple && ple_fold_fits(ple_fold(d, l, d.hbuf[0]));
+    if (fold_o || d.fold_ple) G4_TRY(m.get((void **)&d.oacc, (size_t)2 * H * sizeof(int32_t)));
+    if (d.fold_ple) {
+        for (int l = 0; l < s.layers; ++l) {
+            JoinTail &j = d.joins[join_index(l, 2)];
+            j.src = d.oacc + H;
+            j.src_kind = G4_KIND_I32;
+            j.acc_scales = d.layers[l].ple_proj_s;
+            j.acc_in_scale = in;
+            j.acc_splits = 1;
+            j.acc_split_stride = H;
+            d.carried[join_index(l, 1)] = 1;  // ple_block runs it
+        }
+    }
     if (fold_o) {
-        G4_TRY(m.get((void **)&d.oacc, (size_t)H * sizeof(int32_t)));
         for (int l = 0; l < s.layers; ++l) {
             JoinTail &j = d.joins[join_index(l, 0)];
             j.src = d.oacc;
@@ -410,7 +450,7 @@ int build(g4_decode &d) {
             g.push_back(desc(L.v, L.v_s, d.xcodes, d.vc, 4, H, s.head_dim, G4_KIND_I8, in, out));
         }
         G4_TRY(try_plan(g.data(), (int)g.size(), P[P_QKV]));
-        if (!d.oacc) {
+        if (!d.fold_o) {
             g4_gemv_desc o = desc(L.o, L.o_s, d.attn_codes, d.oc, 4, QW, H, G4_KIND_I8, in, out);
             G4_TRY(try_plan(&o, 1, P[P_O]));
         }
@@ -429,6 +469,7 @@ int build(g4_decode &d) {
         }
         g4_gemv_desc dn = desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out);
         G4_TRY(try_plan(&dn, 1, P[P_DOWN]));
+        if (d.fold_ple) continue;  // the per-layer-input block is one ple_block launch
         // per_layer_input_gate's epilogue multiplies gelu(gate) by the layer's per-layer-input row
         GeluEpilogue pge;
         pge.up_vec = d.per_layer + (size_t)l * s.ple_dim;
@@ -463,7 +504,7 @@ int build(g4_decode &d) {
         const Plan *P = &d.plans[(size_t)l * P_PER_LAYER];
         const bool last = l + 1 == s.layers;
         G4_TRY(carry_join(d, join_index(l, 0), P[P_GATEUP]));
-        G4_TRY(carry_join(d, join_index(l, 1), P[P_PLE_GATE]));
+        if (!d.fold_ple) G4_TRY(carry_join(d, join_index(l, 1), P[P_PLE_GATE]));
         G4_TRY(carry_join(d, join_index(l, 2),
                           last ? d.head_plan : d.plans[(size_t)(l + 1) * P_PER_LAYER + P_QKV]));
     }
@@ -508,7 +549,7 @@ int run_layer(g4_decode &d, int l, void *st) {
     pro.sin_tab = sin_tab;
     pro.eps = s.eps;
     pro.zero = d.oacc;
-    pro.zero_n = d.oacc ? H : 0;
+    pro.zero_n = d.oacc ? 2 * H : 0;
     MergeLinear lin;
     lin.w = L.o;
     lin.n = H;
@@ -516,8 +557,8 @@ int run_layer(g4_decode &d, int l, void *st) {
     lin.part = d.oacc;
     G4_TRY(attention_decode_fused(pro, kb, vb, row_stride, B, s.q_heads, s.kv_capacity - 1, d.pos,
                                   glob ? 0 : s.sliding_window, d.attn_ws, d.attn_ws_bytes, in,
-                                  d.attn_codes, st, d.oacc ? &lin : nullptr));
-    if (!d.oacc)
+                                  d.attn_codes, st, d.fold_o ? &lin : nullptr));
+    if (!d.fold_o)
         G4_TRY(run_linear_rows(d, plan(P_O), desc(L.o, L.o_s, d.attn_codes, d.oc, 4, QW, H, G4_KIND_I8, in, out), st));
     G4_TRY(run_join(d, join_index(l, 0), st));
     // MLP block: gate, up and the gelu-mul pass (one paired launch when folded), then down
@@ -547,7 +588,9 @@ int run_layer(g4_decode &d, int l, void *st) {
     G4_TRY(run_join(d, join_index(l, 1), st));
     // per-layer-input block: the gate (with gelu times the layer's row folded when planned), then
     // per_layer_projection
-    if (plan(P_PLE_GATE).gelu) {
+    if (d.fold_ple) {
+        G4_TRY(ple_block(ple_fold(d, l, d.oacc + H), st));
+    } else if (plan(P_PLE_GATE).gelu) {
         G4_TRY(g4_qgemv_plan_launch(plan(P_PLE_GATE).p, st));
     } else {
         bool fused = false;
@@ -561,16 +604,13 @@ int run_layer(g4_decode &d, int l, void *st) {
                                (int64_t)s.layers * s.ple_dim, B, s.ple_dim, in, d.pac, st));
         }
     }
-    G4_TRY(run_linear_rows(d, plan(P_PLE_PROJ), desc(L.ple_proj, L.ple_proj_s, d.pac, d.ppc, 8, s.ple_dim, H, G4_KIND_I8, in, out), st));
+    if (!d.fold_ple)
+        G4_TRY(run_linear_rows(d, plan(P_PLE_PROJ), desc(L.ple_proj, L.ple_proj_s, d.pac, d.ppc, 8, s.ple_dim, H, G4_KIND_I8, in, out), st));
     // the tail join: residual, layer scalar, then the next input norm (or the final norm)
     // the tail join: residual, layer scalar, then the next input norm (or the final norm); a step
     // that stops here launches it even when the next layer's plan would carry it
     const int k = join_index(l, 2);
-    if (!d.carried[k] || (l == d.stop && l + 1 < s.layers)) {
-        const JoinTail &j = d.joins[k];
-        G4_TRY(g4_rms_join(j.src, j.src_kind, j.src_scale, j.gain, j.resid, j.alpha, j.gain2, B,
-                           j.width, j.eps, j.in_scale, j.hidden, j.codes, st));
-    }
+    if (!d.carried[k] || (l == d.stop && l + 1 < s.layers)) G4_TRY(launch_join(d, k, st));
     return G4_OK;
 }
 

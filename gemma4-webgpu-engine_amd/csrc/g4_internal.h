@@ -162,6 +162,23 @@ struct MergeLinear {
     int32_t *part = nullptr;
 };
 
+// The decode runner's per-layer-input block at one row (decode.hip ple_block_kernel): the join
+// (codes for the gate), the 8-bit gate [p][H] with its gelu x per-layer-row epilogue, and the 8-bit
+// projection [H][p] contracted into acc (H int32, zero on entry: its exact accumulator).
+struct PleFold {
+    JoinTail join;
+    const int8_t *w_gate = nullptr;
+    const float *s_gate = nullptr;
+    const float *up_vec = nullptr;  // the layer's per-layer row (p f32)
+    const int8_t *w_proj = nullptr;
+    int p = 0;                      // the gate's rows, the projection's K
+    float in_scale = 0.0f;          // every input snap (the gate's x, the projection's codes)
+    float out_scale = 0.0f;         // the gate's output snap
+    int32_t *acc = nullptr;
+};
+bool ple_fold_fits(const PleFold &F);
+int ple_block(const PleFold &F, void *stream);
+
 // Whether the merge can fold `lin` in (rows 1, n a multiple of the merge's row block, k = heads * 256).
 bool merge_linear_fits(const MergeLinear &lin, int rows, int heads);
 
