@@ -607,16 +607,16 @@ __global__ __launch_bounds__(kDecThreads) void attn_merge_o_kernel(
 // kPleRows codes with the matching 16 columns of the 8-bit projection: the projection's exact
 // int32 accumulator over that K range, added atomically into acc[n] (zeroed by the split kernel
 // before). The weight loads of both go out before the join, so their memory latency overlaps it.
-constexpr int kPleRows = 16;
+constexpr int kPleRows = 8;
 __global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
     extern __shared__ __align__(16) uint8_t dyn[];
-    constexpr int kGateLanes = kDecThreads / kPleRows;  // 16 lanes per gate row
+    constexpr int kGateLanes = kDecThreads / kPleRows;  // lanes per gate row (16 or 32)
     const int t = threadIdx.x;
     const int r0 = blockIdx.x * kPleRows;
     const int H = F.join.width;
     uint8_t *xs = dyn;                                           // H codes, natural order
     float *red = reinterpret_cast<float *>(dyn + ((H + 15) & ~15));  // 512 floats
-    __shared__ __align__(16) int8_t act[kPleRows];
+    __shared__ __align__(16) int8_t act[16];
     // gate row r0 + t / 16: this lane's 16-byte chunks c = t % 16, c + 16, ... of the row
     constexpr int kGateChunks = kJoinMaxPer * kDecThreads / 16 / kGateLanes;  // chunks per lane, max
     const int gchunks = H / 16;                                                  // chunks per row
@@ -628,11 +628,13 @@ __global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
             F.w_gate + (int64_t)grow * H + min(glane + u * kGateLanes, gchunks - 1) * 16));
     const float gscale = F.s_gate[grow];
     const float up = F.up_vec[grow];
-    // projection rows n = t + 256 i: the 16 bytes of columns r0 .. r0 + 15
-    u32x4 pw[kJoinMaxPer];
+    // projection rows n = t + 256 i: the kPleRows bytes of columns r0 .. r0 + kPleRows - 1
+    typedef unsigned int PW __attribute__((ext_vector_type(2)));
+    static_assert(kPleRows == 8, "the projection operand is one 8-byte word per row");
+    PW pw[kJoinMaxPer];
 #pragma unroll
     for (int i = 0; i < kJoinMaxPer; ++i)
-        pw[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
+        pw[i] = __builtin_nontemporal_load(reinterpret_cast<const PW *>(
             F.w_proj + (int64_t)min(t + i * kDecThreads, H - 1) * F.p + r0));
     JoinTail J = F.join;  // J.codes stays set: the join emits codes only when it has a destination
     if (blockIdx.x != 0) J.hidden = nullptr;
@@ -653,6 +655,7 @@ __global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
         }
     }
     acc = row16_sum_i32(acc);
+    if (kGateLanes == 32) acc += __shfl_xor(acc, 16);
     if (glane == 0) {
         // the gate plan's epilogue: GEMV output code on out_scale, gelu, times the row, snap
         const float y = linear_epilogue(F.in_scale, gscale, (float)acc);
@@ -660,15 +663,13 @@ __global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
         act[t / kGateLanes] = (int8_t)srq_code_i(__fmul_rn(d_gelu(g), up), F.in_scale);
     }
     __syncthreads();
-    const u32x4 a = *reinterpret_cast<const u32x4 *>(act);
+    const PW a = *reinterpret_cast<const PW *>(act);
 #pragma unroll
     for (int i = 0; i < kJoinMaxPer; ++i) {
         const int n = t + i * kDecThreads;
         if (n >= H) break;
         int pa = __builtin_amdgcn_sdot4((int)pw[i].x, (int)a.x, 0, false);
         pa = __builtin_amdgcn_sdot4((int)pw[i].y, (int)a.y, pa, false);
-        pa = __builtin_amdgcn_sdot4((int)pw[i].z, (int)a.z, pa, false);
-        pa = __builtin_amdgcn_sdot4((int)pw[i].w, (int)a.w, pa, false);
         atomicAdd(F.acc + n, pa);
     }
 }
