@@ -73,6 +73,7 @@ static_assert(sizeof(StreamJob) == 112, "StreamJob is one 112-byte record");
 struct StreamArgs {
     const StreamJob *table;  // device table (plan launches); null for kernel-argument jobs
     const int *block_job;    // plan launches: the job of each block's first tile
+    const int *block_tile;   // plan launches: block b takes tiles [block_tile[b], block_tile[b + 1])
     int njobs;
     int total_tiles;
     const JoinTail *pre;     // plan launches: the RMS join whose codes the `pre` jobs read; or null
@@ -490,8 +491,8 @@ __device__ __forceinline__ void stream_body(const StreamArgs &A, uint8_t *xs, in
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const unsigned G = gridDim.x, b = blockIdx.x;
-    const int t0 = (int)(((uint64_t)b * (unsigned)A.total_tiles) / G);
-    const int t1 = (int)(((uint64_t)(b + 1) * (unsigned)A.total_tiles) / G);
+    const int t0 = TABLE ? A.block_tile[b] : (int)(((uint64_t)b * (unsigned)A.total_tiles) / G);
+    const int t1 = TABLE ? A.block_tile[b + 1] : (int)(((uint64_t)(b + 1) * (unsigned)A.total_tiles) / G);
     if (t0 >= t1) return;
     int j;
     if (TABLE) {
@@ -640,9 +641,26 @@ static int plan_from_jobs(std::vector<StreamJob> &jobs, g4_gemv_plan **out) {
     int max_k = 0;
     const int tiles = layout_tiles(jobs.data(), count, max_k);
     const int grid = grid_for(tiles);
-    std::vector<int> block_job(grid);
+    // Blocks take equal shares of the weight bytes, not of the tiles: a tile of o_proj (K 2048)
+    // holds 16 KB where the others hold 12 KB, and with every block resident at once the launch
+    // lasts as long as its heaviest block. block_job[0, grid): the job of each block's first
+    // tile; block_job[grid, 2 grid]: the tile ranges.
+    std::vector<uint64_t> cum(tiles + 1, 0);
+    for (int j = 0; j < count; ++j) {
+        const uint64_t tb = (uint64_t)rows_per_tile(jobs[j].cls) * (jobs[j].bits == 4 ? jobs[j].k / 2 : jobs[j].k) *
+                            (jobs[j].epi == 1 ? 2 : 1);
+        for (int t = jobs[j].tile_begin; t < jobs[j].tile_begin + jobs[j].tiles; ++t) cum[t + 1] = cum[t] + tb;
+    }
+    std::vector<int> block_job(2 * (size_t)grid + 1);
+    int *block_tile = block_job.data() + grid;
+    for (int b = 0, t = 0; b < grid; ++b) {
+        const uint64_t target = cum[tiles] * (uint64_t)b / (uint64_t)grid;
+        while (t < tiles && cum[t] < target) ++t;
+        block_tile[b] = t;
+    }
+    block_tile[grid] = tiles;
     for (int b = 0, j = 0; b < grid; ++b) {
-        const int tb = (int)(((uint64_t)b * (unsigned)tiles) / (unsigned)grid);
+        const int tb = std::min(block_tile[b], tiles - 1);
         while (j + 1 < count && jobs[j + 1].tile_begin <= tb) ++j;
         block_job[b] = j;
     }
@@ -654,11 +672,11 @@ static int plan_from_jobs(std::vector<StreamJob> &jobs, g4_gemv_plan **out) {
     for (const StreamJob &J : jobs) p->paired |= J.epi == 1;
     hipError_t err = hipGetDevice(&p->device);
     if (err == hipSuccess) err = hipMalloc(&p->table, sizeof(StreamJob) * count);
-    if (err == hipSuccess) err = hipMalloc(&p->block_job, sizeof(int) * grid);
+    if (err == hipSuccess) err = hipMalloc(&p->block_job, sizeof(int) * block_job.size());
     if (err == hipSuccess)
         err = hipMemcpy(p->table, jobs.data(), sizeof(StreamJob) * count, hipMemcpyHostToDevice);
     if (err == hipSuccess)
-        err = hipMemcpy(p->block_job, block_job.data(), sizeof(int) * grid, hipMemcpyHostToDevice);
+        err = hipMemcpy(p->block_job, block_job.data(), sizeof(int) * block_job.size(), hipMemcpyHostToDevice);
     if (err != hipSuccess) {
         (void)hipFree(p->table);
         (void)hipFree(p->block_job);
@@ -779,6 +797,7 @@ int g4_qgemv_plan_launch(const g4_gemv_plan *p, void *stream) {
     StreamArgs A{};
     A.table = p->table;
     A.block_job = p->block_job;
+    A.block_tile = p->block_job + p->grid;
     A.njobs = p->njobs;
     A.total_tiles = p->total_tiles;
     A.pre = p->pre;
