@@ -131,7 +131,7 @@ def bench_gemm(h, m=512, reps=50):
             "note": "f16_in includes the activation snap; int8_in takes codes already snapped"}
 
 
-def bench_gemm_sweep(h, ms=(4, 8, 16, 128, 512, 2048), reps=30):
+def bench_gemm_sweep(h, stream_obj, ms=(4, 8, 16, 128, 512, 2048), reps=30):
     """Config 2: the gate projection (K=1536, N=6144, int4) at every BASELINE M, int8 codes in
     (the activation snap is timed separately in bench_gemm). Bytes are weights + scales + x + out."""
     n, k = syn.FFN, syn.HIDDEN
@@ -143,12 +143,20 @@ def bench_gemm_sweep(h, ms=(4, 8, 16, 128, 512, 2048), reps=30):
         codes = g4.DeviceBuffer.empty((m, k), np.int8)
         g4.srq_quantize(x, codes, m * k, syn.IN_SCALE, stream=h)
         d = g4.DeviceBuffer.empty((m, n), np.int8)
-        ms_ = timed(h, lambda: g4.qgemm(4, w, s, codes, d, k, n, m, syn.IN_SCALE, syn.OUT_SCALE,
-                                        stream=h), reps, 5)
+        call = lambda: g4.qgemm(4, w, s, codes, d, k, n, m, syn.IN_SCALE, syn.OUT_SCALE, stream=h)
+        ms_ = timed(h, call, reps, 5)
+        # the same calls captured as one graph of `per` launches and replayed (no host launch cost
+        # per call: what a serving loop that captures its step sees)
+        per = 20
+        graph = g4.Graph(stream_obj, lambda: [call() for _ in range(per)])
+        ms_g = timed(h, graph.launch, max(2, reps // per), 2) / per
+        graph.close()
         by = n * k // 2 + 4 * n + m * k + m * n
         rows.append({"m": m, "kernel": g4.kernel_for_shape(4, m, n, k), "us": round(ms_ * 1e3, 3),
                      "tops": round(2.0 * m * n * k / (ms_ * 1e-3) / 1e12, 2),
-                     "gbs": round(by / (ms_ * 1e-3) / 1e9, 2)})
+                     "gbs": round(by / (ms_ * 1e-3) / 1e9, 2),
+                     "us_graph": round(ms_g * 1e3, 3),
+                     "gbs_graph": round(by / (ms_g * 1e-3) / 1e9, 2)})
     return rows
 
 
@@ -389,13 +397,14 @@ def bench_decode(h, batch, steps=20, warmup=3, probe=False, cpu=False):
 
 
 def gemm_probe(h):
-    """Launches for rocprofv3 --kernel-trace --stats: the config-2 gate GEMM 50 times at M=512
-    and 20 times at M=2048, first with f16 activations (activation snap + tile kernel), then with
-    int8 codes already snapped (the tile kernel alone)."""
+    """Launches for rocprofv3 --kernel-trace --stats: the config-2 gate GEMM 50 times at M=4, 8,
+    16 and 512 and 20 times at M=2048, first with f16 activations (above M=32: the activation snap
+    + the tile kernel; up to 32 the small kernel snaps itself), then with int8 codes already
+    snapped (one kernel)."""
     n, k = syn.FFN, syn.HIDDEN
     w = g4.DeviceBuffer.from_array(syn.int4_weights("c2", "gate", n, k))
     s = g4.DeviceBuffer.from_array(syn.row_scales("c2", "gate", n))
-    for m, reps in ((512, 50), (2048, 20)):
+    for m, reps in ((4, 50), (8, 50), (16, 50), (512, 50), (2048, 20)):
         x = g4.DeviceBuffer.from_array(syn.activations("c2", f"x{m}", m, k, outlier_frac=0.01))
         codes = g4.DeviceBuffer.empty((m, k), np.int8)
         g4.srq_quantize(x, codes, m * k, syn.IN_SCALE, stream=h)
@@ -505,7 +514,7 @@ def main():
         log("config 3 split PLE gather")
         ga = bench_gather(h)
         log("config 2 sweep over M, config 1 int8 down")
-        sweep = bench_gemm_sweep(h)
+        sweep = bench_gemm_sweep(h, stream)
         down8 = bench_int8_down(h)
         log("measured HBM copy rate")
         hbm = hbm_copy_rate(h)
