@@ -552,7 +552,7 @@ __device__ __forceinline__ int chunk_dot4(const u32x4 &w, const uint8_t *x) {
     return acc;
 }
 
-constexpr int kMergeRows = 192;
+constexpr int kMergeRows = 64;
 __global__ __launch_bounds__(kDecThreads) void attn_merge_o_kernel(
     const float *part_ml, const float *part_o, int heads, int pos_host, const int32_t *pos_dev,
     int window, int max_chunks, float in_scale, int8_t *codes, const uint8_t *w, int n_out,
@@ -607,17 +607,29 @@ __global__ __launch_bounds__(kDecThreads) void attn_merge_o_kernel(
 // kPleRows codes with the matching 16 columns of the 8-bit projection: the projection's exact
 // int32 accumulator over that K range, added atomically into acc[n] (zeroed by the split kernel
 // before). The weight loads of both go out before the join, so their memory latency overlaps it.
-constexpr int kPleRows = 8;
+constexpr int kPleRows = 4;
+// The projection's kPleRows int8 weights of a row (and the block's kPleRows codes) as one word.
+template <int ROWS> struct PleWord;
+template <> struct PleWord<4> { typedef uint32_t type; };
+template <> struct PleWord<8> { typedef unsigned int type __attribute__((ext_vector_type(2))); };
+__device__ __forceinline__ int ple_dot(uint32_t w, uint32_t a) { return __builtin_amdgcn_sdot4((int)w, (int)a, 0, false); }
+__device__ __forceinline__ int ple_dot(PleWord<8>::type w, PleWord<8>::type a) {
+    return __builtin_amdgcn_sdot4((int)w.y, (int)a.y, __builtin_amdgcn_sdot4((int)w.x, (int)a.x, 0, false), false);
+}
+
+template <int ROWS>
 __global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
     extern __shared__ __align__(16) uint8_t dyn[];
-    constexpr int kGateLanes = kDecThreads / kPleRows;  // lanes per gate row (16 or 32)
+    constexpr int kGateLanes = kDecThreads / ROWS;  // lanes per gate row (32 or 64)
+    static_assert(kGateLanes == 32 || kGateLanes == 64, "a gate row is half a wave or a wave");
+    typedef typename PleWord<ROWS>::type PW;
     const int t = threadIdx.x;
-    const int r0 = blockIdx.x * kPleRows;
+    const int r0 = blockIdx.x * ROWS;
     const int H = F.join.width;
-    uint8_t *xs = dyn;                                           // H codes, natural order
+    uint8_t *xs = dyn;                                               // H codes, natural order
     float *red = reinterpret_cast<float *>(dyn + ((H + 15) & ~15));  // 512 floats
     __shared__ __align__(16) int8_t act[16];
-    // gate row r0 + t / 16: this lane's 16-byte chunks c = t % 16, c + 16, ... of the row
+    // gate row r0 + t / kGateLanes: this lane's 16-byte chunks c = t % kGateLanes, c + kGateLanes, ...
     constexpr int kGateChunks = kJoinMaxPer * kDecThreads / 16 / kGateLanes;  // chunks per lane, max
     const int gchunks = H / 16;                                                  // chunks per row
     const int grow = r0 + t / kGateLanes, glane = t % kGateLanes;
@@ -628,9 +640,7 @@ __global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
             F.w_gate + (int64_t)grow * H + min(glane + u * kGateLanes, gchunks - 1) * 16));
     const float gscale = F.s_gate[grow];
     const float up = F.up_vec[grow];
-    // projection rows n = t + 256 i: the kPleRows bytes of columns r0 .. r0 + kPleRows - 1
-    typedef unsigned int PW __attribute__((ext_vector_type(2)));
-    static_assert(kPleRows == 8, "the projection operand is one 8-byte word per row");
+    // projection rows n = t + 256 i: the ROWS bytes of columns r0 .. r0 + ROWS - 1
     PW pw[kJoinMaxPer];
 #pragma unroll
     for (int i = 0; i < kJoinMaxPer; ++i)
@@ -655,7 +665,8 @@ __global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
         }
     }
     acc = row16_sum_i32(acc);
-    if (kGateLanes == 32) acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 16);
+    if (kGateLanes == 64) acc += __shfl_xor(acc, 32);
     if (glane == 0) {
         // the gate plan's epilogue: GEMV output code on out_scale, gelu, times the row, snap
         const float y = linear_epilogue(F.in_scale, gscale, (float)acc);
@@ -668,15 +679,13 @@ __global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
     for (int i = 0; i < kJoinMaxPer; ++i) {
         const int n = t + i * kDecThreads;
         if (n >= H) break;
-        int pa = __builtin_amdgcn_sdot4((int)pw[i].x, (int)a.x, 0, false);
-        pa = __builtin_amdgcn_sdot4((int)pw[i].y, (int)a.y, pa, false);
-        atomicAdd(F.acc + n, pa);
+        atomicAdd(F.acc + n, ple_dot(pw[i], a));
     }
 }
 
 bool ple_fold_fits(const PleFold &F) {
     const int H = F.join.width;
-    return F.join.codes && F.w_gate && F.s_gate && F.up_vec && F.w_proj && F.acc && H > 0 && H % (16 * (kDecThreads / kPleRows)) == 0 &&
+    return F.join.codes && F.w_gate && F.s_gate && F.up_vec && F.w_proj && F.acc && H > 0 && H % 16 == 0 &&
            H <= kJoinMaxPer * kDecThreads && F.p > 0 && F.p % kPleRows == 0 &&
            (reinterpret_cast<uintptr_t>(F.w_gate) & 15) == 0 && (reinterpret_cast<uintptr_t>(F.w_proj) & 15) == 0 &&
            F.in_scale != 0.0f && F.out_scale != 0.0f;
@@ -685,7 +694,7 @@ bool ple_fold_fits(const PleFold &F) {
 int ple_block(const PleFold &F, void *stream) {
     if (!ple_fold_fits(F)) return set_error(G4_ERR_INVALID, "per-layer-input block: shape or operands do not fit");
     const size_t lds = ((F.join.width + 15) & ~15) + 2 * kRowThreads * sizeof(float);
-    hipLaunchKernelGGL(ple_block_kernel, dim3(F.p / kPleRows), dim3(kDecThreads), lds, as_stream(stream), F);
+    hipLaunchKernelGGL(ple_block_kernel<kPleRows>, dim3(F.p / kPleRows), dim3(kDecThreads), lds, as_stream(stream), F);
     G4_LAUNCHED("ple_block_kernel");
     return G4_OK;
 }
