@@ -699,6 +699,158 @@ int ple_block(const PleFold &F, void *stream) {
     return G4_OK;
 }
 
+// ---- the FFN block at one decode row: join, gate and up, gelu-mul, down's K range ---------------
+
+// gate_proj, up_proj, the gelu-mul pass and down_proj in one launch (the decode runner at batch 1):
+// block b runs the post-attention join that produces the gate / up input codes (every block, the
+// join kernel's arithmetic; block 0 also stores the join's residual row), the gate and up rows
+// b * R .. + R (4-bit, exact int32 dots, each linear's epilogue and output snap, then the gelu-mul
+// pass: the codes down_proj would read), and contracts those R codes with the matching R columns
+// of every down_proj row: down's exact int32 accumulator over that K range, added atomically into
+// acc[n] (zeroed by the split kernel before). The weight loads go out right behind the join's
+// operand loads, so the join waits for its own operands only and the weights stream in under its
+// arithmetic. H = 512 * CPL: a gate / up row is 16 lanes x CPL 16-byte chunks (2R rows, 16 per
+// pass), and each thread takes 2 * CPL down rows (R / 2 bytes each, consecutive threads consecutive
+// rows of the block's repacked run).
+
+template <int R, int CPL>
+__global__ __launch_bounds__(kDecThreads) void ffn_block_kernel(FfnFold F) {
+    extern __shared__ __align__(16) uint8_t dyn[];
+    constexpr int kPasses = 2 * R / 16;   // gate rows, then up rows, 16 a pass
+    constexpr int kDownRows = 2 * CPL;    // down rows per thread: H / 256
+    constexpr int kDownChunks = R / 32;   // 16-byte chunks of a down row in this K range
+    static_assert(R % 32 == 0 && R <= 64, "a block's K range of down is whole 16-byte chunks, one wave's lanes");
+    const int t = threadIdx.x, lr = t & 15;
+    const int H = F.join.width;
+    const int r0 = blockIdx.x * R;
+    uint8_t *xs = dyn;                                               // H codes, snap layout
+    float *red = reinterpret_cast<float *>(dyn + ((H + 15) & ~15));  // 512 floats
+    __shared__ int accs[2 * R];
+    __shared__ __align__(16) uint8_t act[R];
+    __shared__ int sums[2];
+    const int64_t row_bytes = H / 2;
+    u32x4 gw[kPasses][CPL];
+    u32x4 dw[kDownRows][kDownChunks];
+    float sg, su;
+    // the weights and scales, requested behind the join's own operands
+    auto load_weights = [&]() {
+#pragma unroll
+        for (int p = 0; p < kPasses; ++p) {
+            const bool gate = p < R / 16;
+            const int row = r0 + (gate ? p : p - R / 16) * 16 + (t >> 4);
+            const uint8_t *w = (gate ? F.w_gate : F.w_up) + (int64_t)row * row_bytes + lr * 16;
+#pragma unroll
+            for (int u = 0; u < CPL; ++u)
+                gw[p][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w + u * 256));
+        }
+        const uint8_t *wd = F.w_down + (int64_t)blockIdx.x * H * (R / 2);
+#pragma unroll
+        for (int i = 0; i < kDownRows; ++i)
+#pragma unroll
+            for (int c = 0; c < kDownChunks; ++c)
+                dw[i][c] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4 *>(wd + (int64_t)(t + i * kDecThreads) * (R / 2) + c * 16));
+        sg = F.s_gate[r0 + (t & (R - 1))];
+        su = F.s_up[r0 + (t & (R - 1))];
+        __builtin_amdgcn_sched_barrier(0);  // all of them before the join's arithmetic
+    };
+    if (t == 0) sums[0] = 0;
+    JoinTail J = F.join;  // J.codes stays set: the join emits codes only when it has a destination
+    if (blockIdx.x != 0) J.hidden = nullptr;
+    int local = 0;
+    auto emit = [&](int i, int8_t c) {  // the codes stay in this block's LDS, in the snap layout
+        const int j = i & 7;
+        xs[(i & ~7) + (j & 1 ? 4 : 0) + (j >> 1)] = (uint8_t)c;
+        local += c;
+    };
+    if (J.src_kind == G4_KIND_I32) rms_join_row_emit<1>(J, 0, red, emit, load_weights);
+    else rms_join_row_emit<0>(J, 0, red, emit, load_weights);
+    local = row16_sum_i32(local);
+    if (lr == 0 && local != 0) atomicAdd(&sums[0], local);
+    __syncthreads();
+    const int sx = sums[0];
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        int acc = 0;
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) acc += chunk_dot4(gw[p][u], xs + (lr + 16 * u) * 32);
+        acc = row16_sum_i32(acc);
+        if (lr == 0) accs[p * 16 + (t >> 4)] = acc - 8 * sx;
+    }
+    __syncthreads();
+    if (t < 64) {
+        // the paired tile's gelu epilogue: gate and up each through their linear's epilogue and
+        // output snap, then srq(gelu(gate) * up) on act_scale
+        int a = 0;
+        if (t < R) {
+            const float yg = linear_epilogue(F.in_scale, sg, (float)accs[t]);
+            const float yu = linear_epilogue(F.in_scale, su, (float)accs[R + t]);
+            const float g = __fmul_rn(srq_code_f(yg, F.out_scale), F.out_scale);
+            const float u = __fmul_rn(srq_code_f(yu, F.out_scale), F.out_scale);
+            a = srq_code_i(__fmul_rn(d_gelu(g), u), F.act_scale);
+            const int j = t & 7;
+            act[(t & ~7) + (j & 1 ? 4 : 0) + (j >> 1)] = (uint8_t)a;
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) a += __shfl_xor(a, off);
+        if (t == 0) sums[1] = a;
+    }
+    __syncthreads();
+    const int sa = sums[1];
+#pragma unroll
+    for (int i = 0; i < kDownRows; ++i) {
+        int acc = 0;
+#pragma unroll
+        for (int c = 0; c < kDownChunks; ++c) acc += chunk_dot4(dw[i][c], act + c * 32);
+        atomicAdd(F.acc + t + i * kDecThreads, acc - 8 * sa);
+    }
+}
+
+bool ffn_fold_fits(const FfnFold &F) {
+    const int H = F.join.width;
+    auto a16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    return F.join.codes && F.w_gate && F.w_up && F.s_gate && F.s_up && F.w_down && F.acc && H > 0 &&
+           H % 512 == 0 && H <= kJoinMaxPer * kDecThreads && F.f > 0 && F.f % kFfnRows == 0 &&
+           F.f % 32 == 0 && a16(F.w_gate) && a16(F.w_up) && a16(F.w_down) && F.in_scale != 0.0f &&
+           F.out_scale != 0.0f && F.act_scale != 0.0f;
+}
+
+// One 16-byte piece per thread: piece i of the output is (K range kr, row n, piece c of the run).
+__global__ __launch_bounds__(256) void ffn_repack_kernel(const uint8_t *w, uint8_t *out, int h, int f) {
+    constexpr int kPieces = kFfnRows / 32;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)(f / kFfnRows) * h * kPieces) return;
+    const int c = (int)(i % kPieces);
+    const int64_t n = (i / kPieces) % h, kr = i / ((int64_t)kPieces * h);
+    *reinterpret_cast<u32x4 *>(out + i * 16) =
+        *reinterpret_cast<const u32x4 *>(w + n * (f / 2) + kr * (kFfnRows / 2) + c * 16);
+}
+
+int ffn_repack_down(const uint8_t *w, uint8_t *out, int h, int f, hipStream_t stream) {
+    if (!w || !out || h <= 0 || f <= 0 || f % kFfnRows != 0 || (reinterpret_cast<uintptr_t>(w) & 15) ||
+        (reinterpret_cast<uintptr_t>(out) & 15))
+        return set_error(G4_ERR_INVALID, "FFN block: down_proj repack operands do not fit");
+    const int64_t pieces = (int64_t)(f / kFfnRows) * h * (kFfnRows / 32);
+    hipLaunchKernelGGL(ffn_repack_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, stream, w, out, h, f);
+    G4_LAUNCHED("ffn_repack_kernel");
+    return G4_OK;
+}
+
+int ffn_block(const FfnFold &F, void *stream) {
+    if (!ffn_fold_fits(F)) return set_error(G4_ERR_INVALID, "FFN block: shape or operands do not fit");
+    const size_t lds = ((F.join.width + 15) & ~15) + 2 * kRowThreads * sizeof(float);
+    const dim3 grid(F.f / kFfnRows), block(kDecThreads);
+    hipStream_t s = as_stream(stream);
+    switch (F.join.width / 512) {
+    case 1: hipLaunchKernelGGL((ffn_block_kernel<kFfnRows, 1>), grid, block, lds, s, F); break;
+    case 2: hipLaunchKernelGGL((ffn_block_kernel<kFfnRows, 2>), grid, block, lds, s, F); break;
+    case 3: hipLaunchKernelGGL((ffn_block_kernel<kFfnRows, 3>), grid, block, lds, s, F); break;
+    default: hipLaunchKernelGGL((ffn_block_kernel<kFfnRows, 4>), grid, block, lds, s, F); break;
+    }
+    G4_LAUNCHED("ffn_block_kernel");
+    return G4_OK;
+}
+
 // ---- gelu * up with the consumer's snap ------------------------------------------------------------
 
 // rows x n: codes = srq(gelu(g * gs) * u, in_scale) with u = up codes * us, or (up_f32 given) the

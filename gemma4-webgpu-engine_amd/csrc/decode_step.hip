@@ -92,6 +92,10 @@ struct g4_decode {
     // projection's accumulator in oacc + hidden (cleared with it); the tail join reads it
     bool fold_ple = false;
     bool fold_o = false;  // o_proj inside the attention merge (its accumulator at oacc)
+    // batch 1: gate, up, the gelu-mul pass and down_proj in one launch (ffn_block), down's
+    // accumulator in oacc + 2 * hidden (cleared with it); the post-FFN join reads it
+    bool fold_ffn = false;
+    std::vector<uint8_t *> down_packed;  // per layer: down_proj in the FFN block's layout
     std::vector<float *> kv;  // per producer: [batch][2][capacity][head_dim]
     int stop = -1;
     // M = 1 GEMV plans per layer: qkv (or q), o, gate+up, down, ple gate, ple projection.
@@ -351,6 +355,24 @@ PleFold ple_fold(const g4_decode &d, int l, void *acc) {
     return F;
 }
 
+// The FFN block of layer l at batch 1 (ffn_block), accumulating down_proj into acc.
+FfnFold ffn_fold(const g4_decode &d, int l, int32_t *acc) {
+    const g4_decode_layer &L = d.layers[l];
+    FfnFold F;
+    F.join = d.joins[join_index(l, 0)];
+    F.w_gate = static_cast<const uint8_t *>(L.gate);
+    F.w_up = static_cast<const uint8_t *>(L.up);
+    F.s_gate = L.gate_s;
+    F.s_up = L.up_s;
+    F.w_down = d.down_packed.empty() ? static_cast<const uint8_t *>(L.down) : d.down_packed[l];
+    F.f = d.s.ffn;
+    F.in_scale = d.s.in_scale;
+    F.out_scale = d.s.out_scale;
+    F.act_scale = d.s.in_scale;
+    F.acc = acc;
+    return F;
+}
+
 int build(g4_decode &d) {
     const g4_decode_shape &s = d.s;
     const int B = s.batch, H = s.hidden, F = s.ffn, QW = s.q_heads * s.head_dim;
@@ -415,7 +437,35 @@ int build(g4_decode &d) {
     // K range of those rows, added atomically into one int32 accumulator that the tail join reads
     d.fold_ple = true;
     for (int l = 0; l < s.layers; ++l) d.fold_ple = d.fold_ple && ple_fold_fits(ple_fold(d, l, d.hbuf[0]));
-    if (fold_o || d.fold_ple) G4_TRY(m.get((void **)&d.oacc, (size_t)2 * H * sizeof(int32_t)));
+    // gate / up / gelu-mul / down in one launch when every layer fits it: each block's gate and up
+    // rows, their gelu-mul codes, and down's K range of those codes added atomically into one
+    // int32 accumulator that the post-FFN join reads
+    d.fold_ffn = true;
+    for (int l = 0; l < s.layers; ++l)
+        d.fold_ffn = d.fold_ffn && ffn_fold_fits(ffn_fold(d, l, reinterpret_cast<int32_t *>(d.hbuf[0])));
+    if (fold_o || d.fold_ple || d.fold_ffn)
+        G4_TRY(m.get((void **)&d.oacc, (size_t)3 * H * sizeof(int32_t)));
+    if (d.fold_ffn) {
+        // each layer's down_proj in the block's layout (a copy taken here: the runner reads it in
+        // place of the caller's down weights from now on), after every upload the caller queued
+        G4_HIP(hipDeviceSynchronize());
+        d.down_packed.assign(s.layers, nullptr);
+        for (int l = 0; l < s.layers; ++l) {
+            G4_TRY(m.get((void **)&d.down_packed[l], (size_t)H * F / 2));
+            G4_TRY(ffn_repack_down(static_cast<const uint8_t *>(d.layers[l].down), d.down_packed[l], H, F, nullptr));
+        }
+        G4_HIP(hipDeviceSynchronize());
+        for (int l = 0; l < s.layers; ++l) {
+            JoinTail &j = d.joins[join_index(l, 1)];
+            j.src = d.oacc + 2 * H;
+            j.src_kind = G4_KIND_I32;
+            j.acc_scales = d.layers[l].down_s;
+            j.acc_in_scale = in;
+            j.acc_splits = 1;
+            j.acc_split_stride = H;
+            d.carried[join_index(l, 0)] = 1;  // ffn_block runs it
+        }
+    }
     if (d.fold_ple) {
         for (int l = 0; l < s.layers; ++l) {
             JoinTail &j = d.joins[join_index(l, 2)];
@@ -454,21 +504,23 @@ int build(g4_decode &d) {
             g4_gemv_desc o = desc(L.o, L.o_s, d.attn_codes, d.oc, 4, QW, H, G4_KIND_I8, in, out);
             G4_TRY(try_plan(&o, 1, P[P_O]));
         }
-        // gate and up rows stream through one paired tile whose epilogue is the gelu-mul pass:
-        // act = srq(gelu(gate code * out) * (up code * out), in), the codes down_proj reads
-        GeluEpilogue gue;
-        gue.w_up = L.up;
-        gue.s_up = L.up_s;
-        gue.act_scale = in;
-        G4_TRY(try_gelu_plan(desc(L.gate, L.gate_s, d.xcodes, d.act, 4, H, F, G4_KIND_I8, in, out),
-                             gue, P[P_GATEUP]));
-        if (!P[P_GATEUP].p) {
-            g4_gemv_desc gu[2] = {desc(L.gate, L.gate_s, d.xcodes, d.gc, 4, H, F, G4_KIND_I8, in, out),
-                                  desc(L.up, L.up_s, d.xcodes, d.uc, 4, H, F, G4_KIND_I8, in, out)};
-            G4_TRY(try_plan(gu, 2, P[P_GATEUP]));
+        if (!d.fold_ffn) {
+            // gate and up rows stream through one paired tile whose epilogue is the gelu-mul pass:
+            // act = srq(gelu(gate code * out) * (up code * out), in), the codes down_proj reads
+            GeluEpilogue gue;
+            gue.w_up = L.up;
+            gue.s_up = L.up_s;
+            gue.act_scale = in;
+            G4_TRY(try_gelu_plan(desc(L.gate, L.gate_s, d.xcodes, d.act, 4, H, F, G4_KIND_I8, in, out),
+                                 gue, P[P_GATEUP]));
+            if (!P[P_GATEUP].p) {
+                g4_gemv_desc gu[2] = {desc(L.gate, L.gate_s, d.xcodes, d.gc, 4, H, F, G4_KIND_I8, in, out),
+                                      desc(L.up, L.up_s, d.xcodes, d.uc, 4, H, F, G4_KIND_I8, in, out)};
+                G4_TRY(try_plan(gu, 2, P[P_GATEUP]));
+            }
+            g4_gemv_desc dn = desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out);
+            G4_TRY(try_plan(&dn, 1, P[P_DOWN]));
         }
-        g4_gemv_desc dn = desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out);
-        G4_TRY(try_plan(&dn, 1, P[P_DOWN]));
         if (d.fold_ple) continue;  // the per-layer-input block is one ple_block launch
         // per_layer_input_gate's epilogue multiplies gelu(gate) by the layer's per-layer-input row
         GeluEpilogue pge;
@@ -549,7 +601,7 @@ int run_layer(g4_decode &d, int l, void *st) {
     pro.sin_tab = sin_tab;
     pro.eps = s.eps;
     pro.zero = d.oacc;
-    pro.zero_n = d.oacc ? 2 * H : 0;
+    pro.zero_n = d.oacc ? 3 * H : 0;
     MergeLinear lin;
     lin.w = L.o;
     lin.n = H;
@@ -561,8 +613,11 @@ int run_layer(g4_decode &d, int l, void *st) {
     if (!d.fold_o)
         G4_TRY(run_linear_rows(d, plan(P_O), desc(L.o, L.o_s, d.attn_codes, d.oc, 4, QW, H, G4_KIND_I8, in, out), st));
     G4_TRY(run_join(d, join_index(l, 0), st));
-    // MLP block: gate, up and the gelu-mul pass (one paired launch when folded), then down
-    if (plan(P_GATEUP).gelu) {
+    // MLP block: gate, up and the gelu-mul pass (one paired launch when folded), then down; at
+    // batch 1 all of it is one ffn_block launch
+    if (d.fold_ffn) {
+        G4_TRY(ffn_block(ffn_fold(d, l, d.oacc + 2 * H), st));
+    } else if (plan(P_GATEUP).gelu) {
         G4_TRY(g4_qgemv_plan_launch(plan(P_GATEUP).p, st));
     } else {
         // batch > 1: the small-M kernel with paired gate/up rows and the gelu-mul epilogue
@@ -583,7 +638,7 @@ int run_layer(g4_decode &d, int l, void *st) {
     if (d.acc)
         G4_TRY(linear_split_acc(4, static_cast<const uint8_t *>(L.down), L.down_s, d.act, F, H, B,
                                 kAccSplits, d.acc, as_stream(st)));
-    else
+    else if (!d.fold_ffn)
         G4_TRY(run_linear_rows(d, plan(P_DOWN), desc(L.down, L.down_s, d.act, d.dc, 4, F, H, G4_KIND_I8, in, out), st));
     G4_TRY(run_join(d, join_index(l, 1), st));
     // per-layer-input block: the gate (with gelu times the layer's row folded when planned), then

@@ -179,6 +179,31 @@ struct PleFold {
 bool ple_fold_fits(const PleFold &F);
 int ple_block(const PleFold &F, void *stream);
 
+// The decode runner's FFN block at one row (decode.hip ffn_block_kernel): the join (codes for gate
+// and up), the 4-bit gate and up [f][H] with the gelu-mul epilogue, and the 4-bit down contracted
+// into acc (H int32, zero on entry: its exact accumulator). Block b takes gate / up rows
+// b * kFfnRows .. + kFfnRows, so it reads down's K range of that width in every row; w_down holds
+// down [H][f] repacked by ffn_repack_down so that this range is one contiguous run per block:
+// [f / kFfnRows][H][kFfnRows / 2] bytes.
+constexpr int kFfnRows = 32;
+struct FfnFold {
+    JoinTail join;
+    const uint8_t *w_gate = nullptr;
+    const uint8_t *w_up = nullptr;
+    const float *s_gate = nullptr;
+    const float *s_up = nullptr;
+    const uint8_t *w_down = nullptr;  // repacked
+    int f = 0;                // gate / up rows, down's K
+    float in_scale = 0.0f;    // gate / up input snap
+    float out_scale = 0.0f;   // gate / up output snap
+    float act_scale = 0.0f;   // the gelu-mul codes' snap (down's input)
+    int32_t *acc = nullptr;
+};
+bool ffn_fold_fits(const FfnFold &F);
+int ffn_block(const FfnFold &F, void *stream);
+// down [h][f] (4-bit, row-major) -> out [f / kFfnRows][h][kFfnRows / 2]; f % kFfnRows == 0.
+int ffn_repack_down(const uint8_t *w, uint8_t *out, int h, int f, hipStream_t stream);
+
 // Whether the merge can fold `lin` in (rows 1, n a multiple of the merge's row block, k = heads * 256).
 bool merge_linear_fits(const MergeLinear &lin, int rows, int heads);
 

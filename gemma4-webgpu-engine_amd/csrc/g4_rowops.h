@@ -75,10 +75,17 @@ __device__ __forceinline__ float acc_value(const JoinTail &J, int acc, float sca
     return __fmul_rn((float)snap_code(y, J.src_scale), J.src_scale);
 }
 
+struct NoLoads {
+    __device__ void operator()() const {}
+};
+
 // ACC > 0: the source is at most ACC split int32 accumulators (src_kind G4_KIND_I32).
-template <int ACC = 0, typename Emit>
+// after_loads() runs once every operand load of the join is issued and before any is used: a
+// caller's own loads issued there queue behind the join's, so the join waits for its operands only
+// (a wave's loads complete in issue order) while the caller's stay in flight under its arithmetic.
+template <int ACC = 0, typename Emit, typename Loads = NoLoads>
 __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row, float *lds,
-                                                  Emit emit) {
+                                                  Emit emit, Loads after_loads = Loads()) {
     const int t = threadIdx.x;
     const int width = J.width;
     const int64_t base = row * width;
@@ -113,6 +120,7 @@ __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row
         re[e] = J.resid ? J.resid[base + ic[e]] : 0.0f;
         g2[e] = J.gain2 ? J.gain2[ic[e]] : 0.0f;
     }
+    after_loads();
 #pragma unroll
     for (int e = 0; e < kJoinMaxPer; ++e) {
         const bool in = t + e * kRowThreads < width;
