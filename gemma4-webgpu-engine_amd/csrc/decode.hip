@@ -606,7 +606,8 @@ __global__ __launch_bounds__(kDecThreads) void attn_merge_o_kernel(
 // with the layer's per-layer row: the codes the gate plan would store), and contracts those
 // kPleRows codes with the matching 16 columns of the 8-bit projection: the projection's exact
 // int32 accumulator over that K range, added atomically into acc[n] (zeroed by the split kernel
-// before). The weight loads of both go out before the join, so their memory latency overlaps it.
+// before). The weight loads of both go out right behind the join's operand loads, so their memory
+// latency overlaps the join's arithmetic.
 constexpr int kPleRows = 4;
 // The projection's kPleRows int8 weights of a row (and the block's kPleRows codes) as one word.
 template <int ROWS> struct PleWord;
@@ -634,23 +635,28 @@ __global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
     const int gchunks = H / 16;                                                  // chunks per row
     const int grow = r0 + t / kGateLanes, glane = t % kGateLanes;
     u32x4 gw[kGateChunks];
-#pragma unroll
-    for (int u = 0; u < kGateChunks; ++u)
-        gw[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
-            F.w_gate + (int64_t)grow * H + min(glane + u * kGateLanes, gchunks - 1) * 16));
-    const float gscale = F.s_gate[grow];
-    const float up = F.up_vec[grow];
+    float gscale, up;
     // projection rows n = t + 256 i: the ROWS bytes of columns r0 .. r0 + ROWS - 1
     PW pw[kJoinMaxPer];
+    // the weights, requested behind the join's own operands
+    auto load_weights = [&]() {
 #pragma unroll
-    for (int i = 0; i < kJoinMaxPer; ++i)
-        pw[i] = __builtin_nontemporal_load(reinterpret_cast<const PW *>(
-            F.w_proj + (int64_t)min(t + i * kDecThreads, H - 1) * F.p + r0));
+        for (int u = 0; u < kGateChunks; ++u)
+            gw[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
+                F.w_gate + (int64_t)grow * H + min(glane + u * kGateLanes, gchunks - 1) * 16));
+        gscale = F.s_gate[grow];
+        up = F.up_vec[grow];
+#pragma unroll
+        for (int i = 0; i < kJoinMaxPer; ++i)
+            pw[i] = __builtin_nontemporal_load(reinterpret_cast<const PW *>(
+                F.w_proj + (int64_t)min(t + i * kDecThreads, H - 1) * F.p + r0));
+        __builtin_amdgcn_sched_barrier(0);
+    };
     JoinTail J = F.join;  // J.codes stays set: the join emits codes only when it has a destination
     if (blockIdx.x != 0) J.hidden = nullptr;
     auto emit = [&](int i, int8_t c) { xs[i] = (uint8_t)c; };  // the codes stay in this block's LDS
-    if (J.src_kind == G4_KIND_I32) rms_join_row_emit<1>(J, 0, red, emit);
-    else rms_join_row_emit<0>(J, 0, red, emit);
+    if (J.src_kind == G4_KIND_I32) rms_join_row_emit<1>(J, 0, red, emit, load_weights);
+    else rms_join_row_emit<0>(J, 0, red, emit, load_weights);
     __syncthreads();
     int acc = 0;
 #pragma unroll

@@ -259,7 +259,9 @@ __device__ __forceinline__ int block_code_sum(int local, int *s_sum, int tid) {
 // (the same arithmetic as the join kernel, so the same codes) and stores its codes in the snap
 // layout; block 0 also stores the join's outputs (the new residual row and the codes) for the
 // kernels after this one. Replaces a join launch between the producer GEMV and this one.
-__device__ __forceinline__ int snap_join(const JoinTail *pre, int four, uint8_t *xs) {
+template <typename Loads = NoLoads>
+__device__ __forceinline__ int snap_join(const JoinTail *pre, int four, uint8_t *xs,
+                                         Loads after_loads = Loads()) {
     JoinTail T = *pre;
     // the reduction tree sits in the dynamic LDS after the codes (the launch sizes it so); a
     // static array would shift every code address of the tile loop by its size
@@ -275,8 +277,8 @@ __device__ __forceinline__ int snap_join(const JoinTail *pre, int four, uint8_t 
     };
     // an int32 accumulator source (the decode runner's o_proj folded into the attention merge)
     // runs the producing linear's epilogue and snap first
-    if (T.src_kind == G4_KIND_I32) rms_join_row_emit<1>(T, 0, red, emit);
-    else rms_join_row_emit<0>(T, 0, red, emit);
+    if (T.src_kind == G4_KIND_I32) rms_join_row_emit<1>(T, 0, red, emit, after_loads);
+    else rms_join_row_emit<0>(T, 0, red, emit, after_loads);
     return local;
 }
 
@@ -296,10 +298,12 @@ __device__ __forceinline__ int snap_activations(const StreamJob &J, uint8_t *xs,
     return block_code_sum(local, s_sum, tid);
 }
 
-// The codes of a prologue join in the snap layout, and their sum.
+// The codes of a prologue join in the snap layout, and their sum. after_loads: as for
+// rms_join_row_emit (the caller's tile loads, queued behind the join's operands).
+template <typename Loads = NoLoads>
 __device__ __forceinline__ int snap_join_codes(const JoinTail *pre, bool four, uint8_t *xs,
-                                               int *s_sum, int tid) {
-    return block_code_sum(snap_join(pre, four, xs), s_sum, tid);
+                                               int *s_sum, int tid, Loads after_loads = Loads()) {
+    return block_code_sum(snap_join(pre, four, xs, after_loads), s_sum, tid);
 }
 
 // One output element of job J at row `row` (the reference's epilogue, qgemv.ts:680-686).
@@ -362,9 +366,10 @@ __device__ __forceinline__ void stream_store_gelu(const StreamJob &J, int row, f
 // (row index clamped, so every load is valid) and the row scale, the dot against the LDS codes,
 // the fixed reduction over the row's LPR lanes (exact int32), and the row's output from one lane.
 // PAIR: the same rows of the paired up projection stream beside the gate's, for the gelu epilogue.
-// PRE (a block's first tile): the tile's weight loads go out first, then the block fills the LDS
-// codes (sx is their sum): 1, the plan's prologue join; 2, the job's own snap. The codes' memory
-// latency then overlaps the weight stream's. Returns sx.
+// PRE (a block's first tile): the block fills the LDS codes inside the tile (sx is their sum): 1,
+// the plan's prologue join, whose operand loads go out first and the tile's weight loads right
+// behind them (the join waits for its own operands only); 2, the job's own snap, after the weight
+// loads. Either way the codes' memory latency overlaps the weight stream's. Returns sx.
 template <int BITS, int LPR, int CPL, bool PAIR, int PRE = 0>
 __device__ __forceinline__ int stream_tile(const StreamJob &J, int t, uint8_t *xs, int sx, int wave,
                                            int lane, const JoinTail *pre = nullptr,
@@ -376,18 +381,29 @@ __device__ __forceinline__ int stream_tile(const StreamJob &J, int t, uint8_t *x
     const int rc = min(row, J.rows - 1);
     const uint8_t *base = J.w + (int64_t)rc * ROW_BYTES + lr * 16;
     u32x4 w[CPL];
-#pragma unroll
-    for (int u = 0; u < CPL; ++u) w[u] = load_w16(base + u * LPR * 16);
     u32x4 w2[PAIR ? CPL : 1];
-    if (PAIR) {
-        const uint8_t *base2 = reinterpret_cast<const uint8_t *>(J.aux) + (int64_t)rc * ROW_BYTES + lr * 16;
+    float scale, scale2 = 0.0f;
+    auto load_tile = [&]() {
 #pragma unroll
-        for (int u = 0; u < CPL; ++u) w2[u] = load_w16(base2 + u * LPR * 16);
+        for (int u = 0; u < CPL; ++u) w[u] = load_w16(base + u * LPR * 16);
+        if (PAIR) {
+            const uint8_t *base2 = reinterpret_cast<const uint8_t *>(J.aux) + (int64_t)rc * ROW_BYTES + lr * 16;
+#pragma unroll
+            for (int u = 0; u < CPL; ++u) w2[u] = load_w16(base2 + u * LPR * 16);
+        }
+        scale = gload<float>(J.scales + rc);
+        if (PAIR) scale2 = gload<float>(J.aux_scales + rc);
+    };
+    if (PRE == 1) {
+        // the join's operands go out first, the tile's weights right behind them
+        sx = snap_join_codes(pre, BITS == 4, xs, s_sum, threadIdx.x, [&]() {
+            load_tile();
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    } else {
+        load_tile();
+        if (PRE == 2) sx = snap_activations(J, xs, s_sum, threadIdx.x);
     }
-    const float scale = gload<float>(J.scales + rc);
-    const float scale2 = PAIR ? gload<float>(J.aux_scales + rc) : 0.0f;
-    if (PRE == 1) sx = snap_join_codes(pre, BITS == 4, xs, s_sum, threadIdx.x);
-    if (PRE == 2) sx = snap_activations(J, xs, s_sum, threadIdx.x);
     int acc = 0, acc2 = 0;
 #pragma unroll
     for (int u = 0; u < CPL; ++u) acc = chunk_dot<BITS>(w[u], xs, lr + u * LPR, acc);
