@@ -95,6 +95,7 @@ __device__ __forceinline__ void gather_chunk(uint32_t w, float s0, float s1, voi
 // thread needed a second round (11.9 -> 9.7 us). A small one (a decode step's few tokens) takes 4,
 // which halves each thread's serial work.
 constexpr int kSmallGatherSlots = 256;
+constexpr int kRowScales = 128;  // scale groups of a row staged in LDS (the E2B table: 70)
 
 template <int RPT>
 __device__ __forceinline__ void gather_row(const uint8_t *row_codes, const void *scales,
@@ -105,6 +106,16 @@ __device__ __forceinline__ void gather_row(const uint8_t *row_codes, const void 
     const int T = blockDim.x;
     // a run of 8 codes lies in one group when the group size is a multiple of 8: one scale load
     const bool one_scale = (group_size & 7) == 0;
+    // the row's folded scales, loaded once per block into LDS when they fit (one global load per
+    // thread at most, in place of one per run; staging the codes the same way measured slower)
+    __shared__ float srow[kRowScales];
+    const bool staged = one_scale && row_codes && groups_per_row <= kRowScales && groups_per_row <= T &&
+                        (int64_t)group_size * groups_per_row >= cols;
+    if (staged) {  // uniform
+        if ((int)threadIdx.x < groups_per_row)
+            srow[threadIdx.x] = __fmul_rn(16.0f, scale_at(scales, scale_kind, row * groups_per_row + threadIdx.x));
+        __syncthreads();
+    }
     for (int base = threadIdx.x; base < runs; base += RPT * T) {
         // All of this thread's code words and scales are requested before any is converted.
         uint32_t w[RPT];
@@ -115,7 +126,9 @@ __device__ __forceinline__ void gather_row(const uint8_t *row_codes, const void 
             const bool live = row_codes && ch < runs;
             w[u] = live ? *reinterpret_cast<const uint32_t *>(row_codes + (int64_t)ch * 4)
                         : 0x88888888u;
-            s0[u] = live ? vec4_scale(scales, scale_kind, row, ch * 8, group_size, groups_per_row) : 0.0f;
+            s0[u] = !live ? 0.0f
+                    : staged ? srow[ch * 8 / group_size]
+                             : vec4_scale(scales, scale_kind, row, ch * 8, group_size, groups_per_row);
             s1[u] = !live ? 0.0f
                     : one_scale ? s0[u]
                                 : vec4_scale(scales, scale_kind, row, ch * 8 + 4, group_size, groups_per_row);
