@@ -428,6 +428,8 @@ def main():
                     help="only the config-2 GEMM launches (M=512 and M=2048, f16 then int8 in), for rocprofv3")
     ap.add_argument("--decode-probe", type=int, default=0, metavar="BATCH",
                     help="only config-4 decode steps at this batch (graph replays), for rocprofv3")
+    ap.add_argument("--gather-probe", action="store_true",
+                    help="only the config-3 gather launches (2048 tokens, 5 slices), for rocprofv3")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this path is measured on one GPU; --gpus {args.gpus} is not supported "
@@ -444,6 +446,10 @@ def main():
         return
     if args.decode_probe:
         bench_decode(h, args.decode_probe, steps=10, probe=True)
+        return
+    if args.gather_probe:
+        r = bench_gather(h, reps=50)
+        log(f"gather probe: 53 launches, {r['ms'] * 1e3:.2f} us each event-timed")
         return
     log("building 35 layers of config-1 weights (623.6 MB)")
     layers = build_layers()
