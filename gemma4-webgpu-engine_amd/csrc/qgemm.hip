@@ -273,6 +273,20 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
     const uint8_t *wrow2 = EPI == 1 ? jobs.w_up + (int64_t)n * row_bytes : wrow;
     bool r_ok;
     const float rcp = srq_recip(in_scale, r_ok);
+    // the epilogue's per-output operands (row scales; the paired up rows' scales; the f32 up
+    // vector), requested now so the epilogue does not wait a memory round trip for them
+    constexpr int EQ = (TM * 256 + THREADS - 1) / THREADS;  // outputs per thread
+    float e_scale[EQ], e_scale2[EQ], e_aux[EQ];
+#pragma unroll
+    for (int e = 0; e < EQ; ++e) {
+        const int q = min(tid + e * THREADS, TM * 256 - 1);
+        const int t = q >> 8, ln = (q >> 2) & 63, r = q & 3;
+        const int nn = min(n0 + (ln & 15), N - 1);
+        const int m = min(m0 + t * 16 + 4 * (ln >> 4) + r, M - 1);
+        e_scale[e] = scales[nn];
+        e_scale2[e] = EPI == 1 ? jobs.s_up[nn] : 0.0f;
+        e_aux[e] = EPI == 2 ? jobs.aux[(int64_t)m * jobs.aux_stride + nn] : 0.0f;
+    }
     v4i acc[NACC];
 #pragma unroll
     for (int t = 0; t < NACC; ++t) acc[t] = v4i{0, 0, 0, 0};
@@ -442,7 +456,10 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
     __syncthreads();
     bool o_ok;
     const float orcp = srq_recip(out_scale, o_ok);
-    for (int q = tid; q < TM * 256; q += THREADS) {
+#pragma unroll
+    for (int e = 0; e < EQ; ++e) {
+        const int q = tid + e * THREADS;
+        if (q >= TM * 256) break;
         // D layout: lane l, register r -> row 4 (l / 16) + r of A, column l % 16 of B.
         const int t = q >> 8, ln = (q >> 2) & 63, r = q & 3;
         const int lr = t * 16 + 4 * (ln >> 4) + r;
@@ -459,16 +476,16 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
             v -= 8 * rsum;
             v2 -= 8 * rsum;
         }
-        const float yv = __fmul_rn(__fmul_rn(in_scale, scales[nn]), (float)v);
+        const float yv = __fmul_rn(__fmul_rn(in_scale, e_scale[e]), (float)v);
         const int64_t o = (int64_t)m * N + nn;
         if (EPI != 0) {  // gelu(gate) * up, snapped for the consumer
             const float gq = __fmul_rn(srq_code_fast(yv, out_scale, orcp, o_ok), out_scale);
             float uq;
             if (EPI == 1) {
-                const float yu = __fmul_rn(__fmul_rn(in_scale, jobs.s_up[nn]), (float)v2);
+                const float yu = __fmul_rn(__fmul_rn(in_scale, e_scale2[e]), (float)v2);
                 uq = __fmul_rn(srq_code_fast(yu, out_scale, orcp, o_ok), out_scale);
             } else {
-                uq = jobs.aux[(int64_t)m * jobs.aux_stride + nn];
+                uq = e_aux[e];
             }
             reinterpret_cast<int8_t *>(dst)[o] =
                 (int8_t)srq_code_i(__fmul_rn(d_gelu(gq), uq), jobs.act_scale);
