@@ -599,6 +599,8 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(
     if (tn >= tiles_n) return;  // whole block, before any barrier
     const int m0 = tm * BM, n0 = tn * BN;
     const int tid = threadIdx.x, lane = tid & 63;
+    // the epilogue's column scale, requested now so the epilogue does not wait a memory round trip
+    const float col_scale = tid < BN ? scales[min(n0 + tid, N - 1)] : 0.0f;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 15, g = lane >> 4;
     const int wm = wave >> 1, wn = wave & 1;
@@ -753,7 +755,7 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(
     tile_wait<0>();  // every wave is done with the ring
     int32_t *sacc = reinterpret_cast<int32_t *>(smem);
     float *sscale = reinterpret_cast<float *>(smem + BM * ESTR * 4);
-    if (tid < BN) sscale[tid] = __fmul_rn(in_scale, scales[min(n0 + tid, N - 1)]);
+    if (tid < BN) sscale[tid] = __fmul_rn(in_scale, col_scale);
 #pragma unroll
     for (int t = 0; t < TM; ++t)
 #pragma unroll
