@@ -655,7 +655,8 @@ __global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
     JoinTail J = F.join;  // J.codes stays set: the join emits codes only when it has a destination
     if (blockIdx.x != 0) J.hidden = nullptr;
     auto emit = [&](int i, int8_t c) { xs[i] = (uint8_t)c; };  // the codes stay in this block's LDS
-    if (J.src_kind == G4_KIND_I32) rms_join_row_emit<1>(J, 0, red, emit, load_weights);
+    // an int32 source: down's accumulator, possibly in several copies (the FFN block's)
+    if (J.src_kind == G4_KIND_I32) rms_join_row_emit<kSplitAccMax>(J, 0, red, emit, load_weights);
     else rms_join_row_emit<0>(J, 0, red, emit, load_weights);
     __syncthreads();
     int acc = 0;
@@ -803,19 +804,21 @@ __global__ __launch_bounds__(kDecThreads) void ffn_block_kernel(FfnFold F) {
     }
     __syncthreads();
     const int sa = sums[1];
+    int32_t *dacc = F.acc + (int64_t)(blockIdx.x % F.acc_copies) * H;
 #pragma unroll
     for (int i = 0; i < kDownRows; ++i) {
         int acc = 0;
 #pragma unroll
         for (int c = 0; c < kDownChunks; ++c) acc += chunk_dot4(dw[i][c], act + c * 32);
-        atomicAdd(F.acc + t + i * kDecThreads, acc - 8 * sa);
+        atomicAdd(dacc + t + i * kDecThreads, acc - 8 * sa);
     }
 }
 
 bool ffn_fold_fits(const FfnFold &F) {
     const int H = F.join.width;
     auto a16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-    return F.join.codes && F.w_gate && F.w_up && F.s_gate && F.s_up && F.w_down && F.acc && H > 0 &&
+    return F.join.codes && F.w_gate && F.w_up && F.s_gate && F.s_up && F.w_down && F.acc &&
+           F.acc_copies >= 1 && F.acc_copies <= kSplitAccMax && H > 0 &&
            H % 512 == 0 && H <= kJoinMaxPer * kDecThreads && F.f > 0 && F.f % kFfnRows == 0 &&
            F.f % 32 == 0 && a16(F.w_gate) && a16(F.w_up) && a16(F.w_down) && F.in_scale != 0.0f &&
            F.out_scale != 0.0f && F.act_scale != 0.0f;

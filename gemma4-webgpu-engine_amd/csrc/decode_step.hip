@@ -281,6 +281,10 @@ JoinTail make_join(g4_decode &d, int k, const void *src, int src_kind, float src
 // split, 192 blocks take one chunk each and the join adds the two exact int32 partials (step
 // 4.25 -> 4.08 ms). o_proj (K = 2048, one chunk) split the same way measured no faster at batch
 // 32 and slower at batch 3.
+// The batch-1 folds' int32 accumulators, [kAccRows][hidden]: o_proj, per_layer_projection, then
+// down_proj's kFfnAccCopies copies.
+constexpr int kAccRows = 2 + kFfnAccCopies;
+
 constexpr int kAccSplits = 2;
 static_assert(kAccSplits <= kSplitAccMax, "the join sums at most kSplitAccMax partials");
 
@@ -370,6 +374,8 @@ FfnFold ffn_fold(const g4_decode &d, int l, int32_t *acc) {
     F.out_scale = d.s.out_scale;
     F.act_scale = d.s.in_scale;
     F.acc = acc;
+    // the per-layer-input block's join sums accumulator copies; a plan prologue reads one
+    F.acc_copies = d.fold_ple ? kFfnAccCopies : 1;
     return F;
 }
 
@@ -444,7 +450,7 @@ int build(g4_decode &d) {
     for (int l = 0; l < s.layers; ++l)
         d.fold_ffn = d.fold_ffn && ffn_fold_fits(ffn_fold(d, l, reinterpret_cast<int32_t *>(d.hbuf[0])));
     if (fold_o || d.fold_ple || d.fold_ffn)
-        G4_TRY(m.get((void **)&d.oacc, (size_t)3 * H * sizeof(int32_t)));
+        G4_TRY(m.get((void **)&d.oacc, (size_t)kAccRows * H * sizeof(int32_t)));
     if (d.fold_ffn) {
         // each layer's down_proj in the block's layout (a copy taken here: the runner reads it in
         // place of the caller's down weights from now on), after every upload the caller queued
@@ -461,7 +467,7 @@ int build(g4_decode &d) {
             j.src_kind = G4_KIND_I32;
             j.acc_scales = d.layers[l].down_s;
             j.acc_in_scale = in;
-            j.acc_splits = 1;
+            j.acc_splits = ffn_fold(d, l, d.oacc + 2 * H).acc_copies;
             j.acc_split_stride = H;
             d.carried[join_index(l, 0)] = 1;  // ffn_block runs it
         }
@@ -601,7 +607,7 @@ int run_layer(g4_decode &d, int l, void *st) {
     pro.sin_tab = sin_tab;
     pro.eps = s.eps;
     pro.zero = d.oacc;
-    pro.zero_n = d.oacc ? 3 * H : 0;
+    pro.zero_n = d.oacc ? kAccRows * H : 0;
     MergeLinear lin;
     lin.w = L.o;
     lin.n = H;

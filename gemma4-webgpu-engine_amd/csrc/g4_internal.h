@@ -197,8 +197,14 @@ struct FfnFold {
     float in_scale = 0.0f;    // gate / up input snap
     float out_scale = 0.0f;   // gate / up output snap
     float act_scale = 0.0f;   // the gelu-mul codes' snap (down's input)
+    // acc_copies accumulators [H] at acc + c * H (block b adds into copy b % acc_copies): the
+    // atomics of one address serialize, so spreading the blocks over copies takes their cost off
+    // the kernel's tail; the reader sums the copies (a JoinTail with acc_splits = acc_copies)
     int32_t *acc = nullptr;
+    int acc_copies = 1;
 };
+constexpr int kFfnAccCopies = 4;
+static_assert(kFfnAccCopies <= kSplitAccMax, "the join sums at most kSplitAccMax copies");
 bool ffn_fold_fits(const FfnFold &F);
 int ffn_block(const FfnFold &F, void *stream);
 // down [h][f] (4-bit, row-major) -> out [f / kFfnRows][h][kFfnRows / 2]; f % kFfnRows == 0.
