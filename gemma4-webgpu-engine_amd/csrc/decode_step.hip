@@ -18,10 +18,12 @@
 //   norm-residual-norm (post_per_layer_input_norm, residual, layer_scalar, then the next layer's
 //   input_layernorm, or the final norm on the last layer)
 // The residual stream alternates between two rows: a join reads one and writes the other. At
-// batch 1 every join is the prologue of the projection plan that reads its codes (the layer's
-// gate/up, per_layer_input_gate, the next layer's q/k/v, or the head), computed by each of that
-// plan's blocks in place of its activation snap, so it costs no launch of its own; block 0 writes
-// the new residual row, which the other blocks never read.
+// batch 1 every join but the final norm runs inside the launch that reads its codes (the FFN block,
+// the per-layer-input block, the next layer's q/k/v plan), computed by each of its blocks in place
+// of an activation snap, so it costs no launch of its own; block 0 writes the new residual row,
+// which the other blocks never read. o_proj, down_proj and per_layer_projection add exact int32
+// partials into accumulators inside the attention merge, the FFN block and the per-layer-input
+// block, and the join after each reads the accumulator through the linear's epilogue and snap.
 // Embedding phase (plan.ts:720-729): tied int4 embed gather (x sqrt(hidden) folded), PLE gather,
 // per_layer_model_projection (int4 GEMV, then hidden^-0.5), per_layer_projection_norm, + identity,
 // x 2^-0.5. Head (plan.ts:768-777): tied int4 GEMV to f32 logits, softcap, two-stage argmax.
@@ -563,8 +565,10 @@ int build(g4_decode &d) {
         const bool last = l + 1 == s.layers;
         G4_TRY(carry_join(d, join_index(l, 0), P[P_GATEUP]));
         if (!d.fold_ple) G4_TRY(carry_join(d, join_index(l, 1), P[P_PLE_GATE]));
-        G4_TRY(carry_join(d, join_index(l, 2),
-                          last ? d.head_plan : d.plans[(size_t)(l + 1) * P_PER_LAYER + P_QKV]));
+        // the final norm runs as a join launch of its own: carried, it would put the 201 MB head
+        // plan on the join instantiation of the stream kernel (half its occupancy), which costs
+        // more than the launch (1.422 against 1.415 ms per step)
+        if (!last) G4_TRY(carry_join(d, join_index(l, 2), d.plans[(size_t)(l + 1) * P_PER_LAYER + P_QKV]));
     }
     return G4_OK;
 }
