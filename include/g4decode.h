@@ -187,7 +187,10 @@ typedef struct g4_decode_weights {
 typedef struct g4_decode g4_decode;
 
 /* Validates the shape and weights, allocates the KV caches ([batch][2][kv_capacity][head_dim] f32
- * per producer, K then V) and every work buffer, and builds the per-layer GEMV plans. */
+ * per producer, K then V) and every work buffer, and builds the per-layer GEMV plans. At batch 1
+ * it also keeps a copy of every layer's down_proj in the FFN block's layout (hidden * ffn / 2
+ * bytes per layer), taken after the device has finished the work queued before the call: the
+ * weights are read at creation and must not change while the runner lives. */
 int g4_decode_create(const g4_decode_shape *shape, const g4_decode_weights *weights,
                      g4_decode **out);
 int g4_decode_destroy(g4_decode *d);
