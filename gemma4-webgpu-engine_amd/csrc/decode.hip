@@ -618,7 +618,8 @@ __device__ __forceinline__ int ple_dot(PleWord<8>::type w, PleWord<8>::type a) {
     return __builtin_amdgcn_sdot4((int)w.y, (int)a.y, __builtin_amdgcn_sdot4((int)w.x, (int)a.x, 0, false), false);
 }
 
-template <int ROWS>
+// PER: join elements per thread (hidden <= PER * 256).
+template <int ROWS, int PER>
 __global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
     extern __shared__ __align__(16) uint8_t dyn[];
     constexpr int kGateLanes = kDecThreads / ROWS;  // lanes per gate row (32 or 64)
@@ -637,7 +638,7 @@ __global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
     u32x4 gw[kGateChunks];
     float gscale, up;
     // projection rows n = t + 256 i: the ROWS bytes of columns r0 .. r0 + ROWS - 1
-    PW pw[kJoinMaxPer];
+    PW pw[PER];
     // the weights, requested behind the join's own operands
     auto load_weights = [&]() {
 #pragma unroll
@@ -647,7 +648,7 @@ __global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
         gscale = F.s_gate[grow];
         up = F.up_vec[grow];
 #pragma unroll
-        for (int i = 0; i < kJoinMaxPer; ++i)
+        for (int i = 0; i < PER; ++i)
             pw[i] = __builtin_nontemporal_load(reinterpret_cast<const PW *>(
                 F.w_proj + (int64_t)min(t + i * kDecThreads, H - 1) * F.p + r0));
         __builtin_amdgcn_sched_barrier(0);
@@ -656,8 +657,8 @@ __global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
     if (blockIdx.x != 0) J.hidden = nullptr;
     auto emit = [&](int i, int8_t c) { xs[i] = (uint8_t)c; };  // the codes stay in this block's LDS
     // an int32 source: down's accumulator, possibly in several copies (the FFN block's)
-    if (J.src_kind == G4_KIND_I32) rms_join_row_emit<kSplitAccMax>(J, 0, red, emit, load_weights);
-    else rms_join_row_emit<0>(J, 0, red, emit, load_weights);
+    if (J.src_kind == G4_KIND_I32) rms_join_row_emit<kSplitAccMax, PER>(J, 0, red, emit, load_weights);
+    else rms_join_row_emit<0, PER>(J, 0, red, emit, load_weights);
     __syncthreads();
     int acc = 0;
 #pragma unroll
@@ -683,7 +684,7 @@ __global__ __launch_bounds__(kDecThreads) void ple_block_kernel(PleFold F) {
     __syncthreads();
     const PW a = *reinterpret_cast<const PW *>(act);
 #pragma unroll
-    for (int i = 0; i < kJoinMaxPer; ++i) {
+    for (int i = 0; i < PER; ++i) {
         const int n = t + i * kDecThreads;
         if (n >= H) break;
         atomicAdd(F.acc + n, ple_dot(pw[i], a));
@@ -701,7 +702,12 @@ bool ple_fold_fits(const PleFold &F) {
 int ple_block(const PleFold &F, void *stream) {
     if (!ple_fold_fits(F)) return set_error(G4_ERR_INVALID, "per-layer-input block: shape or operands do not fit");
     const size_t lds = ((F.join.width + 15) & ~15) + 2 * kRowThreads * sizeof(float);
-    hipLaunchKernelGGL(ple_block_kernel<kPleRows>, dim3(F.p / kPleRows), dim3(kDecThreads), lds, as_stream(stream), F);
+    if (F.join.width <= 6 * kDecThreads)
+        hipLaunchKernelGGL((ple_block_kernel<kPleRows, 6>), dim3(F.p / kPleRows), dim3(kDecThreads), lds,
+                           as_stream(stream), F);
+    else
+        hipLaunchKernelGGL((ple_block_kernel<kPleRows, kJoinMaxPer>), dim3(F.p / kPleRows), dim3(kDecThreads),
+                           lds, as_stream(stream), F);
     G4_LAUNCHED("ple_block_kernel");
     return G4_OK;
 }
@@ -770,8 +776,8 @@ __global__ __launch_bounds__(kDecThreads) void ffn_block_kernel(FfnFold F) {
         xs[(i & ~7) + (j & 1 ? 4 : 0) + (j >> 1)] = (uint8_t)c;
         local += c;
     };
-    if (J.src_kind == G4_KIND_I32) rms_join_row_emit<1>(J, 0, red, emit, load_weights);
-    else rms_join_row_emit<0>(J, 0, red, emit, load_weights);
+    if (J.src_kind == G4_KIND_I32) rms_join_row_emit<1, 2 * CPL>(J, 0, red, emit, load_weights);
+    else rms_join_row_emit<0, 2 * CPL>(J, 0, red, emit, load_weights);
     local = row16_sum_i32(local);
     if (lr == 0 && local != 0) atomicAdd(&sums[0], local);
     __syncthreads();

@@ -83,9 +83,12 @@ struct NoLoads {
 // after_loads() runs once every operand load of the join is issued and before any is used: a
 // caller's own loads issued there queue behind the join's, so the join waits for its operands only
 // (a wave's loads complete in issue order) while the caller's stay in flight under its arithmetic.
-template <int ACC = 0, typename Emit, typename Loads = NoLoads>
+// PER: elements per thread the caller provides for (width <= PER * 256; a caller that knows the
+// width issues no loads past it).
+template <int ACC = 0, int PER = kJoinMaxPer, typename Emit, typename Loads = NoLoads>
 __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row, float *lds,
                                                   Emit emit, Loads after_loads = Loads()) {
+    static_assert(PER >= 1 && PER <= kJoinMaxPer, "an RMS join serves widths up to 8 * 256");
     const int t = threadIdx.x;
     const int width = J.width;
     const int64_t base = row * width;
@@ -93,36 +96,36 @@ __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row
     // load scheduling, so later loads would each cost a memory latency of their own), at indices
     // clamped into the row and with no branch between them, so no load waits for another; the
     // conversions and the selects of the out-of-row elements come after all of them
-    float v[kJoinMaxPer], ga[kJoinMaxPer], re[kJoinMaxPer], g2[kJoinMaxPer];
-    int raw[kJoinMaxPer];  // the source element's bits: an int8 code, an f32, or the int32 sum
-    float as[ACC ? kJoinMaxPer : 1];
-    int ic[kJoinMaxPer];
+    float v[PER], ga[PER], re[PER], g2[PER];
+    int raw[PER];  // the source element's bits: an int8 code, an f32, or the int32 sum
+    float as[ACC ? PER : 1];
+    int ic[PER];
 #pragma unroll
-    for (int e = 0; e < kJoinMaxPer; ++e) ic[e] = min(t + e * kRowThreads, width - 1);
+    for (int e = 0; e < PER; ++e) ic[e] = min(t + e * kRowThreads, width - 1);
     if constexpr (ACC > 0) {
 #pragma unroll
-        for (int e = 0; e < kJoinMaxPer; ++e) {
+        for (int e = 0; e < PER; ++e) {
             raw[e] = acc_sum<ACC>(J, base + ic[e]);
             as[e] = J.acc_scales[ic[e]];
         }
     } else if (J.src_kind == G4_KIND_I8) {
         const int8_t *src = reinterpret_cast<const int8_t *>(J.src) + base;
 #pragma unroll
-        for (int e = 0; e < kJoinMaxPer; ++e) raw[e] = src[ic[e]];
+        for (int e = 0; e < PER; ++e) raw[e] = src[ic[e]];
     } else {
         const int *src = reinterpret_cast<const int *>(J.src) + base;
 #pragma unroll
-        for (int e = 0; e < kJoinMaxPer; ++e) raw[e] = src[ic[e]];
+        for (int e = 0; e < PER; ++e) raw[e] = src[ic[e]];
     }
 #pragma unroll
-    for (int e = 0; e < kJoinMaxPer; ++e) {
+    for (int e = 0; e < PER; ++e) {
         ga[e] = J.gain ? J.gain[ic[e]] : 1.0f;
         re[e] = J.resid ? J.resid[base + ic[e]] : 0.0f;
         g2[e] = J.gain2 ? J.gain2[ic[e]] : 0.0f;
     }
     after_loads();
 #pragma unroll
-    for (int e = 0; e < kJoinMaxPer; ++e) {
+    for (int e = 0; e < PER; ++e) {
         const bool in = t + e * kRowThreads < width;
         float x;
         if constexpr (ACC > 0) x = acc_value(J, raw[e], as[e]);
@@ -134,12 +137,12 @@ __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row
     }
     float part = 0.0f;
 #pragma unroll
-    for (int e = 0; e < kJoinMaxPer; ++e)
+    for (int e = 0; e < PER; ++e)
         if (t + e * kRowThreads < width) part = __fadd_rn(part, __fmul_rn(v[e], v[e]));
     const float inv = inv_rms(block_tree_sum(part, lds), width, J.eps);
     float part2 = 0.0f;
 #pragma unroll
-    for (int e = 0; e < kJoinMaxPer; ++e) {
+    for (int e = 0; e < PER; ++e) {
         const int i = t + e * kRowThreads;
         if (i >= width) continue;
         float y = __fmul_rn(v[e], inv);
@@ -156,13 +159,13 @@ __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row
     if (J.gain2) {
         const float inv2 = inv_rms(block_tree_sum(part2, lds + kRowThreads), width, J.eps);
 #pragma unroll
-        for (int e = 0; e < kJoinMaxPer; ++e) {
+        for (int e = 0; e < PER; ++e) {
             const int i = t + e * kRowThreads;
             if (i < width) emit(i, snap_code(__fmul_rn(__fmul_rn(v[e], inv2), g2[e]), J.in_scale));
         }
     } else {
 #pragma unroll
-        for (int e = 0; e < kJoinMaxPer; ++e) {
+        for (int e = 0; e < PER; ++e) {
             const int i = t + e * kRowThreads;
             if (i < width) emit(i, snap_code(v[e], J.in_scale));
         }
