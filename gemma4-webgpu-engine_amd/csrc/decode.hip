@@ -37,10 +37,10 @@ static_assert(kDecThreads == kRowThreads, "the glue kernels run the shared 256-l
 // ---- rms-norm / norm-residual / norm-residual-norm --------------------------------------------------
 
 // One block per row (rms_join_row). ACC: the source is split accumulators (acc_sum, acc_value).
-template <bool ACC>
+template <bool ACC, int PER>
 __global__ __launch_bounds__(kDecThreads) void join_kernel(JoinTail J) {
     __shared__ float lds[2 * kDecThreads];
-    rms_join_row<ACC ? kSplitAccMax : 0>(J, blockIdx.x, lds);
+    rms_join_row<ACC ? kSplitAccMax : 0, PER>(J, blockIdx.x, lds);
 }
 
 int join_acc(const JoinTail &J, int rows, hipStream_t stream) {
@@ -49,7 +49,10 @@ int join_acc(const JoinTail &J, int rows, hipStream_t stream) {
         J.width > kJoinMaxPer * kDecThreads || J.src_scale == 0.0f || !J.codes ||
         J.in_scale == 0.0f)
         return set_error(G4_ERR_INVALID, "join over split accumulators: bad arguments");
-    hipLaunchKernelGGL((join_kernel<true>), dim3(rows), dim3(kDecThreads), 0, stream, J);
+    if (join_narrow(J.width))
+        hipLaunchKernelGGL((join_kernel<true, kJoinPerNarrow>), dim3(rows), dim3(kDecThreads), 0, stream, J);
+    else
+        hipLaunchKernelGGL((join_kernel<true, kJoinMaxPer>), dim3(rows), dim3(kDecThreads), 0, stream, J);
     G4_LAUNCHED("join_kernel");
     return G4_OK;
 }
@@ -1115,7 +1118,12 @@ int g4_rms_join(const void *src, int src_kind, float src_scale, const float *gai
     J.in_scale = in_scale;
     J.hidden = hidden;
     J.codes = codes;
-    hipLaunchKernelGGL((join_kernel<false>), dim3(rows), dim3(kDecThreads), 0, as_stream(stream), J);
+    if (join_narrow(J.width))
+        hipLaunchKernelGGL((join_kernel<false, kJoinPerNarrow>), dim3(rows), dim3(kDecThreads), 0,
+                           as_stream(stream), J);
+    else
+        hipLaunchKernelGGL((join_kernel<false, kJoinMaxPer>), dim3(rows), dim3(kDecThreads), 0,
+                           as_stream(stream), J);
     G4_LAUNCHED("join_kernel");
     return G4_OK;
 }

@@ -173,11 +173,16 @@ __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row
 }
 
 // The join kernel's form: codes to J.codes[row][i]. lds: 512 floats.
-template <int ACC = 0>
+template <int ACC = 0, int PER = kJoinMaxPer>
 __device__ __forceinline__ void rms_join_row(const JoinTail &J, int64_t row, float *lds) {
     int8_t *codes = J.codes;
     const int64_t base = row * J.width;
-    rms_join_row_emit<ACC>(J, row, lds, [=](int i, int8_t c) { codes[base + i] = c; });
+    rms_join_row_emit<ACC, PER>(J, row, lds, [=](int i, int8_t c) { codes[base + i] = c; });
 }
+
+// The elements per thread a launcher instantiates for a row of `width`: 6 up to 1536 (the E2B
+// hidden size), else 8.
+constexpr int kJoinPerNarrow = 6;
+__host__ __device__ inline bool join_narrow(int width) { return width <= kJoinPerNarrow * kRowThreads; }
 
 }  // namespace g4

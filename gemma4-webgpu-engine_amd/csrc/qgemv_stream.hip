@@ -277,8 +277,14 @@ __device__ __forceinline__ int snap_join(const JoinTail *pre, int four, uint8_t 
     };
     // an int32 accumulator source (the decode runner's o_proj folded into the attention merge)
     // runs the producing linear's epilogue and snap first
-    if (T.src_kind == G4_KIND_I32) rms_join_row_emit<1>(T, 0, red, emit, after_loads);
-    else rms_join_row_emit<0>(T, 0, red, emit, after_loads);
+    // rows up to 1536 wide take 6 elements per thread (no loads past the row)
+    if (join_narrow(T.width)) {
+        if (T.src_kind == G4_KIND_I32) rms_join_row_emit<1, kJoinPerNarrow>(T, 0, red, emit, after_loads);
+        else rms_join_row_emit<0, kJoinPerNarrow>(T, 0, red, emit, after_loads);
+    } else {
+        if (T.src_kind == G4_KIND_I32) rms_join_row_emit<1>(T, 0, red, emit, after_loads);
+        else rms_join_row_emit<0>(T, 0, red, emit, after_loads);
+    }
     return local;
 }
 
