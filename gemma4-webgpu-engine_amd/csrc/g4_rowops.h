@@ -15,10 +15,31 @@ namespace g4 {
 constexpr int kRowThreads = 256;
 constexpr int kJoinMaxPer = 8;  // an RMS join serves widths up to 8 * 256
 
+// The in-wave levels s = 32 .. 1 of the pairwise tree (lane l adds lane l + s for l < s), with
+// the total in every lane: s = 32 and 16 by the gfx950 lane swaps (v_permlane32_swap hands lanes
+// 0-31 the values of lanes 32-63, v_permlane16_swap row 0 those of row 1), s = 8 .. 1 by DPP
+// row_shl, each a register move instead of an LDS round trip; the same adds on the same lanes as
+// __shfl_down(v, s), so the same sum bit for bit.
+__device__ __forceinline__ float wave_tree_sum(float v) {
+    {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __fadd_rn(v, __uint_as_float(r[1]));
+    }
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __fadd_rn(v, __uint_as_float(r[1]));
+    }
+    v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xF, 0xF, true)));
+    v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x104, 0xF, 0xF, true)));
+    v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x102, 0xF, 0xF, true)));
+    v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x101, 0xF, 0xF, true)));
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+
 // The pairwise tree over 256 lanes: level s adds lane l + s into lane l for l < s, s = 128 .. 1
 // (every thread of the block calls it; returns the total). The 256 partials go through LDS once;
 // then every wave evaluates the whole tree itself: lane l takes levels 128 and 64 in-lane
-// ((p[l] + p[l+128]) + (p[l+64] + p[l+192])) and the six in-wave levels by shuffles. One barrier.
+// ((p[l] + p[l+128]) + (p[l+64] + p[l+192])) and the six in-wave levels in registers. One barrier.
 // lds: 256 floats that the block does not write again before another barrier (two trees in a row
 // take two regions).
 __device__ __forceinline__ float block_tree_sum(float part, float *lds) {
@@ -27,10 +48,7 @@ __device__ __forceinline__ float block_tree_sum(float part, float *lds) {
     __syncthreads();
     const float a = __fadd_rn(lds[lane], lds[lane + 128]);       // s = 128, lanes l < 64
     const float b = __fadd_rn(lds[lane + 64], lds[lane + 192]);  // s = 128, lanes 64 .. 127
-    float v = __fadd_rn(a, b);                                   // s = 64
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = __fadd_rn(v, __shfl_down(v, off));
-    return __shfl(v, 0);
+    return wave_tree_sum(__fadd_rn(a, b));                       // s = 64, then 32 .. 1
 }
 
 // sqrtf, not __fsqrt_rn: on this toolchain __fsqrt_rn is the native (approximate) v_sqrt_f32
