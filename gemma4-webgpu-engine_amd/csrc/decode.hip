@@ -163,9 +163,7 @@ __device__ __forceinline__ void wave_norm_rope(const NormRopeIn &in, float scale
     for (int k = 0; k < 4; ++k) x[k] = __fmul_rn((float)in.code[k], scale);
     float part = __fadd_rn(__fadd_rn(__fmul_rn(x[0], x[0]), __fmul_rn(x[2], x[2])),
                            __fadd_rn(__fmul_rn(x[1], x[1]), __fmul_rn(x[3], x[3])));
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) part = __fadd_rn(part, __shfl_down(part, off));
-    const float inv = inv_rms(__shfl(part, 0), kDecThreads, eps);
+    const float inv = inv_rms(wave_tree_sum(part), kDecThreads, eps);
     float y[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -376,8 +374,7 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
         for (int off = 16; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 32));
         const float e = p < cnt ? d_expf(__fsub_rn(x, m)) : 0.0f;
         float l = e;
-#pragma unroll
-        for (int off = 16; off >= 1; off >>= 1) l = __fadd_rn(l, __shfl_down(l, off, 32));
+        l = half_wave_tree_sum(l);  // lane p = 0 of each 32-lane group holds its head's sum
         es[hh * kAttnChunk + p] = e;
         if (p == 0) {
             const int64_t slot = (row * heads + hh) * max_chunks + c;

@@ -36,6 +36,19 @@ __device__ __forceinline__ float wave_tree_sum(float v) {
     return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
 }
 
+// The same tree over each 32-lane half of the wave (levels 16 .. 1): the half's total in its
+// first lane (lanes 0 and 32).
+__device__ __forceinline__ float half_wave_tree_sum(float v) {
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __fadd_rn(v, __uint_as_float(r[1]));
+    }
+    v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xF, 0xF, true)));
+    v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x104, 0xF, 0xF, true)));
+    v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x102, 0xF, 0xF, true)));
+    return __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x101, 0xF, 0xF, true)));
+}
+
 // The pairwise tree over 256 lanes: level s adds lane l + s into lane l for l < s, s = 128 .. 1
 // (every thread of the block calls it; returns the total). The 256 partials go through LDS once;
 // then every wave evaluates the whole tree itself: lane l takes levels 128 and 64 in-lane
