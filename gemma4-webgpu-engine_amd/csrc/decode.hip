@@ -370,8 +370,12 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
     if (half == 0 && hh < heads) {
         const float x = es[hh * kAttnChunk + p];
         float m = x;
-#pragma unroll
-        for (int off = 16; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 32));
+        {  // the group's maximum, in every lane of the group
+            const float mg = half_wave_max(m);
+            const float m0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mg), 0));
+            const float m1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mg), 32));
+            m = (t & 32) ? m1 : m0;
+        }
         const float e = p < cnt ? d_expf(__fsub_rn(x, m)) : 0.0f;
         float l = e;
         l = half_wave_tree_sum(l);  // lane p = 0 of each 32-lane group holds its head's sum
@@ -459,8 +463,7 @@ __device__ __forceinline__ float merge_head_dim(const float *part_ml, const floa
     float m = -__int_as_float(0x7f800000), lt = 0.0f;
     for (int c = t; c < chunks; c += kDecThreads) m = fmaxf(m, part_ml[(slot0 + c) * 2]);
     if (t < chunks) lt = part_ml[(slot0 + t) * 2 + 1];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    m = wave_max(m);  // lane 0 holds the wave's maximum
     if ((t & 63) == 0) red[t >> 6] = m;
     __syncthreads();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));

@@ -49,6 +49,23 @@ __device__ __forceinline__ float half_wave_tree_sum(float v) {
     return __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x101, 0xF, 0xF, true)));
 }
 
+// The maximum over each 32-lane half of the wave in its first lane (lanes 0 and 32), and over the
+// whole wave in lane 0, by the same lane moves (a maximum is exact in any order).
+__device__ __forceinline__ float dpp_max_rows(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xF, 0xF, true)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x104, 0xF, 0xF, true)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x102, 0xF, 0xF, true)));
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x101, 0xF, 0xF, true)));
+}
+__device__ __forceinline__ float half_wave_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return dpp_max_rows(fmaxf(v, __uint_as_float(r[1])));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return half_wave_max(fmaxf(v, __uint_as_float(r[1])));
+}
+
 // The pairwise tree over 256 lanes: level s adds lane l + s into lane l for l < s, s = 128 .. 1
 // (every thread of the block calls it; returns the total). The 256 partials go through LDS once;
 // then every wave evaluates the whole tree itself: lane l takes levels 128 and 64 in-lane
