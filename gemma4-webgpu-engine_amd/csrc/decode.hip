@@ -583,9 +583,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_merge_o_kernel(
     // codes in the 4-bit snap layout: each 8-code group as [x0 x2 x4 x6 | x1 x3 x5 x7]
     const int j = t & 7;
     xs[(t & ~7) + (j & 1 ? 4 : 0) + (j >> 1)] = (uint8_t)c;
-    int s = c;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+    const int s = wave_sum_i32_first(c);  // lane 0: the wave's code sum
     if ((t & 63) == 0) csum[t >> 6] = s;
     __syncthreads();
     const int xsum = csum[0] + csum[1] + csum[2] + csum[3];
@@ -807,8 +805,7 @@ __global__ __launch_bounds__(kDecThreads) void ffn_block_kernel(FfnFold F) {
             const int j = t & 7;
             act[(t & ~7) + (j & 1 ? 4 : 0) + (j >> 1)] = (uint8_t)a;
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) a += __shfl_xor(a, off);
+        a = wave_sum_i32_first(a);  // lane 0: the block's code sum
         if (t == 0) sums[1] = a;
     }
     __syncthreads();

@@ -49,6 +49,22 @@ __device__ __forceinline__ float half_wave_tree_sum(float v) {
     return __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x101, 0xF, 0xF, true)));
 }
 
+// The wave's int32 sum in lane 0 (exact in any order), by the same lane moves.
+__device__ __forceinline__ int wave_sum_i32_first(int v) {
+    {
+        const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+        v += (int)r[1];
+    }
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+        v += (int)r[1];
+    }
+    v += __builtin_amdgcn_update_dpp(0, v, 0x108, 0xF, 0xF, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x104, 0xF, 0xF, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x102, 0xF, 0xF, true);
+    return v + __builtin_amdgcn_update_dpp(0, v, 0x101, 0xF, 0xF, true);
+}
+
 // The maximum over each 32-lane half of the wave in its first lane (lanes 0 and 32), and over the
 // whole wave in lane 0, by the same lane moves (a maximum is exact in any order).
 __device__ __forceinline__ float dpp_max_rows(float v) {
