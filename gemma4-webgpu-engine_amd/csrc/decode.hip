@@ -22,6 +22,8 @@
 // give int8 codes: every kernel here that feeds a projection emits its input snap directly.
 #include "g4_rowops.h"
 #include "../../include/g4decode.h"
+#include <algorithm>
+#include <cmath>
 
 namespace g4 {
 
@@ -881,6 +883,23 @@ __global__ void gelu_mul_kernel(const int8_t *g, float gs, const int8_t *u, floa
     }
 }
 
+// gelu-mul on the reference's f32 buffers (geluMul.ts:101-116 and its main, 4 elements per vec4
+// lane): dst = gelu_tanh(gate) * up, then q * s with q = srq(v, s) when s != 0.
+__global__ void gelu_mul_f32_kernel(const float4 *g, const float4 *u, float4 *dst, int64_t n4,
+                                    float srq_scale) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float4 a = g[i], b = u[i];
+        float v[4] = {__fmul_rn(d_gelu(a.x), b.x), __fmul_rn(d_gelu(a.y), b.y),
+                      __fmul_rn(d_gelu(a.z), b.z), __fmul_rn(d_gelu(a.w), b.w)};
+        if (srq_scale != 0.0f) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = __fmul_rn(srq_code_f(v[j], srq_scale), srq_scale);
+        }
+        dst[i] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
+
 // ---- the token embedding (tied int4 table) -----------------------------------------------------------
 
 // One block per row: x = (code - 8) * f32(scale[id] * embed_scale); also the codes of x snapped on
@@ -1199,6 +1218,26 @@ int g4_gelu_mul(const int8_t *g_codes, float g_scale, const int8_t *u_codes, flo
     hipLaunchKernelGGL(gelu_mul_kernel, dim3(bx, rows), dim3(kDecThreads), 0, as_stream(stream),
                        g_codes, g_scale, u_codes, u_scale, up_f32, up_stride, n, in_scale, codes);
     G4_LAUNCHED("gelu_mul_kernel");
+    return G4_OK;
+}
+
+int g4_gelu_mul_f32(const float *gate, const float *up, float *dst, int64_t count,
+                    float srq_scale, void *stream) {
+    if (count <= 0 || count % 4 != 0)
+        return set_error(G4_ERR_INVALID, "gelu-mul needs params.count a positive multiple of 4, got %lld",
+                         (long long)count);
+    if (!gate || !up) return set_error(G4_ERR_INVALID, "gelu-mul needs inputs named gate and up");
+    if (!dst) return set_error(G4_ERR_INVALID, "gelu-mul needs an output");
+    if (((reinterpret_cast<uintptr_t>(gate) | reinterpret_cast<uintptr_t>(up) |
+          reinterpret_cast<uintptr_t>(dst)) & 15) != 0)
+        return set_error(G4_ERR_INVALID, "gelu-mul: gate, up and dst must be 16-byte aligned");
+    if (!std::isfinite(srq_scale)) return set_error(G4_ERR_INVALID, "gelu-mul: srqScale must be finite");
+    const int64_t n4 = count / 4;
+    const int blocks = (int)std::min<int64_t>((n4 + kDecThreads - 1) / kDecThreads, 8 * 1024);
+    hipLaunchKernelGGL(gelu_mul_f32_kernel, dim3(blocks), dim3(kDecThreads), 0, as_stream(stream),
+                       reinterpret_cast<const float4 *>(gate), reinterpret_cast<const float4 *>(up),
+                       reinterpret_cast<float4 *>(dst), n4, srq_scale);
+    G4_LAUNCHED("gelu_mul_f32_kernel");
     return G4_OK;
 }
 

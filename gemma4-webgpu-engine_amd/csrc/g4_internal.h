@@ -44,11 +44,19 @@ int device_cu_count();
 // The gelu activation prologue of one GEMV job (qgemv.ts:359-400): the job's x is the gate, and
 // the GEMV reads gelu_tanh(gate[i]) * up[i] in place of x[i]. `up` already carries the offset;
 // null means no prologue. gate codes (x_kind int8) are times g_scale, up codes times u_scale.
+// With fold_parts set (ple-fold-projection, pleSplit.ts:24-41) the gate is not read from x: gate
+// element i is the fold of the split partials fold_parts[(i / 4) * 4 * fold_splits + s * 4 + i % 4]
+// (ascending s from 0), times f32(fold_in * fold_scales[i]), snapped on fold_out when non-zero.
 struct GeluAct {
     const void *up = nullptr;
     float g_scale = 0.0f;
     float u_scale = 0.0f;
     int up_kind = G4_KIND_F32;
+    const float *fold_parts = nullptr;
+    const float *fold_scales = nullptr;
+    int fold_splits = 0;
+    float fold_in = 0.0f;
+    float fold_out = 0.0f;
 };
 
 // The gelu-mul pass folded into the gate's GEMV epilogue (the decode runner's form, no reference
@@ -245,10 +253,13 @@ int stream_class_for(int bits, int k);
 int workspace_forget_stream(void *stream);
 
 // g4_qgemm with the caller's buffer for the snapped activation codes in place of the stream's
-// workspace (codes_bytes bytes; refused when the call's path needs more). Allocates nothing.
+// workspace (codes_bytes bytes; refused when the call's path needs more). Allocates nothing. The
+// call is validated and routed first; `source` gives the buffer's address and is called only when
+// the routed path needs one.
+typedef int (*CodesSource)(int8_t **codes);
 int qgemm_given_codes(int bits, const void *wq, const float *scales, const void *x, int x_kind,
                       void *dst, int out_kind, int k, int num_rows, int m_cols, float in_scale,
-                      float out_scale, void *stream, int8_t *codes, size_t codes_bytes,
+                      float out_scale, void *stream, CodesSource source, size_t codes_bytes,
                       const char *who);
 
 // ---- device: the static range quantization arithmetic (src/quant.ts:248-357) -----------------
@@ -343,8 +354,6 @@ __device__ __forceinline__ float d_gelu(float x) {
 }
 
 
-// The closing expression of every quantized linear (qgemv.ts:1168-1172, :680-686), in its order:
-// one f32 multiply folds the input scale into the row scale, one more multiplies the reduced sum.
 // Eight activation values e .. e + 7 of an f32 vector, or of int8 codes times `scale`.
 __device__ __forceinline__ void act_vals8(const void *p, int kind, float scale, int64_t e,
                                           float v[8]) {
@@ -376,6 +385,62 @@ __device__ __forceinline__ void gelu_codes8(const void *gate, int g_kind, float 
     for (int i = 0; i < 8; ++i) c[i] = (int)srq_code_fast(__fmul_rn(d_gelu(g[i]), u[i]), s, r, r_ok);
 }
 
+// foldGate (pleSplit.ts:33-41) for the four gate elements of vec4 index i: the split partials
+// summed in split order from 0, the gate linear's epilogue f32(f32(in * scale) * total), then its
+// output snap (srqOut with the IEEE divide) when out != 0.
+__device__ __forceinline__ float4 fold_gate4(const GeluAct &a, int64_t i) {
+    const float4 *parts = reinterpret_cast<const float4 *>(a.fold_parts) + i * a.fold_splits;
+    float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int s = 0; s < a.fold_splits; ++s) {
+        const float4 p = parts[s];
+        t.x = __fadd_rn(t.x, p.x);
+        t.y = __fadd_rn(t.y, p.y);
+        t.z = __fadd_rn(t.z, p.z);
+        t.w = __fadd_rn(t.w, p.w);
+    }
+    const float4 sc = reinterpret_cast<const float4 *>(a.fold_scales)[i];
+    float v[4] = {__fmul_rn(__fmul_rn(a.fold_in, sc.x), t.x), __fmul_rn(__fmul_rn(a.fold_in, sc.y), t.y),
+                  __fmul_rn(__fmul_rn(a.fold_in, sc.z), t.z), __fmul_rn(__fmul_rn(a.fold_in, sc.w), t.w)};
+    if (a.fold_out != 0.0f) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = __fmul_rn(srq_code_f(v[j], a.fold_out), a.fold_out);
+    }
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// The ple-fold-projection prologue's codes for activations e .. e + 7 (e a multiple of 8):
+// srq(gelu_tanh(foldGate) * up) on s.
+__device__ __forceinline__ void fold_gelu_codes8(const GeluAct &a, int64_t e, float s, float r,
+                                                 bool r_ok, int c[8]) {
+    const float4 g0 = fold_gate4(a, e >> 2), g1 = fold_gate4(a, (e >> 2) + 1);
+    const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    float u[8];
+    act_vals8(a.up, a.up_kind, a.u_scale, e, u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = (int)srq_code_fast(__fmul_rn(d_gelu(g[i]), u[i]), s, r, r_ok);
+}
+
+// One prologue activation as f32 (the uncalibrated path reads it unsnapped, qgemv.ts:359-400):
+// gelu_tanh(gate[i]) * up[i], the gate from x (f32 or codes times g_scale) or from the fold.
+__device__ __forceinline__ float gelu_act_value(const GeluAct &a, const void *gate, int g_kind,
+                                                int64_t i) {
+    float g;
+    if (a.fold_parts) {
+        const float4 g4v = fold_gate4(a, i >> 2);
+        const int j = (int)(i & 3);
+        g = j == 0 ? g4v.x : j == 1 ? g4v.y : j == 2 ? g4v.z : g4v.w;
+    } else {
+        g = g_kind == G4_KIND_I8 ? __fmul_rn((float)reinterpret_cast<const int8_t *>(gate)[i], a.g_scale)
+                                 : reinterpret_cast<const float *>(gate)[i];
+    }
+    const float u = a.up_kind == G4_KIND_I8
+                        ? __fmul_rn((float)reinterpret_cast<const int8_t *>(a.up)[i], a.u_scale)
+                        : reinterpret_cast<const float *>(a.up)[i];
+    return __fmul_rn(d_gelu(g), u);
+}
+
+// The closing expression of every quantized linear (qgemv.ts:1168-1172, :680-686), in its order:
+// one f32 multiply folds the input scale into the row scale, one more multiplies the reduced sum.
 __device__ __forceinline__ float linear_epilogue(float in_scale, float row_scale, float sum) {
     return __fmul_rn(__fmul_rn(in_scale, row_scale), sum);
 }

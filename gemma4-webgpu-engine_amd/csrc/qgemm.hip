@@ -1578,18 +1578,21 @@ static int check_qgemm(int bits, const void *wq, const float *scales, const void
 // nothing is allocated. A call whose path needs more codes than that is refused.
 int qgemm_given_codes(int bits, const void *wq, const float *scales, const void *x, int x_kind,
                       void *dst, int out_kind, int k, int num_rows, int m_cols, float in_scale,
-                      float out_scale, void *stream, int8_t *codes, size_t codes_bytes,
+                      float out_scale, void *stream, CodesSource source, size_t codes_bytes,
                       const char *who) {
     int rc = check_qgemm(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols, in_scale,
                          out_scale);
     if (rc) return rc;
+    int8_t *codes = nullptr;
     if (needs_codes_buffer(bits, m_cols, num_rows, k, in_scale, x_kind, true)) {
         const size_t need = (size_t)m_cols * (size_t)k;
-        if (!codes || need > codes_bytes)
+        if (need > codes_bytes)
             return set_error(G4_ERR_INVALID,
                              "%s: M * K = %zu activation codes exceed the %zu-byte scratch buffer "
                              "(pass int8 codes already snapped, or a smaller M)",
                              who, need, codes_bytes);
+        rc = source(&codes);
+        if (rc) return rc;
     }
     return run_linear(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols, in_scale,
                       out_scale, as_stream(stream), bits == 4 ? "qgemm-4bit" : "qmatmul-8bit", true,

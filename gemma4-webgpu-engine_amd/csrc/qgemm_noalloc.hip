@@ -51,17 +51,10 @@ size_t g4_qgemm_noalloc_max_codes(void) { return kScratchBytes; }
 int g4_qgemm_noalloc(int bits, const void *wq, const float *scales, const void *x, int x_kind,
                      void *dst, int out_kind, int k, int num_rows, int m_cols, float in_scale,
                      float out_scale, void *stream) {
-    // refuse an oversized call before touching the device
-    if (x_kind != G4_KIND_I8 && m_cols > 32 && k > 0 && (size_t)m_cols * (size_t)k > kScratchBytes)
-        return g4::set_error(G4_ERR_INVALID,
-                             "g4_qgemm_noalloc: M * K = %zu activation codes exceed the %zu-byte "
-                             "scratch array (pass int8 codes already snapped, or a smaller M)",
-                             (size_t)m_cols * (size_t)k, kScratchBytes);
-    int8_t *ptr = nullptr;
-    int rc = scratch_ptr(&ptr);
-    if (rc) return rc;
+    // the call is checked and routed first (the reference's refusals come before any size
+    // message); the scratch array's address is looked up only when the routed path snaps codes
     return g4::qgemm_given_codes(bits, wq, scales, x, x_kind, dst, out_kind, k, num_rows, m_cols,
-                                 in_scale, out_scale, stream, ptr, kScratchBytes,
+                                 in_scale, out_scale, stream, scratch_ptr, kScratchBytes,
                                  "g4_qgemm_noalloc");
 }
 

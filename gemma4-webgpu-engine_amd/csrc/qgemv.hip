@@ -52,9 +52,19 @@ struct GemvJob {
 struct GemvLaunch {
     GemvJob job[G4_MAX_GROUP];
     int count;
-    int splits;       // 1: plain GEMV. > 1: split-K partials [rows][splits] (one job, one column)
+    int splits;       // 1: plain GEMV. > 1: split-K partials (one job, one column)
     int split_exact;  // split only: 1 writes raw integer partials, 0 the scaled ones
+    int split_layout; // split only: 0 [rows][splits]; 1 the PLE gate's row-interleaved layout
 };
+
+// Index of (row, split) in the partials: [rows][splits], or ple-gate-split's interleave
+// dst[(row / 4) * 4 * splits + split * 4 + row % 4] (pleSplit.ts:17-23), which the fold reads as
+// one vec4 per (4 rows, split).
+__device__ __forceinline__ int64_t split_index(const GemvLaunch &L, int row, int split) {
+    if (L.split_layout)
+        return (int64_t)(row >> 2) * 4 * L.splits + split * 4 + (row & 3);
+    return (int64_t)row * L.splits + split;
+}
 
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
     return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
@@ -245,7 +255,9 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_int_kernel(GemvLaunch L) {
             const int gi = COLS == 1 ? g : g - col * groups;
             int c[8];
             const int64_t e = (int64_t)col * k + c_lo + gi * 8;
-            if (J.act.up)
+            if (J.act.fold_parts)
+                fold_gelu_codes8(J.act, e, J.in_scale, r, r_ok, c);
+            else if (J.act.up)
                 gelu_codes8(J.x, J.x_kind, J.act.g_scale, J.act.up, J.act.up_kind, J.act.u_scale, e,
                             J.in_scale, r, r_ok, c);
             else
@@ -309,7 +321,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_int_kernel(GemvLaunch L) {
             const int s = bits == 4 ? acc[c] - 8 * sx[c] : acc[c];
             if (L.splits > 1) {
                 const float part = L.split_exact ? (float)s : linear_epilogue(J.in_scale, scale, (float)s);
-                reinterpret_cast<float *>(J.dst)[(int64_t)row * L.splits + split] = part;
+                reinterpret_cast<float *>(J.dst)[split_index(L, row, split)] = part;
             } else {
                 const float y = linear_epilogue(J.in_scale, scale, (float)s);
                 store_linear_out(J.dst, (int64_t)c * J.rows + row, J.out_kind, y, s, J.out_scale);
@@ -331,7 +343,7 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_int_kernel(GemvLaunch L) {
             const float scale = J.scales[row];
             if (L.splits > 1) {
                 const float part = L.split_exact ? (float)s : linear_epilogue(J.in_scale, scale, (float)s);
-                reinterpret_cast<float *>(J.dst)[(int64_t)row * L.splits + split] = part;
+                reinterpret_cast<float *>(J.dst)[split_index(L, row, split)] = part;
             } else {
                 const float y = linear_epilogue(J.in_scale, scale, (float)s);
                 store_linear_out(J.dst, (int64_t)c * J.rows + row, J.out_kind, y, s, J.out_scale);
@@ -352,7 +364,10 @@ __global__ __launch_bounds__(kGemvThreads) void qgemv_f32_kernel(GemvLaunch L) {
     const int tid = threadIdx.x;
     const int k = J.k;
     const int col = blockIdx.z;
-    for (int i = tid; i < k; i += kGemvThreads) xs[i] = load_act(J.x, J.x_kind, (int64_t)col * k + i);
+    for (int i = tid; i < k; i += kGemvThreads) {
+        const int64_t e = (int64_t)col * k + i;
+        xs[i] = J.act.up ? gelu_act_value(J.act, J.x, J.x_kind, e) : load_act(J.x, J.x_kind, e);
+    }
     __syncthreads();
     const int lane = tid & 63, wave = tid >> 6, lane16 = lane & 15;
     const int bits = J.bits;
@@ -443,12 +458,20 @@ int check_job(const GemvJob &J, int cols, const char *who) {
         return set_error(G4_ERR_INVALID, "%s: wq and x must be 16-byte aligned", who);
     if (cols < 1 || cols > 2) return set_error(G4_ERR_INVALID, "%s: cols %d not in 1..2", who, cols);
     if (J.act.up) {
-        // qgemv.ts:359-400: the prologue binds gate and up in place of x
-        if (J.in_scale == 0.0f)
-            return set_error(G4_ERR_UNSUPPORTED,
-                             "%s: the fused gelu prologue runs calibrated sites (inScale != 0); run "
-                             "g4_gelu_mul then the GEMV", who);
-        if (cols != 1) return set_error(G4_ERR_INVALID, "%s: the gelu prologue is single-column", who);
+        // qgemv.ts:359-400 (and the wide form, qgemvWide.ts:193-283): the prologue binds gate and
+        // up in place of x; on an uncalibrated site the f32 code dot reads the product unsnapped
+        if (J.act.fold_parts) {
+            // pleSplit.ts:24-41: the gate is the fold of the split partials, one token
+            if (cols != 1) return set_error(G4_ERR_INVALID, "PLE split needs one token");
+            if (J.act.fold_splits != 2 && J.act.fold_splits != 4 && J.act.fold_splits != 8)
+                return set_error(G4_ERR_INVALID, "PLE splits must be 1, 2, 4 or 8");
+            if (!J.act.fold_scales)
+                return set_error(G4_ERR_INVALID, "%s needs inputs named gate, up and gateScales", who);
+            if (!aligned16(J.act.fold_parts) || !aligned16(J.act.fold_scales))
+                return set_error(G4_ERR_INVALID, "%s: gate partials and gateScales must be 16-byte aligned", who);
+            if (!std::isfinite(J.act.fold_in) || !std::isfinite(J.act.fold_out))
+                return set_error(G4_ERR_INVALID, "%s: gateInScale and gateOutScale must be finite", who);
+        }
         if (J.x_kind != G4_KIND_F32 && J.x_kind != G4_KIND_I8)
             return set_error(G4_ERR_INVALID, "%s: gate must be f32 or int8 codes", who);
         if (J.act.up_kind != G4_KIND_F32 && J.act.up_kind != G4_KIND_I8)
@@ -520,6 +543,7 @@ static int try_stream(const GemvLaunch &L, int cols, hipStream_t stream, bool *l
     g4_gemv_desc d[G4_MAX_GROUP];
     GeluAct a[G4_MAX_GROUP];
     for (int i = 0; i < L.count; ++i) {
+        if (L.job[i].act.fold_parts) return G4_OK;  // the fold prologue runs on qgemv_int_kernel
         d[i] = desc_of(L.job[i]);
         a[i] = L.job[i].act;
     }
@@ -764,18 +788,20 @@ int g4_qgemv_split(int bits, const void *wq, const float *scales, const void *x,
     return launch_gemv(L, 1, as_stream(stream));
 }
 
-// qgemv-4bit-gelu / qgemv-8bit-gelu and the gelu exact split (qgemv.ts:359-400, 1668-1696;
-// exactSplit.ts:19-31): the GEMV or split build with the prologue reading gate and up.
+// qgemv-4bit-gelu / qgemv-8bit-gelu, their -m2 forms, the gelu exact split and the PLE fold
+// projection (qgemv.ts:359-400, 1668-1696; qgemvWide.ts:660-709; exactSplit.ts:19-31;
+// pleSplit.ts:24-84): the GEMV or split build with the prologue reading gate and up. `fold` (may be
+// null) makes the gate the fold of ple-gate-split's partials; `gate` is then those partials.
 static int gelu_gemv(int bits, const void *wq, const float *scales, const void *gate,
-                     int gate_kind, const g4_gelu_act *act, void *dst, int out_kind, int k,
-                     int num_rows, int k_splits, int exact, float in_scale, float out_scale,
-                     void *stream) {
+                     int gate_kind, const g4_gelu_act *act, const GeluAct *fold, void *dst,
+                     int out_kind, int k, int num_rows, int cols, int k_splits, int exact,
+                     float in_scale, float out_scale, void *stream, const char *who) {
     const bool split = k_splits > 0;
-    char who[40];
-    snprintf(who, sizeof who, "qgemv-%dbit-gelu%s", bits, split ? (exact ? "-exact-split" : "-split") : "");
     if (!act || !act->up) return set_error(G4_ERR_INVALID, "%s needs inputs named gate and up", who);
     if (bits != 4 && bits != 8) return set_error(G4_ERR_INVALID, "%s: bits must be 4 or 8", who);
     if (k <= 0 || num_rows <= 0) return set_error(G4_ERR_INVALID, "%s needs params.k and params.numRows", who);
+    if (cols <= 0 || cols > 2)
+        return set_error(G4_ERR_INVALID, "%s needs params.cols in 1..2, got %d", who, cols);
     const int span = bits == 4 ? 256 : 128;
     if (k % span != 0)
         return set_error(G4_ERR_INVALID, "%s needs K a multiple of %d, got %d", who, span, k);
@@ -784,6 +810,8 @@ static int gelu_gemv(int bits, const void *wq, const float *scales, const void *
         return set_error(G4_ERR_INVALID, "gemv geometry: kSplits must be 1, 2, 4 or 8, got %d", k_splits);
     if (split && exact && (!(in_scale > 0.0f) || k > 16384))
         return set_error(G4_ERR_INVALID, "exact split needs calibrated int8 input and K <= 16384");
+    if (split && in_scale == 0.0f)
+        return set_error(G4_ERR_UNSUPPORTED, "the split-K build runs the calibrated path only");
     GemvLaunch L{};
     L.count = 1;
     L.splits = split ? k_splits : 1;
@@ -801,16 +829,35 @@ static int gelu_gemv(int bits, const void *wq, const float *scales, const void *
     J.in_scale = in_scale;
     J.out_scale = split ? 0.0f : out_scale;
     J.act = gelu_act_of(act);
-    int rc = check_job(J, 1, who);
+    if (fold) {
+        J.act.fold_parts = fold->fold_parts;
+        J.act.fold_scales = fold->fold_scales;
+        J.act.fold_splits = fold->fold_splits;
+        J.act.fold_in = fold->fold_in;
+        J.act.fold_out = fold->fold_out;
+    }
+    int rc = check_job(J, cols, who);
     if (rc) return rc;
-    return launch_gemv(L, 1, as_stream(stream));
+    return launch_gemv(L, cols, as_stream(stream));
 }
 
 int g4_qgemv_gelu(int bits, const void *wq, const float *scales, const void *gate, int gate_kind,
                   const g4_gelu_act *act, void *dst, int out_kind, int k, int num_rows,
                   float in_scale, float out_scale, void *stream) {
-    return gelu_gemv(bits, wq, scales, gate, gate_kind, act, dst, out_kind, k, num_rows, 0, 0,
-                     in_scale, out_scale, stream);
+    char who[32];
+    snprintf(who, sizeof who, "qgemv-%dbit-gelu", bits);
+    return gelu_gemv(bits, wq, scales, gate, gate_kind, act, nullptr, dst, out_kind, k, num_rows,
+                     1, 0, 0, in_scale, out_scale, stream, who);
+}
+
+// qgemv-4bit-gelu-m2 / qgemv-8bit-gelu-m2 (qgemvWide.ts:660-669, 698-709; bindGemvWide :515-574).
+int g4_qgemv_gelu_m2(int bits, const void *wq, const float *scales, const void *gate, int gate_kind,
+                     const g4_gelu_act *act, void *dst, int out_kind, int k, int num_rows, int cols,
+                     float in_scale, float out_scale, void *stream) {
+    char who[32];
+    snprintf(who, sizeof who, "qgemv-%dbit-gelu-m2", bits);
+    return gelu_gemv(bits, wq, scales, gate, gate_kind, act, nullptr, dst, out_kind, k, num_rows,
+                     cols, 0, 0, in_scale, out_scale, stream, who);
 }
 
 int g4_qgemv_gelu_split(int bits, const void *wq, const float *scales, const void *gate,
@@ -818,8 +865,69 @@ int g4_qgemv_gelu_split(int bits, const void *wq, const float *scales, const voi
                         int num_rows, int k_splits, int exact, float in_scale, void *stream) {
     if (k_splits < 1)
         return set_error(G4_ERR_INVALID, "gemv geometry: kSplits must be 1, 2, 4 or 8, got %d", k_splits);
-    return gelu_gemv(bits, wq, scales, gate, gate_kind, act, partials, G4_KIND_F32, k, num_rows,
-                     k_splits, exact, in_scale, 0.0f, stream);
+    char who[40];
+    snprintf(who, sizeof who, "qgemv-%dbit-gelu%s", bits, exact ? "-exact-split" : "-split");
+    return gelu_gemv(bits, wq, scales, gate, gate_kind, act, nullptr, partials, G4_KIND_F32, k,
+                     num_rows, 1, k_splits, exact, in_scale, 0.0f, stream, who);
+}
+
+// pleSplit.ts:10-16: the split count the two PLE kernels run (pleGateSplits(), 1 runs as 2).
+static int ple_active_splits(int k_splits) { return k_splits == 1 ? 2 : k_splits; }
+
+// ple-gate-split (pleSplit.ts:17-23, bind :50-63).
+int g4_ple_gate_split(const void *wq, const float *scales, const void *x, int x_kind,
+                      float *partials, int k, int num_rows, int k_splits, float in_scale,
+                      void *stream) {
+    if (k_splits != 1 && k_splits != 2 && k_splits != 4 && k_splits != 8)
+        return set_error(G4_ERR_INVALID, "PLE splits must be 1, 2, 4 or 8");
+    if (num_rows % 4 != 0)
+        return set_error(G4_ERR_INVALID, "PLE split row count must be divisible by four");
+    if (!(in_scale > 0.0f)) return set_error(G4_ERR_INVALID, "PLE split needs calibrated input");
+    if (k <= 0 || num_rows <= 0)
+        return set_error(G4_ERR_INVALID, "ple-gate-split needs params.k and params.numRows");
+    if (k % 128 != 0)
+        return set_error(G4_ERR_INVALID, "qgemv-8bit needs K a multiple of 128, got %d", k);
+    if (k > kMaxGemvK)
+        return set_error(G4_ERR_INVALID, "exact split needs calibrated int8 input and K <= 16384");
+    GemvLaunch L{};
+    L.count = 1;
+    L.splits = ple_active_splits(k_splits);
+    L.split_exact = 1;
+    L.split_layout = 1;
+    GemvJob &J = L.job[0];
+    J.w = reinterpret_cast<const uint8_t *>(wq);
+    J.scales = scales;
+    J.x = x;
+    J.dst = partials;
+    J.bits = 8;
+    J.x_kind = x_kind;
+    J.out_kind = G4_KIND_F32;
+    J.k = k;
+    J.rows = num_rows;
+    J.in_scale = in_scale;
+    J.out_scale = 0.0f;
+    int rc = check_job(J, 1, "ple-gate-split");
+    if (rc) return rc;
+    return launch_gemv(L, 1, as_stream(stream));
+}
+
+// ple-fold-projection (pleSplit.ts:24-41, bind :64-84).
+int g4_ple_fold_projection(const void *wq, const float *scales, const float *gate_parts,
+                           const float *gate_scales, int k_splits, float gate_in_scale,
+                           float gate_out_scale, const g4_gelu_act *act, void *dst, int out_kind,
+                           int k, int num_rows, float in_scale, float out_scale, void *stream) {
+    if (k_splits != 1 && k_splits != 2 && k_splits != 4 && k_splits != 8)
+        return set_error(G4_ERR_INVALID, "PLE splits must be 1, 2, 4 or 8");
+    if (!gate_parts || !gate_scales)
+        return set_error(G4_ERR_INVALID, "ple-fold-projection needs inputs named gate, up and gateScales");
+    GeluAct fold;
+    fold.fold_parts = gate_parts;
+    fold.fold_scales = gate_scales;
+    fold.fold_splits = ple_active_splits(k_splits);
+    fold.fold_in = gate_in_scale;
+    fold.fold_out = gate_out_scale;
+    return gelu_gemv(8, wq, scales, gate_parts, G4_KIND_F32, act, &fold, dst, out_kind, k,
+                     num_rows, 1, 0, 0, in_scale, out_scale, stream, "ple-fold-projection");
 }
 
 static int merge_common(const float *partials, const float *scales, void *dst, int out_kind,

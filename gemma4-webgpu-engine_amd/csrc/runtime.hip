@@ -114,6 +114,26 @@ int g4_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream) {
     return G4_OK;
 }
 
+int g4_host_alloc(void **ptr, size_t bytes) {
+    if (!ptr) return set_error(G4_ERR_INVALID, "g4_host_alloc: ptr is NULL");
+    *ptr = nullptr;
+    if (bytes == 0) bytes = 1;
+    G4_HIP(hipHostMalloc(ptr, bytes, hipHostMallocDefault));
+    return G4_OK;
+}
+
+int g4_host_free(void *ptr) {
+    if (ptr) G4_HIP(hipHostFree(ptr));
+    return G4_OK;
+}
+
+int g4_memcpy_d2h_async(void *dst, const void *src, size_t bytes, void *stream) {
+    if (bytes == 0) return G4_OK;
+    if (!dst || !src) return set_error(G4_ERR_INVALID, "g4_memcpy_d2h_async: a NULL address");
+    G4_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream)));
+    return G4_OK;
+}
+
 int g4_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream) {
     if (bytes == 0) return G4_OK;
     if (!dst || !src) return set_error(G4_ERR_INVALID, "g4_memcpy_d2d: a NULL address");
@@ -197,6 +217,14 @@ int g4_graph_begin_capture(void *stream) {
     return G4_OK;
 }
 
+// The handle of a captured graph: the executable and an event recorded after each launch, so
+// destroy waits for this graph's own replays and nothing else on the device.
+struct G4Graph {
+    hipGraphExec_t exec = nullptr;
+    hipEvent_t done = nullptr;
+    bool launched = false;
+};
+
 int g4_graph_end_capture(void *stream, void **graph_exec) {
     if (!stream || !graph_exec) return set_error(G4_ERR_INVALID, "g4_graph_end_capture: NULL argument");
     hipGraph_t graph = nullptr;
@@ -205,21 +233,42 @@ int g4_graph_end_capture(void *stream, void **graph_exec) {
     hipError_t err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);
     if (err != hipSuccess) return hip_status(err, "hipGraphInstantiate");
-    *graph_exec = exec;
+    hipEvent_t done = nullptr;
+    err = hipEventCreateWithFlags(&done, hipEventDisableTiming);
+    if (err != hipSuccess) {
+        (void)hipGraphExecDestroy(exec);
+        return hip_status(err, "hipEventCreateWithFlags");
+    }
+    G4Graph *g = new G4Graph;
+    g->exec = exec;
+    g->done = done;
+    *graph_exec = g;
     return G4_OK;
 }
 
 int g4_graph_launch(void *graph_exec, void *stream) {
     if (!graph_exec) return set_error(G4_ERR_INVALID, "g4_graph_launch: no graph");
-    G4_HIP(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph_exec), as_stream(stream)));
+    G4Graph *g = static_cast<G4Graph *>(graph_exec);
+    G4_HIP(hipGraphLaunch(g->exec, as_stream(stream)));
+    G4_HIP(hipEventRecord(g->done, as_stream(stream)));
+    g->launched = true;
     return G4_OK;
 }
 
 int g4_graph_destroy(void *graph_exec) {
     if (!graph_exec) return G4_OK;
-    // the exec may still be running from its last launch (on any stream): finish it first
-    G4_HIP(hipDeviceSynchronize());
-    G4_HIP(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph_exec)));
+    G4Graph *g = static_cast<G4Graph *>(graph_exec);
+    // Replays are ordered on their streams, and each launch re-records `done` after it, so the
+    // event completes once the last launch (on whichever stream) has finished. Waiting on it
+    // touches no other stream (a capture in progress elsewhere stays valid). The graph and the
+    // event are released even when the wait reports an error.
+    hipError_t wait = g->launched ? hipEventSynchronize(g->done) : hipSuccess;
+    hipError_t d1 = hipGraphExecDestroy(g->exec);
+    hipError_t d2 = hipEventDestroy(g->done);
+    delete g;
+    if (wait != hipSuccess) return hip_status(wait, "g4_graph_destroy: waiting for the last launch");
+    if (d1 != hipSuccess) return hip_status(d1, "hipGraphExecDestroy");
+    if (d2 != hipSuccess) return hip_status(d2, "hipEventDestroy");
     return G4_OK;
 }
 

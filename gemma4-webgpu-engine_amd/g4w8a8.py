@@ -145,6 +145,9 @@ SIGNATURES = {
     "g4_event_elapsed_ms": (_c_int, [ctypes.POINTER(_c_float), _vp, _vp]),
     "g4_graph_begin_capture": (_c_int, [_vp]),
     "g4_graph_end_capture": (_c_int, [_vp, ctypes.POINTER(_vp)]),
+    "g4_host_alloc": (_c_int, [ctypes.POINTER(_vp), _sz]),
+    "g4_host_free": (_c_int, [_vp]),
+    "g4_memcpy_d2h_async": (_c_int, [_vp, _vp, _sz, _vp]),
     "g4_graph_launch": (_c_int, [_vp, _vp]),
     "g4_graph_destroy": (_c_int, [_vp]),
     "g4_qgemv": (_c_int, [_c_int, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
@@ -176,6 +179,13 @@ SIGNATURES = {
                                _c_int, _c_int, _c_float, _c_float, _vp]),
     "g4_qgemv_gelu_split": (_c_int, [_c_int, _vp, _vp, _vp, _c_int, ctypes.POINTER(GeluAct), _vp,
                                      _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
+    "g4_qgemv_gelu_m2": (_c_int, [_c_int, _vp, _vp, _vp, _c_int, ctypes.POINTER(GeluAct), _vp,
+                                  _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _vp]),
+    "g4_ple_gate_split": (_c_int, [_vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_float,
+                                   _vp]),
+    "g4_ple_fold_projection": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_float, _c_float,
+                                        ctypes.POINTER(GeluAct), _vp, _c_int, _c_int, _c_int,
+                                        _c_float, _c_float, _vp]),
     "g4_qgemv_plan_create_gelu": (_c_int, [ctypes.POINTER(GemvDesc), ctypes.POINTER(GeluAct),
                                            _c_int, ctypes.POINTER(_vp)]),
     "g4_srq_quantize": (_c_int, [_vp, _c_int, _vp, _i64, _c_float, _vp]),
@@ -202,6 +212,7 @@ SIGNATURES = {
     "g4_attention_workspace_bytes": (_sz, [_c_int, _c_int, _c_int, _c_int]),
     "g4_gelu_mul": (_c_int, [_vp, _c_float, _vp, _c_float, _vp, _i64, _c_int, _c_int, _c_float,
                              _vp, _vp]),
+    "g4_gelu_mul_f32": (_c_int, [_vp, _vp, _vp, _i64, _c_float, _vp]),
     "g4_embed_tokens": (_c_int, [_vp, _vp, _vp, _c_int, _i64, _c_int, _c_float, _c_float, _vp,
                                  _vp, _vp]),
     "g4_ple_combine": (_c_int, [_vp, _c_float, _c_float, _vp, _vp, _c_int, _c_int, _c_int,
@@ -542,6 +553,34 @@ def qgemv_gelu(bits, wq, scales, gate, act: GeluAct, dst, k, num_rows, in_scale,
                                float(in_scale), float(out_scale), stream))
 
 
+def qgemv_gelu_m2(bits, wq, scales, gate, act: GeluAct, dst, k, num_rows, cols, in_scale,
+                  out_scale, gate_kind=None, out_kind=None, stream=None):
+    """qgemv-4bit-gelu-m2 / qgemv-8bit-gelu-m2: the prologue over cols (1..2) token columns, gate
+    and up [cols][K], dst [cols][num_rows]."""
+    _check(lib().g4_qgemv_gelu_m2(bits, _ptr(wq), _ptr(scales), _ptr(gate),
+                                  gate.kind if gate_kind is None else gate_kind, ctypes.byref(act),
+                                  _ptr(dst), dst.kind if out_kind is None else out_kind, k,
+                                  num_rows, cols, float(in_scale), float(out_scale), stream))
+
+
+def ple_gate_split(wq, scales, x, partials, k, num_rows, k_splits, in_scale, stream=None):
+    """ple-gate-split: exact 8-bit split partials, row-interleaved for the fold (pleSplit.ts:17-23)."""
+    _check(lib().g4_ple_gate_split(_ptr(wq), _ptr(scales), _ptr(x), x.kind, _ptr(partials), k,
+                                   num_rows, k_splits, float(in_scale), stream))
+
+
+def ple_fold_projection(wq, scales, gate_parts, gate_scales, k_splits, gate_in_scale,
+                        gate_out_scale, act: GeluAct, dst, k, num_rows, in_scale, out_scale,
+                        out_kind=None, stream=None):
+    """ple-fold-projection: qgemv-8bit-gelu over the fold of ple-gate-split's partials
+    (pleSplit.ts:24-41)."""
+    _check(lib().g4_ple_fold_projection(_ptr(wq), _ptr(scales), _ptr(gate_parts),
+                                        _ptr(gate_scales), k_splits, float(gate_in_scale),
+                                        float(gate_out_scale), ctypes.byref(act), _ptr(dst),
+                                        dst.kind if out_kind is None else out_kind, k, num_rows,
+                                        float(in_scale), float(out_scale), stream))
+
+
 def qgemv_gelu_split(bits, wq, scales, gate, act: GeluAct, partials, k, num_rows, k_splits, exact,
                      in_scale, gate_kind=None, stream=None):
     """qgemv-4bit-gelu-exact-split (exact) or the scaled split over the gelu prologue's codes."""
@@ -549,6 +588,13 @@ def qgemv_gelu_split(bits, wq, scales, gate, act: GeluAct, partials, k, num_rows
                                      gate.kind if gate_kind is None else gate_kind,
                                      ctypes.byref(act), _ptr(partials), k, num_rows, k_splits,
                                      1 if exact else 0, float(in_scale), stream))
+
+
+def gelu_mul(gate, up, dst, count, srq_scale=0.0, stream=None):
+    """gelu-mul on f32 buffers (geluMul.ts:101-116): dst = gelu_tanh(gate) * up, snapped on
+    srq_scale when it is non-zero."""
+    _check(lib().g4_gelu_mul_f32(_ptr(gate), _ptr(up), _ptr(dst), int(count), float(srq_scale),
+                                 stream))
 
 
 def qgemv_split(bits, wq, scales, x, partials, k, num_rows, k_splits, exact, in_scale,
@@ -695,26 +741,79 @@ def _bind_exact_merge(inputs, output, params, stream=None):
                       _p(params, "outScale", 0.0), stream=stream)
 
 
-def _bind_gelu(bits, split):
-    """qgemv-4bit-gelu / qgemv-8bit-gelu and the gelu exact split: gate and up in place of x
-    (qgemv.ts:359-400, 1668-1696; exactSplit.ts:19-31). gate/up are f32 buffers (the reference's)
-    or int8 codes with params gateScale / upScale."""
-    who = f"qgemv-{bits}bit-gelu-exact-split" if split else f"qgemv-{bits}bit-gelu"
+def _up_offset(params) -> int:
+    """params.upOffset counts vec4s (qgemv.ts:398, execute.ts:886 layer * dim / 4); the C ABI
+    takes elements."""
+    return 4 * int(_p(params, "upOffset", 0))
+
+
+def _bind_gelu(bits, split, wide=False):
+    """qgemv-4bit-gelu / qgemv-8bit-gelu, their -m2 forms and the gelu exact split: gate and up in
+    place of x (qgemv.ts:359-400, 1668-1696; qgemvWide.ts:660-709; exactSplit.ts:19-31). gate/up
+    are f32 buffers (the reference's) or int8 codes with params gateScale / upScale."""
+    who = (f"qgemv-{bits}bit-gelu-exact-split" if split else
+           f"qgemv-{bits}bit-gelu-m2" if wide else f"qgemv-{bits}bit-gelu")
 
     def run(inputs, output, params, stream=None):
         _need(inputs, ["wq", "scales", "gate", "up"], who)
         act = gelu_act(inputs["up"], gate_scale=_p(params, "gateScale", 0.0),
-                       up_scale=_p(params, "upScale", 0.0), up_offset=int(_p(params, "upOffset", 0)))
+                       up_scale=_p(params, "upScale", 0.0), up_offset=_up_offset(params))
         if split:
             qgemv_gelu_split(bits, inputs["wq"], inputs["scales"], inputs["gate"], act, output,
                              int(_p(params, "k", 0)), int(_p(params, "numRows", 0)),
                              int(_p(params, "kSplits", 1)), True, _p(params, "inScale", 0.0),
                              stream=stream)
+        elif wide:
+            qgemv_gelu_m2(bits, inputs["wq"], inputs["scales"], inputs["gate"], act, output,
+                          int(_p(params, "k", 0)), int(_p(params, "numRows", 0)),
+                          int(_p(params, "cols", 0)), _p(params, "inScale", 0.0),
+                          _p(params, "outScale", 0.0), stream=stream)
         else:
             qgemv_gelu(bits, inputs["wq"], inputs["scales"], inputs["gate"], act, output,
                        int(_p(params, "k", 0)), int(_p(params, "numRows", 0)),
                        _p(params, "inScale", 0.0), _p(params, "outScale", 0.0), stream=stream)
     return run
+
+
+_ple_gate_splits = 1
+
+
+def set_ple_gate_splits(value: int):
+    """setPleGateSplits (pleSplit.ts:11-15): the split count both PLE split kernels run."""
+    global _ple_gate_splits
+    if value not in (1, 2, 4, 8):
+        raise G4Error(1, "PLE splits must be 1, 2, 4 or 8")
+    _ple_gate_splits = int(value)
+
+
+def ple_gate_splits() -> int:
+    return _ple_gate_splits
+
+
+def _bind_ple_gate_split(inputs, output, params, stream=None):
+    """ple-gate-split (pleSplit.ts:50-63): x in, exact partials out."""
+    _need(inputs, ["wq", "scales", "x"], "ple-gate-split")
+    ple_gate_split(inputs["wq"], inputs["scales"], inputs["x"], output, int(_p(params, "k", 0)),
+                   int(_p(params, "numRows", 0)), _ple_gate_splits, _p(params, "inScale", 0.0),
+                   stream=stream)
+
+
+def _bind_ple_fold(inputs, output, params, stream=None):
+    """ple-fold-projection (pleSplit.ts:64-84): gate (the partials), up, gateScales."""
+    _need(inputs, ["wq", "scales", "gate", "up", "gateScales"], "ple-fold-projection")
+    act = gelu_act(inputs["up"], up_scale=_p(params, "upScale", 0.0), up_offset=_up_offset(params))
+    ple_fold_projection(inputs["wq"], inputs["scales"], inputs["gate"], inputs["gateScales"],
+                        _ple_gate_splits, _p(params, "gateInScale", 0.0),
+                        _p(params, "gateOutScale", 0.0), act, output, int(_p(params, "k", 0)),
+                        int(_p(params, "numRows", 0)), _p(params, "inScale", 0.0),
+                        _p(params, "outScale", 0.0), stream=stream)
+
+
+def _bind_gelu_mul(inputs, output, params, stream=None):
+    """gelu-mul (geluMul.ts:250-278): gate and up, params count and srqScale."""
+    _need(inputs, ["gate", "up"], "gelu-mul")
+    gelu_mul(inputs["gate"], inputs["up"], output, int(_p(params, "count", 0)),
+             _p(params, "srqScale", 0.0), stream=stream)
 
 
 PLE_COLS, PLE_GROUP_SIZE = 8960, 256  # PLE_ROW_VALUES and PLE_GROUP_SIZE (quant.ts:35-37)
@@ -752,7 +851,12 @@ KERNELS = {
     "gate-up-batch-4bit": _bind_batch(2),
     "qgemv-4bit-gelu": _bind_gelu(4, False),
     "qgemv-8bit-gelu": _bind_gelu(8, False),
+    "qgemv-4bit-gelu-m2": _bind_gelu(4, False, True),
+    "qgemv-8bit-gelu-m2": _bind_gelu(8, False, True),
     "qgemv-4bit-gelu-exact-split": _bind_gelu(4, True),
+    "gelu-mul": _bind_gelu_mul,
+    "ple-gate-split": _bind_ple_gate_split,
+    "ple-fold-projection": _bind_ple_fold,
     "qgemv-4bit-split": _bind_split(4),
     "qgemv-8bit-split": _bind_split(8),
     "qgemv-merge": _bind_merge,

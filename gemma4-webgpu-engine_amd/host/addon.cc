@@ -391,6 +391,50 @@ napi_value QgemvGeluSplit(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// qgemv-4bit-gelu-m2 / qgemv-8bit-gelu-m2: (bits, wq, scales, gate, gateKind, up, upKind,
+// upOffset, dst, outKind, k, numRows, cols, inScale, outScale[, gateScale, upScale, stream])
+napi_value QgemvGeluM2(napi_env env, napi_callback_info info) {
+    Args a(env, info, 18);
+    g4_gelu_act act{a.ptr(5), a.i32(6), (float)a.num(15), (float)a.num(16), (int64_t)a.num(7)};
+    int st = g4_qgemv_gelu_m2(a.i32(0), a.ptr(1), (const float *)a.ptr(2), a.ptr(3), a.i32(4), &act,
+                              a.ptr(8), a.i32(9), a.i32(10), a.i32(11), a.i32(12),
+                              (float)a.num(13), (float)a.num(14), a.ptr(17));
+    if (throw_status(env, st)) return nullptr;
+    return undefined(env);
+}
+
+// ple-gate-split: (wq, scales, x, xKind, partials, k, numRows, kSplits, inScale[, stream])
+napi_value PleGateSplit(napi_env env, napi_callback_info info) {
+    Args a(env, info, 10);
+    int st = g4_ple_gate_split(a.ptr(0), (const float *)a.ptr(1), a.ptr(2), a.i32(3),
+                               (float *)a.ptr(4), a.i32(5), a.i32(6), a.i32(7), (float)a.num(8),
+                               a.ptr(9));
+    if (throw_status(env, st)) return nullptr;
+    return undefined(env);
+}
+
+// ple-fold-projection: (wq, scales, gateParts, gateScales, kSplits, gateInScale, gateOutScale,
+// up, upKind, upOffset, dst, outKind, k, numRows, inScale, outScale[, upScale, stream])
+napi_value PleFoldProjection(napi_env env, napi_callback_info info) {
+    Args a(env, info, 18);
+    g4_gelu_act act{a.ptr(7), a.i32(8), 0.0f, (float)a.num(16), (int64_t)a.num(9)};
+    int st = g4_ple_fold_projection(a.ptr(0), (const float *)a.ptr(1), (const float *)a.ptr(2),
+                                    (const float *)a.ptr(3), a.i32(4), (float)a.num(5),
+                                    (float)a.num(6), &act, a.ptr(10), a.i32(11), a.i32(12),
+                                    a.i32(13), (float)a.num(14), (float)a.num(15), a.ptr(17));
+    if (throw_status(env, st)) return nullptr;
+    return undefined(env);
+}
+
+// gelu-mul: (gate, up, dst, count, srqScale[, stream])
+napi_value GeluMulF32(napi_env env, napi_callback_info info) {
+    Args a(env, info, 6);
+    int st = g4_gelu_mul_f32((const float *)a.ptr(0), (const float *)a.ptr(1), (float *)a.ptr(2),
+                             (int64_t)a.num(3), (float)a.num(4), a.ptr(5));
+    if (throw_status(env, st)) return nullptr;
+    return undefined(env);
+}
+
 napi_value QgemvMerge(napi_env env, napi_callback_info info) {
     Args a(env, info, 7);
     int st = g4_qgemv_merge((const float *)a.ptr(0), a.ptr(1), a.i32(2), a.i32(3), a.i32(4),
@@ -621,18 +665,30 @@ struct AsyncWait {
     napi_async_work work = nullptr;
     napi_deferred deferred = nullptr;
     napi_ref buffer = nullptr;  // the ArrayBuffer a download fills (null: a plain synchronize)
-    void *host = nullptr;
-    const void *device = nullptr;
+    void *host = nullptr;       // the ArrayBuffer's bytes
+    void *staging = nullptr;    // pinned host memory the copy lands in (a download)
+    void *done = nullptr;       // event recorded behind the copy (a download)
     size_t bytes = 0;
     void *stream = nullptr;
     int status = G4_OK;
     std::string message;
+
+    ~AsyncWait() {
+        if (done) g4_event_destroy(done);
+        if (staging) g4_host_free(staging);
+    }
 };
 
+// The worker: a download waits for its copy's event, then moves the pinned bytes into the
+// ArrayBuffer; a synchronize waits for the stream.
 void async_execute(napi_env, void *data) {
     AsyncWait *w = static_cast<AsyncWait *>(data);
-    w->status = w->buffer ? g4_memcpy_d2h(w->host, w->device, w->bytes, w->stream)
-                          : g4_stream_synchronize(w->stream);
+    if (w->buffer) {
+        w->status = g4_event_synchronize(w->done);
+        if (w->status == G4_OK && w->bytes) memcpy(w->host, w->staging, w->bytes);
+    } else {
+        w->status = g4_stream_synchronize(w->stream);
+    }
     if (w->status != G4_OK) w->message = g4_last_error();
 }
 
@@ -674,14 +730,26 @@ napi_value SynchronizeAsync(napi_env env, napi_callback_info info) {
     return queue_wait(env, w);
 }
 
-// downloadAsync(ptr, bytes, stream?) -> Promise<ArrayBuffer>: the copy is ordered after the work
-// already enqueued on the stream.
+// downloadAsync(ptr, bytes, stream?) -> Promise<ArrayBuffer>: the device-to-host copy is enqueued
+// here, on the calling thread, into pinned staging memory, with an event behind it. So it is
+// ordered after the work already enqueued on the stream and before anything the caller enqueues
+// next (a later step rewriting the same buffer cannot overtake it); the worker only waits for the
+// event and copies the staged bytes into the ArrayBuffer.
 napi_value DownloadAsync(napi_env env, napi_callback_info info) {
     Args a(env, info, 3);
     AsyncWait *w = new AsyncWait();
-    w->device = a.ptr(0);
+    const void *device = a.ptr(0);
     w->bytes = (size_t)a.num(1);
     w->stream = a.ptr(2);
+    int st = g4_host_alloc(&w->staging, w->bytes);
+    if (st == G4_OK) st = g4_memcpy_d2h_async(w->staging, device, w->bytes, w->stream);
+    if (st == G4_OK) st = g4_event_create(&w->done);
+    if (st == G4_OK) st = g4_event_record(w->done, w->stream);
+    if (st != G4_OK) {
+        throw_status(env, st);  // reads the message before the cleanup below runs
+        delete w;
+        return nullptr;
+    }
     napi_value ab;
     napi_create_arraybuffer(env, w->bytes, &w->host, &ab);
     napi_create_reference(env, ab, 1, &w->buffer);
@@ -917,6 +985,8 @@ napi_value Init(napi_env env, napi_value exports) {
         {"projectionBatch", ProjectionBatch}, {"qgemvGrouped", QgemvGrouped},
         {"qgemvSplit", QgemvSplit}, {"qgemvMerge", QgemvMerge},
         {"qgemvGelu", QgemvGelu}, {"qgemvGeluSplit", QgemvGeluSplit},
+        {"qgemvGeluM2", QgemvGeluM2}, {"pleGateSplit", PleGateSplit},
+        {"pleFoldProjection", PleFoldProjection}, {"geluMulF32", GeluMulF32},
         {"qgemvExactMerge", QgemvExactMerge}, {"srqQuantize", SrqQuantize},
         {"pleGather", PleGather}, {"pleGatherSplit", PleGatherSplit},
         {"planTableSplit", PlanTableSplit}, {"qgemvPlanCreate", QgemvPlanCreate},

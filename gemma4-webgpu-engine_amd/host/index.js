@@ -163,23 +163,66 @@ function splitKernel(bits) {
   };
 }
 
-// qgemv-4bit-gelu / qgemv-8bit-gelu (qgemv.ts:1668-1696) and the gelu exact split (exactSplit.ts:
-// 19-31): gate and up bound in place of x, upOffset selecting the per-layer row.
-function geluKernel(bits, split) {
-  const who = split ? `qgemv-${bits}bit-gelu-exact-split` : `qgemv-${bits}bit-gelu`;
+// qgemv-4bit-gelu / qgemv-8bit-gelu (qgemv.ts:1668-1696), their -m2 forms (qgemvWide.ts:660-709)
+// and the gelu exact split (exactSplit.ts:19-31): gate and up bound in place of x. params.upOffset
+// counts vec4s, as the reference's (qgemv.ts:398, execute.ts:886 layer * dim / 4); the addon takes
+// elements.
+function geluKernel(bits, split, wide) {
+  const who = split ? `qgemv-${bits}bit-gelu-exact-split` : `qgemv-${bits}bit-gelu${wide ? '-m2' : ''}`;
   return ({ inputs, output, params, stream }) => {
     need(inputs, ['wq', 'scales', 'gate', 'up'], who);
     const head = [bits, inputs.wq.addr, inputs.scales.addr, inputs.gate.addr, inputs.gate.kind,
-      inputs.up.addr, inputs.up.kind, num(params, 'upOffset', 0), output.addr];
+      inputs.up.addr, inputs.up.kind, 4 * num(params, 'upOffset', 0), output.addr];
     const scales = [num(params, 'gateScale', 0), num(params, 'upScale', 0)];
     if (split) {
       g4().qgemvGeluSplit(...head, num(params, 'k', 0), num(params, 'numRows', 0),
         num(params, 'kSplits', 1), 1, num(params, 'inScale', 0), ...scales, streamHandle(stream));
+    } else if (wide) {
+      g4().qgemvGeluM2(...head, output.kind, num(params, 'k', 0), num(params, 'numRows', 0),
+        num(params, 'cols', 0), num(params, 'inScale', 0), num(params, 'outScale', 0), ...scales,
+        streamHandle(stream));
     } else {
       g4().qgemvGelu(...head, output.kind, num(params, 'k', 0), num(params, 'numRows', 0),
         num(params, 'inScale', 0), num(params, 'outScale', 0), ...scales, streamHandle(stream));
     }
   };
+}
+
+// pleGateSplits / setPleGateSplits (pleSplit.ts:10-15): the split count both PLE split kernels run,
+// a module setting as in the reference (a device profile sets it); 1 runs as 2 (pleSplit.ts:16).
+let pleSplits = 1;
+function pleGateSplits() { return pleSplits; }
+function setPleGateSplits(value) {
+  if (![1, 2, 4, 8].includes(value)) throw new Error('PLE splits must be 1, 2, 4 or 8');
+  pleSplits = value;
+}
+function pleActiveSplits() { return pleSplits === 1 ? 2 : pleSplits; }
+
+// ple-gate-split (pleSplit.ts:50-63): exact 8-bit split partials, row-interleaved for the fold.
+function pleGateSplitKernel({ inputs, output, params, stream }) {
+  need(inputs, ['wq', 'scales', 'x'], 'ple-gate-split');
+  g4().pleGateSplit(inputs.wq.addr, inputs.scales.addr, inputs.x.addr, inputs.x.kind, output.addr,
+    num(params, 'k', 0), num(params, 'numRows', 0), pleSplits, num(params, 'inScale', 0),
+    streamHandle(stream));
+}
+
+// ple-fold-projection (pleSplit.ts:64-84): gate (the partials), up, gateScales; gateInScale and
+// gateOutScale are the gate linear's own scales.
+function pleFoldProjectionKernel({ inputs, output, params, stream }) {
+  need(inputs, ['wq', 'scales', 'gate', 'up', 'gateScales'], 'ple-fold-projection');
+  g4().pleFoldProjection(inputs.wq.addr, inputs.scales.addr, inputs.gate.addr,
+    inputs.gateScales.addr, pleSplits, num(params, 'gateInScale', 0),
+    num(params, 'gateOutScale', 0), inputs.up.addr, inputs.up.kind, 4 * num(params, 'upOffset', 0),
+    output.addr, output.kind, num(params, 'k', 0), num(params, 'numRows', 0),
+    num(params, 'inScale', 0), num(params, 'outScale', 0), num(params, 'upScale', 0),
+    streamHandle(stream));
+}
+
+// gelu-mul (geluMul.ts:250-278): the prefill chunk's separate pass over f32 gate and up.
+function geluMulKernel({ inputs, output, params, stream }) {
+  need(inputs, ['gate', 'up'], 'gelu-mul');
+  g4().geluMulF32(inputs.gate.addr, inputs.up.addr, output.addr, num(params, 'count', 0),
+    num(params, 'srqScale', 0), streamHandle(stream));
 }
 
 const PLE_COLS = 8960; // PLE_ROW_VALUES (quant.ts:35-37)
@@ -220,7 +263,12 @@ const BINDS = {
   'gate-up-batch-4bit': batchKernel(2),
   'qgemv-4bit-gelu': geluKernel(4, false),
   'qgemv-8bit-gelu': geluKernel(8, false),
+  'qgemv-4bit-gelu-m2': geluKernel(4, false, true),
+  'qgemv-8bit-gelu-m2': geluKernel(8, false, true),
   'qgemv-4bit-gelu-exact-split': geluKernel(4, true),
+  'gelu-mul': geluMulKernel,
+  'ple-gate-split': pleGateSplitKernel,
+  'ple-fold-projection': pleFoldProjectionKernel,
   'qgemv-4bit-split': splitKernel(4),
   'qgemv-8bit-split': splitKernel(8),
   'qgemv-merge': ({ inputs, output, params, stream }) => {
@@ -445,6 +493,115 @@ function geluCases(bits, split) {
     expected: gridExpected(geluOp, rows, k, 1, inScale, 0.0625, KIND.i8) }];
 }
 
+/** gelu-mul on the saturated grid (gelu exact at 0 and |g| >= 6), with and without the snap. */
+function geluMulCases() {
+  const count = 64;
+  const next = rng(83);
+  const gate = new Float32Array(count).map(() => [-8, -6, 0, 6, 8][randInt(next, 0, 4)]);
+  const up = new Float32Array(count).map(() => randInt(next, -24, 24) / 16);
+  // gelu(g) in f32 on this grid: g for g >= 6, +0 at 0, and 0.5 * g * (1 - 1) = -0 for g <= -6
+  const gelu = g => (g > 0 ? g : (g < 0 ? -0 : 0));
+  const v = new Float32Array(count).map((_, i) => gelu(gate[i]) * up[i]);
+  return [0, 0.125].map(srqScale => ({
+    name: `saturated-gelu-mul-srq-${srqScale}`, inputs: { gate, up }, params: { count, srqScale },
+    expected: srqScale === 0 ? v : v.map(x => snap(x, srqScale) * srqScale),
+    note: 'geluMul.ts:101-116 with the consumer snap; exact on this grid',
+  }));
+}
+
+/** The -m2 gelu forms: every column on the saturated-gelu grid, calibrated and uncalibrated. */
+function geluWideCases(bits) {
+  const rows = 10;
+  const k = bits === 4 ? 512 : 256;
+  const cols = 2;
+  const op = gridOperands(84 + bits, bits, rows, k, cols);
+  const next = rng(85 + bits);
+  const gate = new Float32Array(cols * k).map(() => [-8, -6, 0, 6, 8][randInt(next, 0, 4)]);
+  const up = new Float32Array(cols * k).map(() => randInt(next, -8, 8) / 8);
+  const act = new Float32Array(cols * k).map((_, i) => (gate[i] > 0 ? gate[i] : 0) * up[i]);
+  const geluOp = { codes: op.codes, scales: op.scales, x: act };
+  const inputs = { wq: op.wq, scales: op.scales, gate, up };
+  return [
+    { name: 'saturated-gelu-m2-srq', inputs, params: { k, numRows: rows, cols, inScale: 0.125, outScale: 0.0625 },
+      expected: gridExpected(geluOp, rows, k, cols, 0.125, 0.0625, KIND.i8),
+      note: 'qgemvWide.ts:20-27: column for column the one-column gelu GEMV' },
+    { name: 'saturated-gelu-m2-uncalibrated', inputs, params: { k, numRows: rows, cols },
+      expected: gridExpected(geluOp, rows, k, cols, 0, 0, KIND.f32),
+      note: 'the f32 path over the unsnapped product, exact on the grid' },
+  ];
+}
+
+/** ple-gate-split: integer partials of each split band, interleaved (row/4)*4n + s*4 + row%4. */
+function pleGateSplitCases() {
+  const rows = 8;
+  const k = 512;
+  const n = pleActiveSplits();
+  const op = gridOperands(91, 8, rows, k, 1);
+  const inScale = 0.125;
+  const bands = splitBands(8, k, n, true);
+  const part = new Float32Array(rows * n);
+  for (let r = 0; r < rows; ++r) {
+    bands.forEach(([lo, hi], sp) => {
+      let sum = 0;
+      for (let i = lo; i < hi; ++i) sum += op.codes[r * k + i] * snap(op.x[i], inScale);
+      part[Math.floor(r / 4) * 4 * n + sp * 4 + (r % 4)] = sum;
+    });
+  }
+  return [{ name: `grid-raw-partials-${n}`, inputs: { wq: op.wq, scales: op.scales, x: op.x },
+    params: { k, numRows: rows, inScale }, expected: part,
+    note: 'pleSplit.ts:17-23: the exact partials in the fold\'s vec4 layout' }];
+}
+
+/**
+ * ple-fold-projection: integer partials whose folded gate is 0 or at least 6 in magnitude (gelu is
+ * then exact in f32: tanh saturates under the 10 clamp), at gateInScale 0.125 and gateScales 0.5
+ * (v = total / 16 exactly), with gateOutScale 0 and 0.125 (the reference's two cases,
+ * pleSplit.ts:66-71); odd totals land the gate snap on ties. The up row is read at upOffset.
+ */
+function pleFoldCases() {
+  const rows = 10;
+  const k = 256;
+  const n = pleActiveSplits();
+  const op = gridOperands(93, 8, rows, k, 1);
+  const next = rng(94);
+  const totals = new Float32Array(k).map(() => {
+    const c = randInt(next, 0, 2);
+    return c === 0 ? 0 : (c === 1 ? 1 : -1) * randInt(next, 96, 250);
+  });
+  const part = new Float32Array(k * n);
+  for (let i = 0; i < k; ++i) {
+    const base = Math.floor(i / 4) * 4 * n + (i % 4);
+    let rest = totals[i];
+    for (let sp = 0; sp < n - 1; ++sp) {
+      const piece = randInt(next, -20, 20);
+      part[base + sp * 4] = piece;
+      rest -= piece;
+    }
+    part[base + (n - 1) * 4] = rest;
+  }
+  const gateScales = new Float32Array(k).fill(0.5);
+  const layerRow = 3;
+  const upAll = new Float32Array(5 * k).map(() => randInt(next, -8, 8) / 8);
+  const out = [];
+  for (const gateOutScale of [0, 0.125]) {
+    const act = new Float32Array(k).map((_, i) => {
+      let v = totals[i] / 16;
+      if (gateOutScale !== 0) v = snap(v, gateOutScale) * gateOutScale;
+      const g = v >= 6 ? v : 0;  // gelu at |v| >= 6 and at 0, exact in f32
+      return g * upAll[layerRow * k + i];
+    });
+    out.push({
+      name: `grid-fold-${n}-gate-srq-${gateOutScale}`,
+      inputs: { wq: op.wq, scales: op.scales, gate: part, up: upAll, gateScales },
+      params: { k, numRows: rows, inScale: 0.125, outScale: 0.0625, upOffset: layerRow * k / 4,
+        gateInScale: 0.125, gateOutScale },
+      expected: gridExpected({ codes: op.codes, scales: op.scales, x: act }, rows, k, 1, 0.125, 0.0625, KIND.i8),
+      note: 'pleSplit.ts:33-41 foldGate, then the qgemv-8bit-gelu prologue',
+    });
+  }
+  return out;
+}
+
 function gatherCase(sliced) {
   const rows = 48;
   const cols = 512;
@@ -472,7 +629,16 @@ function gatherCase(sliced) {
     note: 'embedGather.ts:149-152, 188-196: (code - 8) * f32(16 * scale), a non-owner writes nothing' }];
 }
 
-function registered(name, bind, cases, note) { return { name, bind, cases, note }; }
+// The PLE split kernels' cases depend on the active split count (pleSplit.ts:43-49, 65-71 build
+// them in getters for the same reason), so those two entries compute theirs when read.
+const LIVE_CASES = {
+  'ple-gate-split': pleGateSplitCases,
+  'ple-fold-projection': pleFoldCases,
+};
+function registered(name, bind, cases, note) {
+  if (cases !== null) return { name, bind, cases, note };
+  return { name, bind, note, get cases() { return LIVE_CASES[name](); } };
+}
 
 const KERNELS = {
   'qgemv-4bit': registered('qgemv-4bit', BINDS['qgemv-4bit'], linearCases(4, null, 1)),
@@ -487,8 +653,13 @@ const KERNELS = {
   'gate-up-batch-4bit': registered('gate-up-batch-4bit', BINDS['gate-up-batch-4bit'], batchCases(2)),
   'qgemv-4bit-gelu': registered('qgemv-4bit-gelu', BINDS['qgemv-4bit-gelu'], geluCases(4, false)),
   'qgemv-8bit-gelu': registered('qgemv-8bit-gelu', BINDS['qgemv-8bit-gelu'], geluCases(8, false)),
+  'qgemv-4bit-gelu-m2': registered('qgemv-4bit-gelu-m2', BINDS['qgemv-4bit-gelu-m2'], geluWideCases(4)),
+  'qgemv-8bit-gelu-m2': registered('qgemv-8bit-gelu-m2', BINDS['qgemv-8bit-gelu-m2'], geluWideCases(8)),
   'qgemv-4bit-gelu-exact-split': registered('qgemv-4bit-gelu-exact-split',
     BINDS['qgemv-4bit-gelu-exact-split'], geluCases(4, true)),
+  'gelu-mul': registered('gelu-mul', BINDS['gelu-mul'], geluMulCases()),
+  'ple-gate-split': registered('ple-gate-split', BINDS['ple-gate-split'], null),
+  'ple-fold-projection': registered('ple-fold-projection', BINDS['ple-fold-projection'], null),
   'qgemv-4bit-split': registered('qgemv-4bit-split', BINDS['qgemv-4bit-split'], [splitCase(4, false), splitCase(4, true)]),
   'qgemv-8bit-split': registered('qgemv-8bit-split', BINDS['qgemv-8bit-split'], [splitCase(8, false), splitCase(8, true)]),
   'qgemv-merge': registered('qgemv-merge', BINDS['qgemv-merge'], mergeCases(false)),
@@ -595,6 +766,128 @@ function matmulKernel(geometry, stepKernel) {
   return gemvWide(geometry, stepKernel);
 }
 
+// ---- the plan's projection steps (plan.ts:487-665, 725-753, 775-785) -----------------------------
+//
+// The kernel names planLayer / planEmbed / planHead give the steps of the projection path, for the
+// families this build serves (4-bit attention, MLP and head; the 8-bit PLE linears), and
+// resolveStep's choice among them (execute.ts:566-600, 721-726, 765-895, 956-968). A caller can
+// check that every name a plan under its options binds is registered here.
+
+const PLAN_GEMV = { 4: 'qgemv-4bit', 8: 'qmatmul-8bit' };                 // plan.ts:369
+const PLAN_GEMM = { 4: 'qgemm-4bit', 8: 'qmatmul-8bit' };                 // plan.ts:370
+const PLAN_GEMV_GELU = { 4: 'qgemv-4bit-gelu', 8: 'qgemv-8bit-gelu' };    // plan.ts:433
+
+/** planLayer's projection steps for one layer (plan.ts:487-640): {kernel, role, kSplits?}. */
+function planLayerProjections(producer, mode, options) {
+  const o = options || {};
+  const mm = mode === 'gemv' ? PLAN_GEMV : PLAN_GEMM;
+  const steps = [];
+  const push = (kernel, role, extra) => steps.push(Object.assign({ kernel, role }, extra || {}));
+  const fusedPrologue = mode === 'gemv' && o.attentionPrologue !== false;
+  const attnSplit = fusedPrologue && (o.attnKSplits || 1) > 1;
+  const proj = attnSplit ? 'qgemv-4bit-split' : mm[4];
+  if (mode === 'gemv' && o.batchProjections && producer && !attnSplit) {
+    push('qkv-batch-4bit', 'q_proj, k_proj, v_proj');
+  } else {
+    push(proj, 'q_proj');
+    if (producer) {
+      push(proj, 'k_proj');
+      push(proj, 'v_proj');
+    }
+  }
+  push(mm[4], 'o_proj');
+  if (mode === 'gemv' && o.batchProjections) {
+    push('gate-up-batch-4bit', 'gate_proj, up_proj');
+  } else {
+    push(mm[4], 'gate_proj');
+    push(mm[4], 'up_proj');
+  }
+  if (mode === 'gemv') {
+    if ((o.producerDownKSplits || 1) > 1) {
+      push('qgemv-4bit-gelu-exact-split', 'producer down exact partials');
+      push('qgemv-exact-merge', 'producer down exact fold', { kSplits: o.producerDownKSplits });
+    } else {
+      push(PLAN_GEMV_GELU[4], 'gelu down');
+    }
+  } else {
+    push('gelu-mul', 'gelu times up');
+    push(mm[4], 'down_proj');
+  }
+  const pleSplit = mode === 'gemv' && (o.pleGateKSplits || 1) > 1;
+  push(pleSplit ? 'ple-gate-split' : mm[8], 'per_layer_input_gate');
+  if (mode === 'gemv') {
+    push(pleSplit ? 'ple-fold-projection' : PLAN_GEMV_GELU[8], 'gelu ple');
+  } else {
+    push('gelu-mul', 'gate times per layer row');
+    push(mm[8], 'per_layer_projection');
+  }
+  return steps;
+}
+
+/** resolveStep's registry name for a projection step (execute.ts:566-895, 956-968); throws where it does. */
+function resolveProjectionKernel(step, geometry) {
+  const tokens = geometry.tokens;
+  switch (step.role) {
+    case 'q_proj, k_proj, v_proj':
+    case 'gate_proj, up_proj':
+      if (tokens !== 1) throw new Error('batched projections require a single token');
+      return step.kernel;
+    case 'q_proj':
+    case 'k_proj':
+    case 'v_proj': {
+      const wide = geometry.mode === 'gemv' && tokens !== 1;  // attnUnsplitOnWide, execute.ts:396-403
+      return matmulKernel(geometry, wide && step.kernel === 'qgemv-4bit-split' ? 'qgemv-4bit' : step.kernel);
+    }
+    case 'o_proj':
+    case 'gate_proj':
+    case 'up_proj':
+    case 'down_proj':
+      return matmulKernel(geometry, step.kernel);
+    case 'producer down exact partials':
+      if (tokens !== 1) throw new Error('producer split needs one token');
+      return step.kernel;
+    case 'producer down exact fold':
+      return step.kernel;
+    case 'gelu down':
+      return gemvWide(geometry, step.kernel);
+    case 'per_layer_input_gate':
+    case 'per_layer_projection':
+      return pleKernel(geometry, step.kernel);
+    case 'gelu ple':
+      if (step.kernel === 'ple-fold-projection') {
+        if (tokens !== 1) throw new Error('PLE split needs one token');
+        return step.kernel;
+      }
+      return gemvWide(geometry, step.kernel);
+    case 'gelu times up':
+    case 'gate times per layer row':
+      return step.kernel;  // gelu-mul: the elementwise pass (g4_gelu_mul), not a projection
+    case 'lm_head':
+      return gemvWide(geometry, step.kernel);
+    default:
+      throw new Error(`gemma4 engine: no projection step with role ${step.role}`);
+  }
+}
+
+/**
+ * Every registry name one decode step (mode 'gemv') or prefill chunk ('gemm') binds on the
+ * projection path under `options` (PlanOptions: batchProjections, producerDownKSplits,
+ * pleGateKSplits, attnKSplits, attentionPrologue): the per-layer linears of producer and consumer
+ * layers, the PLE gather (one sliced step per slice when `pleSlices` > 1, plan.ts:775-785) and
+ * the head (plan.ts:745-753). Throws what resolveStep throws for an unservable combination.
+ */
+function planProjectionKernels(geometry, options, pleSlices) {
+  const names = new Set();
+  for (const producer of [true, false]) {
+    for (const step of planLayerProjections(producer, geometry.mode, options)) {
+      names.add(resolveProjectionKernel(step, geometry));
+    }
+  }
+  names.add((pleSlices || 1) > 1 ? 'ple-gather-4bit-sliced' : 'ple-gather-4bit');
+  if (geometry.mode === 'gemv') names.add(resolveProjectionKernel({ kernel: PLAN_GEMV[4], role: 'lm_head' }, geometry));
+  return [...names];
+}
+
 // ---- the split planner (tableSplit.ts) ----------------------------------------------------------
 
 /** planTableSplit (tableSplit.ts:125-215), computed by the library (pure host code). */
@@ -692,6 +985,11 @@ module.exports = {
   gemvWide,
   pleKernel,
   matmulKernel,
+  planLayerProjections,
+  resolveProjectionKernel,
+  planProjectionKernels,
+  pleGateSplits,
+  setPleGateSplits,
   planTableSplit,
   sliceForRow,
   slicedGatherDispatches,

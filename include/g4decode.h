@@ -85,6 +85,15 @@ int g4_gelu_mul(const int8_t *g_codes, float g_scale, const int8_t *u_codes, flo
                 int8_t *codes, void *stream);
 
 /*
+ * gelu-mul on the reference's f32 buffers (src/kernels/geluMul.ts:101-116, bind :250-278): dst[i] =
+ * gelu_tanh(gate[i]) * up[i], then clamp(RNE(v / srq_scale), -128, 127) * srq_scale when srq_scale
+ * != 0 (the consuming linear's input scale; 0 = uncalibrated, no rounding). count must be a
+ * positive multiple of 4 (:253-255); the buffers 16-byte aligned.
+ */
+int g4_gelu_mul_f32(const float *gate, const float *up, float *dst, int64_t count,
+                    float srq_scale, void *stream);
+
+/*
  * The token embedding of a tied int4 table (embed-gather, src/kernels/embedGather.ts:93-113 and
  * :176-261 with the embed scale folded into the row scale once): x[r] = (code - 8) *
  * f32(row_scales[id] * embed_scale) over `cols` codes of row ids[r] (two per byte, low nibble

@@ -64,6 +64,13 @@ int g4_free(void *ptr);
 int g4_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream);
 int g4_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream);
 int g4_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream);
+/* Pinned host memory (hipHostMalloc), the staging side of an asynchronous readback: the
+ * reference's MAP_READ staging buffers and mapAsync (src/runtime.ts:866-878). */
+int g4_host_alloc(void **ptr, size_t bytes);
+int g4_host_free(void *ptr);
+/* A device-to-host copy enqueued on `stream` without waiting (g4_memcpy_d2h waits): dst must be
+ * g4_host_alloc memory, read only after an event recorded behind the copy has completed. */
+int g4_memcpy_d2h_async(void *dst, const void *src, size_t bytes, void *stream);
 /* Byte fill through a kernel (safe under graph capture). */
 int g4_fill_u8(void *dst, uint8_t value, size_t bytes, void *stream);
 int g4_stream_create(void **stream);
@@ -84,7 +91,10 @@ int g4_event_elapsed_ms(float *ms, void *start, void *end);
  * the capture starts (run the same shape once on the stream first); a call that would grow it
  * inside a capture is refused with G4_ERR_INVALID. A workspace whose address a capture took is never
  * freed (a graph may be replayed later, on any stream); g4_stream_destroy frees the stream's
- * workspace otherwise. g4_graph_destroy waits for the device before it destroys the graph. */
+ * workspace otherwise. g4_graph_destroy waits for the graph's own last launch (an event recorded
+ * after each g4_graph_launch, on the stream it was launched on), not for the whole device, and
+ * releases the graph even when that wait fails. Launches of one graph on several streams must be
+ * ordered by the caller (the event marks the most recent launch). */
 int g4_graph_begin_capture(void *stream);
 int g4_graph_end_capture(void *stream, void **graph_exec);
 int g4_graph_launch(void *graph_exec, void *stream);
@@ -219,15 +229,17 @@ int g4_qgemv_exact_merge(const float *partials, const float *scales, void *dst, 
  * (geluMul.ts:101-116), snapped on inScale. The gate is passed where x goes (f32, the reference's
  * gate output, or int8 codes times gate_scale); `up` is f32 or int8 codes times up_scale. On a
  * calibrated site the result is bit for bit the unfused gelu-mul + GEMV chain (qgemv.ts:362-368).
- * Calibrated (inScale != 0), single column only. f32 operands need 16-byte alignment (after the
- * offset), int8 codes 8-byte.
+ * An uncalibrated site (inScale 0, f32 gate) runs the f32 code dot over the unsnapped product, as
+ * the reference's f32 path does. f32 operands need 16-byte alignment (after the offset), int8
+ * codes 8-byte.
  */
 typedef struct g4_gelu_act {
     const void *up;    /* NULL in a plan entry: that projection has no prologue */
     int up_kind;       /* G4_KIND_F32 or G4_KIND_I8 */
     float gate_scale;  /* the gate's int8 codes (x_kind G4_KIND_I8) times this */
     float up_scale;    /* up_kind G4_KIND_I8: the codes times this */
-    int64_t up_offset; /* elements, the reference's params.upOffset (the per-layer-input slice) */
+    int64_t up_offset; /* in ELEMENTS. The reference's params.upOffset counts vec4s
+                          (qgemv.ts:398, execute.ts:886 layer * dim / 4): up_offset = 4 * upOffset */
 } g4_gelu_act;
 
 /* qgemv-4bit-gelu / qgemv-8bit-gelu (registry src/kernels/qgemv.ts:1668-1696, bindGemv(bits,
@@ -235,6 +247,40 @@ typedef struct g4_gelu_act {
 int g4_qgemv_gelu(int bits, const void *wq, const float *scales, const void *gate, int gate_kind,
                   const g4_gelu_act *act, void *dst, int out_kind, int k, int num_rows,
                   float in_scale, float out_scale, void *stream);
+
+/* qgemv-4bit-gelu-m2 / qgemv-8bit-gelu-m2 (src/kernels/qgemvWide.ts:660-669, 698-709; bind
+ * bindGemvWide(bits, 'gelu') :515-574): the gelu prologue over `cols` token columns (1..2, the
+ * draft-verify pass, execute.ts:382-390). gate and up are [cols][K] (column c at element c * K; up
+ * also offset by act->up_offset), dst is [cols][num_rows]. Column for column g4_qgemv_gelu. */
+int g4_qgemv_gelu_m2(int bits, const void *wq, const float *scales, const void *gate, int gate_kind,
+                     const g4_gelu_act *act, void *dst, int out_kind, int k, int num_rows, int cols,
+                     float in_scale, float out_scale, void *stream);
+
+/*
+ * ple-gate-split (src/kernels/pleSplit.ts:17-23, bind :50-63): per_layer_input_gate (8-bit) as
+ * exact split-K integer partials (qgemv.ts:521-548 with exactPartials), written row-interleaved
+ * for the fold's vec4 read: partials[(row / 4) * 4 * n + split * 4 + row % 4] = f32(sum of the
+ * split's K band), n = k_splits, which is pleGateSplits() (1, 2, 4 or 8; 1 runs as 2,
+ * pleSplit.ts:16). partials holds num_rows * n floats. Refuses num_rows % 4 != 0 and an
+ * uncalibrated inScale with the reference's messages (pleSplit.ts:58-59).
+ */
+int g4_ple_gate_split(const void *wq, const float *scales, const void *x, int x_kind,
+                      float *partials, int k, int num_rows, int k_splits, float in_scale,
+                      void *stream);
+
+/*
+ * ple-fold-projection (src/kernels/pleSplit.ts:24-41, bind :64-84): per_layer_projection
+ * (qgemv-8bit-gelu) whose gate is folded from ple-gate-split's partials (gate_parts, k_splits as
+ * there): gate[i] = total = sum over s of the partials in split order from 0;
+ * v = f32(f32(gate_in_scale * gate_scales[i]) * total), then clamp(RNE(v / gate_out_scale)) *
+ * gate_out_scale when gate_out_scale != 0; the GEMV reads gelu_tanh(gate[i]) * up[up_offset + i].
+ * act gives up (act->gate_scale is not used); gate_scales are the gate linear's row scales [K].
+ * gate_parts and gate_scales need 16-byte alignment. One token (execute.ts:880-881).
+ */
+int g4_ple_fold_projection(const void *wq, const float *scales, const float *gate_parts,
+                           const float *gate_scales, int k_splits, float gate_in_scale,
+                           float gate_out_scale, const g4_gelu_act *act, void *dst, int out_kind,
+                           int k, int num_rows, float in_scale, float out_scale, void *stream);
 
 /* qgemv-4bit-gelu-exact-split (src/kernels/exactSplit.ts:19-31 with the gelu prologue; plan.ts
  * :594-597 producer down exact partials): the split-K partials of g4_qgemv_split over the gelu

@@ -346,6 +346,31 @@ void or_qgemv_exact_merge(const float *partials, const float *scales, int64_t nu
     }
 }
 
+int or_ple_gate_split(const uint8_t *packed, const float *scales, const float *x,
+                      int64_t num_rows, int64_t k, int splits, float in_scale, float *partials) {
+    if (num_rows <= 0 || num_rows % 4 || splits < 1) return -1;
+    float *rm = (float *)malloc((size_t)num_rows * (size_t)splits * sizeof(float));
+    if (!rm) return -1;
+    int rc = or_qgemv_split(8, packed, scales, x, num_rows, k, splits, 1, in_scale, rm);
+    if (rc == 0)
+        for (int64_t r = 0; r < num_rows; r++)
+            for (int s = 0; s < splits; s++)
+                partials[(r / 4) * 4 * splits + s * 4 + r % 4] = rm[r * splits + s];
+    free(rm);
+    return rc;
+}
+
+void or_ple_fold_gate(const float *partials, int64_t k, int splits, const float *gate_scales,
+                      float gate_in, float gate_out, float *out) {
+    for (int64_t i = 0; i < k; i++) {
+        float total = 0.0f;
+        for (int s = 0; s < splits; s++) total = total + partials[(i / 4) * 4 * splits + s * 4 + i % 4];
+        float v = (gate_in * gate_scales[i]) * total;
+        or_apply_srq(&v, 1, gate_out, &v);
+        out[i] = v;
+    }
+}
+
 float or_qgemv_ref_lane_sum(int bits, const uint8_t *row_packed, const int8_t *xq, int64_t k) {
     int64_t cpw = bits == 4 ? 8 : 4;
     int64_t k_words = k / cpw;

@@ -23,6 +23,11 @@
  *   or_qgemv_split_scaled  per-band sums checked against numpy slices; fold vs numpy cumulative f32
  *   or_qgemv8_ref_lanes    equals fround(exact) whenever every lane partial < 2^24 (checked), and
  *                          brute-forced against a pure-Python replay of the 32-lane butterfly
+ *   or_ple_gate_split      the buffer read as numpy [N/4][splits][4] equals or_qgemv_split's
+ *                          [N][splits] partials; the bands sum to the unsplit exact accumulator
+ *   or_ple_fold_gate       fold(gate split) equals the unsplit qgemv-8bit f32 output (or_qgemv with
+ *                          outScale gate_out) bit for bit at every split count; a pure-Python
+ *                          replay on tiny K; ties and clamps at the gate snap
  */
 #ifndef G4_ORACLE_H
 #define G4_ORACLE_H
@@ -106,6 +111,18 @@ void or_qgemv_merge(const float *partials, int64_t num_rows, int splits, float o
  * snapped when out_scale != 0. */
 void or_qgemv_exact_merge(const float *partials, const float *scales, int64_t num_rows,
                           int splits, float in_scale, float out_scale, float *out);
+
+/* pleSplit.ts:17-23 ple-gate-split: the exact 8-bit split partials of or_qgemv_split (exact = 1,
+ * qgemv.ts:521-548 with exactPartials) laid out for the fold's vec4 read,
+ * partials[(row / 4) * 4 * splits + split * 4 + row % 4]. num_rows % 4 == 0. Returns 0 or -1. */
+int or_ple_gate_split(const uint8_t *packed, const float *scales, const float *x,
+                      int64_t num_rows, int64_t k, int splits, float in_scale, float *partials);
+
+/* pleSplit.ts:33-41 foldGate over k gate elements: total = the splits' partials summed in split
+ * order from 0 (the layout above, read as vec4 [k / 4][splits]); v = f32(f32(gate_in *
+ * gate_scales[i]) * total); applySrq(v, gate_out). out[k]. */
+void or_ple_fold_gate(const float *partials, int64_t k, int splits, const float *gate_scales,
+                      float gate_in, float gate_out, float *out);
 
 /* The reference qgemv-8bit reduction structure (qgemv.ts:497-519, 680; subgroupReduce.ts:49-59):
  * 32 lanes, lane l sums words l + 32 i exactly in i32, f32(acc) per lane, then the f32 xor

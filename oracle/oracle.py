@@ -66,6 +66,11 @@ def lib():
         L.or_qgemv_merge.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, _f32p]
         L.or_qgemv_exact_merge.argtypes = [_f32p, _f32p, ctypes.c_int64, ctypes.c_int,
                                            ctypes.c_float, ctypes.c_float, _f32p]
+        L.or_ple_gate_split.restype = ctypes.c_int
+        L.or_ple_gate_split.argtypes = [_u8p, _f32p, _f32p, ctypes.c_int64, ctypes.c_int64,
+                                        ctypes.c_int, ctypes.c_float, _f32p]
+        L.or_ple_fold_gate.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int, _f32p, ctypes.c_float,
+                                       ctypes.c_float, _f32p]
         L.or_qgemv_ref_lane_sum.restype = ctypes.c_float
         L.or_qgemv_ref_lane_sum.argtypes = [ctypes.c_int, _u8p, _i8p, ctypes.c_int64]
         L.or_embed_gather.restype = ctypes.c_int
@@ -193,6 +198,29 @@ def qgemv_split(bits, packed, scales, x, num_rows, k, splits, exact, in_scale) -
                               k, splits, 1 if exact else 0, float(np.float32(in_scale)),
                               _p(out, _f32p))
     assert rc == 0
+    return out
+
+
+# pleSplit.ts:17-23: exact 8-bit split partials, row-interleaved; flat [num_rows * splits]
+def ple_gate_split(packed, scales, x, num_rows, k, splits, in_scale) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(num_rows * splits, dtype=np.float32)
+    rc = lib().or_ple_gate_split(_p(packed, _u8p), _p(scales, _f32p), _p(x, _f32p), num_rows, k,
+                                 splits, float(np.float32(in_scale)), _p(out, _f32p))
+    assert rc == 0
+    return out
+
+
+# pleSplit.ts:33-41 foldGate over the interleaved partials: the gate's f32 values [k]
+def ple_fold_gate(partials, k, splits, gate_scales, gate_in, gate_out) -> np.ndarray:
+    partials = np.ascontiguousarray(partials, dtype=np.float32)
+    gate_scales = np.ascontiguousarray(gate_scales, dtype=np.float32)
+    assert partials.size == k * splits and gate_scales.size >= k
+    out = np.empty(k, dtype=np.float32)
+    lib().or_ple_fold_gate(_p(partials, _f32p), k, splits, _p(gate_scales, _f32p),
+                           float(np.float32(gate_in)), float(np.float32(gate_out)), _p(out, _f32p))
     return out
 
 

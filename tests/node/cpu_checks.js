@@ -15,7 +15,8 @@ function throwsWith(fn, fragment) {
 // registry
 for (const n of ['qgemv-4bit', 'qgemv-8bit', 'qgemv-4bit-m2', 'qgemm-4bit', 'qmatmul-8bit',
   'qkv-batch-4bit', 'gate-up-batch-4bit', 'qgemv-merge', 'qgemv-exact-merge', 'ple-gather-4bit',
-  'ple-gather-4bit-sliced', 'qgemv-4bit-gelu', 'qgemv-8bit-gelu', 'qgemv-4bit-gelu-exact-split'])
+  'ple-gather-4bit-sliced', 'qgemv-4bit-gelu', 'qgemv-8bit-gelu', 'qgemv-4bit-gelu-exact-split',
+  'qgemv-4bit-gelu-m2', 'qgemv-8bit-gelu-m2', 'ple-gate-split', 'ple-fold-projection', 'gelu-mul'])
   assert.ok(h.kernelNames().includes(n), n);
 throwsWith(() => h.bind('qgemv-4bit-gelu', { inputs: { wq: { addr: 1 } }, output: {}, params: {} }), 'needs inputs named wq, scales, gate, up');
 throwsWith(() => h.bind('qgemv-3bit', { inputs: {}, output: {}, params: {} }), 'no registered kernel named qgemv-3bit');
@@ -26,6 +27,50 @@ throwsWith(() => h.bind('gate-up-batch-4bit', { inputs: { x: {} }, output: {}, p
 const fake = { addr: 4096, bytes: 4096, kind: h.KIND.f16 };
 throwsWith(() => h.bind('qgemv-4bit', { inputs: { wq: fake, scales: fake, x: fake }, output: { addr: 4096, kind: h.KIND.i8 }, params: { k: 100, numRows: 8, inScale: 0.05, outScale: 0.1 } }), 'qgemv-4bit needs K a multiple of 256, got 100');
 throwsWith(() => h.bind('qgemv-4bit-m2', { inputs: { wq: fake, scales: fake, x: fake }, output: { addr: 4096, kind: h.KIND.i8 }, params: { k: 256, numRows: 8, cols: 3, inScale: 0.05, outScale: 0.1 } }), 'needs params.cols in 1..2, got 3');
+
+// the PLE split pair and the wide gelu forms refuse with the reference's messages (pleSplit.ts:
+// 11-15, 58-59; qgemvWide.ts:522-526; execute.ts:881) before any device call
+const f32b = { addr: 4096, bytes: 4096, kind: h.KIND.f32 };
+throwsWith(() => h.setPleGateSplits(3), 'PLE splits must be 1, 2, 4 or 8');
+throwsWith(() => h.bind('ple-gate-split', { inputs: { wq: fake, scales: fake, x: f32b }, output: f32b, params: { k: 1536, numRows: 250, inScale: 0.05 } }), 'PLE split row count must be divisible by four');
+throwsWith(() => h.bind('ple-gate-split', { inputs: { wq: fake, scales: fake, x: f32b }, output: f32b, params: { k: 1536, numRows: 256, inScale: 0 } }), 'PLE split needs calibrated input');
+throwsWith(() => h.bind('ple-fold-projection', { inputs: { wq: fake, scales: fake, gate: f32b, up: f32b }, output: f32b, params: {} }), 'needs inputs named wq, scales, gate, up, gateScales');
+throwsWith(() => h.bind('qgemv-8bit-gelu-m2', { inputs: { wq: fake, scales: fake, gate: f32b, up: f32b }, output: { addr: 4096, kind: h.KIND.i8 }, params: { k: 256, numRows: 8, cols: 3, inScale: 0.05, outScale: 0.1 } }), 'needs params.cols in 1..2, got 3');
+throwsWith(() => h.bind('gelu-mul', { inputs: { gate: f32b, up: f32b }, output: f32b, params: { count: 6 } }), 'gelu-mul needs params.count a positive multiple of 4, got 6');
+assert.strictEqual(h.pleGateSplits(), 1);
+
+// every name a plan binds on the projection path is registered (plan.ts:487-665 through
+// execute.ts's resolution): a decode step with the split PLE gate and the producer down split, a
+// verify pass of two tokens, batched projections, and a prefill chunk; and what resolveStep
+// refuses is refused the same way
+const planned = (geometry, options, slices) => {
+  const names = h.planProjectionKernels(geometry, options, slices);
+  for (const n of names) assert.ok(h.kernelNames().includes(n), `${n} (${JSON.stringify(options)}, tokens ${geometry.tokens})`);
+  return names;
+};
+const splitPle = planned({ mode: 'gemv', tokens: 1 }, { pleGateKSplits: 2, producerDownKSplits: 2 }, 5);
+for (const n of ['ple-gate-split', 'ple-fold-projection', 'qgemv-4bit-gelu-exact-split', 'qgemv-exact-merge', 'ple-gather-4bit-sliced', 'qgemv-4bit'])
+  assert.ok(splitPle.includes(n), n);
+const verify = planned({ mode: 'gemv', tokens: 2 }, {}, 1);
+for (const n of ['qgemv-4bit-m2', 'qgemv-8bit-m2', 'qgemv-4bit-gelu-m2', 'qgemv-8bit-gelu-m2', 'ple-gather-4bit'])
+  assert.ok(verify.includes(n), n);
+assert.ok(!verify.includes('qgemv-4bit'));
+const batched = planned({ mode: 'gemv', tokens: 1 }, { batchProjections: true, pleGateKSplits: 8 });
+for (const n of ['qkv-batch-4bit', 'gate-up-batch-4bit', 'qgemv-4bit-gelu', 'ple-fold-projection'])
+  assert.ok(batched.includes(n), n);
+const prefill = planned({ mode: 'gemm', tokens: 64 }, { pleGateKSplits: 2 });
+for (const n of ['qgemm-4bit', 'qmatmul-8bit', 'gelu-mul']) assert.ok(prefill.includes(n), n);
+assert.ok(!prefill.includes('ple-gate-split'));  // prefill never splits (plan.ts:633)
+planned({ mode: 'gemv', tokens: 2 }, { attnKSplits: 2 });  // the wide pass drops the q/k/v split
+throwsWith(() => h.planProjectionKernels({ mode: 'gemv', tokens: 2 }, { pleGateKSplits: 2 }), 'PLE split needs one token');
+throwsWith(() => h.planProjectionKernels({ mode: 'gemv', tokens: 2 }, { producerDownKSplits: 2 }), 'producer split needs one token');
+throwsWith(() => h.planProjectionKernels({ mode: 'gemv', tokens: 2 }, { batchProjections: true }), 'batched projections require a single token');
+// the PLE split kernels' cases follow the active split count (pleSplit.ts:43-49)
+h.setPleGateSplits(8);
+assert.strictEqual(h.KERNELS['ple-gate-split'].cases[0].expected.length, 8 * 8);
+assert.ok(h.KERNELS['ple-fold-projection'].cases[0].name.includes('fold-8'));
+h.setPleGateSplits(1);
+assert.strictEqual(h.KERNELS['ple-gate-split'].cases[0].expected.length, 8 * 2);
 
 // routing (execute.ts:372-430)
 const dec = { mode: 'gemv', tokens: 1 }, ver = { mode: 'gemv', tokens: 2 }, pre = { mode: 'gemm', tokens: 64 };
@@ -83,6 +128,8 @@ for (const name of h.kernelNames()) {
 }
 // the gelu cases saturate tanh, so their expected codes are not all zero
 assert.ok(h.KERNELS['qgemv-4bit-gelu'].cases[0].expected.some(v => v !== 0));
+for (const n of ['qgemv-4bit-gelu-m2', 'qgemv-8bit-gelu-m2', 'ple-fold-projection', 'gelu-mul'])
+  for (const c of h.KERNELS[n].cases) assert.ok(c.expected.some(v => v !== 0), `${n}/${c.name}`);
 assert.ok(h.KERNELS['ple-gather-4bit-sliced'].cases[0].expected.some(v => v !== 0));
 assert.strictEqual(typeof h.Stream, 'function');
 assert.strictEqual(typeof h.Decoder, 'function');

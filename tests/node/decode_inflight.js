@@ -45,17 +45,21 @@ async function main() {
   const tokens = h.DeviceBuffer.from(new Int32Array(spec.tokens));
   const next0 = new h.DeviceBuffer(4 * spec.shape.batch, h.KIND.i32);
   const next1 = new h.DeviceBuffer(4 * spec.shape.batch, h.KIND.i32);
-  // both steps enqueued before any wait: the second reads next0 on the device
-  dec.setPosition(spec.pos, stream);
-  dec.step(tokens, next0, stream);
-  dec.setPosition(spec.pos + 1, stream);
-  dec.step(next0, next1, stream);
+  // both steps enqueued before any wait: the second reads next0 on the device. Step t's logits
+  // are requested (downloadAsync) before step t + 1 is enqueued, and step t + 1 rewrites the same
+  // buffer: the copy must hold step t's values, so it has to be ordered at the call.
   const logits = dec.buffer('logits');
   const hidden = dec.buffer('hidden');
-  const [a, b, lg, hd] = await Promise.all([
-    next0.downloadAsync(stream), next1.downloadAsync(stream),
+  dec.setPosition(spec.pos, stream);
+  dec.step(tokens, next0, stream);
+  const lg0p = h.addon().downloadAsync(logits.addr, logits.bytes, stream.handle);
+  dec.setPosition(spec.pos + 1, stream);
+  dec.step(next0, next1, stream);
+  const [a, b, lg0, lg, hd] = await Promise.all([
+    next0.downloadAsync(stream), next1.downloadAsync(stream), lg0p,
     h.addon().downloadAsync(logits.addr, logits.bytes, stream.handle),
     h.addon().downloadAsync(hidden.addr, hidden.bytes, stream.handle)]);
+  fs.writeFileSync(path.join(dir, 'logits0.out'), Buffer.from(lg0));
   fs.writeFileSync(path.join(dir, 'next0.out'), Buffer.from(a));
   fs.writeFileSync(path.join(dir, 'next1.out'), Buffer.from(b));
   fs.writeFileSync(path.join(dir, 'logits1.out'), Buffer.from(lg));

@@ -34,8 +34,8 @@ async function main() {
     asyncOk = asyncOk && again.every((v, i) => v === c.expected[i]);
   }
   graph.destroy();
-  // an async wait on a refused copy (a NULL address, refused on the host) rejects with the
-  // library's message
+  // a refused copy (a NULL address, refused on the host when the copy is enqueued at the call)
+  // throws with the library's message
   let rejected = null;
   try {
     await h.addon().downloadAsync(0, 64, stream.handle);

@@ -69,6 +69,41 @@ def test_gemm_batch_merge_gather_refusals(g4):
                                                  35, 0, 0, 100, None)), 1, "does not divide")
 
 
+def test_ple_split_wide_gelu_and_gelu_mul_refusals(g4):
+    """pleSplit.ts:11-15, 58-59; qgemvWide.ts:522-526; geluMul.ts:253-255: refused before any
+    device call, with the reference's wording."""
+    import ctypes
+    L = g4.lib()
+    act = g4.GeluAct(0x1000, g4.KIND_F32, 0.0, 0.0, 0)
+    gate_split = lambda **kw: g4._check(L.g4_ple_gate_split(
+        0x1000, 0x1000, 0x1000, g4.KIND_F32, 0x1000, kw.get("k", 1536), kw.get("n", 256),
+        kw.get("splits", 2), kw.get("ins", 0.05), None))
+    expect(g4, lambda: gate_split(n=250), 1, "PLE split row count must be divisible by four")
+    expect(g4, lambda: gate_split(ins=0.0), 1, "PLE split needs calibrated input")
+    expect(g4, lambda: gate_split(splits=3), 1, "PLE splits must be 1, 2, 4 or 8")
+    expect(g4, lambda: gate_split(k=1000), 1, "qgemv-8bit needs K a multiple of 128")
+    fold = lambda **kw: g4._check(L.g4_ple_fold_projection(
+        0x1000, 0x1000, kw.get("parts", 0x1000), kw.get("gs", 0x1000), kw.get("splits", 2), 0.05,
+        0.1, ctypes.byref(kw.get("act", act)), 0x1000, g4.KIND_I8, 256, 1536, 0.05, 0.1, None))
+    expect(g4, lambda: fold(splits=5), 1, "PLE splits must be 1, 2, 4 or 8")
+    expect(g4, lambda: fold(gs=0), 1, "needs inputs named gate, up and gateScales")
+    expect(g4, lambda: fold(parts=0x1004), 1, "16-byte aligned")
+    expect(g4, lambda: fold(act=g4.GeluAct(None, g4.KIND_F32, 0.0, 0.0, 0)), 1,
+           "needs inputs named gate and up")
+    m2 = lambda cols: g4._check(L.g4_qgemv_gelu_m2(
+        8, 0x1000, 0x1000, 0x1000, g4.KIND_F32, ctypes.byref(act), 0x1000, g4.KIND_I8, 256, 8, cols,
+        0.05, 0.1, None))
+    expect(g4, lambda: m2(3), 1, "qgemv-8bit-gelu-m2 needs params.cols in 1..2, got 3")
+    expect(g4, lambda: g4._check(L.g4_gelu_mul_f32(0x1000, 0x1000, 0x1000, 6, 0.0, None)), 1,
+           "gelu-mul needs params.count a positive multiple of 4, got 6")
+    expect(g4, lambda: g4.bind("ple-fold-projection", {"wq": 1, "scales": 1, "gate": 1, "up": 1},
+                               None, {}), 1, "needs inputs named wq, scales, gate, up, gateScales")
+    expect(g4, lambda: g4.set_ple_gate_splits(3), 1, "PLE splits must be 1, 2, 4 or 8")
+    for n in ("ple-gate-split", "ple-fold-projection", "qgemv-4bit-gelu-m2", "qgemv-8bit-gelu-m2",
+              "gelu-mul"):
+        assert n in g4.kernel_names(), n
+
+
 def test_registry_refuses_unknown_names_and_missing_inputs(g4):
     expect(g4, lambda: g4.bind("qgemv-3bit", {}, None, {}), 2, "no registered kernel named qgemv-3bit")
     expect(g4, lambda: g4.bind("qgemv-4bit", {"wq": 1}, None, {}), 1,

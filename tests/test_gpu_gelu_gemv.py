@@ -126,8 +126,8 @@ def test_gelu_refusals(gpu):
         gpu._check(L.g4_qgemv_gelu(args["bits"], 0x1000, 0x1000, 0x1000, args["gk"],
                                    ctypes.byref(args["act"]), 0x1000, gpu.KIND_I8, args["k"],
                                    args["n"], args["ins"], OUT, None))
-    with pytest.raises(gpu.G4Error, match="calibrated"):
-        call(ins=0.0)
+    with pytest.raises(gpu.G4Error, match="uncalibrated f32 path, which has no int8 input codes"):
+        call(ins=0.0)  # an uncalibrated site takes the f32 gate, not codes
     with pytest.raises(gpu.G4Error, match="multiple of 256"):
         call(k=300)
     with pytest.raises(gpu.G4Error, match="gate must be f32 or int8"):

@@ -1,9 +1,8 @@
 """GPU parity of the M-column linears on int8 MFMA (qgemm-4bit, qmatmul-8bit) against the oracle.
 
 Config 2: the gate projection (N 6144, K 1536) with int4 weights and f16 activations carrying 1%
-outliers at +-8 sigma, at M in {4, 8, 16, 128, 512, 2048}. Up to M = 512 every output is compared;
-at M = 2048 a seeded sample of 96 columns is compared with the oracle and, as a size-independent
-property, every sampled column also equals the GEMV kernel's answer for that column alone.
+outliers at +-8 sigma, at M in {4, 8, 16, 128, 512, 2048}: every output is compared, at M = 2048
+with f16 and with int8-code activations.
 """
 import numpy as np
 import pytest
@@ -71,22 +70,30 @@ def test_config2_gate_full_compare(gpu, oracle, gate, m):
         assert f32_equal(of.download(), want)
 
 
-def test_config2_gate_m2048_sampled(gpu, oracle, gate):
+@pytest.mark.parametrize("x_kind", ["f16", "i8"])
+def test_config2_gate_m2048_full(gpu, oracle, gate, x_kind):
+    """Every output of the M = 2048 gate call against the oracle: f16 activations (the snap pass,
+    then the wide kernel on interleaved codes) and int8 codes (the wide kernel's NAT instantiation
+    reading the caller's codes in place); int8 codes and int32 accumulators. As a size-independent
+    property, a few columns also equal the GEMV kernel's answer for that column alone."""
     n, k, w, s, wb, sb = gate
     m = 2048
     x = syn.activations("c2", "x2048", m, k, outlier_frac=0.01)
-    print("config2 m=2048", flush=True)
+    print(f"config2 m=2048 x={x_kind} kernel={gpu.kernel_for_shape(4, m, n, k)}", flush=True)
+    _, acc, codes = oracle.qgemm(4, w, s, x.astype(np.float32), n, k, m, syn.IN_SCALE,
+                                 syn.OUT_SCALE)
+    xin = x if x_kind == "f16" else oracle.srq_codes(x.astype(np.float32), syn.IN_SCALE).reshape(m, k)
+    xb = dev(gpu, xin)
     o8 = out_buf(gpu, (m, n), np.int8)
-    gpu.qgemm(4, wb, sb, dev(gpu, x), o8, k, n, m, syn.IN_SCALE, syn.OUT_SCALE)
+    gpu.qgemm(4, wb, sb, xb, o8, k, n, m, syn.IN_SCALE, syn.OUT_SCALE)
     got = o8.download()
-    cols = np.sort(np.random.default_rng(52).choice(m, size=96, replace=False))
-    cols[0], cols[-1] = 0, m - 1
-    sub = x[cols].astype(np.float32)
-    _, _, codes = oracle.qgemm(4, w, s, sub, n, k, cols.size, syn.IN_SCALE, syn.OUT_SCALE)
-    assert np.array_equal(got[cols], codes)
-    for c in cols[:8]:
+    assert np.array_equal(got, codes)
+    o32 = out_buf(gpu, (m, n), np.int32)
+    gpu.qgemm(4, wb, sb, xb, o32, k, n, m, syn.IN_SCALE, syn.OUT_SCALE)
+    assert np.array_equal(o32.download(), acc)
+    for c in (0, 1000, m - 1):
         o1 = out_buf(gpu, (n,), np.int8)
-        gpu.qgemv(4, wb, sb, dev(gpu, x[c]), o1, k, n, 1, syn.IN_SCALE, syn.OUT_SCALE)
+        gpu.qgemv(4, wb, sb, dev(gpu, xin[c]), o1, k, n, 1, syn.IN_SCALE, syn.OUT_SCALE)
         assert np.array_equal(o1.download(), got[c])
 
 

@@ -96,7 +96,7 @@ def test_node_host_gpu_parity(tmp_path, oracle):
                              "up": {"file": put("gelu.u", up), "kind": "f32"}},
                   "output": {"bytes": n3, "kind": "i8"},
                   "params": {"k": k3, "numRows": n3, "inScale": syn.IN_SCALE,
-                             "outScale": syn.OUT_SCALE, "upOffset": off}})
+                             "outScale": syn.OUT_SCALE, "upOffset": off // 4}})  # vec4s
     (tmp_path / "manifest.json").write_text(json.dumps({"cases": cases}))
     print("node gpu parity: running node", flush=True)
     r = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "gpu_parity.js"), str(tmp_path)],
@@ -119,6 +119,13 @@ def _load(tmp_path, spec):
     return np.fromfile(tmp_path / spec["file"], _NP[spec["type"]])
 
 
+def _gelu_mul_f32(g, u):
+    """geluMul.ts:101-116 without a snap: f32(gelu_tanh(g)) * u in f32, the oracle's gelu."""
+    import decode_oracle as d
+    gv = np.array([d.gelu_tanh(float(v)) for v in np.asarray(g, np.float32)], np.float32)
+    return gv * np.asarray(u, np.float32)
+
+
 @needs_node
 def test_node_registry_cases_match_the_oracle(tmp_path, oracle):
     """The known answers the Node registry carries (registry.ts:72-119 `cases`), computed in JS on
@@ -133,7 +140,8 @@ def test_node_registry_cases_match_the_oracle(tmp_path, oracle):
         name, p = c["kernel"], c["params"]
         I = {k: _load(tmp_path, v) for k, v in c["inputs"].items()}
         want = _load(tmp_path, c["expected"])
-        bits = 8 if "8bit" in name else 4
+        bits = 8 if ("8bit" in name or name.startswith("ple-gate-split")
+                     or name == "ple-fold-projection") else 4
         if name.startswith(("qgemv-4bit", "qgemv-8bit", "qgemm", "qmatmul")) and "gelu" not in name \
                 and "split" not in name:
             m = p.get("cols", p.get("mCols", 1))
@@ -153,7 +161,7 @@ def test_node_registry_cases_match_the_oracle(tmp_path, oracle):
             i = p["outputIndex"]
             got = oracle.qgemv(4, I[f"w{i}"], I[f"s{i}"], I["x"], p[f"rows{i}"], p["k"],
                                p[f"inScale{i}"], p[f"outScale{i}"])[0]
-        elif name.endswith("-split") and "gelu" not in name:
+        elif name.endswith("-split") and "gelu" not in name and not name.startswith("ple-"):
             got = oracle.qgemv_split(bits, I["wq"], I["scales"], I["x"], p["numRows"], p["k"],
                                      p["kSplits"], p["exact"], p["inScale"]).reshape(-1)
         elif name == "qgemv-merge":
@@ -161,15 +169,35 @@ def test_node_registry_cases_match_the_oracle(tmp_path, oracle):
         elif name == "qgemv-exact-merge":
             got = oracle.qgemv_exact_merge(I["part"].reshape(p["numRows"], -1), I["scales"],
                                            p["inScale"], p["outScale"])
-        elif "gelu" in name:
-            act = d.gelu_mul_f32_codes(I["gate"], I["up"], p["inScale"])
-            x = act.astype(np.float32) * np.float32(p["inScale"])
-            if name.endswith("exact-split"):
-                got = oracle.qgemv_split(bits, I["wq"], I["scales"], x, p["numRows"], p["k"],
-                                         p["kSplits"], True, p["inScale"]).reshape(-1)
+        elif name == "gelu-mul":
+            got = oracle.apply_srq(_gelu_mul_f32(I["gate"], I["up"]), p.get("srqScale", 0.0))
+        elif name == "ple-gate-split":
+            n, k = p["numRows"], p["k"]
+            got = oracle.ple_gate_split(I["wq"], I["scales"], I["x"], n, k, want.size // n,
+                                        p["inScale"])
+        elif "gelu" in name or name == "ple-fold-projection":
+            k, n, m = p["k"], p["numRows"], p.get("cols", 1)
+            off = 4 * p.get("upOffset", 0)  # vec4s (qgemv.ts:398)
+            up = I["up"][off:off + m * k].reshape(m, k)
+            if name == "ple-fold-projection":
+                splits = I["gate"].size // k
+                gate = oracle.ple_fold_gate(I["gate"], k, splits, I["gateScales"],
+                                            p["gateInScale"], p["gateOutScale"]).reshape(1, k)
             else:
-                got = oracle.qgemv(bits, I["wq"], I["scales"], x, p["numRows"], p["k"],
-                                   p["inScale"], p["outScale"])[2]
+                gate = I["gate"].reshape(m, k)
+            ins = p.get("inScale", 0.0)
+            if ins:
+                x = np.stack([d.gelu_mul_f32_codes(gate[c], up[c], ins) for c in range(m)])
+                x = x.astype(np.float32) * np.float32(ins)
+            else:
+                x = np.stack([_gelu_mul_f32(gate[c], up[c]) for c in range(m)])
+            if name.endswith("exact-split"):
+                got = oracle.qgemv_split(bits, I["wq"], I["scales"], x[0], n, k, p["kSplits"],
+                                         True, ins).reshape(-1)
+            else:
+                y, _, q = oracle.qgemm(bits, I["wq"], I["scales"], x, n, k, m, ins,
+                                       p.get("outScale", 0.0))
+                got = (q if want.dtype == np.int8 else y).reshape(-1)
         elif name.startswith("ple-gather"):
             sliced = name.endswith("sliced")
             out = np.zeros((p["slots"], p["cols"]), np.float32)
@@ -184,7 +212,7 @@ def test_node_registry_cases_match_the_oracle(tmp_path, oracle):
         assert np.array_equal(np.asarray(got, want.dtype).view(np.uint8), want.view(np.uint8)), \
             (name, c["case"])
         seen.add(name)
-    assert len(seen) == 19
+    assert len(seen) == 24
 
 
 @needs_node
@@ -246,6 +274,9 @@ def test_node_two_decode_steps_in_flight(gpu, tmp_path):
     want0 = ref.step(shape, W, kv, toks, pos)
     want1 = ref.step(shape, W, kv, [int(t) for t in want0["next"]], pos + 1)
     assert np.array_equal(next0, want0["next"]) and np.array_equal(next1, want1["next"])
+    logits0 = np.fromfile(tmp_path / "logits0.out", np.float32).reshape(shape.batch, -1)
+    assert np.array_equal(logits0.view(np.uint32),
+                          np.asarray(want0["logits"], np.float32).view(np.uint32))
     logits = np.fromfile(tmp_path / "logits1.out", np.float32).reshape(shape.batch, -1)
     hidden = np.fromfile(tmp_path / "hidden1.out", np.float32).reshape(shape.batch, -1)
     assert np.array_equal(logits.view(np.uint32), np.asarray(want1["logits"], np.float32).view(np.uint32))

@@ -76,4 +76,32 @@ def test_noalloc_refuses_oversized(gpu):
                                     syn.IN_SCALE, syn.OUT_SCALE, None)
     assert rc == 1
     msg = gpu.lib().g4_last_error().decode()
-    assert "scratch array" in msg and str(cap) in msg
+    assert "g4_qgemm_noalloc" in msg and "scratch" in msg and str(cap) in msg
+    # an invalid call gets the reference's refusal, not the size message (checked first)
+    rc = gpu.lib().g4_qgemm_noalloc(4, 16, 16, 16, gpu.KIND_F16, 16, gpu.KIND_I8, 300, n, m,
+                                    syn.IN_SCALE, syn.OUT_SCALE, None)
+    assert rc == 1 and "K a multiple of 256" in gpu.lib().g4_last_error().decode()
+
+
+@pytest.mark.parametrize("bits,k,ins", [(8, 4096, 0.0), (4, 4096, 0.0), (8, 4112, syn.IN_SCALE)])
+def test_noalloc_large_calls_that_need_no_scratch(gpu, bits, k, ins):
+    """M * K above the scratch size on paths that snap nothing into it: the uncalibrated serial
+    qmatmul-8bit and f32 code dot (inScale 0), and 8-bit K % 128 != 0 (K 4112, the per-column
+    GEMV). They run, and give g4_qgemm's outputs."""
+    m, n = 4096 if k == 4096 else 2100, 64
+    assert m * k > gpu.lib().g4_qgemm_noalloc_max_codes()
+    print(f"noalloc large bits={bits} m={m} k={k} in={ins}", flush=True)
+    w = syn.weights("noalloc", f"big{bits}_{k}", n, k, bits)
+    s = syn.row_scales("noalloc", f"bigs{k}", n)
+    x = syn.activations("noalloc", f"bigx{k}", m, k).astype(np.float32)
+    dw, ds, dx = (gpu.DeviceBuffer.from_array(a) for a in (w, s, x))
+    dt, outs_scale = (np.float32, 0.0) if ins == 0.0 else (np.int8, syn.OUT_SCALE)
+    outs = []
+    for which in ("noalloc", "qgemm"):
+        dst = gpu.DeviceBuffer.empty((m, n), dt)
+        dst.fill(0x7B)
+        fn = gpu.qgemm_noalloc if which == "noalloc" else gpu.qgemm
+        fn(bits, dw, ds, dx, dst, k, n, m, ins, outs_scale)
+        gpu.synchronize()
+        outs.append(dst.download())
+    assert np.array_equal(outs[0].view(np.uint8), outs[1].view(np.uint8))
