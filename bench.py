@@ -12,8 +12,9 @@ Reported beside it (under "extra", not the headline):
   - the same 35 layers as one grouped launch per layer (7 projections per launch) and in the decode
     dependency shape (4 launches per layer: qkv batch, o, gate/up batch, down), which show what
     launch granularity costs;
-  - config 0 (one 1536 x 1536 GEMV) as a single launch;
-  - config 2's gate GEMM at M = 512 in int8 TOPS (MFMA), with and without the activation snap;
+  - config 0 (one 1536 x 1536 GEMV) as a single launch, warm and cold (512 rotated copies);
+  - config 2's gate GEMM at M = 512 in int8 TOPS (MFMA), with and without the activation snap, and
+    at every config-2 M with int8 and f16 input, M <= 128 also cold (a rotated 607 MB pool);
   - config 3's split PLE gather (5 slices, 2048 Zipf tokens, f16 out) in GB/s;
   - a measured HBM reference (a 1 GiB device-to-device copy) beside the 8 TB/s spec peak.
 
@@ -131,46 +132,117 @@ def bench_gemm(h, m=512, reps=50):
             "note": "f16_in includes the activation snap; int8_in takes codes already snapped"}
 
 
+POOL_BYTES = 512 << 20  # cold rows rotate weight copies totalling at least 2x the 256 MB MALL
+
+
+def weight_pool(w_host, s_host, min_bytes=POOL_BYTES):
+    """Copies of one weight matrix (and its scales) totalling at least `min_bytes`, so calls that
+    rotate through them read their weights from HBM, not from the memory-side cache."""
+    count = max(2, -(-min_bytes // w_host.nbytes))
+    return [(g4.DeviceBuffer.from_array(w_host), g4.DeviceBuffer.from_array(s_host))
+            for _ in range(count)]
+
+
+def timed_pair(h, stream_obj, call, pool_len, reps):
+    """Event-timed back-to-back calls (call(i) uses pool entry i) and the same calls captured as
+    one graph and replayed: returns (us per call, us per call from a graph)."""
+    i = [0]
+
+    def one():
+        call(i[0] % pool_len)
+        i[0] += 1
+    ms = timed(h, one, max(reps, pool_len), 3)
+    per = pool_len if pool_len > 1 else 20
+    graph = g4.Graph(stream_obj, lambda: [call(j % pool_len) for j in range(per)])
+    ms_g = timed(h, graph.launch, max(2, reps // per), 2) / per
+    graph.close()
+    return ms * 1e3, ms_g * 1e3
+
+
 def bench_gemm_sweep(h, stream_obj, ms=(4, 8, 16, 128, 512, 2048), reps=30):
-    """Config 2: the gate projection (K=1536, N=6144, int4) at every BASELINE M, int8 codes in
-    (the activation snap is timed separately in bench_gemm). Bytes are weights + scales + x + out."""
+    """Config 2: the gate projection (K=1536, N=6144, int4) at every BASELINE M. Each row gives
+    the kernel that served it, with int8 codes in and with f16 activations in (the snap included),
+    timed back to back and replayed from a graph. "warm" repeats one weight buffer (served from the
+    256 MB memory-side cache after the first call); "cold" (M <= 128, where the weights are the
+    bytes) rotates through a 607 MB pool of weight copies, so every call reads HBM. Bytes are
+    weights + scales + x (1 B int8 or 2 B f16 per code) + int8 out."""
     n, k = syn.FFN, syn.HIDDEN
-    w = g4.DeviceBuffer.from_array(syn.int4_weights("c2", "gate", n, k))
-    s = g4.DeviceBuffer.from_array(syn.row_scales("c2", "gate", n))
+    w_host = syn.int4_weights("c2", "gate", n, k)
+    s_host = syn.row_scales("c2", "gate", n)
+    pool = weight_pool(w_host, s_host)
     rows = []
     for m in ms:
-        x = g4.DeviceBuffer.from_array(syn.activations("c2", f"x{m}", m, k, outlier_frac=0.01))
+        xh = syn.activations("c2", f"x{m}", m, k, outlier_frac=0.01)
+        x = g4.DeviceBuffer.from_array(xh)
         codes = g4.DeviceBuffer.empty((m, k), np.int8)
         g4.srq_quantize(x, codes, m * k, syn.IN_SCALE, stream=h)
         d = g4.DeviceBuffer.empty((m, n), np.int8)
-        call = lambda: g4.qgemm(4, w, s, codes, d, k, n, m, syn.IN_SCALE, syn.OUT_SCALE, stream=h)
-        ms_ = timed(h, call, reps, 5)
-        # the same calls captured as one graph of `per` launches and replayed (no host launch cost
-        # per call: what a serving loop that captures its step sees)
-        per = 20
-        graph = g4.Graph(stream_obj, lambda: [call() for _ in range(per)])
-        ms_g = timed(h, graph.launch, max(2, reps // per), 2) / per
-        graph.close()
-        by = n * k // 2 + 4 * n + m * k + m * n
-        rows.append({"m": m, "kernel": g4.kernel_for_shape(4, m, n, k), "us": round(ms_ * 1e3, 3),
-                     "tops": round(2.0 * m * n * k / (ms_ * 1e-3) / 1e12, 2),
-                     "gbs": round(by / (ms_ * 1e-3) / 1e9, 2),
-                     "us_graph": round(ms_g * 1e3, 3),
-                     "gbs_graph": round(by / (ms_g * 1e-3) / 1e9, 2)})
+        row = {"m": m, "kernel": g4.kernel_for_shape(4, m, n, k)}
+        ops = 2.0 * m * n * k
+        for src, xb, tag in ((codes, 1, "int8_in"), (x, 2, "f16_in")):
+            by = n * k // 2 + 4 * n + xb * m * k + m * n
+            temps = (("warm", 1), ("cold", len(pool))) if m <= 128 else (("warm", 1),)
+            for temp, plen in temps:
+                call = (lambda j, src=src: g4.qgemm(4, pool[j][0], pool[j][1], src, d, k, n, m,
+                                                    syn.IN_SCALE, syn.OUT_SCALE, stream=h))
+                us, us_g = timed_pair(h, stream_obj, call, plen, reps)
+                key = f"{tag}_{temp}"
+                row[key] = {"us": round(us, 3), "us_graph": round(us_g, 3),
+                            "tops": round(ops / (us * 1e-6) / 1e12, 2),
+                            "gbs": round(by / (us * 1e-6) / 1e9, 2),
+                            "gbs_graph": round(by / (us_g * 1e-6) / 1e9, 2)}
+        # the headline keys of earlier rounds: int8 in, warm, back to back
+        row.update({"us": row["int8_in_warm"]["us"], "tops": row["int8_in_warm"]["tops"],
+                    "us_graph": row["int8_in_warm"]["us_graph"]})
+        rows.append(row)
+    for wb, sb in pool:
+        wb.close()
+        sb.close()
     return rows
 
 
-def bench_int8_down(h, reps=50):
-    """Config 1's int8-weight variant of down (6144 -> 1536, I8 codes U[-127,127]) at M=1."""
+def bench_int8_down(h, stream_obj, reps=64):
+    """Config 1's int8-weight variant of down (6144 -> 1536, I8 codes U[-127,127]) at M=1, warm
+    (one weight buffer) and cold (a 604 MB pool of copies, rotated)."""
     n, k = syn.HIDDEN, syn.FFN
-    w = g4.DeviceBuffer.from_array(syn.int8_weights("c1", "down8", n, k))
-    s = g4.DeviceBuffer.from_array(syn.row_scales("c1", "down8", n))
+    pool = weight_pool(syn.int8_weights("c1", "down8", n, k), syn.row_scales("c1", "down8", n))
     x = g4.DeviceBuffer.from_array(syn.activations("c1", "down8", 1, k)[0])
     d = g4.DeviceBuffer.empty((n,), np.int8)
-    ms_ = timed(h, lambda: g4.qgemv(8, w, s, x, d, k, n, 1, syn.IN_SCALE, syn.OUT_SCALE, stream=h),
-                reps, 5)
-    return {"n": n, "k": k, "kernel": g4.kernel_for_shape(8, 1, n, k), "us": round(ms_ * 1e3, 3),
-            "gbs": round(proj_bytes(n, k, 8) / (ms_ * 1e-3) / 1e9, 2)}
+    out = {"n": n, "k": k, "kernel": g4.kernel_for_shape(8, 1, n, k), "pool_copies": len(pool)}
+    for temp, plen in (("warm", 1), ("cold", len(pool))):
+        call = lambda j: g4.qgemv(8, pool[j][0], pool[j][1], x, d, k, n, 1, syn.IN_SCALE,
+                                  syn.OUT_SCALE, stream=h)
+        us, us_g = timed_pair(h, stream_obj, call, plen, reps)
+        out[temp] = {"us": round(us, 3), "gbs": round(proj_bytes(n, k, 8) / (us * 1e-6) / 1e9, 2),
+                     "us_graph": round(us_g, 3),
+                     "gbs_graph": round(proj_bytes(n, k, 8) / (us_g * 1e-6) / 1e9, 2)}
+    for wb, sb in pool:
+        wb.close()
+        sb.close()
+    out.update({"us": out["warm"]["us"], "gbs": out["warm"]["gbs"]})
+    return out
+
+
+def bench_config0(h, stream_obj, reps=512):
+    """Config 0 (one 1536 x 1536 int4 GEMV) as a single launch, warm (one weight buffer, the
+    memory-side cache serves it) and cold (512 copies, 609 MB, rotated)."""
+    n = k = 1536
+    pool = weight_pool(syn.int4_weights("c0", "w", n, k), syn.row_scales("c0", "w", n))
+    x = g4.DeviceBuffer.from_array(syn.activations("c0", "x", 1, k)[0])
+    d = g4.DeviceBuffer.empty((n,), np.int8)
+    by = proj_bytes(n, k)
+    out = {"bytes": by, "kernel": g4.kernel_for_shape(4, 1, n, k), "pool_copies": len(pool)}
+    for temp, plen in (("warm", 1), ("cold", len(pool))):
+        call = lambda j: g4.qgemv(4, pool[j][0], pool[j][1], x, d, k, n, 1, syn.IN_SCALE,
+                                  syn.OUT_SCALE, stream=h)
+        us, us_g = timed_pair(h, stream_obj, call, plen, reps)
+        out[temp] = {"us": round(us, 3), "gbs": round(by / (us * 1e-6) / 1e9, 2),
+                     "us_graph": round(us_g, 3), "gbs_graph": round(by / (us_g * 1e-6) / 1e9, 2)}
+    for wb, sb in pool:
+        wb.close()
+        sb.close()
+    out.update({"us": out["warm"]["us"], "gbs": out["warm"]["gbs"]})
+    return out
 
 
 def cpu_extra(seconds=4.0):
@@ -398,13 +470,13 @@ def bench_decode(h, batch, steps=20, warmup=3, probe=False, cpu=False):
 
 def gemm_probe(h):
     """Launches for rocprofv3 --kernel-trace --stats: the config-2 gate GEMM 50 times at M=4, 8,
-    16 and 512 and 20 times at M=2048, first with f16 activations (above M=32: the activation snap
-    + the tile kernel; up to 32 the small kernel snaps itself), then with int8 codes already
+    16, 128 and 512 and 20 times at M=2048, first with f16 activations (above M=32: the activation
+    snap + the tile kernel; up to 32 the small kernel snaps itself), then with int8 codes already
     snapped (one kernel)."""
     n, k = syn.FFN, syn.HIDDEN
     w = g4.DeviceBuffer.from_array(syn.int4_weights("c2", "gate", n, k))
     s = g4.DeviceBuffer.from_array(syn.row_scales("c2", "gate", n))
-    for m, reps in ((4, 50), (8, 50), (16, 50), (512, 50), (2048, 20)):
+    for m, reps in ((4, 50), (8, 50), (16, 50), (128, 50), (512, 50), (2048, 20)):
         x = g4.DeviceBuffer.from_array(syn.activations("c2", f"x{m}", m, k, outlier_frac=0.01))
         codes = g4.DeviceBuffer.empty((m, k), np.int8)
         g4.srq_quantize(x, codes, m * k, syn.IN_SCALE, stream=h)
@@ -425,7 +497,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true")
     ap.add_argument("--gemm-probe", action="store_true",
-                    help="only the config-2 GEMM launches (M=512 and M=2048, f16 then int8 in), for rocprofv3")
+                    help="only the config-2 GEMM launches (M=4..2048, f16 then int8 in), for rocprofv3")
     ap.add_argument("--decode-probe", type=int, default=0, metavar="BATCH",
                     help="only config-4 decode steps at this batch (graph replays), for rocprofv3")
     ap.add_argument("--gather-probe", action="store_true",
@@ -506,22 +578,15 @@ def main():
         ms_layer = timed(h, lambda: [g4.qgemv_grouped(a, h) for a in groups], 20, 3)
         log("decode-shaped launches")
         ms_dec = timed(h, decode_shaped(layers, h), 20, 3)
-        log("config 0 single GEMV")
-        c0 = layers[0]["q"]
-        w0 = g4.DeviceBuffer.from_array(syn.int4_weights("c0", "w", 1536, 1536))
-        s0 = g4.DeviceBuffer.from_array(syn.row_scales("c0", "w", 1536))
-        x0 = g4.DeviceBuffer.from_array(syn.activations("c0", "x", 1, 1536)[0])
-        d0 = g4.DeviceBuffer.empty((1536,), np.int8)
-        ms_c0 = timed(h, lambda: g4.qgemv(4, w0, s0, x0, d0, 1536, 1536, 1, syn.IN_SCALE,
-                                          syn.OUT_SCALE, stream=h), 200, 10)
-        del c0
+        log("config 0 single GEMV, warm and cold")
+        c0 = bench_config0(h, stream)
         log("config 2 gate GEMM at M=512")
         gm = bench_gemm(h)
         log("config 3 split PLE gather")
         ga = bench_gather(h)
         log("config 2 sweep over M, config 1 int8 down")
         sweep = bench_gemm_sweep(h, stream)
-        down8 = bench_int8_down(h)
+        down8 = bench_int8_down(h, stream)
         log("measured HBM copy rate")
         hbm = hbm_copy_rate(h)
         log("config 4 decode step, batch 1 and 32")
@@ -533,9 +598,7 @@ def main():
                                   "gbs": round(step_bytes / (ms_layer * 1e-3) / 1e9, 2)},
             "decode_shaped": {"launches_per_step": 4 * LAYERS, "ms_per_step": round(ms_dec, 6),
                               "gbs": round(step_bytes / (ms_dec * 1e-3) / 1e9, 2)},
-            "config0_single_gemv": {"bytes": proj_bytes(1536, 1536), "us": round(ms_c0 * 1e3, 3),
-                                    "gbs": round(proj_bytes(1536, 1536) / (ms_c0 * 1e-3) / 1e9, 2),
-                                    "kernel": g4.kernel_for_shape(4, 1, 1536, 1536)},
+            "config0_single_gemv": c0,
             "int8_gemm_m512": gm,
             "gemm_sweep_config2": sweep,
             "config1_int8_down": down8,
