@@ -43,43 +43,60 @@ __device__ __forceinline__ uint32_t pack4b(int a, int b, int c, int d) {
            ((uint32_t)(d & 0xff) << 24);
 }
 
-// One block per token row: snap K activations into codes (interleaved per 8-code group when PERM)
-// and zero the pad up to kp.
-template <bool PERM>
-__global__ __launch_bounds__(kQuantThreads) void quantize_rows_kernel(
-    const void *x, int x_kind, int k, int kp, float scale, int8_t *codes) {
-    const int m = blockIdx.x;
-    const int tid = threadIdx.x;
-    const int groups = kp >> 3;
-    const int live = k >> 3;
+constexpr int kQuantGroups = 4;  // 8-code groups per thread per pass, all loaded before any snap
+
+// The activation snap of the tile kernels: n8 groups of 8 activations (f16 or f32; x 16-byte
+// aligned, each group one or two 16-byte loads) into codes, interleaved per 8-code group when
+// PERM. A flat grid over the groups: each thread issues the loads of kQuantGroups groups, then
+// snaps and stores them (one 8-byte store per group), so a pass costs one memory latency.
+template <bool PERM, bool F16>
+__global__ __launch_bounds__(kQuantThreads) void quantize_rows_kernel(const void *x, int64_t n8,
+                                                                      float scale, int8_t *codes) {
     bool r_ok;
     const float r = srq_recip(scale, r_ok);
-    for (int g = tid; g < groups; g += kQuantThreads) {
-        int c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (g < live) {
-            const int64_t e = (int64_t)m * k + (int64_t)g * 8;
-            if (x_kind == G4_KIND_I8) {
-                const uint2 v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const int8_t *>(x) + e);
+    const int64_t stride = (int64_t)gridDim.x * kQuantThreads * kQuantGroups;
+    for (int64_t g0 = (int64_t)blockIdx.x * kQuantThreads * kQuantGroups + threadIdx.x; g0 < n8;
+         g0 += stride) {
+        u32x4 raw[kQuantGroups][F16 ? 1 : 2];
+#pragma unroll
+        for (int u = 0; u < kQuantGroups; ++u) {
+            const int64_t g = min(g0 + (int64_t)u * kQuantThreads, n8 - 1);  // clamped: valid
+            const u32x4 *p = reinterpret_cast<const u32x4 *>(x) + g * (F16 ? 1 : 2);
+            raw[u][0] = p[0];
+            if (!F16) raw[u][F16 ? 0 : 1] = p[1];
+        }
+#pragma unroll
+        for (int u = 0; u < kQuantGroups; ++u) {
+            const int64_t g = g0 + (int64_t)u * kQuantThreads;
+            if (g >= n8) break;
+            float v[8];
+            if (F16) {
+                const uint32_t h[4] = {raw[u][0].x, raw[u][0].y, raw[u][0].z, raw[u][0].w};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    c[i] = (int)(int8_t)((v.x >> (8 * i)) & 0xff);
-                    c[4 + i] = (int)(int8_t)((v.y >> (8 * i)) & 0xff);
+                    v[2 * i] = __half2float(__ushort_as_half((unsigned short)(h[i] & 0xffff)));
+                    v[2 * i + 1] = __half2float(__ushort_as_half((unsigned short)(h[i] >> 16)));
                 }
             } else {
+                const uint32_t w[8] = {raw[u][0].x, raw[u][0].y, raw[u][0].z, raw[u][0].w,
+                                       raw[u][F16 ? 0 : 1].x, raw[u][F16 ? 0 : 1].y,
+                                       raw[u][F16 ? 0 : 1].z, raw[u][F16 ? 0 : 1].w};
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    c[i] = (int)srq_code_fast(load_act(x, x_kind, e + i), scale, r, r_ok);
+                for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(w[i]);
             }
+            int c[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) c[i] = (int)srq_code_fast(v[i], scale, r, r_ok);
+            uint2 out;
+            if (PERM) {
+                out.x = pack4b(c[0], c[2], c[4], c[6]);
+                out.y = pack4b(c[1], c[3], c[5], c[7]);
+            } else {
+                out.x = pack4b(c[0], c[1], c[2], c[3]);
+                out.y = pack4b(c[4], c[5], c[6], c[7]);
+            }
+            reinterpret_cast<uint2 *>(codes)[g] = out;
         }
-        uint2 out;
-        if (PERM) {
-            out.x = pack4b(c[0], c[2], c[4], c[6]);
-            out.y = pack4b(c[1], c[3], c[5], c[7]);
-        } else {
-            out.x = pack4b(c[0], c[1], c[2], c[3]);
-            out.y = pack4b(c[4], c[5], c[6], c[7]);
-        }
-        *reinterpret_cast<uint2 *>(codes + (int64_t)m * kp + (int64_t)g * 8) = out;
     }
 }
 
@@ -551,13 +568,14 @@ template <int N> __device__ __forceinline__ void tile_wait() {
     asm volatile("" ::: "memory");
 }
 
-template <int DPS> __device__ __forceinline__ void tile_wait_stages(int later) {
-    switch (later) {
-        case 0: tile_wait<0>(); break;
-        case 1: tile_wait<1 * DPS>(); break;
-        case 2: tile_wait<2 * DPS>(); break;
-        case 3: tile_wait<3 * DPS>(); break;
-        default: tile_wait<0>(); break;
+// tile_wait for `later` stages of DPS loads each still allowed in flight (a runtime count mapped
+// onto the immediate vmcnt; a count beyond the counter's range waits for everything).
+template <int DPS, int L = 0> __device__ __forceinline__ void tile_wait_stages(int later) {
+    if constexpr (L * DPS >= 64 || L > 15) {
+        tile_wait<0>();
+    } else {
+        if (later == L) tile_wait<L * DPS>();
+        else tile_wait_stages<DPS, L + 1>(later);
     }
 }
 
@@ -574,19 +592,23 @@ __device__ __forceinline__ void nib_natural16(uint32_t w, int &lo, int &hi) {
 
 // NAT (4-bit): A holds natural-order codes and B is permuted to match in registers; otherwise A is
 // the per-8 interleaved row the nibble lanes read directly (no permutes).
-template <int BITS, int NS, bool NAT>
+// BM: 64 tile rows (each wave 32 x 48), or 32 (each wave 16 x 48) for grids that would leave CUs
+// idle at 64: a block keeps about as many bytes in flight as the CU allows, so the launch's
+// bandwidth grows with the number of CUs it occupies.
+template <int BITS, int NS, bool NAT, int BM = kTileBM>
 __global__ __launch_bounds__(256) void qgemm_tile_kernel(
     const int8_t *__restrict__ A, const uint8_t *__restrict__ W, const float *__restrict__ scales,
     void *dst, int M, int N, int K, float in_scale, float out_scale, int out_kind, int tiles_m,
     int tiles_n) {
-    constexpr int BM = kTileBM, BN = kTileBN, TM = 2, TN = 3;
+    static_assert(BM == 64 || BM == 32, "tile rows");
+    constexpr int BN = kTileBN, TM = BM / 32, TN = 3, WR = BM / 2;  // WR: rows of a wave's tile
     constexpr int BROW = BITS == 4 ? 64 : 128;  // weight bytes of one column per stage
     constexpr int A_BYTES = BM * 128, B_BYTES = BN * BROW, SB = A_BYTES + B_BYTES;
     constexpr int A_PW = A_BYTES / 1024 / 4;                   // loads per wave per stage
     constexpr int B_INS = B_BYTES / 1024, B_PW = (B_INS + 3) / 4;
     constexpr int DPS = A_PW + B_PW;
     constexpr int ESTR = kTileEpiStride;
-    static_assert(NS >= 3 && NS <= 5, "ring depth");
+    static_assert(NS >= 3 && NS * SB <= 160 * 1024, "ring depth");
     static_assert(NS * SB >= BM * ESTR * 4 + BN * 4, "the epilogue staging fits the ring");
     __shared__ __align__(1024) uint8_t smem[NS * SB];
 
@@ -649,7 +671,7 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(
     uint32_t aoff[2], boff[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-        aoff[s] = (wm * 32 / 8 + (j >> 3)) * 1024 + (j & 7) * 128 + 16 * ((2 * g + s) ^ sig);
+        aoff[s] = (wm * WR / 8 + (j >> 3)) * 1024 + (j & 7) * 128 + 16 * ((2 * g + s) ^ sig);
         boff[s] = A_BYTES + (wn * 48 / 8 + (j >> 3)) * 1024 + (j & 7) * 128 + 16 * ((2 * g + s) ^ sig);
     }
     const uint32_t boff4 = A_BYTES + (wn * 48 + j) * 64 + 16 * (g ^ (((j >> 1) ^ (j >> 3)) & 3));
@@ -762,7 +784,7 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(
         for (int u = 0; u < TN; ++u)
 #pragma unroll
             for (int r = 0; r < 4; ++r)  // D layout: lane l, register r -> row 4 (l / 16) + r, column l % 16
-                sacc[(wm * 32 + t * 16 + 4 * g + r) * ESTR + wn * 48 + u * 16 + j] =
+                sacc[(wm * WR + t * 16 + 4 * g + r) * ESTR + wn * 48 + u * 16 + j] =
                     BITS == 4 ? acc[t][u][r] >> 4 : acc[t][u][r];
     __syncthreads();
     bool r_ok;
@@ -1346,19 +1368,31 @@ template <int BITS>
 static int launch_tile(const int8_t *codes, bool natural, const uint8_t *w, const float *scales,
                        void *dst, int m, int n, int k, float in_scale, float out_scale,
                        int out_kind, hipStream_t stream) {
-    const int tiles_m = (m + kTileBM - 1) / kTileBM;
     const int tiles_n = (n + kTileBN - 1) / kTileBN;
+    // 32-row tiles when 64-row ones would not give every CU a block (config 2 at M = 128: 256
+    // blocks in place of 128)
+    const bool half = (int64_t)((m + kTileBM - 1) / kTileBM) * tiles_n < device_cu_count() && m > 32;
+    const int bm = half ? kTileBM / 2 : kTileBM;
+    const int tiles_m = (m + bm - 1) / bm;
     const int blocks = tiles_m * ((tiles_n + 7) / 8) * 8;  // XCD-aware order: whole groups of 8
     const int nk = k / kTileBK;  // >= 2 (k % 128 == 0 and k >= 256 here)
     // 8-bit weights are natural-order bytes already: their A is natural either way
     const bool nat = BITS == 4 && natural;
-#define G4_TILE(NS_, NAT_)                                                                        \
-    hipLaunchKernelGGL((qgemm_tile_kernel<BITS, NS_, NAT_>), dim3(blocks), dim3(256), 0, stream,   \
-                       codes, w, scales, dst, m, n, k, in_scale, out_scale, out_kind, tiles_m, tiles_n)
-    if (nk >= 3 && nat) G4_TILE(4, true);
-    else if (nk >= 3) G4_TILE(4, false);
-    else if (nat) G4_TILE(3, true);
-    else G4_TILE(3, false);
+#define G4_TILE(NS_, NAT_, BM_)                                                                   \
+    hipLaunchKernelGGL((qgemm_tile_kernel<BITS, NS_, NAT_, BM_>), dim3(blocks), dim3(256), 0,      \
+                       stream, codes, w, scales, dst, m, n, k, in_scale, out_scale, out_kind,     \
+                       tiles_m, tiles_n)
+    if (half) {
+        if (nk >= 3 && nat) G4_TILE(4, true, 32);
+        else if (nk >= 3) G4_TILE(4, false, 32);
+        else if (nat) G4_TILE(3, true, 32);
+        else G4_TILE(3, false, 32);
+    } else {
+        if (nk >= 3 && nat) G4_TILE(4, true, 64);
+        else if (nk >= 3) G4_TILE(4, false, 64);
+        else if (nat) G4_TILE(3, true, 64);
+        else G4_TILE(3, false, 64);
+    }
 #undef G4_TILE
     G4_LAUNCHED("qgemm_tile_kernel");
     return G4_OK;
@@ -1389,12 +1423,57 @@ static int check_linear(int bits, const void *wq, const float *scales, const voi
     return G4_OK;
 }
 
-// Whether a call takes the tile kernel with f16 / f32 activations, which are snapped into a
-// buffer of M * K codes first (the only path of this file that needs memory beyond its operands).
+// The small-M kernel snaps f16 / f32 activations itself, in every one of its blocks: past about
+// 4 Mi snaps in total (M * K per block times the blocks along N), one snap pass over the M * K
+// activations into a buffer of codes, then the kernel on int8 codes, costs less (config 2: M = 8,
+// K = 1536 over 384 blocks is 4.7 Mi).
+static bool small_presnap(int m, int n, int k) {
+    return (int64_t)m * k * ((n + 15) / 16) >= ((int64_t)1 << 22);
+}
+
+// Whether a call snaps f16 / f32 activations into a buffer of M * K codes first (the tile kernels,
+// and the small-M kernel past small_presnap): the only paths of this file that need memory beyond
+// their operands.
 static bool needs_codes_buffer(int bits, int m, int n, int k, float in_scale, int x_kind,
                                bool gemm_mode) {
     const KernelChoice c = pick_kernel(bits, m, n, k, in_scale, gemm_mode);
-    return (c == K_TILE128 || c == K_WIDE) && x_kind != G4_KIND_I8;
+    if (x_kind == G4_KIND_I8) return false;
+    if (c == K_TILE128 || c == K_WIDE) return true;
+    return (c == K_SKINNY16 || c == K_SKINNY32) && small_presnap(m, n, k);
+}
+
+// The snap pass: M * K f16 / f32 activations (16-byte aligned, K % 128 == 0) into int8 codes in
+// `given` or the stream's workspace, interleaved per 8-code group when perm (the tile kernels'
+// 4-bit layout) or in natural order.
+static int snap_pass(const void *x, int x_kind, int m, int k, float in_scale, bool perm,
+                     hipStream_t stream, int8_t *given, const int8_t **codes) {
+    void *ws = given;
+    if (!ws) {
+        int rc = workspace(stream, (size_t)m * k, &ws);
+        if (rc) return rc;
+    }
+    const int64_t n8 = (int64_t)m * k / 8;
+    const int64_t per_block = (int64_t)kQuantThreads * kQuantGroups;
+    const int qblocks = (int)std::min<int64_t>((n8 + per_block - 1) / per_block, 8 * 1024);
+    int8_t *wsc = reinterpret_cast<int8_t *>(ws);
+    if (x_kind == G4_KIND_F16) {
+        if (perm)
+            hipLaunchKernelGGL((quantize_rows_kernel<true, true>), dim3(qblocks), dim3(kQuantThreads), 0,
+                               stream, x, n8, in_scale, wsc);
+        else
+            hipLaunchKernelGGL((quantize_rows_kernel<false, true>), dim3(qblocks), dim3(kQuantThreads), 0,
+                               stream, x, n8, in_scale, wsc);
+    } else {
+        if (perm)
+            hipLaunchKernelGGL((quantize_rows_kernel<true, false>), dim3(qblocks), dim3(kQuantThreads), 0,
+                               stream, x, n8, in_scale, wsc);
+        else
+            hipLaunchKernelGGL((quantize_rows_kernel<false, false>), dim3(qblocks), dim3(kQuantThreads), 0,
+                               stream, x, n8, in_scale, wsc);
+    }
+    G4_LAUNCHED("quantize_rows_kernel");
+    *codes = wsc;
+    return G4_OK;
 }
 
 // given_codes: a caller's buffer for the snapped codes (at least M * K bytes, checked by the
@@ -1423,7 +1502,15 @@ static int run_linear(int bits, const void *wq, const float *scales, const void 
     if (k > 16384)
         return set_error(G4_ERR_INVALID, "%s: K %d exceeds 16384 (the exact int32/f32 bound)", who, k);
     if (c == K_SKINNY16 || c == K_SKINNY32) {
-        // One launch: the activation snap is fused into the small-M kernel.
+        // One launch, the activation snap fused into the small-M kernel; or, past small_presnap,
+        // the snap pass first (natural order: the kernel's int8 path interleaves for 4-bit).
+        if (x_kind != G4_KIND_I8 && small_presnap(m, n, k)) {
+            const int8_t *codes = nullptr;
+            int rc = snap_pass(x, x_kind, m, k, in_scale, false, stream, given_codes, &codes);
+            if (rc) return rc;
+            x = codes;
+            x_kind = G4_KIND_I8;
+        }
         SmallJobs jobs{};
         jobs.w[0] = reinterpret_cast<const uint8_t *>(wq);
         jobs.scales[0] = scales;
@@ -1440,20 +1527,8 @@ static int run_linear(int bits, const void *wq, const float *scales, const void 
     const int8_t *codes = reinterpret_cast<const int8_t *>(x);
     const bool natural = x_kind == G4_KIND_I8;
     if (!natural) {
-        const int kp = k;  // k % 128 == 0 on the MFMA kernels
-        void *ws = given_codes;
-        if (!ws) {
-            int rc = workspace(stream, (size_t)m * kp, &ws);
-            if (rc) return rc;
-        }
-        if (bits == 4)
-            hipLaunchKernelGGL(quantize_rows_kernel<true>, dim3(m), dim3(kQuantThreads), 0, stream,
-                               x, x_kind, k, kp, in_scale, reinterpret_cast<int8_t *>(ws));
-        else
-            hipLaunchKernelGGL(quantize_rows_kernel<false>, dim3(m), dim3(kQuantThreads), 0, stream,
-                               x, x_kind, k, kp, in_scale, reinterpret_cast<int8_t *>(ws));
-        G4_LAUNCHED("quantize_rows_kernel");
-        codes = reinterpret_cast<const int8_t *>(ws);
+        int rc = snap_pass(x, x_kind, m, k, in_scale, bits == 4, stream, given_codes, &codes);
+        if (rc) return rc;
     }
     const uint8_t *w = reinterpret_cast<const uint8_t *>(wq);
     if (c == K_WIDE) {

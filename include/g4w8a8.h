@@ -87,7 +87,9 @@ int g4_event_elapsed_ms(float *ms, void *start, void *end);
  * decode loop is launch-bound (a launch costs microseconds of host time, more than a small GEMV
  * runs); the reference caches its per-token encode the same way (runtime.ts:702-767). Kernels of
  * this library never allocate or memset inside a capture. g4_qgemm / g4_linear with f16 or f32
- * activations at M > 32 snap them into a per-stream workspace: it must already be large enough when
+ * activations at M > 32 (and at M >= 3 once M * K * ceil(N / 16) reaches 4 Mi, where one snap pass
+ * beats the small-M kernel snapping in every block) snap them into a per-stream workspace: it must
+ * already be large enough when
  * the capture starts (run the same shape once on the stream first); a call that would grow it
  * inside a capture is refused with G4_ERR_INVALID. A workspace whose address a capture took is never
  * freed (a graph may be replayed later, on any stream); g4_stream_destroy frees the stream's
@@ -141,7 +143,7 @@ int g4_linear(int bits, const void *wq, const float *scales, const void *x, int 
  * g4_qgemm for callers that cannot allocate device memory: code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc. No counterpart in the reference. Same arguments,
  * routing and results as g4_qgemm. The one buffer g4_qgemm needs beyond its operands (the snapped
- * activation codes of the tile path: f16 / f32 x at M > 32, M * K bytes) is a static device array of
+ * activation codes: f16 / f32 x on the paths that snap first, M * K bytes) is a static device array of
  * g4_qgemm_noalloc_max_codes() bytes (8 MiB) that each GPU holds until the process ends; a call
  * whose path needs more is refused with G4_ERR_INVALID before anything is enqueued. It calls no
  * hipMalloc / hipFree. Every call on one GPU shares that GPU's array: calls that overlap on one GPU
