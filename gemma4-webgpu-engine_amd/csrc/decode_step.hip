@@ -183,6 +183,7 @@ int check_shape(const g4_decode_shape &s) {
         return set_error(G4_ERR_INVALID, "decode: vocab %lld", (long long)s.vocab);
     if (s.in_scale <= 0.0f || s.out_scale <= 0.0f)
         return set_error(G4_ERR_INVALID, "decode: the static scales must be calibrated (non-zero)");
+    if (s.fold_off < 0 || s.fold_off > 7) return set_error(G4_ERR_INVALID, "decode: fold_off %d (bits 0..2)", s.fold_off);
     for (int l = 0; l < s.layers; ++l)
         if (kv_source(s, l) < 0)
             return set_error(G4_ERR_INVALID, "decode: layer %d has no producer of its kind", l);
@@ -431,7 +432,7 @@ int build(g4_decode &d) {
     // partial into one int32 accumulator; the post-attention join applies o_proj's epilogue and
     // snap to it, so it reads o_proj's own codes (one launch fewer per layer)
     bool &fold_o = d.fold_o;
-    fold_o = true;
+    fold_o = !(s.fold_off & 1);
     for (int l = 0; l < s.layers; ++l) {
         MergeLinear lin;
         lin.w = d.layers[l].o;
@@ -443,12 +444,12 @@ int build(g4_decode &d) {
     // per_layer_input_gate and per_layer_projection in one launch when every layer fits it: the
     // post-FFN join, the gate rows with their gelu x per-layer-row epilogue and the projection's
     // K range of those rows, added atomically into one int32 accumulator that the tail join reads
-    d.fold_ple = true;
+    d.fold_ple = !(s.fold_off & 4);
     for (int l = 0; l < s.layers; ++l) d.fold_ple = d.fold_ple && ple_fold_fits(ple_fold(d, l, d.hbuf[0]));
     // gate / up / gelu-mul / down in one launch when every layer fits it: each block's gate and up
     // rows, their gelu-mul codes, and down's K range of those codes added atomically into one
     // int32 accumulator that the post-FFN join reads
-    d.fold_ffn = true;
+    d.fold_ffn = !(s.fold_off & 2);
     for (int l = 0; l < s.layers; ++l)
         d.fold_ffn = d.fold_ffn && ffn_fold_fits(ffn_fold(d, l, reinterpret_cast<int32_t *>(d.hbuf[0])));
     if (fold_o || d.fold_ple || d.fold_ffn)

@@ -217,6 +217,65 @@ int g4_graph_begin_capture(void *stream) {
     return G4_OK;
 }
 
+namespace {
+
+bool device_address(const void *p) {
+    hipPointerAttribute_t a{};
+    if (!p || hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError();  // an address the runtime does not know is host memory
+        return false;
+    }
+    return a.type == hipMemoryTypeDevice;
+}
+
+// G4_OK when every node of a captured graph is one a replay can run without touching host
+// storage: kernels, device-to-device copies, empty, event record and event wait nodes.
+int captured_node_refusal(hipGraph_t graph) {
+    size_t count = 0;
+    G4_HIP(hipGraphGetNodes(graph, nullptr, &count));
+    std::vector<hipGraphNode_t> nodes(count);
+    if (count) G4_HIP(hipGraphGetNodes(graph, nodes.data(), &count));
+    for (hipGraphNode_t n : nodes) {
+        hipGraphNodeType type;
+        G4_HIP(hipGraphNodeGetType(n, &type));
+        switch (type) {
+        case hipGraphNodeTypeKernel:
+        case hipGraphNodeTypeEmpty:
+        case hipGraphNodeTypeEventRecord:
+        case hipGraphNodeTypeWaitEvent:
+            break;
+        case hipGraphNodeTypeMemcpy: {
+            hipMemcpy3DParms p{};
+            if (hipGraphMemcpyNodeGetParams(n, &p) != hipSuccess) {
+                (void)hipGetLastError();
+                return set_error(G4_ERR_INVALID,
+                                 "graph capture: the graph holds a copy whose ends cannot be inspected; "
+                                 "enqueue host copies outside the capture");
+            }
+            const bool d2d = p.kind == hipMemcpyDeviceToDevice ||
+                             (p.kind == hipMemcpyDefault && device_address(p.srcPtr.ptr) &&
+                              device_address(p.dstPtr.ptr));
+            if (!d2d)
+                return set_error(G4_ERR_INVALID,
+                                 "graph capture: the graph holds a copy to or from host memory, which "
+                                 "every replay would touch after the enqueuing call returned; enqueue "
+                                 "host copies outside the capture");
+            break;
+        }
+        case hipGraphNodeTypeMemset:
+            return set_error(G4_ERR_INVALID,
+                             "graph capture: the graph holds a memset node; clear device memory "
+                             "with a fill kernel (g4_fill_u8) inside a graph");
+        default:
+            return set_error(G4_ERR_INVALID, "graph capture: the graph holds a node of type %d; "
+                             "only kernels, device copies and events are replayed", (int)type);
+        }
+    }
+    return G4_OK;
+}
+
+}  // namespace
+
 // The handle of a captured graph: the executable and an event recorded after each launch, so
 // destroy waits for this graph's own replays and nothing else on the device.
 struct G4Graph {
@@ -229,6 +288,17 @@ int g4_graph_end_capture(void *stream, void **graph_exec) {
     if (!stream || !graph_exec) return set_error(G4_ERR_INVALID, "g4_graph_end_capture: NULL argument");
     hipGraph_t graph = nullptr;
     G4_HIP(hipStreamEndCapture(as_stream(stream), &graph));
+    // A kernel node holds copies of its arguments, so a replay reads no storage of the caller's
+    // beyond the device buffers those arguments name. A copy node would read or write its host
+    // buffer at every replay, long after the call that enqueued it returned (and a host buffer
+    // freed by then is a host fault inside the graph launch), and memset nodes have given wrong
+    // results on replays after the first. The graph keeps kernels, device-to-device copies and
+    // the stream's own event and empty nodes only.
+    const int bad = captured_node_refusal(graph);
+    if (bad != G4_OK) {
+        (void)hipGraphDestroy(graph);
+        return bad;
+    }
     hipGraphExec_t exec = nullptr;
     hipError_t err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);

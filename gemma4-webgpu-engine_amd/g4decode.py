@@ -39,6 +39,9 @@ class Shape:
     final_softcap: float = 30.0
     in_scale: float = float(np.float32(0.05))
     out_scale: float = float(np.float32(0.1))
+    # batch 1: launch folds left out even where they fit (bit 0 o_proj in the merge, bit 1 the
+    # FFN block, bit 2 the per-layer-input block); a test switch, results are identical
+    fold_off: int = 0
 
     def c(self) -> g4.DecodeShape:
         return g4.DecodeShape(**{f.name: getattr(self, f.name) for f in fields(self)})

@@ -81,7 +81,7 @@ class DecodeShape(ctypes.Structure):
                                       "head_dim", "ple_dim", "global_period", "sliding_window",
                                       "kv_capacity", "batch")] + [
         ("vocab", _i64), ("eps", _c_float), ("final_softcap", _c_float), ("in_scale", _c_float),
-        ("out_scale", _c_float)]
+        ("out_scale", _c_float), ("fold_off", _c_int)]
 
 
 DECODE_LAYER_FIELDS = ("q", "k", "v", "o", "gate", "up", "down", "ple_gate", "ple_proj",

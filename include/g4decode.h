@@ -151,6 +151,12 @@ typedef struct g4_decode_shape {
     float final_softcap; /* 30 */
     float in_scale;      /* the static input snap every calibrated linear uses */
     float out_scale;     /* the static output snap every calibrated linear uses */
+    /* Batch 1 only, a test switch: the launch folds the runner leaves out even where they fit.
+     * Bit 0: o_proj stays a GEMV plan (not inside the attention merge); bit 1: gate / up /
+     * gelu-mul / down stay plans (no FFN block); bit 2: per_layer_input_gate and
+     * per_layer_projection stay plans (no per-layer-input block). 0 (a zeroed shape) folds every
+     * one that fits. Results are identical either way. */
+    int fold_off;
 } g4_decode_shape;
 
 /* One layer's weights (device pointers). Projections: int4 packed [N][K/2] (q, k, v, o, gate, up,

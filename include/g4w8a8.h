@@ -96,7 +96,11 @@ int g4_event_elapsed_ms(float *ms, void *start, void *end);
  * workspace otherwise. g4_graph_destroy waits for the graph's own last launch (an event recorded
  * after each g4_graph_launch, on the stream it was launched on), not for the whole device, and
  * releases the graph even when that wait fails. Launches of one graph on several streams must be
- * ordered by the caller (the event marks the most recent launch). */
+ * ordered by the caller (the event marks the most recent launch). g4_graph_end_capture refuses
+ * (G4_ERR_INVALID, nothing instantiated, the stream out of capture) a graph holding anything but
+ * kernels, device-to-device copies, events and empty nodes: a captured copy to or from host memory
+ * would touch that host buffer at every replay, after the enqueuing call returned, and memset
+ * nodes have given wrong results on replays after the first (clear with g4_fill_u8 instead). */
 int g4_graph_begin_capture(void *stream);
 int g4_graph_end_capture(void *stream, void **graph_exec);
 int g4_graph_launch(void *graph_exec, void *stream);

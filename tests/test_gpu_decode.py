@@ -328,6 +328,26 @@ def test_decode_step_tiny(gpu, batch, ffn, pos0):
             print("next tokens", got["next"], flush=True)
 
 
+# Batch 1 folds o_proj into the attention merge (bit 0), gate / up / gelu-mul / down into the FFN
+# block (bit 1) and the per-layer-input pair into its block (bit 2) wherever they fit; each mix of
+# folded and plan forms hands its int32 accumulators or codes to a different join. Hidden 512 fits
+# all three, so fold_off walks every combination; hidden 768 (not a multiple of 512) leaves the FFN
+# block out by shape, with the merge and per-layer-input folds on, then with the latter off.
+@pytest.mark.parametrize("hidden,fold_off", [(512, f) for f in range(1, 8)] + [(768, 0), (768, 4)])
+def test_decode_batch1_fold_combinations(gpu, hidden, fold_off):
+    print(f"decode batch 1 hidden={hidden} fold_off={fold_off}", flush=True)
+    shape = tiny_shape(1, hidden=hidden, fold_off=fold_off)
+    for got, want, dkv, rkv in run_steps(gpu, shape, [[5], [2999]], pos0=700):
+        check_step(got, want, dkv, rkv)
+
+
+def test_decode_fold_off_range(gpu):
+    import g4decode as gd
+    shape = tiny_shape(1, fold_off=8)
+    with pytest.raises(gpu.G4Error, match="fold_off 8"):
+        gd.Decoder(shape, gd.SyntheticModel(tiny_shape(1), seed=4))
+
+
 def test_decode_stop_after_each_layer(gpu):
     shape = tiny_shape(1, layers=5, kv_producers=3)
     for stop in range(shape.layers - 1):
