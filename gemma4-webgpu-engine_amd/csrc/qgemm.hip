@@ -257,11 +257,15 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
     constexpr int BATCH = WAVES >= 16 ? 1 : 4;
     constexpr int NP = EPI == 1 ? 2 : 1;             // product sets: the gate's (and the up's)
     constexpr int NACC = BITS == 4 ? (NP + 1) * TM : NP * TM;  // products, then the row sums
-    // the codes during the K loop, then every wave's partial tiles for the fold (the same bytes)
+    // the codes during the K loop, and every wave's partial tiles for the fold: in a region of
+    // their own when both fit (two blocks of 4 waves per CU, or one of 16), so the fold needs no
+    // barrier for the last reads of the codes; else over the codes' bytes
     constexpr int XS_BYTES = MT * XSTR, RED_BYTES = WAVES * NACC * 64 * 16;
-    __shared__ __align__(16) int8_t smem[XS_BYTES > RED_BYTES ? XS_BYTES : RED_BYTES];
+    constexpr bool SEP_RED = XS_BYTES + RED_BYTES <= (WAVES >= 16 ? 160 * 1024 : 80 * 1024);
+    __shared__ __align__(16) int8_t smem[SEP_RED ? XS_BYTES + RED_BYTES
+                                                 : (XS_BYTES > RED_BYTES ? XS_BYTES : RED_BYTES)];
     int8_t *xs = smem;
-    v4i(*red)[NACC][64] = reinterpret_cast<v4i(*)[NACC][64]>(smem);
+    v4i(*red)[NACC][64] = reinterpret_cast<v4i(*)[NACC][64]>(smem + (SEP_RED ? XS_BYTES : 0));
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -319,7 +323,9 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
         const int ksteps = kcn / kTileBK;
         const int kbase = kc0 / kTileBK;
         // The chunk's first batch of weights is requested before the codes are copied, so the two
-        // memory latencies overlap (the weights do not depend on the codes).
+        // memory latencies overlap (the weights do not depend on the codes). Requesting the codes
+        // first measured slower: every block reads the same few KB of codes, and at the head of
+        // the queue those requests pile onto the same L2 lines.
         u32x4 bw_first[NP][BATCH][BITS == 4 ? 1 : 2];
         load_small_weights<BITS, NP, BATCH, WAVES>(bw_first, wrow, wrow2, wave, ksteps, kbase, g);
         lds_barrier();  // the previous chunk's codes are no longer read
@@ -432,6 +438,19 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
             } else {
                 load_small_weights<BITS, NP, BATCH, WAVES>(bw, wrow, wrow2, kb0, ksteps, kbase, g);
             }
+            // every A operand of the batch read from LDS before the first MFMA, so the reads'
+            // latencies overlap (step indices clamped: a step past the end is read, not used)
+            v4i av[BATCH][2][TM];
+#pragma unroll
+            for (int u = 0; u < BATCH; ++u) {
+                const int kb = min(kb0 + WAVES * u, ksteps - 1);
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+#pragma unroll
+                    for (int t = 0; t < TM; ++t)
+                        av[u][s][t] = *reinterpret_cast<const v4i *>(
+                            &xs[(t * 16 + j) * XSTR + kb * kTileBK + g * 32 + s * 16]);
+            }
 #pragma unroll
             for (int u = 0; u < BATCH; ++u) {
                 const int kb = kb0 + WAVES * u;
@@ -449,8 +468,7 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
                         }
 #pragma unroll
                         for (int t = 0; t < TM; ++t) {
-                            const v4i a = *reinterpret_cast<const v4i *>(
-                                &xs[(t * 16 + j) * XSTR + kb * kTileBK + g * 32 + s * 16]);
+                            const v4i a = av[u][s][t];
 #pragma unroll
                             for (int p = 0; p < NP; ++p)
                                 acc[p * TM + t] =
@@ -463,11 +481,16 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_small_kernel(
                 }
             }
         }
+        // A batch's clamped loads past the last step are never read; without this wait the
+        // compiler counts them as pending into the next chunk and waits for every load in flight
+        // (the epilogue's early operand loads included) before the next chunk's first request.
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
     // Fold: every wave leaves its partial tiles in LDS (over the codes, once all waves are done
-    // with them); then the block's threads take the outputs, each summing the waves' partials of
-    // one (row, column) in wave order, so the epilogue (a gelu for EPI) is spread over all waves.
-    __syncthreads();
+    // with them, when the two share bytes); then the block's threads take the outputs, each
+    // summing the waves' partials of one (row, column) in wave order, so the epilogue (a gelu for
+    // EPI) is spread over all waves.
+    if (!SEP_RED) __syncthreads();
 #pragma unroll
     for (int t = 0; t < NACC; ++t) red[wave][t][lane] = acc[t];
     __syncthreads();
