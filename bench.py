@@ -245,6 +245,36 @@ def bench_config0(h, stream_obj, reps=512):
     return out
 
 
+def bench_tile8u(h, stream_obj, reps=64):
+    """qgemv-4bit's tile8u geometry (qgemv.ts:870-1015) beside the classic routing, on config 1's
+    gate (6144 x 1536) and down (1536 x 6144) shapes, f32 activations, calibrated, int8 out: each
+    warm (one weight buffer) and graph-replayed. Bytes as the classic row: weights + scales + x
+    (f32 here) + out."""
+    rows = []
+    for name, n, k in (("gate", syn.FFN, syn.HIDDEN), ("down", syn.HIDDEN, syn.FFN)):
+        w = g4.DeviceBuffer.from_array(syn.int4_weights("t8b", name, n, k))
+        s = g4.DeviceBuffer.from_array(syn.row_scales("t8b", name, n))
+        tw = g4.DeviceBuffer(g4.tile8u_bytes(k, n), np.uint32)
+        g4.tile8u_repack(w, tw, k, n, stream=h)
+        x = g4.DeviceBuffer.from_array(syn.activations("t8b", name, 1, k)[0].astype(np.float32))
+        d = g4.DeviceBuffer.empty((n,), np.int8)
+        by = n * k // 2 + 4 * n + 4 * k + n
+        row = {"shape": name, "n": n, "k": k, "bytes": by}
+        for form, call in (
+                ("classic", lambda j: g4.qgemv(4, w, s, x, d, k, n, 1, syn.IN_SCALE, syn.OUT_SCALE,
+                                               stream=h)),
+                ("tile8u", lambda j: g4.qgemv_tile8u(tw, s, x, d, k, n, syn.IN_SCALE, syn.OUT_SCALE,
+                                                     stream=h))):
+            us, us_g = timed_pair(h, stream_obj, call, 1, reps)
+            row[form] = {"us": round(us, 3), "us_graph": round(us_g, 3),
+                         "gbs_graph": round(by / (us_g * 1e-6) / 1e9, 2)}
+        row["classic_kernel"] = g4.kernel_for_shape(4, 1, n, k)
+        rows.append(row)
+        for b in (w, s, tw, x, d):
+            b.close()
+    return rows
+
+
 def cpu_extra(seconds=4.0):
     """The oracle on the host cores for the other rows (bounded samples): the config-2 GEMM at
     M=16 and the config-3 gather at 64 tokens."""
@@ -512,6 +542,8 @@ def main():
                     help="only config-4 decode steps at this batch (graph replays), for rocprofv3")
     ap.add_argument("--gather-probe", action="store_true",
                     help="only the config-3 gather launches (2048 tokens, 5 slices), for rocprofv3")
+    ap.add_argument("--tile8u-probe", action="store_true",
+                    help="only the tile8u and classic GEMV launches on config 1's gate and down")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this path is measured on one GPU; --gpus {args.gpus} is not supported "
@@ -525,6 +557,9 @@ def main():
     h = stream.handle
     if args.gemm_probe:
         gemm_probe(h)
+        return
+    if args.tile8u_probe:
+        print(json.dumps(bench_tile8u(h, stream)))
         return
     if args.decode_probe:
         bench_decode(h, args.decode_probe, steps=10, probe=True)
@@ -598,6 +633,8 @@ def main():
         log("config 2 sweep over M, config 1 int8 down")
         sweep = bench_gemm_sweep(h, stream)
         down8 = bench_int8_down(h, stream)
+        log("qgemv-4bit tile8u geometry beside the classic loop")
+        t8 = bench_tile8u(h, stream)
         log("measured HBM copy rate")
         hbm = hbm_copy_rate(h)
         log("config 4 decode step, batch 1 and 32")
@@ -613,6 +650,7 @@ def main():
             "int8_gemm_m512": gm,
             "gemm_sweep_config2": sweep,
             "config1_int8_down": down8,
+            "tile8u_config1": t8,
             "ple_gather": ga,
             "hbm_measured": hbm,
         }

@@ -177,6 +177,9 @@ SIGNATURES = {
                                       _vp]),
     "g4_qgemv_gelu": (_c_int, [_c_int, _vp, _vp, _vp, _c_int, ctypes.POINTER(GeluAct), _vp, _c_int,
                                _c_int, _c_int, _c_float, _c_float, _vp]),
+    "g4_tile8u_repack": (_c_int, [_vp, _vp, _c_int, _c_int, _vp]),
+    "g4_qgemv_tile8u": (_c_int, [_vp, _vp, _vp, _c_int, ctypes.POINTER(GeluAct), _vp, _c_int, _c_int,
+                                 _c_int, _c_float, _c_float, _vp]),
     "g4_qgemv_gelu_split": (_c_int, [_c_int, _vp, _vp, _vp, _c_int, ctypes.POINTER(GeluAct), _vp,
                                      _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
     "g4_qgemv_gelu_m2": (_c_int, [_c_int, _vp, _vp, _vp, _c_int, ctypes.POINTER(GeluAct), _vp,
@@ -597,6 +600,26 @@ def gelu_mul(gate, up, dst, count, srq_scale=0.0, stream=None):
                                  stream))
 
 
+def tile8u_bytes(k, num_rows) -> int:
+    """Bytes of a 4-bit matrix in the tile8u layout: ceil(N / 8) tiles of K u32 words."""
+    return (num_rows + 7) // 8 * k * 4
+
+
+def tile8u_repack(wq, tile_wq, k, num_rows, stream=None):
+    """The eight-row tile layout of a row-layout 4-bit matrix (qgemv.ts:871-876)."""
+    _check(lib().g4_tile8u_repack(_ptr(wq), _ptr(tile_wq), k, num_rows, stream))
+
+
+def qgemv_tile8u(tile_wq, scales, x, dst, k, num_rows, in_scale=0.0, out_scale=0.0,
+                 act: "GeluAct | None" = None, x_kind=None, out_kind=None, stream=None):
+    """qgemv-4bit (or qgemv-4bit-gelu with act) on the tile8u geometry (qgemv.ts:870-1015)."""
+    _check(lib().g4_qgemv_tile8u(_ptr(tile_wq), _ptr(scales), _ptr(x),
+                                 x.kind if x_kind is None else x_kind,
+                                 ctypes.byref(act) if act is not None else None, _ptr(dst),
+                                 dst.kind if out_kind is None else out_kind, k, num_rows,
+                                 float(in_scale), float(out_scale), stream))
+
+
 def qgemv_split(bits, wq, scales, x, partials, k, num_rows, k_splits, exact, in_scale,
                 stream=None):
     _check(lib().g4_qgemv_split(bits, _ptr(wq), _ptr(scales), _ptr(x), x.kind, _ptr(partials), k,
@@ -680,9 +703,36 @@ def _need(inputs, names, who):
         raise G4Error(1, f"{who} needs inputs named {', '.join(names)}")
 
 
+# GemvGeometry.inner per bit width (qgemv.ts:146, 239-241; the device profile's setGemvGeometry):
+# 'tile8u' makes the 4-bit pipeline the tile loop (qgemv.ts:440), which reads wq in the eight-row
+# tile layout (tile8u_repack). The 8-bit family has no tile loop, so there it runs the classic one.
+_gemv_inner = {4: "classic", 8: "classic"}
+
+
+def set_gemv_inner(bits: int, inner: str):
+    if bits not in _gemv_inner:
+        raise G4Error(1, f"gemv geometry: bits must be 4 or 8, got {bits}")
+    if inner not in ("classic", "tile8u"):
+        raise G4Error(1, f"gemv geometry: inner must be classic or tile8u on this build, got {inner}")
+    _gemv_inner[bits] = inner
+
+
+def gemv_inner(bits: int) -> str:
+    return _gemv_inner[bits]
+
+
+def _tile8u(bits) -> bool:
+    return bits == 4 and _gemv_inner[4] == "tile8u"
+
+
 def _bind_gemv(bits, wide):
     def run(inputs, output, params, stream=None):
         _need(inputs, ["wq", "scales", "x"], f"qgemv-{bits}bit")
+        if not wide and _tile8u(bits):
+            qgemv_tile8u(inputs["wq"], inputs["scales"], inputs["x"], output, int(_p(params, "k", 0)),
+                         int(_p(params, "numRows", 0)), _p(params, "inScale", 0.0),
+                         _p(params, "outScale", 0.0), stream=stream)
+            return
         cols = int(_p(params, "cols", 1)) if wide else 1
         qgemv(bits, inputs["wq"], inputs["scales"], inputs["x"], output, int(_p(params, "k", 0)),
               int(_p(params, "numRows", 0)), cols, _p(params, "inScale", 0.0),
@@ -720,6 +770,8 @@ def _bind_batch(count):
 def _bind_split(bits):
     def run(inputs, output, params, stream=None):
         _need(inputs, ["wq", "scales", "x"], f"qgemv-{bits}bit-split")
+        if _tile8u(bits):
+            raise G4Error(1, "qgemv-4bit tile8u has no K split yet")
         qgemv_split(bits, inputs["wq"], inputs["scales"], inputs["x"], output,
                     int(_p(params, "k", 0)), int(_p(params, "numRows", 0)),
                     int(_p(params, "kSplits", 1)), bool(_p(params, "exact", 0)),
@@ -763,6 +815,11 @@ def _bind_gelu(bits, split, wide=False):
                              int(_p(params, "k", 0)), int(_p(params, "numRows", 0)),
                              int(_p(params, "kSplits", 1)), True, _p(params, "inScale", 0.0),
                              stream=stream)
+        elif not wide and _tile8u(bits):
+            qgemv_tile8u(inputs["wq"], inputs["scales"], inputs["gate"], output,
+                         int(_p(params, "k", 0)), int(_p(params, "numRows", 0)),
+                         _p(params, "inScale", 0.0), _p(params, "outScale", 0.0), act=act,
+                         stream=stream)
         elif wide:
             qgemv_gelu_m2(bits, inputs["wq"], inputs["scales"], inputs["gate"], act, output,
                           int(_p(params, "k", 0)), int(_p(params, "numRows", 0)),

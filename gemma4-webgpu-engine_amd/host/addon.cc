@@ -379,6 +379,25 @@ napi_value QgemvGelu(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// tile8u (qgemv.ts:870-1015): (wq, tileWq, k, numRows[, stream]) and (tileWq, scales, x, xKind,
+// up, upKind, upOffset, dst, outKind, k, numRows, inScale, outScale[, gateScale, upScale, stream]);
+// up null: no gelu prologue.
+napi_value Tile8uRepack(napi_env env, napi_callback_info info) {
+    Args a(env, info, 5);
+    if (throw_status(env, g4_tile8u_repack(a.ptr(0), a.ptr(1), a.i32(2), a.i32(3), a.ptr(4)))) return nullptr;
+    return undefined(env);
+}
+
+napi_value QgemvTile8u(napi_env env, napi_callback_info info) {
+    Args a(env, info, 16);
+    g4_gelu_act act{a.ptr(4), a.i32(5), (float)a.num(13), (float)a.num(14), (int64_t)a.num(6)};
+    int st = g4_qgemv_tile8u(a.ptr(0), (const float *)a.ptr(1), a.ptr(2), a.i32(3), act.up ? &act : nullptr,
+                             a.ptr(7), a.i32(8), a.i32(9), a.i32(10), (float)a.num(11), (float)a.num(12),
+                             a.ptr(15));
+    if (throw_status(env, st)) return nullptr;
+    return undefined(env);
+}
+
 // qgemv-4bit-gelu-exact-split: (bits, wq, scales, gate, gateKind, up, upKind, upOffset, partials,
 // k, numRows, kSplits, exact, inScale[, gateScale, upScale])
 napi_value QgemvGeluSplit(napi_env env, napi_callback_info info) {
@@ -985,6 +1004,7 @@ napi_value Init(napi_env env, napi_value exports) {
         {"projectionBatch", ProjectionBatch}, {"qgemvGrouped", QgemvGrouped},
         {"qgemvSplit", QgemvSplit}, {"qgemvMerge", QgemvMerge},
         {"qgemvGelu", QgemvGelu}, {"qgemvGeluSplit", QgemvGeluSplit},
+        {"tile8uRepack", Tile8uRepack}, {"qgemvTile8u", QgemvTile8u},
         {"qgemvGeluM2", QgemvGeluM2}, {"pleGateSplit", PleGateSplit},
         {"pleFoldProjection", PleFoldProjection}, {"geluMulF32", GeluMulF32},
         {"qgemvExactMerge", QgemvExactMerge}, {"srqQuantize", SrqQuantize},

@@ -116,9 +116,38 @@ function num(params, key, dflt) {
 
 // ---- the registry seam ------------------------------------------------------------------------
 
+// GemvGeometry.inner per bit width (qgemv.ts:146, 239-241; setGemvGeometry in the device profile):
+// 'tile8u' makes the 4-bit pipeline the tile loop (qgemv.ts:440), whose wq is the eight-row tile
+// layout (tile8uRepack). The 8-bit family has no tile loop and keeps the classic one.
+const gemvInnerOf = { 4: 'classic', 8: 'classic' };
+function gemvInner(bits) { return gemvInnerOf[bits]; }
+function setGemvInner(bits, inner) {
+  if (!(bits in gemvInnerOf)) throw new Error(`gemv geometry: bits must be 4 or 8, got ${bits}`);
+  if (inner !== 'classic' && inner !== 'tile8u') {
+    throw new Error(`gemv geometry: inner must be classic or tile8u on this build, got ${inner}`);
+  }
+  gemvInnerOf[bits] = inner;
+}
+const tile8u = bits => bits === 4 && gemvInnerOf[4] === 'tile8u';
+function tile8uBytes(k, numRows) { return Math.ceil(numRows / 8) * k * 4; }
+function tile8uRepack(wq, tileWq, k, numRows, stream) {
+  g4().tile8uRepack(wq.addr, tileWq.addr, k, numRows, streamHandle(stream));
+}
+// qgemv-4bit (up null) or qgemv-4bit-gelu on the tile8u geometry (qgemv.ts:870-1015)
+function qgemvTile8u(tileWq, scales, x, up, upOffsetElems, output, params, stream) {
+  g4().qgemvTile8u(tileWq.addr, scales.addr, x.addr, x.kind, up ? up.addr : 0, up ? up.kind : 0,
+    upOffsetElems, output.addr, output.kind, num(params, 'k', 0), num(params, 'numRows', 0),
+    num(params, 'inScale', 0), num(params, 'outScale', 0), num(params, 'gateScale', 0),
+    num(params, 'upScale', 0), streamHandle(stream));
+}
+
 function gemvKernel(bits, wide) {
   return ({ inputs, output, params, stream }) => {
     need(inputs, ['wq', 'scales', 'x'], `qgemv-${bits}bit`);
+    if (!wide && tile8u(bits)) {
+      qgemvTile8u(inputs.wq, inputs.scales, inputs.x, null, 0, output, params, stream);
+      return;
+    }
     g4().qgemv(bits, inputs.wq.addr, inputs.scales.addr, inputs.x.addr, inputs.x.kind, output.addr,
       output.kind, num(params, 'k', 0), num(params, 'numRows', 0), wide ? num(params, 'cols', 1) : 1,
       num(params, 'inScale', 0), num(params, 'outScale', 0), streamHandle(stream));
@@ -157,6 +186,7 @@ function batchKernel(count) {
 function splitKernel(bits) {
   return ({ inputs, output, params, stream }) => {
     need(inputs, ['wq', 'scales', 'x'], `qgemv-${bits}bit-split`);
+    if (tile8u(bits)) throw new Error('qgemv-4bit tile8u has no K split yet');
     g4().qgemvSplit(bits, inputs.wq.addr, inputs.scales.addr, inputs.x.addr, inputs.x.kind,
       output.addr, num(params, 'k', 0), num(params, 'numRows', 0), num(params, 'kSplits', 1),
       num(params, 'exact', 0) ? 1 : 0, num(params, 'inScale', 0), streamHandle(stream));
@@ -177,6 +207,9 @@ function geluKernel(bits, split, wide) {
     if (split) {
       g4().qgemvGeluSplit(...head, num(params, 'k', 0), num(params, 'numRows', 0),
         num(params, 'kSplits', 1), 1, num(params, 'inScale', 0), ...scales, streamHandle(stream));
+    } else if (!wide && tile8u(bits)) {
+      qgemvTile8u(inputs.wq, inputs.scales, inputs.gate, inputs.up, 4 * num(params, 'upOffset', 0),
+        output, params, stream);
     } else if (wide) {
       g4().qgemvGeluM2(...head, output.kind, num(params, 'k', 0), num(params, 'numRows', 0),
         num(params, 'cols', 0), num(params, 'inScale', 0), num(params, 'outScale', 0), ...scales,
@@ -990,6 +1023,11 @@ module.exports = {
   planProjectionKernels,
   pleGateSplits,
   setPleGateSplits,
+  gemvInner,
+  setGemvInner,
+  tile8uBytes,
+  tile8uRepack,
+  qgemvTile8u,
   planTableSplit,
   sliceForRow,
   slicedGatherDispatches,

@@ -254,6 +254,23 @@ int g4_qgemv_gelu(int bits, const void *wq, const float *scales, const void *gat
                   const g4_gelu_act *act, void *dst, int out_kind, int k, int num_rows,
                   float in_scale, float out_scale, void *stream);
 
+/*
+ * The tile8u geometry of qgemv-4bit and qgemv-4bit-gelu (src/kernels/qgemv.ts:870-1015; compiled in
+ * place of the classic loop when GemvGeometry.inner is 'tile8u', qgemv.ts:440, the bind unchanged,
+ * bindGemv :1299-1363). The weights are in the eight-row tile layout (qgemv.ts:871-876): tile t =
+ * rows 8t .. 8t + 7, K u32 words, word k holding row 8t + r's unsigned code (0..15) at bits 4r.
+ * g4_tile8u_repack builds it from the checkpoint's row layout (tile_wq: ceil(num_rows / 8) * K * 4
+ * bytes; rows past num_rows padded with code 8); the reference ships no repack (the layout was
+ * priced on a sweep page before anything read it, qgemv.ts:893-895). g4_qgemv_tile8u: x as for
+ * g4_qgemv, or with act != NULL the gelu prologue (x is the gate, as g4_qgemv_gelu); dst f32 or
+ * int8 codes; no K split (qgemv.ts:907). Results: calibrated, the classic loop's exactly (the sum
+ * is the same exact integer); uncalibrated, the tile loop's own f32 order (per lane over k =
+ * 128 i + 4 l + j, then the 32-lane tree). */
+int g4_tile8u_repack(const void *wq, void *tile_wq, int k, int num_rows, void *stream);
+int g4_qgemv_tile8u(const void *tile_wq, const float *scales, const void *x, int x_kind,
+                    const g4_gelu_act *act, void *dst, int out_kind, int k, int num_rows,
+                    float in_scale, float out_scale, void *stream);
+
 /* qgemv-4bit-gelu-m2 / qgemv-8bit-gelu-m2 (src/kernels/qgemvWide.ts:660-669, 698-709; bind
  * bindGemvWide(bits, 'gelu') :515-574): the gelu prologue over `cols` token columns (1..2, the
  * draft-verify pass, execute.ts:382-390). gate and up are [cols][K] (column c at element c * K; up

@@ -476,3 +476,70 @@ int64_t or_plan_table_split(int64_t rows_in, int64_t row_bytes_in, int64_t max_b
     }
     return n;
 }
+
+/* qgemv.ts:870-1015 qgemv4TileWgsl (the tile8u loop) on a row-layout 4-bit matrix: lane l of the
+ * 32-lane group takes k = 128 i + 4 l + j (i over K / 128, j = 0..3).
+ *  calibrated: exact sum(u x) and sum(x) in integers (the packed-pair arithmetic of :940-948 is
+ *    exact), f32(sum(u x) - 8 sum(x)) per lane;
+ *  f32: acc_r = acc_r + f32(u) * x_j, one rounding each (no contraction), sxf = sxf + x_j, in
+ *    the loop's order, then acc_r - f32(8 * sxf);
+ *  then sgSum32 (subgroupReduce.ts:49-59): x = x + x[l ^ m] for m = 1, 2, 4, 8, 16, lane 0's value;
+ *  then f32(f32(xs * scale) * sum) (xs = in_scale, or 1 uncalibrated) and srqOut on out_scale. */
+int or_qgemv_tile8u(const uint8_t *packed, const float *scales, const float *x, int64_t num_rows,
+                    int64_t k, float in_scale, float out_scale, float *out_f32, int8_t *codes) {
+    if (k <= 0 || k % 128 != 0) return 1;
+    int calibrated = isfinite(in_scale) && in_scale != 0.0f;
+    int64_t rb = k / 2, iters = k / 128;
+    int8_t *xq = (int8_t *)malloc((size_t)k);
+    if (!xq) return 2;
+    if (calibrated)
+        for (int64_t i = 0; i < k; i++) xq[i] = or_srq_code(x[i], in_scale);
+#pragma omp parallel for schedule(static)
+    for (int64_t row = 0; row < num_rows; row++) {
+        const uint8_t *w = packed + row * rb;
+        float lane[32];
+        for (int l = 0; l < 32; l++) {
+            if (calibrated) {
+                int64_t sux = 0, sx = 0;
+                for (int64_t i = 0; i < iters; i++)
+                    for (int j = 0; j < 4; j++) {
+                        int64_t kk = 128 * i + 4 * l + j;
+                        int u = (w[kk >> 1] >> (4 * (kk & 1))) & 15;
+                        sux += (int64_t)u * xq[kk];
+                        sx += xq[kk];
+                    }
+                lane[l] = (float)(int32_t)(sux - 8 * sx);
+            } else {
+                float acc = 0.0f, sxf = 0.0f;
+                for (int64_t i = 0; i < iters; i++)
+                    for (int j = 0; j < 4; j++) {
+                        int64_t kk = 128 * i + 4 * l + j;
+                        int u = (w[kk >> 1] >> (4 * (kk & 1))) & 15;
+                        sxf = sxf + x[kk];
+                        acc = acc + (float)u * x[kk];
+                    }
+                float sx8f = 8.0f * sxf;
+                lane[l] = acc - sx8f;
+            }
+        }
+        for (int m = 1; m < 32; m <<= 1) {
+            float nxt[32];
+            for (int l = 0; l < 32; l++) nxt[l] = lane[l] + lane[l ^ m];
+            memcpy(lane, nxt, sizeof(lane));
+        }
+        float scale = isfinite(scales[row]) ? scales[row] : 0.0f;
+        float xs_s = (calibrated ? in_scale : 1.0f) * scale;
+        float y = xs_s * lane[0];
+        float snapped = y;
+        if (isfinite(out_scale) && out_scale != 0.0f) {
+            float c = or_srq_code_f32(y, out_scale);
+            snapped = c * out_scale;
+            if (codes) codes[row] = isnan(c) ? (int8_t)-128 : (int8_t)(int)c;
+        } else if (codes) {
+            codes[row] = 0;
+        }
+        if (out_f32) out_f32[row] = snapped;
+    }
+    free(xq);
+    return 0;
+}

@@ -28,6 +28,12 @@
  *   or_ple_fold_gate       fold(gate split) equals the unsplit qgemv-8bit f32 output (or_qgemv with
  *                          outScale gate_out) bit for bit at every split count; a pure-Python
  *                          replay on tiny K; ties and clamps at the gate snap
+ *   or_qgemv_tile8u        calibrated: equals or_qgemv (the classic oracle) bit for bit on random
+ *                          codes (the same exact integer); f32 on exact-grid fixtures equals
+ *                          or_qgemv bit for bit (every order is exact there); f32 on random data
+ *                          within 2^-18 relative of or_qgemv's f64 sum and equal to a pure-Python
+ *                          replay of the lane order and the butterfly on tiny K; a dropped zero
+ *                          point or a transposed lane mapping fails the grid check
  */
 #ifndef G4_ORACLE_H
 #define G4_ORACLE_H
@@ -129,6 +135,14 @@ void or_ple_fold_gate(const float *partials, int64_t k, int splits, const float 
  * butterfly 1,2,4,8,16. Returns that f32 sum for one row of codes, so a test can say when the
  * reference's per-lane handoff rounds (partials above 2^24) and where it agrees with fround(exact). */
 float or_qgemv_ref_lane_sum(int bits, const uint8_t *row_packed, const int8_t *xq, int64_t k);
+
+/* qgemv.ts:870-1015, the tile8u loop of qgemv-4bit, over the ROW layout (the tile layout is a
+ * permutation of the same codes): calibrated, the exact integer sum per lane, f32 per lane, then
+ * the sgSum32 butterfly; uncalibrated, the loop's own f32 order per lane (k = 128 i + 4 l + j),
+ * then the butterfly. x is f32 (the gelu prologue's values already formed). out_f32 / codes as
+ * or_qgemv. Returns 0, or non-zero when K is not a multiple of 128. */
+int or_qgemv_tile8u(const uint8_t *packed, const float *scales, const float *x, int64_t num_rows,
+                    int64_t k, float in_scale, float out_scale, float *out_f32, int8_t *codes);
 
 /*
  * embedGather.ts:319-344 embedGatherOracle (4-bit row layout) with the sliced guard of

@@ -71,6 +71,9 @@ def lib():
                                         ctypes.c_int, ctypes.c_float, _f32p]
         L.or_ple_fold_gate.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int, _f32p, ctypes.c_float,
                                        ctypes.c_float, _f32p]
+        L.or_qgemv_tile8u.restype = ctypes.c_int
+        L.or_qgemv_tile8u.argtypes = [_u8p, _f32p, _f32p, ctypes.c_int64, ctypes.c_int64,
+                                      ctypes.c_float, ctypes.c_float, _f32p, _i8p]
         L.or_qgemv_ref_lane_sum.restype = ctypes.c_float
         L.or_qgemv_ref_lane_sum.argtypes = [ctypes.c_int, _u8p, _i8p, ctypes.c_int64]
         L.or_embed_gather.restype = ctypes.c_int
@@ -251,6 +254,21 @@ def qgemv_ref_lane_sum(bits: int, row_packed: np.ndarray, xq: np.ndarray, k: int
     row_packed = np.ascontiguousarray(row_packed, dtype=np.uint8)
     xq = np.ascontiguousarray(xq, dtype=np.int8)
     return lib().or_qgemv_ref_lane_sum(bits, _p(row_packed, _u8p), _p(xq, _i8p), k)
+
+
+# qgemv.ts:870-1015 (the tile8u loop; row-layout weights in, the tile layout being a permutation)
+def qgemv_tile8u(packed, scales, x, num_rows, k, in_scale, out_scale):
+    """Returns (dst_f32 [N], codes_i8 [N]) as the tile8u geometry of qgemv-4bit computes them."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(num_rows, dtype=np.float32)
+    codes = np.empty(num_rows, dtype=np.int8)
+    rc = lib().or_qgemv_tile8u(_p(packed, _u8p), _p(scales, _f32p), _p(x, _f32p), num_rows, k,
+                               float(np.float32(in_scale)), float(np.float32(out_scale)),
+                               _p(out, _f32p), _p(codes, _i8p))
+    assert rc == 0, "or_qgemv_tile8u rejected its arguments"
+    return out, codes
 
 
 # embedGather.ts:319-344 (+ sliced guard :188-196)

@@ -39,6 +39,16 @@ throwsWith(() => h.bind('qgemv-8bit-gelu-m2', { inputs: { wq: fake, scales: fake
 throwsWith(() => h.bind('gelu-mul', { inputs: { gate: f32b, up: f32b }, output: f32b, params: { count: 6 } }), 'gelu-mul needs params.count a positive multiple of 4, got 6');
 assert.strictEqual(h.pleGateSplits(), 1);
 
+// the 4-bit geometry's inner loop (qgemv.ts:146, 239-241): classic by default, tile8u selectable,
+// anything else refused; the tile layout's size is ceil(N / 8) tiles of K words
+assert.strictEqual(h.gemvInner(4), 'classic');
+throwsWith(() => h.setGemvInner(4, 'tile16u'), 'inner must be classic or tile8u');
+throwsWith(() => h.setGemvInner(2, 'tile8u'), 'bits must be 4 or 8');
+h.setGemvInner(4, 'tile8u');
+assert.strictEqual(h.gemvInner(4), 'tile8u');
+h.setGemvInner(4, 'classic');
+assert.strictEqual(h.tile8uBytes(1536, 77), 10 * 1536 * 4);
+
 // every name a plan binds on the projection path is registered (plan.ts:487-665 through
 // execute.ts's resolution): a decode step with the split PLE gate and the producer down split, a
 // verify pass of two tokens, batched projections, and a prefill chunk; and what resolveStep

@@ -1,6 +1,6 @@
 'use strict';
 // Every registry kernel's known-answer cases on the GPU through the Node host (runCases, on a
-// stream of its own), then the asynchronous boundary: a bind enqueued on a stream and read back by
+// stream of its own), qgemv-4bit's again on the tile8u geometry, then the asynchronous boundary: a bind enqueued on a stream and read back by
 // downloadAsync, with the event loop shown to run while the device works. Prints one JSON line.
 const path = require('path');
 const h = require(path.join(__dirname, '..', '..', 'gemma4-webgpu-engine_amd', 'host', 'index.js'));
@@ -34,6 +34,40 @@ async function main() {
     asyncOk = asyncOk && again.every((v, i) => v === c.expected[i]);
   }
   graph.destroy();
+  // qgemv-4bit's known-answer cases (exact-grid fixtures: every order is exact) on the tile8u
+  // geometry: the row-layout wq repacked into the eight-row tile layout, bound under
+  // setGemvInner(4, 'tile8u'); the split is refused there, as the reference's generator does
+  let tileOk = true;
+  h.setGemvInner(4, 'tile8u');
+  try {
+    for (const tc of h.KERNELS['qgemv-4bit'].cases) {
+      const ins = {};
+      for (const key of Object.keys(tc.inputs)) ins[key] = h.DeviceBuffer.from(tc.inputs[key]);
+      const tw = new h.DeviceBuffer(h.tile8uBytes(tc.params.k, tc.params.numRows), h.KIND.f32);
+      h.tile8uRepack(ins.wq, tw, tc.params.k, tc.params.numRows, stream);
+      const o = new h.DeviceBuffer(tc.expected.byteLength, tc.expected instanceof Int8Array ? h.KIND.i8 : h.KIND.f32);
+      o.fill(0x7b, stream);
+      h.bind('qgemv-4bit', { inputs: { wq: tw, scales: ins.scales, x: ins.x }, output: o, params: tc.params, stream });
+      const got = new Uint8Array(await o.downloadAsync(stream));
+      const want = new Uint8Array(tc.expected.buffer, tc.expected.byteOffset, tc.expected.byteLength);
+      const same = got.every((v, i) => v === want[i]);
+      if (!same) console.log(`tile8u case ${tc.name} differs`);
+      tileOk = tileOk && same;
+      let refused = false;
+      try {
+        h.bind('qgemv-4bit-split', { inputs: ins, output: o, params: { ...tc.params, kSplits: 2 }, stream });
+      } catch (e) {
+        refused = /tile8u has no K split/.test(e.message);
+      }
+      tileOk = tileOk && refused;
+      Object.values(ins).forEach(b => b.free());
+      tw.free();
+      o.free();
+    }
+  } finally {
+    h.setGemvInner(4, 'classic');
+  }
+  console.log(`tile8u geometry: ${tileOk ? 'ok' : 'FAILED'}`);
   // a refused copy (a NULL address, refused on the host when the copy is enqueued at the call)
   // throws with the library's message
   let rejected = null;
@@ -45,7 +79,7 @@ async function main() {
   Object.values(inputs).forEach(b => b.free());
   out.free();
   stream.destroy();
-  console.log(JSON.stringify({ cases: results.length, failed, asyncOk, rejected: rejected !== null }));
-  if (failed.length || !asyncOk || rejected === null) process.exit(1);
+  console.log(JSON.stringify({ cases: results.length, failed, asyncOk, tileOk, rejected: rejected !== null }));
+  if (failed.length || !asyncOk || !tileOk || rejected === null) process.exit(1);
 }
 main().catch(e => { console.error(e); process.exit(1); });
