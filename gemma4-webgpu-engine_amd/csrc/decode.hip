@@ -325,7 +325,8 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
             if (u == jp) vv[u] = kvnew[kDecThreads + t];
     }
 
-    // scores of this half's heads: eight sequential 32-dim dot products (segment sg) per score,
+    // scores of this half's heads: eight sequential 32-dim dot products (segment sg) per score, one
+    // fused multiply-add (a single rounding) per element, as the CPU restatement's fmaf;
     // then the pairwise tree over the segments by DPP within each aligned 8-lane group:
     // quad_perm(1,0,3,2) and (2,3,0,1) give every lane of a quad ((s0+s1)+(s2+s3)), then
     // row_half_mirror brings the other quad's sum (a commutative last add). With every head
@@ -338,10 +339,10 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
         for (int i4 = 0; i4 < 8; ++i4) {
             const float4 qv = *reinterpret_cast<const float4 *>(qh + 4 * i4);
             const float4 kv = kq[i4];
-            a = __fadd_rn(a, __fmul_rn(qv.x, kv.x));
-            a = __fadd_rn(a, __fmul_rn(qv.y, kv.y));
-            a = __fadd_rn(a, __fmul_rn(qv.z, kv.z));
-            a = __fadd_rn(a, __fmul_rn(qv.w, kv.w));
+            a = __fmaf_rn(qv.x, kv.x, a);
+            a = __fmaf_rn(qv.y, kv.y, a);
+            a = __fmaf_rn(qv.z, kv.z, a);
+            a = __fmaf_rn(qv.w, kv.w, a);
         }
         return a;
     };
@@ -390,7 +391,8 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
     }
     __syncthreads();
 
-    // o[h][d] = sum over positions (ascending) of e[h][j] * v[j][d], for this half's heads; a
+    // o[h][d] = sum over positions (ascending) of e[h][j] * v[j][d] (one fused multiply-add each),
+    // for this half's heads; a
     // whole chunk with every head present takes the guard-free form, whose chains interleave
     auto pv = [&](int h, bool whole) {
         float o = 0.0f;
@@ -400,7 +402,7 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
             const float e[4] = {e4.x, e4.y, e4.z, e4.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                if (whole || u4 + i < cnt) o = __fadd_rn(o, __fmul_rn(e[i], vv[u4 + i]));
+                if (whole || u4 + i < cnt) o = __fmaf_rn(e[i], vv[u4 + i], o);
         }
         return o;
     };
@@ -451,6 +453,41 @@ static void launch_split(int chunks, int rows, hipStream_t st, const float *q, c
 // returns O / L. Every load that does not depend on M goes out first (the chunk's (m, l) pairs
 // and the first kB partials of the thread's dim); M is a shuffle max in each wave and a max over
 // the four waves (max is exact in any order). red: 4 floats, ws / ls: kDecThreads floats of LDS.
+// Up to NB chunks (NB <= 256): every partial of the thread's dimension requested at once (indices
+// clamped, so all valid), then the same ascending sum as the batched form below, so the same bits.
+// The batched form waits one memory round trip per batch of 16 chunks (a 4096-position layer has
+// 128): 1.290 -> 1.277 ms per batch-1 step. Staging the partials through LDS with 16-byte loads
+// instead (a quarter of the load instructions, 146 KB of LDS per block) measured 1.69 ms.
+template <int NB>
+__device__ __forceinline__ float merge_head_dim_all(const float *part_ml, const float *part_o, int64_t slot0,
+                                                    int chunks, float *red, float *ws, float *ls) {
+    const int t = threadIdx.x;
+    float oa[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) oa[u] = part_o[(slot0 + min(u, chunks - 1)) * kDecThreads + t];
+    const float mt = t < chunks ? part_ml[(slot0 + t) * 2] : -__int_as_float(0x7f800000);
+    const float lt = t < chunks ? part_ml[(slot0 + t) * 2 + 1] : 0.0f;
+    const float m = wave_max(mt);  // lane 0 holds the wave's maximum
+    if ((t & 63) == 0) red[t >> 6] = m;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    if (t < chunks) {
+        ws[t] = d_expf(__fsub_rn(mt, M));
+        ls[t] = lt;
+    }
+    __syncthreads();
+    float L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+        if (u < chunks) {
+            L = __fadd_rn(L, __fmul_rn(ls[u], ws[u]));
+            O = __fadd_rn(O, __fmul_rn(oa[u], ws[u]));
+        }
+    }
+    __syncthreads();
+    return __fdiv_rn(O, L);
+}
+
 __device__ __forceinline__ float merge_head_dim(const float *part_ml, const float *part_o, int heads,
                                                 int h, int64_t row, int pos, int window,
                                                 int max_chunks, float *red, float *ws, float *ls) {
@@ -459,6 +496,10 @@ __device__ __forceinline__ float merge_head_dim(const float *part_ml, const floa
     const int lo = window > 0 ? max(0, pos - window + 1) : 0;
     const int chunks = (pos - lo + 1 + kAttnChunk - 1) / kAttnChunk;
     const int64_t slot0 = (row * heads + h) * max_chunks;
+    if (chunks <= 16) return merge_head_dim_all<16>(part_ml, part_o, slot0, chunks, red, ws, ls);
+    if (chunks <= 32) return merge_head_dim_all<32>(part_ml, part_o, slot0, chunks, red, ws, ls);
+    if (chunks <= 64) return merge_head_dim_all<64>(part_ml, part_o, slot0, chunks, red, ws, ls);
+    if (chunks <= 128) return merge_head_dim_all<128>(part_ml, part_o, slot0, chunks, red, ws, ls);
     float oo[kB];
 #pragma unroll
     for (int u = 0; u < kB; ++u) oo[u] = part_o[(slot0 + min(u, chunks - 1)) * kDecThreads + t];

@@ -192,7 +192,7 @@ float g4d_score(const float *q, const float *k, int64_t head_dim) {
     float s[8];
     for (int g = 0; g < 8; ++g) {
         float acc = 0.0f;
-        for (int64_t i = g * seg; i < (g + 1) * seg; ++i) acc = acc + q[i] * k[i];
+        for (int64_t i = g * seg; i < (g + 1) * seg; ++i) acc = fmaf(q[i], k[i], acc);
         s[g] = acc;
     }
     return ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
@@ -224,7 +224,7 @@ void g4d_attention_decode(const float *q, const float *k, const float *v, int64_
             l[c] = g4d_sum(e, cnt);
             for (int64_t i = 0; i < head_dim; ++i) {
                 float a = 0.0f;
-                for (int64_t j = 0; j < cnt; ++j) a = a + e[j] * v[(start + j) * head_dim + i];
+                for (int64_t j = 0; j < cnt; ++j) a = fmaf(e[j], v[(start + j) * head_dim + i], a);
                 o[c * head_dim + i] = a;
             }
         }

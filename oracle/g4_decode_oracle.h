@@ -15,6 +15,8 @@
  *   - 1/sqrt is the IEEE square root then the IEEE divide (WGSL's inverseSqrt allows 2 ULP);
  *   - exp and tanh are g4d_expf / g4d_tanhf below: Cody-Waite range reduction and a degree-6
  *     Taylor polynomial, every operation separately rounded (no FMA), identical on the device;
+ *   - the attention score and P·V sums take one fused multiply-add per element (C fmaf, a single
+ *     IEEE rounding, as the device's v_fma_f32); every other product and sum is rounded apart;
  *   - products and sums follow the WGSL expression order of each reference shader.
  * tests/test_oracle_decode.py pins each function against the reference's own f64 formulation
  * within the reference's stated tolerance, and the math functions against libm.
@@ -86,15 +88,16 @@ void g4d_kv_norm_rope(const int8_t *k_codes, float k_scale, const int8_t *v_code
  * attention.ts:858-918 attention decode of one query position p for `heads` heads sharing one KV
  * head, scale 1.0 (plan.ts:518-519), window w (0: unwindowed; else positions p-w+1 .. p).
  * Split form: positions lo .. p in chunks of G4D_ATTN_CHUNK; per chunk m = max score,
- * e = g4d_expf(s - m), l = fixed-order sum of e, o[d] = sum over positions ascending of e * v[d];
+ * e = g4d_expf(s - m), l = fixed-order sum of e, o[d] = sum over positions ascending of e * v[d]
+ * (each step one fmaf);
  * merge in ascending chunk order with w_c = g4d_expf(m_c - M): L = sum l_c * w_c,
  * O[d] = sum o_c[d] * w_c, out = O / L. A score is eight sequential f32 dot products over the
  * eighths of d, combined by a pairwise tree ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7))
  * (g4d_score).
  * q: [heads][head_dim]; k, v: [positions][head_dim]; out: [heads][head_dim].
  */
-/* The attention score q . k over head_dim (a multiple of 8): sequential sums over each eighth,
- * then the pairwise tree ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)). */
+/* The attention score q . k over head_dim (a multiple of 8): sequential fmaf sums over each
+ * eighth, then the pairwise tree ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)). */
 float g4d_score(const float *q, const float *k, int64_t head_dim);
 
 void g4d_attention_decode(const float *q, const float *k, const float *v, int64_t heads,
