@@ -30,6 +30,8 @@ namespace g4 {
 constexpr int kDecThreads = 256;
 constexpr int kAttnChunk = 32;
 constexpr int kAttnMaxHeads = 8;
+// Word 3 of a gfx9 buffer resource for untyped dword loads (DATA_FORMAT 32, no swizzle).
+constexpr int kBufferRsrcWord3 = 0x00020000;
 
 // d_expf, d_tanhf and d_gelu (the deterministic exp / tanh / gelu) live in g4_internal.h, shared
 // with the GEMV gelu prologues; block_tree_sum, inv_rms and the RMS join row in g4_rowops.h, shared
@@ -138,20 +140,22 @@ struct NormRopeIn {
     float gt[4], c[2], sn[2];
 };
 
+// Every operand is loaded unconditionally (the caller passes valid pointers even for a gain or a
+// rotation it will not apply): a load under a branch makes the compiler wait for it at the branch's
+// end, which put a memory round trip per head ahead of the chunk's K and V loads.
 __device__ __forceinline__ NormRopeIn wave_norm_rope_load(const int8_t *src, const float *gain,
-                                                          const float *cos_row, const float *sin_row,
-                                                          bool rotate) {
+                                                          const float *cos_row, const float *sin_row) {
     const int l = threadIdx.x & 63;
     NormRopeIn in;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         in.code[k] = src[l + 64 * k];
-        in.gt[k] = gain ? gain[l + 64 * k] : 1.0f;
+        in.gt[k] = gain[l + 64 * k];
     }
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-        in.c[k] = rotate ? cos_row[l + 64 * k] : 0.0f;
-        in.sn[k] = rotate ? sin_row[l + 64 * k] : 0.0f;
+        in.c[k] = cos_row[l + 64 * k];
+        in.sn[k] = sin_row[l + 64 * k];
     }
     return in;
 }
@@ -244,20 +248,22 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
     const float *cos_row = PRO ? pro.cos_tab + (int64_t)pos * (kDecThreads / 2) : nullptr;
     const float *sin_row = PRO ? pro.sin_tab + (int64_t)pos * (kDecThreads / 2) : nullptr;
     if (PRO) {
+        // heads past the last and the K / V rows of waves that do not build them read valid
+        // stand-ins (the last head, this row's first query head) whose values go unused
 #pragma unroll
         for (int i = 0; i < QPW; ++i) {
-            const int h = w + WAVES * i;
-            if (h < heads)
-                qin[i] = wave_norm_rope_load(pro.q_codes + (row * heads + h) * kDecThreads,
-                                             pro.q_gain, cos_row, sin_row, true);
+            const int h = min(w + WAVES * i, heads - 1);
+            qin[i] = wave_norm_rope_load(pro.q_codes + (row * heads + h) * kDecThreads, pro.q_gain,
+                                         cos_row, sin_row);
         }
-        if (store_kv && w == 0)
-            kvin = wave_norm_rope_load(pro.k_codes + row * kDecThreads, pro.k_gain, cos_row, sin_row,
-                                       true);
-        if (store_kv && w == 1)
-            kvin = wave_norm_rope_load(pro.v_codes + row * kDecThreads, nullptr, cos_row, sin_row,
-                                       false);
+        const bool kv_wave = store_kv && w < 2;  // wave 0: the K row, wave 1: the V row
+        const int8_t *kv_src = !kv_wave ? pro.q_codes + row * heads * kDecThreads
+                               : w == 0 ? pro.k_codes + row * kDecThreads
+                                        : pro.v_codes + row * kDecThreads;
+        kvin = wave_norm_rope_load(kv_src, kv_wave && w == 0 ? pro.k_gain : pro.q_gain, cos_row,
+                                   sin_row);
     }
+    __builtin_amdgcn_sched_barrier(0);  // the prologue's loads first, then K, then V
     const int j = t >> 3, sg = t & 7;
     float4 kq[8];
     // KST: the chunk's K rows come in as whole-row float4 runs (one load instruction covers
@@ -265,12 +271,24 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
     // each lane reads its own segment (eight loads, each spread over 64 lines)
     constexpr int KPT = KST ? kAttnChunk * kDecThreads / 4 / THREADS : 1;
     float4 kl[KPT];
+    // The chunk's rows start .. start + cnt - 1 of K and V as buffer resources: a load is the
+    // lane's byte offset (one VGPR for every load) plus a scalar row offset, where 64-bit vector
+    // addresses per load would hold two VGPRs each until it issues. Every offset stays inside the
+    // cnt rows (rows clamped to cnt - 1).
+    constexpr int kRowBytes = kDecThreads * 4;
+    const __amdgpu_buffer_rsrc_t kres = __builtin_amdgcn_make_buffer_rsrc(
+        kb + (int64_t)start * kDecThreads, (short)0, cnt * kRowBytes, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vres = __builtin_amdgcn_make_buffer_rsrc(
+        vb + (int64_t)start * kDecThreads, (short)0, cnt * kRowBytes, kBufferRsrcWord3);
     if (KST) {
+        // load i: thread f = tid + i * THREADS takes row f / 64 (wave-uniform), float4 column f % 64
+        const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int lane = tid & 63;
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
-            const int f = tid + i * THREADS, r = f / (kDecThreads / 4), c4 = f % (kDecThreads / 4);
-            kl[i] = reinterpret_cast<const float4 *>(
-                kb + (int64_t)(start + min(r, cnt - 1)) * kDecThreads)[c4];
+            const int r = min(wv + WAVES * i, cnt - 1);
+            kl[i] = __builtin_bit_cast(
+                float4, __builtin_amdgcn_raw_buffer_load_b128(kres, lane * 16, r * kRowBytes, 0));
         }
     } else {
         const float4 *kr = reinterpret_cast<const float4 *>(
@@ -278,10 +296,13 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
 #pragma unroll
         for (int i4 = 0; i4 < 8; ++i4) kq[i4] = kr[i4];
     }
+    __builtin_amdgcn_sched_barrier(0);  // K ahead of V: the wait for K leaves V in flight
     float vv[kAttnChunk];
 #pragma unroll
     for (int u = 0; u < kAttnChunk; ++u)
-        vv[u] = vb[(int64_t)(start + min(u, cnt - 1)) * kDecThreads + t];
+        vv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                              vres, t * 4, min(u, cnt - 1) * kRowBytes, 0));
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the prologue's arithmetic
     if (PRO) {
 #pragma unroll
         for (int i = 0; i < QPW; ++i) {

@@ -328,6 +328,19 @@ def test_decode_step_tiny(gpu, batch, ffn, pos0):
             print("next tokens", got["next"], flush=True)
 
 
+# Fewer than eight query heads: the split kernel's prologue waves past the last head (and the
+# waves that build no K / V row) load stand-in rows whose values go unused; the scores and P.V
+# take the guarded forms. Batch 1 (two halves, K in LDS), batch 32 at position 700 (K in LDS) and
+# at 1000 (per-lane K segments).
+@pytest.mark.parametrize("batch,pos0", [(1, 700), (32, 700), (32, 1000)])
+def test_decode_step_six_heads(gpu, batch, pos0):
+    print(f"decode 6 heads batch={batch} pos0={pos0}", flush=True)
+    shape = tiny_shape(batch, q_heads=6)
+    toks = [[(97 * i + 5) % 3000 for i in range(batch)]]
+    for got, want, dkv, rkv in run_steps(gpu, shape, toks, pos0=pos0):
+        check_step(got, want, dkv, rkv)
+
+
 # Batch 1 folds o_proj into the attention merge (bit 0), gate / up / gelu-mul / down into the FFN
 # block (bit 1) and the per-layer-input pair into its block (bit 2) wherever they fit; each mix of
 # folded and plan forms hands its int32 accumulators or codes to a different join. Hidden 512 fits
