@@ -134,39 +134,56 @@ __global__ __launch_bounds__(kDecThreads) void attn_prologue_kernel(
 // elements l, l + 64, l + 128 and l + 192, so the block tree's levels 128 and 64 are in-lane adds
 // in the same order (x[l]^2 + x[l+128]^2, then + (x[l+64]^2 + x[l+192]^2)) and the rest is the same
 // shuffle tree; the RoPE pairs (i, i + 128) are in-lane too. The operands are loaded first and kept
-// raw (NormRopeIn), so a caller can put them ahead of a longer stream of loads without waiting.
-struct NormRopeIn {
-    int code[4];
-    float gt[4], c[2], sn[2];
+// raw, so a caller can put them ahead of a longer stream of loads without waiting. Every operand is
+// loaded unconditionally (callers pass valid stand-ins for what they will not use): a load under a
+// branch makes the compiler wait for it at the branch's end, which put a memory round trip per
+// head ahead of the chunk's K and V loads. Each load instruction costs the wave the same address
+// work whatever its width, so the codes come as one 4-byte load per lane and the gain and the
+// position's cos / sin row once per wave for all of its vectors.
+struct RopeRow {
+    float c[2], sn[2];
 };
 
-// Every operand is loaded unconditionally (the caller passes valid pointers even for a gain or a
-// rotation it will not apply): a load under a branch makes the compiler wait for it at the branch's
-// end, which put a memory round trip per head ahead of the chunk's K and V loads.
-__device__ __forceinline__ NormRopeIn wave_norm_rope_load(const int8_t *src, const float *gain,
-                                                          const float *cos_row, const float *sin_row) {
+__device__ __forceinline__ RopeRow wave_rope_row(const float *cos_row, const float *sin_row) {
     const int l = threadIdx.x & 63;
-    NormRopeIn in;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        in.code[k] = src[l + 64 * k];
-        in.gt[k] = gain[l + 64 * k];
-    }
+    RopeRow r;
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-        in.c[k] = cos_row[l + 64 * k];
-        in.sn[k] = sin_row[l + 64 * k];
+        r.c[k] = cos_row[l + 64 * k];
+        r.sn[k] = sin_row[l + 64 * k];
     }
-    return in;
+    return r;
+}
+
+__device__ __forceinline__ void wave_gain_load(const float *gain, float (&gt)[4]) {
+    const int l = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) gt[k] = gain[l + 64 * k];
+}
+
+// A 256-code vector (4-byte aligned) as codes 4 l .. 4 l + 3 in lane l; wave_codes_spread hands
+// lane l its codes l + 64 k (from lane l / 4 + 16 k, byte l % 4) by cross-lane reads.
+__device__ __forceinline__ uint32_t wave_codes_word(const int8_t *src) {
+    return reinterpret_cast<const uint32_t *>(src)[threadIdx.x & 63];
+}
+
+__device__ __forceinline__ void wave_codes_spread(uint32_t word, int (&code)[4]) {
+    const int l = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t v = (uint32_t)__builtin_amdgcn_ds_bpermute(((l >> 2) + 16 * k) << 2, (int)word);
+        code[k] = (int)(int8_t)(v >> (8 * (l & 3)));
+    }
 }
 
 // Writes the four results of the lane to out[l + 64 k].
-__device__ __forceinline__ void wave_norm_rope(const NormRopeIn &in, float scale, bool gain,
+__device__ __forceinline__ void wave_norm_rope(const int (&code)[4], const float (&gt)[4],
+                                               const RopeRow &rope, float scale, bool gain,
                                                bool rotate, float eps, float *out) {
     const int l = threadIdx.x & 63;
     float x[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) x[k] = __fmul_rn((float)in.code[k], scale);
+    for (int k = 0; k < 4; ++k) x[k] = __fmul_rn((float)code[k], scale);
     float part = __fadd_rn(__fadd_rn(__fmul_rn(x[0], x[0]), __fmul_rn(x[2], x[2])),
                            __fadd_rn(__fmul_rn(x[1], x[1]), __fmul_rn(x[3], x[3])));
     const float inv = inv_rms(wave_tree_sum(part), kDecThreads, eps);
@@ -174,7 +191,7 @@ __device__ __forceinline__ void wave_norm_rope(const NormRopeIn &in, float scale
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         y[k] = __fmul_rn(x[k], inv);
-        if (gain) y[k] = __fmul_rn(y[k], in.gt[k]);
+        if (gain) y[k] = __fmul_rn(y[k], gt[k]);
     }
     if (!rotate) {
 #pragma unroll
@@ -184,8 +201,8 @@ __device__ __forceinline__ void wave_norm_rope(const NormRopeIn &in, float scale
 #pragma unroll
     for (int k = 0; k < 2; ++k) {  // pair (l + 64 k, l + 64 k + 128)
         const float lo = y[k], hi = y[k + 2];
-        out[l + 64 * k] = __fsub_rn(__fmul_rn(lo, in.c[k]), __fmul_rn(hi, in.sn[k]));
-        out[l + 64 * k + 128] = __fadd_rn(__fmul_rn(hi, in.c[k]), __fmul_rn(lo, in.sn[k]));
+        out[l + 64 * k] = __fsub_rn(__fmul_rn(lo, rope.c[k]), __fmul_rn(hi, rope.sn[k]));
+        out[l + 64 * k + 128] = __fadd_rn(__fmul_rn(hi, rope.c[k]), __fmul_rn(lo, rope.sn[k]));
     }
 }
 
@@ -244,24 +261,27 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
     const bool store_kv = PRO && pro.k_codes && c == chunks - 1;
     // the prologue's few operands go out first, then the chunk's K segment and V rows, so the
     // prologue's arithmetic waits for its own loads only and overlaps the chunk's
-    NormRopeIn qin[QPW], kvin;
-    const float *cos_row = PRO ? pro.cos_tab + (int64_t)pos * (kDecThreads / 2) : nullptr;
-    const float *sin_row = PRO ? pro.sin_tab + (int64_t)pos * (kDecThreads / 2) : nullptr;
+    uint32_t qw[QPW], kvw = 0;
+    float qg[4], kg[4];
+    RopeRow rope;
     if (PRO) {
         // heads past the last and the K / V rows of waves that do not build them read valid
-        // stand-ins (the last head, this row's first query head) whose values go unused
+        // stand-ins (the last head, this row's first query head, the q gain) whose values go unused
+        const float *cos_row = pro.cos_tab + (int64_t)pos * (kDecThreads / 2);
+        const float *sin_row = pro.sin_tab + (int64_t)pos * (kDecThreads / 2);
 #pragma unroll
         for (int i = 0; i < QPW; ++i) {
             const int h = min(w + WAVES * i, heads - 1);
-            qin[i] = wave_norm_rope_load(pro.q_codes + (row * heads + h) * kDecThreads, pro.q_gain,
-                                         cos_row, sin_row);
+            qw[i] = wave_codes_word(pro.q_codes + (row * heads + h) * kDecThreads);
         }
         const bool kv_wave = store_kv && w < 2;  // wave 0: the K row, wave 1: the V row
         const int8_t *kv_src = !kv_wave ? pro.q_codes + row * heads * kDecThreads
                                : w == 0 ? pro.k_codes + row * kDecThreads
                                         : pro.v_codes + row * kDecThreads;
-        kvin = wave_norm_rope_load(kv_src, kv_wave && w == 0 ? pro.k_gain : pro.q_gain, cos_row,
-                                   sin_row);
+        kvw = wave_codes_word(kv_src);
+        wave_gain_load(pro.q_gain, qg);
+        wave_gain_load(kv_wave && w == 0 ? pro.k_gain : pro.q_gain, kg);
+        rope = wave_rope_row(cos_row, sin_row);
     }
     __builtin_amdgcn_sched_barrier(0);  // the prologue's loads first, then K, then V
     const int j = t >> 3, sg = t & 7;
@@ -280,10 +300,11 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
         kb + (int64_t)start * kDecThreads, (short)0, cnt * kRowBytes, kBufferRsrcWord3);
     const __amdgpu_buffer_rsrc_t vres = __builtin_amdgcn_make_buffer_rsrc(
         vb + (int64_t)start * kDecThreads, (short)0, cnt * kRowBytes, kBufferRsrcWord3);
+    // KST, load i: thread f = tid + i * THREADS takes row f / 64 (wave-uniform), float4 column
+    // f % 64, of K and of V
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
     if (KST) {
-        // load i: thread f = tid + i * THREADS takes row f / 64 (wave-uniform), float4 column f % 64
-        const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-        const int lane = tid & 63;
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int r = min(wv + WAVES * i, cnt - 1);
@@ -297,21 +318,40 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
         for (int i4 = 0; i4 < 8; ++i4) kq[i4] = kr[i4];
     }
     __builtin_amdgcn_sched_barrier(0);  // K ahead of V: the wait for K leaves V in flight
-    float vv[kAttnChunk];
+    // KST: V as whole-row float4 runs too, staged through the K copy's LDS once the scores are
+    // done; otherwise lane t loads dim t of every position
+    float4 vl[KST ? KPT : 1];
+    float vv[KST ? 1 : kAttnChunk];
+    if (KST) {
 #pragma unroll
-    for (int u = 0; u < kAttnChunk; ++u)
-        vv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                              vres, t * 4, min(u, cnt - 1) * kRowBytes, 0));
+        for (int i = 0; i < KPT; ++i) {
+            const int r = min(wv + WAVES * i, cnt - 1);
+            vl[i] = __builtin_bit_cast(
+                float4, __builtin_amdgcn_raw_buffer_load_b128(vres, lane * 16, r * kRowBytes, 0));
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < kAttnChunk; ++u)
+            vv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                  vres, t * 4, min(u, cnt - 1) * kRowBytes, 0));
+    }
     __builtin_amdgcn_sched_barrier(0);  // every load issued before the prologue's arithmetic
     if (PRO) {
 #pragma unroll
         for (int i = 0; i < QPW; ++i) {
             const int h = w + WAVES * i;
-            if (h < heads) wave_norm_rope(qin[i], pro.q_scale, true, true, pro.eps, qs + h * kDecThreads);
+            if (h < heads) {
+                int code[4];
+                wave_codes_spread(qw[i], code);
+                wave_norm_rope(code, qg, rope, pro.q_scale, true, true, pro.eps, qs + h * kDecThreads);
+            }
         }
-        if (store_kv && w == 0) wave_norm_rope(kvin, pro.k_scale, true, true, pro.eps, kvnew);
-        if (store_kv && w == 1)
-            wave_norm_rope(kvin, pro.v_scale, false, false, pro.eps, kvnew + kDecThreads);
+        if (store_kv && w < 2) {
+            int code[4];
+            wave_codes_spread(kvw, code);
+            if (w == 0) wave_norm_rope(code, kg, rope, pro.k_scale, true, true, pro.eps, kvnew);
+            else wave_norm_rope(code, kg, rope, pro.v_scale, false, false, pro.eps, kvnew + kDecThreads);
+        }
     } else {
         for (int i = tid; i < heads * kDecThreads; i += THREADS)
             qs[i] = q[row * heads * kDecThreads + i];
@@ -341,9 +381,11 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
             for (int i4 = 0; i4 < 8; ++i4)
                 kq[i4] = *reinterpret_cast<const float4 *>(kvnew + sg * 32 + 4 * i4);
         }
+        if (!KST) {  // KST: the V row is replaced where the rows go to LDS
 #pragma unroll
-        for (int u = 0; u < kAttnChunk; ++u)
-            if (u == jp) vv[u] = kvnew[kDecThreads + t];
+            for (int u = 0; u < kAttnChunk; ++u)
+                if (u == jp) vv[u] = kvnew[kDecThreads + t];
+        }
     }
 
     // scores of this half's heads: eight sequential 32-dim dot products (segment sg) per score, one
@@ -388,6 +430,21 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
         }
     }
     __syncthreads();
+    if (KST) {
+        // the chunk's V rows into the K copy's LDS (every thread read its K operands before the
+        // barrier above), row-major: position u's 256 dims at u * 256 floats; a producer's last
+        // chunk takes the position's new row from kvnew
+        int jp = -1;
+        if constexpr (PRO) jp = store_kv ? pos - start : -1;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int r = wv + WAVES * i;
+            float4 v = vl[i];
+            if constexpr (PRO)
+                if (r == jp) v = *reinterpret_cast<const float4 *>(kvnew + kDecThreads + 4 * lane);
+            ks[r * (kDecThreads / 4) + lane] = v;
+        }
+    }
 
     // per head, uniform within its 32-lane group of half 0: max, exp, the pairwise sum
     const int hh = t >> 5, p = t & 31;
@@ -413,24 +470,28 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
     __syncthreads();
 
     // o[h][d] = sum over positions (ascending) of e[h][j] * v[j][d] (one fused multiply-add each),
-    // for this half's heads; a
-    // whole chunk with every head present takes the guard-free form, whose chains interleave
-    auto pv = [&](int h, bool whole) {
-        float o = 0.0f;
-#pragma unroll
-        for (int u4 = 0; u4 < kAttnChunk; u4 += 4) {  // four weights per LDS read
-            const float4 e4 = *reinterpret_cast<const float4 *>(es + h * kAttnChunk + u4);
-            const float e[4] = {e4.x, e4.y, e4.z, e4.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (whole || u4 + i < cnt) o = __fmaf_rn(e[i], vv[u4 + i], o);
-        }
-        return o;
-    };
+    // for this half's heads; a whole chunk with every head present takes the guard-free form, whose
+    // chains interleave (each V value read once for all of them)
+    const float *vsf = reinterpret_cast<const float *>(ks);
+    auto vval = [&](int u) { return KST ? vsf[u * kDecThreads + t] : vv[u]; };
     if (heads == kAttnMaxHeads && cnt == kAttnChunk) {
         float o[HH];
 #pragma unroll
-        for (int g = 0; g < HH; ++g) o[g] = pv(half * HH + g, true);
+        for (int g = 0; g < HH; ++g) o[g] = 0.0f;
+#pragma unroll
+        for (int u4 = 0; u4 < kAttnChunk; u4 += 4) {  // four weights per LDS read
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = vval(u4 + i);
+#pragma unroll
+            for (int g = 0; g < HH; ++g) {
+                const float4 e4 = *reinterpret_cast<const float4 *>(es + (half * HH + g) * kAttnChunk + u4);
+                o[g] = __fmaf_rn(e4.x, v[0], o[g]);
+                o[g] = __fmaf_rn(e4.y, v[1], o[g]);
+                o[g] = __fmaf_rn(e4.z, v[2], o[g]);
+                o[g] = __fmaf_rn(e4.w, v[3], o[g]);
+            }
+        }
 #pragma unroll
         for (int g = 0; g < HH; ++g)
             part_o[((row * heads + half * HH + g) * max_chunks + c) * kDecThreads + t] = o[g];
@@ -438,7 +499,17 @@ __global__ __launch_bounds__(HALVES * kDecThreads) void attn_split_kernel(
 #pragma unroll
         for (int g = 0; g < HH; ++g) {
             const int h = half * HH + g;
-            if (h < heads) part_o[((row * heads + h) * max_chunks + c) * kDecThreads + t] = pv(h, false);
+            if (h >= heads) continue;
+            float o = 0.0f;
+#pragma unroll
+            for (int u4 = 0; u4 < kAttnChunk; u4 += 4) {
+                const float4 e4 = *reinterpret_cast<const float4 *>(es + h * kAttnChunk + u4);
+                const float e[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (u4 + i < cnt) o = __fmaf_rn(e[i], vval(u4 + i), o);
+            }
+            part_o[((row * heads + h) * max_chunks + c) * kDecThreads + t] = o;
         }
     }
 }
