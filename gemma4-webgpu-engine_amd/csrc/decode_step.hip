@@ -283,7 +283,8 @@ JoinTail make_join(g4_decode &d, int k, const void *src, int src_kind, float src
 // shape's 96 column blocks each walked K = 6144 as two LDS chunks one after the other (18 us);
 // split, 192 blocks take one chunk each and the join adds the two exact int32 partials (step
 // 4.25 -> 4.08 ms). o_proj (K = 2048, one chunk) split the same way measured no faster at batch
-// 32 and slower at batch 3.
+// 32 and slower at batch 3. Four K ranges (384 blocks, so 4 waves each in place of 16, and half
+// the codes copied per block) measured slower: 2.95 against 2.87 ms per batch-32 step.
 // The batch-1 folds' int32 accumulators, [kAccRows][hidden]: o_proj, per_layer_projection, then
 // down_proj's kFfnAccCopies copies.
 constexpr int kAccRows = 2 + kFfnAccCopies;
