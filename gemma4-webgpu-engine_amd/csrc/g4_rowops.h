@@ -14,6 +14,8 @@ namespace g4 {
 
 constexpr int kRowThreads = 256;
 constexpr int kJoinMaxPer = 8;  // an RMS join serves widths up to 8 * 256
+// The stand-in row an RMS join reads for an absent operand (zero-initialized, never written).
+static __device__ float g_join_zero_row[kJoinMaxPer * kRowThreads];
 
 // The in-wave levels s = 32 .. 1 of the pairwise tree (lane l adds lane l + s for l < s), with
 // the total in every lane: s = 32 and 16 by the gfx950 lane swaps (v_permlane32_swap hands lanes
@@ -149,7 +151,9 @@ struct NoLoads {
 // (a wave's loads complete in issue order) while the caller's stay in flight under its arithmetic.
 // PER: elements per thread the caller provides for (width <= PER * 256; a caller that knows the
 // width issues no loads past it).
-template <int ACC = 0, int PER = kJoinMaxPer, typename Emit, typename Loads = NoLoads>
+// G2 false: the join has no second gain (J.gain2 null, checked by the launcher), so that operand
+// is neither loaded nor tested.
+template <int ACC = 0, int PER = kJoinMaxPer, bool G2 = true, typename Emit, typename Loads = NoLoads>
 __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row, float *lds,
                                                   Emit emit, Loads after_loads = Loads()) {
     static_assert(PER >= 1 && PER <= kJoinMaxPer, "an RMS join serves widths up to 8 * 256");
@@ -181,13 +185,24 @@ __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row
 #pragma unroll
         for (int e = 0; e < PER; ++e) raw[e] = src[ic[e]];
     }
+    // An absent gain, residual or second gain is read from a row of zeros in its place, so the
+    // loads stay unconditional: a load in one arm of a branch and a constant in the other made the
+    // compiler wait for every load in flight on the constant's path.
+    const bool g2on = G2 && J.gain2 != nullptr;
+    const float *gp = J.gain ? J.gain : g_join_zero_row;
+    const float *rp = J.resid ? J.resid + base : g_join_zero_row;
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
-        ga[e] = J.gain ? J.gain[ic[e]] : 1.0f;
-        re[e] = J.resid ? J.resid[base + ic[e]] : 0.0f;
-        g2[e] = J.gain2 ? J.gain2[ic[e]] : 0.0f;
+        ga[e] = gp[ic[e]];
+        re[e] = rp[ic[e]];
+        g2[e] = g2on ? J.gain2[ic[e]] : 0.0f;
     }
     after_loads();
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        ga[e] = J.gain ? ga[e] : 1.0f;
+        re[e] = J.resid ? re[e] : 0.0f;
+    }
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
         const bool in = t + e * kRowThreads < width;
@@ -217,10 +232,10 @@ __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row
         }
         v[e] = y;
         if (J.hidden) J.hidden[base + i] = y;
-        if (J.gain2) part2 = __fadd_rn(part2, __fmul_rn(y, y));
+        if (g2on) part2 = __fadd_rn(part2, __fmul_rn(y, y));
     }
     if (!J.codes) return;
-    if (J.gain2) {
+    if (g2on) {
         const float inv2 = inv_rms(block_tree_sum(part2, lds + kRowThreads), width, J.eps);
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
@@ -237,11 +252,11 @@ __device__ __forceinline__ void rms_join_row_emit(const JoinTail &J, int64_t row
 }
 
 // The join kernel's form: codes to J.codes[row][i]. lds: 512 floats.
-template <int ACC = 0, int PER = kJoinMaxPer>
+template <int ACC = 0, int PER = kJoinMaxPer, bool G2 = true>
 __device__ __forceinline__ void rms_join_row(const JoinTail &J, int64_t row, float *lds) {
     int8_t *codes = J.codes;
     const int64_t base = row * J.width;
-    rms_join_row_emit<ACC, PER>(J, row, lds, [=](int i, int8_t c) { codes[base + i] = c; });
+    rms_join_row_emit<ACC, PER, G2>(J, row, lds, [=](int i, int8_t c) { codes[base + i] = c; });
 }
 
 // The elements per thread a launcher instantiates for a row of `width`: 6 up to 1536 (the E2B
