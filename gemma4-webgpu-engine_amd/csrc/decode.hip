@@ -1216,6 +1216,9 @@ int attention_decode_fused(const AttnPrologue &pro, float *k_cache, float *v_cac
         return set_error(G4_ERR_INVALID, "attention (fused prologue): bad arguments");
     if (pro.k_codes && (!pro.v_codes || !pro.k_gain))
         return set_error(G4_ERR_INVALID, "attention (fused prologue): k without v or k gain");
+    // the prologue reads each 256-code vector as one 4-byte word per lane
+    if (((uintptr_t)pro.q_codes | (uintptr_t)pro.k_codes | (uintptr_t)pro.v_codes) & 3)
+        return set_error(G4_ERR_INVALID, "attention (fused prologue): code rows not 4-byte aligned");
     const int chunks = attn_chunks(pos, window);
     if (workspace_bytes < g4_attention_workspace_bytes(rows, heads, pos, window))
         return set_error(G4_ERR_INVALID, "attention (fused prologue): workspace too small");
